@@ -1,0 +1,231 @@
+/*
+ * jk.h -- C ABI of the MI355X (gfx950) quantized-matmul library `libjk.so`.
+ *
+ * Drop-in replacement for the quant / quant_q8 / repack / BitLinear hot path of
+ * jero-kernels-rvv. Every entry point below names the reference interface it
+ * replaces (file:line relative to the reference crate root). Signatures are
+ * plain C: pointers and sizes, no C++ or torch types.
+ *
+ * Two tiers:
+ *  - device tier (jk_*):   weights live on the GPU in a jk_weight handle, activations
+ *                          and outputs are device pointers, work is enqueued on a
+ *                          stream (hipStream_t, NULL = default stream) and returns
+ *                          without synchronizing;
+ *  - host tier (jk_host_*): synchronous, host-memory mirrors of the reference's
+ *                          signatures (copy in, launch, copy out, synchronize).
+ *
+ * Errors: every call validates its arguments before touching any memory and returns
+ * a jk_status. JK_TENSOR_BOUNDS and JK_CAPABILITY_MISMATCH mirror
+ * K3Error::TensorBoundsError / K3Error::CapabilityMismatch; jk_last_error() returns a
+ * thread-local description of the most recent failure on the calling thread.
+ * Outputs are fully overwritten, never accumulated into.
+ *
+ * Numerics: activation quantization and block dequantization are bit-exact with the
+ * reference's portable scalar fallback; dot products, GEMV, GEMM and BitLinear are
+ * evaluated with the reference's per-block arithmetic and its block-order f32
+ * accumulation, so they are bit-exact as well.
+ */
+#ifndef JK_H
+#define JK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JK_ABI_VERSION 1
+
+typedef enum jk_status {
+    JK_OK = 0,
+    JK_TENSOR_BOUNDS = 1,       /* K3Error::TensorBoundsError */
+    JK_CAPABILITY_MISMATCH = 2, /* K3Error::CapabilityMismatch */
+    JK_DEVICE_ERROR = 3         /* HIP runtime failure (no reference counterpart) */
+} jk_status;
+
+/* GGML type ids of the jero_core::QuantType variants on this path. */
+typedef enum jk_quant {
+    JK_Q4_0 = 2,
+    JK_Q8_0 = 8,
+    JK_Q4_K = 12, /* QuantType::Q4_K_M */
+    JK_Q6_K = 14,
+    JK_TQ2_0 = 35,
+    JK_I2_S = 36
+} jk_quant;
+
+/* BlockQ8_0 (quant_q8.rs:37-44): #[repr(C)] { d: f32, qs: [i8; 32] }, 36 bytes. */
+typedef struct jk_block_q8_0 {
+    float d;
+    int8_t qs[32];
+} jk_block_q8_0;
+
+/* BlockQ8K (quant_q8.rs:62-72): #[repr(C)] { d: f32, qs: [i8; 256], bsums: [i16; 16] }, 292 bytes. */
+typedef struct jk_block_q8k {
+    float d;
+    int8_t qs[256];
+    int16_t bsums[16];
+} jk_block_q8k;
+
+/* The fields of jero_core::TensorView the path reads (name, quant, shape, bytes). */
+typedef struct jk_tensor_view {
+    const char *name;
+    int32_t quant; /* jk_quant */
+    const size_t *shape;
+    size_t ndim;
+    const void *bytes; /* host memory */
+    size_t byte_len;
+} jk_tensor_view;
+
+/* QuantizedActQ8 (repack.rs:462-486) on the device, as logical row-major arrays carved
+ * from one caller-owned device buffer by jk_act_q8_bind. */
+typedef struct jk_act_q8 {
+    size_t m, k, k_padded, k_blocks32, k_chunks, sb256;
+    int8_t *qs;      /* [m][k_padded]   quantized values (repack.rs:474 tiles, untiled) */
+    float *scales;   /* [m][k_blocks32] x_scales */
+    float *sums;     /* [m][k_blocks32] x_sums (sequential f32 sums) */
+    float *sums16;   /* [m][k_chunks]   x_sums_16 */
+    float *super256; /* [m][sb256]      super_scales_256 */
+} jk_act_q8;
+
+typedef void *jk_stream; /* hipStream_t; NULL is the default stream */
+typedef struct jk_weight jk_weight;
+
+typedef struct jk_weight_info {
+    int32_t quant;
+    size_t rows, cols;
+    size_t device_bytes; /* bytes of the device layout */
+    size_t gguf_bytes;   /* bytes of the GGUF payload it was built from */
+} jk_weight_info;
+
+/* ---------------------------------------------------------------- runtime */
+const char *jk_last_error(void);
+int jk_abi_version(void);
+/* Selects the device for this thread's subsequent calls. */
+jk_status jk_init(int device);
+jk_status jk_stream_create(jk_stream *out);
+jk_status jk_stream_destroy(jk_stream s);
+jk_status jk_stream_sync(jk_stream s);
+/* Plain device memory for callers that bring no allocator of their own. */
+jk_status jk_device_alloc(size_t bytes, void **out);
+jk_status jk_device_free(void *p);
+jk_status jk_copy_to_device(jk_stream s, void *dst, const void *src, size_t bytes);
+jk_status jk_copy_to_host(jk_stream s, void *dst, const void *src, size_t bytes);
+
+/* ---------------------------------------------------------------- weights */
+/* RepackedWeight::from_tensor (repack.rs:2288-2300) / RepackedWeight::repack when
+ * rows == cols == 0 (repack.rs:2255-2285): copies the GGUF payload to the device and
+ * rewrites it there into the plane layout (same byte count as GGUF). Validation follows
+ * validate_matrix_view (repack.rs:1208-1281). The handle is immutable and may be used
+ * from any thread and stream once the upload stream has completed. */
+jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, size_t cols,
+                           jk_weight **out);
+jk_status jk_weight_free(jk_weight *w);
+jk_status jk_weight_get_info(const jk_weight *w, jk_weight_info *out);
+/* dequantize_tensor_row (quant.rs:2492-2568) over output rows [row_begin, row_end):
+ * out[(row - row_begin) * cols + col], bit-exact with the GGUF block dequantizers.
+ * RepackedWeight::dequantize_row (repack.rs:2529-2598) agrees up to the sign of zero. */
+jk_status jk_weight_dequantize_rows(jk_stream s, const jk_weight *w, size_t row_begin,
+                                    size_t row_end, float *out, size_t out_len);
+
+/* ------------------------------------------------- activation quantization */
+/* quantize_row_q8_0 (quant_q8.rs:395) over n = out_blocks * 32 values (any number of
+ * rows laid end to end). */
+jk_status jk_quantize_row_q8_0(jk_stream s, const float *x, size_t n, jk_block_q8_0 *out,
+                               size_t out_blocks);
+/* quantize_row_q8_k (quant_q8.rs:576-594). */
+jk_status jk_quantize_row_q8_k(jk_stream s, const float *x, size_t n, jk_block_q8k *out,
+                               size_t out_blocks);
+/* Device bytes that jk_act_q8_bind needs for an [m, k] batch. */
+size_t jk_act_q8_bytes(size_t m, size_t k);
+jk_status jk_act_q8_bind(void *storage, size_t storage_len, size_t m, size_t k, jk_act_q8 *out);
+/* QuantizedActQ8::quantize_into (repack.rs:542-650). */
+jk_status jk_quantize_act_q8(jk_stream s, const float *x, size_t m, size_t k, const jk_act_q8 *act);
+/* subln_quantize_absmax_i8 (lib.rs:1042-1101) applied to each of m rows:
+ * q[m][k], scales[m]. */
+jk_status jk_subln_quantize_absmax_i8(jk_stream s, const float *x, const float *norm_w,
+                                      size_t m, size_t k, float eps, int8_t *q, float *scales);
+/* The same per-token absmax recipe (lib.rs:1072-1098) without the RMSNorm step. */
+jk_status jk_quantize_absmax_i8(jk_stream s, const float *x, size_t m, size_t k, int8_t *q,
+                                float *scales);
+
+/* ---------------------------------------------- quant_q8 integer GEMV (M=1) */
+/* gemv_q4_0_q8_0 (quant_q8.rs:1586-1605), gemv_q8_0_q8_0 (1670-1689),
+ * gemv_q4_k_q8_k (3101-3123), gemv_q6_k_q8_k (3189-3211), gemv_tq2_0_q8_k (3250-3273):
+ * y[rows] from the weight handle and nx pre-quantized activation blocks. */
+jk_status jk_gemv_q4_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx,
+                            float *y, size_t y_len);
+jk_status jk_gemv_q8_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx,
+                            float *y, size_t y_len);
+jk_status jk_gemv_q4_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx,
+                            float *y, size_t y_len);
+jk_status jk_gemv_q6_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx,
+                            float *y, size_t y_len);
+jk_status jk_gemv_tq2_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx,
+                             float *y, size_t y_len);
+/* Row-sliced form of the five above (format taken from the handle): writes
+ * y[row - row_begin] for rows [row_begin, row_end), identical to the full call. */
+jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t nx, float *y,
+                          size_t row_begin, size_t row_end);
+
+/* ------------------------------------------ f32-activation matvec (vec_dot) */
+/* vec_dot_q4_0 (quant.rs:1458), vec_dot_q8_0 (1069), vec_dot_q6_k (1089),
+ * VectorKernel::vec_dot_q4_k_m (lib.rs:157, scalar impl 1268-1303), vec_dot_i2_s
+ * (quant.rs:2199-2240): dequantize each block and dot it with f32 x. */
+jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y,
+                         size_t y_len);
+
+/* ----------------------------------------------------- repacked GEMV / GEMM */
+/* gemm_repacked_rows (repack.rs:4087-4094) / RepackedWeight::gemm_rows (2661-2668):
+ * y[m][row - row_begin] for rows [row_begin, row_end), y_len = m * (row_end - row_begin).
+ * gemv_repacked_rows (repack.rs:4014-4061) is the m == 1 case. */
+jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
+                           size_t y_len, size_t row_begin, size_t row_end);
+/* gemv_repacked_view_rows (repack.rs:4045-4061): requires act->m == 1. */
+jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
+                           size_t y_len, size_t row_begin, size_t row_end);
+
+/* -------------------------------------------------------------- BitLinear */
+/* bitlinear_i8_rvv (ime.rs:882-938) applied to m tokens: y[m][rows] from act[m][k]
+ * and one f32 scale per token (TQ2_0, I2_S and Q8_0 weights). */
+jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act,
+                          const float *act_scales, size_t m, size_t k, float *y, size_t y_len);
+
+/* ------------------------------------------- host tier (synchronous mirrors) */
+/* quantize_row_q8_0 (quant_q8.rs:395), quantize_row_q8_k (576). */
+jk_status jk_host_quantize_row_q8_0(const float *x, size_t n, jk_block_q8_0 *out, size_t out_len);
+jk_status jk_host_quantize_row_q8_k(const float *x, size_t n, jk_block_q8k *out, size_t out_len);
+/* vec_dot_q4_0_q8_0 (quant_q8.rs:1463), vec_dot_q8_0_q8_0 (1493), vec_dot_q4_k_q8_k (3019),
+ * vec_dot_q6_k_q8_k (3056), vec_dot_tq2_0_q8_k (3086): one row of blocks -> *out. */
+jk_status jk_host_vec_dot_q4_0_q8_0(const void *w, size_t w_len, const jk_block_q8_0 *x, size_t nx, float *out);
+jk_status jk_host_vec_dot_q8_0_q8_0(const void *w, size_t w_len, const jk_block_q8_0 *x, size_t nx, float *out);
+jk_status jk_host_vec_dot_q4_k_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
+jk_status jk_host_vec_dot_q6_k_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
+jk_status jk_host_vec_dot_tq2_0_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
+/* gemv_q4_0_q8_0 (quant_q8.rs:1586) ... gemv_tq2_0_q8_k (3250) with a TensorView. */
+jk_status jk_host_gemv_q4_0_q8_0(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx);
+jk_status jk_host_gemv_q8_0_q8_0(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx);
+jk_status jk_host_gemv_q4_k_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
+jk_status jk_host_gemv_q6_k_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
+jk_status jk_host_gemv_tq2_0_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
+/* vec_dot_q4_0 (quant.rs:1458), vec_dot_q8_0 (1069), vec_dot_q6_k (1089),
+ * VectorKernel::vec_dot_q4_k_m (lib.rs:157), vec_dot_i2_s (quant.rs:2199). */
+jk_status jk_host_vec_dot_q4_0(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q8_0(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q6_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q4_k_m(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_i2_s(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+/* dequantize_tensor_row / dequantize_token_row (quant.rs:2492, 2580). */
+jk_status jk_host_dequantize_tensor_row(const jk_tensor_view *w, size_t row, float *out, size_t out_len);
+/* gemm_repacked_f32_rows (repack.rs:4143-4165): quantizes input [m, cols] with
+ * QuantizedActQ8 semantics, then the repacked GEMM; out[m][row_end - row_begin]. */
+jk_status jk_host_gemm_repacked_f32(float *out, size_t out_len, const jk_weight *w, const float *input,
+                                   size_t m, size_t row_begin, size_t row_end);
+/* bitlinear_i8_rvv (ime.rs:882-938). */
+jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view *w, const int8_t *act,
+                               size_t act_len, float act_scale);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JK_H */

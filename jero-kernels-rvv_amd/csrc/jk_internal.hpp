@@ -1,0 +1,117 @@
+// jk_internal.hpp -- shared host/device definitions of libjk (gfx950 only).
+//
+// Device weight layout ("plane layout"). A GGUF block of a row is cut into C
+// 16-byte chunks; chunk c of block b of row r lives in plane c at
+//     planes + ((c * rows + r) * nb + b) * 16
+// and the block's f16 scale, when it is not inside a chunk, lives in the scale
+// plane at dplane[r * nb + b]. Lanes that walk consecutive blocks of one row
+// therefore read consecutive 16-byte chunks (one coalesced 128-bit load per
+// lane per plane), and the layout holds exactly the GGUF bytes:
+//
+//   format  block  bytes  chunks (16 B)                         scale plane
+//   Q4_0     32     18    qs[0..16)                             d
+//   Q8_0     32     34    qs[0..16), qs[16..32)                 d
+//   Q4_K    256    144    [d dmin scales12], qs[16c..16c+16)    -
+//   Q6_K    256    210    ql x8, qh x4, scales x1               d
+//   TQ2_0   256     66    qs x4 (2-bit fields transposed 4x4    d
+//                         inside every dword, see below)
+//   I2_S    128     32    bytes[0..16), bytes[16..32)           - (tensor scale)
+//
+// TQ2_0 transposition: GGUF byte i of a dword holds elements 4i+j in bits 2j.
+// The device dword holds element 4j+i in bits 2j of byte i, so that
+// (w >> 2j) & 0x03030303 is the four elements of activation dword j.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/jk.h"
+
+namespace jk {
+
+struct Fmt {
+    int quant;
+    int be;      // elements per block
+    int bb;      // GGUF bytes per block
+    int chunks;  // 16-byte chunks per block in the planes
+    int d_off;   // byte offset of the f16 scale inside the GGUF block, -1 if none
+    int q_off;   // byte offset of chunk 0 inside the GGUF block
+};
+
+__host__ __device__ constexpr Fmt fmt_of(int q) {
+    return q == JK_Q4_0   ? Fmt{JK_Q4_0, 32, 18, 1, 0, 2}
+           : q == JK_Q8_0 ? Fmt{JK_Q8_0, 32, 34, 2, 0, 2}
+           : q == JK_Q4_K ? Fmt{JK_Q4_K, 256, 144, 9, -1, 0}
+           : q == JK_Q6_K ? Fmt{JK_Q6_K, 256, 210, 13, 208, 0}
+           : q == JK_TQ2_0 ? Fmt{JK_TQ2_0, 256, 66, 4, 0, 2}
+           : q == JK_I2_S  ? Fmt{JK_I2_S, 128, 32, 2, -1, 0}
+                           : Fmt{0, 0, 0, 0, -1, 0};
+}
+
+inline bool fmt_known(int q) { return fmt_of(q).be != 0; }
+inline size_t trailer_bytes(int q) { return q == JK_I2_S ? 32 : 0; }
+
+// Plain-old-data view of a weight handle that kernels take by value.
+struct WeightDev {
+    const uint8_t *planes;
+    const uint16_t *dplane;
+    float tensor_scale;
+    int quant;
+    int rows;
+    int cols;
+    int nb;
+};
+
+}  // namespace jk
+
+struct jk_weight {
+    jk::WeightDev dev;
+    int device;
+    size_t device_bytes;
+    size_t gguf_bytes;
+    void *alloc;  // base of the device allocation (planes, then scale plane)
+};
+
+namespace jk {
+
+// Thread-local error reporting behind jk_last_error().
+jk_status fail(jk_status st, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+jk_status hip_fail(hipError_t e, const char *what);
+void clear_error();
+
+#define JK_HIP(expr)                                          \
+    do {                                                      \
+        hipError_t e_ = (expr);                               \
+        if (e_ != hipSuccess) return ::jk::hip_fail(e_, #expr); \
+    } while (0)
+
+#define JK_TRY(expr)                    \
+    do {                                \
+        jk_status s_ = (expr);          \
+        if (s_ != JK_OK) return s_;     \
+    } while (0)
+
+// Orientation / byte-length validation shared by the matvec entry points.
+jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, size_t in_len, size_t *rows,
+                          size_t *cols);
+
+// Checks the last kernel launch on the current thread.
+jk_status check_launch(const char *what);
+
+// Kernel launchers (device tier internals). All arguments are validated by callers.
+jk_status launch_repack(hipStream_t s, const WeightDev &w, const uint8_t *gguf);
+jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1, float *out);
+jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk_block_q8_0 *out);
+jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk_block_q8k *out);
+jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 &a);
+jk_status launch_absmax_i8(hipStream_t s, const float *x, const float *norm_w, size_t m, size_t k,
+                           float eps, int8_t *q, float *scales);
+jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1);
+jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y);
+jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act,
+                           const float *act_scales, int m, float *y);
+jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y,
+                               int r0, int r1);
+
+}  // namespace jk

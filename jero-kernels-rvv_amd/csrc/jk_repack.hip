@@ -1,0 +1,181 @@
+// jk_repack.hip -- GGUF -> plane layout on the device, and row dequantization from it.
+#include "jk_device.hpp"
+
+namespace jk {
+
+// 4x4 transpose of the 2-bit fields of one TQ2_0 dword (see jk_internal.hpp).
+__device__ __forceinline__ uint32_t tq2_transpose(uint32_t v) {
+    uint32_t o = 0;
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) {
+            uint32_t t = (v >> (8 * j + 2 * i)) & 3u;  // element 4j+i of the GGUF dword
+            o |= t << (8 * i + 2 * j);                  // byte i, field j
+        }
+    return o;
+}
+
+// One thread per (row, block): cut the GGUF block into its 16-byte chunks and scale.
+// The stores are the only writes of the planes; the weight handle is read-only after.
+__global__ __launch_bounds__(256) void repack_kernel(WeightDev w, const uint8_t *__restrict__ g) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)w.rows * (size_t)w.nb;
+    if (idx >= total) return;
+    const Fmt f = fmt_of(w.quant);
+    const uint8_t *src = g + idx * (size_t)f.bb;
+    const int r = (int)(idx / (size_t)w.nb), b = (int)(idx % (size_t)w.nb);
+    for (int c = 0; c < f.chunks; ++c) {
+        uint32_t d4[4];
+        for (int k = 0; k < 4; ++k) {
+            const uint8_t *p = src + f.q_off + 16 * c + 4 * k;
+            d4[k] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+            if (f.quant == JK_TQ2_0) d4[k] = tq2_transpose(d4[k]);
+        }
+        uint4 *dst = const_cast<uint4 *>(chunk_ptr(w, c, r, b));
+        *dst = make_uint4(d4[0], d4[1], d4[2], d4[3]);
+    }
+    if (f.d_off >= 0) {
+        uint16_t h = (uint16_t)(src[f.d_off] | (src[f.d_off + 1] << 8));
+        const_cast<uint16_t *>(w.dplane)[idx] = h;
+    }
+}
+
+jk_status launch_repack(hipStream_t s, const WeightDev &w, const uint8_t *gguf) {
+    const size_t total = (size_t)w.rows * (size_t)w.nb;
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, w, gguf);
+    return check_launch("repack_kernel");
+}
+
+__device__ __forceinline__ uint8_t chunk_byte(const uint4 &v, int i) {
+    const uint32_t d = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return (uint8_t)(d >> (8 * (i & 3)));
+}
+
+// Dequantizes block b of row r into out[0..be) with the GGUF block dequantizers' arithmetic:
+// dequantize_q4_0_block (quant.rs:550-568), dequantize_q8_0_block (571-588),
+// dequantize_q4_k_m_block (lib.rs:720-766), dequantize_q6_k_block (quant.rs:594-648),
+// the TQ2_0 arm (quant.rs:2369-2378) and dequantize_i2_s_block (quant.rs:380-387).
+__device__ void dequant_block(const WeightDev &w, int r, int b, float *out) {
+    switch (w.quant) {
+    case JK_Q4_0: {
+        const float d = ld_dscale(w, r, b);
+        const uint4 q = ld_chunk(w, 0, r, b);
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t x = chunk_byte(q, i);
+            out[i] = d == 0.0f ? 0.0f : d * (float)((int)(x & 15) - 8);
+            out[i + 16] = d == 0.0f ? 0.0f : d * (float)((int)(x >> 4) - 8);
+        }
+        break;
+    }
+    case JK_Q8_0: {
+        const float d = ld_dscale(w, r, b);
+        for (int c = 0; c < 2; ++c) {
+            const uint4 q = ld_chunk(w, c, r, b);
+            for (int i = 0; i < 16; ++i) out[16 * c + i] = d == 0.0f ? 0.0f : d * (float)(int8_t)chunk_byte(q, i);
+        }
+        break;
+    }
+    case JK_Q4_K: {
+        const uint4 h = ld_chunk(w, 0, r, b);
+        const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
+        uint8_t s[12], sc[8], m[8];
+        for (int i = 0; i < 12; ++i) s[i] = chunk_byte(h, 4 + i);
+        for (int j = 0; j < 4; ++j) { sc[j] = s[j] & 63; m[j] = s[j + 4] & 63; }
+        for (int j = 4; j < 8; ++j) {
+            sc[j] = (uint8_t)((s[j + 4] & 15) | ((s[j - 4] >> 6) << 4));
+            m[j] = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+        }
+        for (int c = 0; c < 4; ++c) {
+            const float d1 = d * (float)sc[2 * c], m1 = dmin * (float)m[2 * c];
+            const float d2 = d * (float)sc[2 * c + 1], m2 = dmin * (float)m[2 * c + 1];
+            for (int half = 0; half < 2; ++half) {
+                const uint4 q = ld_chunk(w, 1 + 2 * c + half, r, b);
+                for (int i = 0; i < 16; ++i) {
+                    const uint8_t x = chunk_byte(q, i);
+                    const int l = 16 * half + i;
+                    out[64 * c + l] = d1 * (float)(x & 15) - m1;
+                    out[64 * c + 32 + l] = d2 * (float)(x >> 4) - m2;
+                }
+            }
+        }
+        break;
+    }
+    case JK_Q6_K: {
+        const float d = ld_dscale(w, r, b);
+        if (d == 0.0f) {
+            for (int i = 0; i < 256; ++i) out[i] = 0.0f;
+            break;
+        }
+        const uint4 scv = ld_chunk(w, 12, r, b);
+        for (int h = 0; h < 2; ++h) {
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int li = 64 * h + l, hi = 64 * h + l + 32, qi = 32 * h + l;
+                const uint8_t L = chunk_byte(ld_chunk(w, li / 16, r, b), li % 16);
+                const uint8_t H = chunk_byte(ld_chunk(w, hi / 16, r, b), hi % 16);
+                const uint8_t Q = chunk_byte(ld_chunk(w, 8 + qi / 16, r, b), qi % 16);
+                const int q1 = (int)((L & 15) | ((Q & 3) << 4)) - 32;
+                const int q2 = (int)((H & 15) | (((Q >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((L >> 4) | (((Q >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((H >> 4) | (((Q >> 6) & 3) << 4)) - 32;
+                const int sb = 8 * h + is;
+                out[128 * h + l] = d * (float)(int8_t)chunk_byte(scv, sb) * (float)q1;
+                out[128 * h + l + 32] = d * (float)(int8_t)chunk_byte(scv, sb + 2) * (float)q2;
+                out[128 * h + l + 64] = d * (float)(int8_t)chunk_byte(scv, sb + 4) * (float)q3;
+                out[128 * h + l + 96] = d * (float)(int8_t)chunk_byte(scv, sb + 6) * (float)q4;
+            }
+        }
+        break;
+    }
+    case JK_TQ2_0: {
+        const float d = ld_dscale(w, r, b);
+        for (int c = 0; c < 4; ++c) {
+            const uint4 q = ld_chunk(w, c, r, b);
+            const uint32_t dw[4] = {q.x, q.y, q.z, q.w};
+            for (int k = 0; k < 4; ++k)
+                for (int p = 0; p < 16; ++p) {  // element p of the dword: byte p%4, field p/4
+                    const int t = (int)((dw[k] >> (8 * (p & 3) + 2 * (p >> 2))) & 3u) - 1;
+                    out[64 * c + 16 * k + p] = d == 0.0f ? 0.0f : d * (float)t;
+                }
+        }
+        break;
+    }
+    case JK_I2_S: {
+        const float sc = w.tensor_scale;
+        for (int c = 0; c < 2; ++c) {
+            const uint4 q = ld_chunk(w, c, r, b);
+            for (int i = 0; i < 16; ++i) {
+                const uint8_t x = chunk_byte(q, i);
+                const int g = 16 * c + i;
+                const int t0 = ((x >> 6) & 3) - 1, t1 = ((x >> 4) & 3) - 1, t2 = ((x >> 2) & 3) - 1, t3 = (x & 3) - 1;
+                out[g] = sc == 0.0f ? 0.0f : sc * (float)t0;
+                out[32 + g] = sc == 0.0f ? 0.0f : sc * (float)t1;
+                out[64 + g] = sc == 0.0f ? 0.0f : sc * (float)t2;
+                out[96 + g] = sc == 0.0f ? 0.0f : sc * (float)t3;
+            }
+        }
+        break;
+    }
+    default: break;
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_rows_kernel(WeightDev w, int r0, int r1, float *__restrict__ out) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)(r1 - r0) * (size_t)w.nb;
+    if (idx >= total) return;
+    const int r = r0 + (int)(idx / (size_t)w.nb), b = (int)(idx % (size_t)w.nb);
+    const Fmt f = fmt_of(w.quant);
+    float buf[256];
+    dequant_block(w, r, b, buf);
+    float *dst = out + (size_t)(r - r0) * (size_t)w.cols + (size_t)b * f.be;
+    for (int i = 0; i < f.be; ++i) dst[i] = buf[i];
+}
+
+jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1, float *out) {
+    const size_t total = (size_t)(r1 - r0) * (size_t)w.nb;
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, w, r0, r1, out);
+    return check_launch("dequant_rows_kernel");
+}
+
+}  // namespace jk

@@ -1,0 +1,463 @@
+// jk_runtime.hip -- device-tier C ABI of libjk: errors, streams, weight handles,
+// activation buffers and the argument validation of every entry point.
+//
+// Validation mirrors the reference validators cited at each entry and always runs
+// before any device work is enqueued (fail closed).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <cmath>
+#include <string>
+
+#include "jk_internal.hpp"
+
+namespace jk {
+
+static thread_local std::string g_err;
+
+jk_status fail(jk_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return st;
+}
+
+jk_status hip_fail(hipError_t e, const char *what) {
+    return fail(JK_DEVICE_ERROR, "%s failed: %s", what, hipGetErrorString(e));
+}
+
+void clear_error() { g_err.clear(); }
+
+jk_status check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return JK_OK;
+}
+
+static const char *quant_name(int q) {
+    switch (q) {
+    case JK_Q4_0: return "Q4_0";
+    case JK_Q8_0: return "Q8_0";
+    case JK_Q4_K: return "Q4_K_M";
+    case JK_Q6_K: return "Q6_K";
+    case JK_TQ2_0: return "TQ2_0";
+    case JK_I2_S: return "I2_S";
+    default: return "unsupported";
+    }
+}
+
+static size_t num_elements(const jk_tensor_view *w) {
+    if (w->ndim == 0) return 0;
+    size_t n = 1;
+    for (size_t i = 0; i < w->ndim; i++) n *= w->shape[i];
+    return n;
+}
+
+static const char *tname(const jk_tensor_view *w) { return w->name ? w->name : "<tensor>"; }
+
+// Orientation and byte-length rule of validate_quant_matvec_dimensions (quant.rs:1810-1894),
+// validate_q4_0/q8_0/q6_k_dimensions (quant.rs:762-892, 1315-1394) and
+// validate_q4_k_m_dimensions (lib.rs:1195-1260). A quant mismatch is a TensorBoundsError
+// there. The byte-length check is applied to every format (the Q8_0/Q6_K/Q4_K validators
+// rely on a slice bound that panics instead).
+jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, size_t in_len,
+                          size_t *rows, size_t *cols) {
+    if (!w || (!w->bytes && w->byte_len) || (w->ndim && !w->shape))
+        return fail(JK_TENSOR_BOUNDS, "null tensor view");
+    if (w->quant != quant)
+        return fail(JK_TENSOR_BOUNDS, "%s: expected %s quant type, got %s", tname(w),
+                    quant_name(quant), quant_name(w->quant));
+    if (w->ndim == 0) return fail(JK_TENSOR_BOUNDS, "%s: empty tensor shape", tname(w));
+    const Fmt f = fmt_of(quant);
+    if (w->ndim == 2) {
+        size_t d0 = w->shape[0], d1 = w->shape[1];
+        if (out_len == d0 && in_len == d1 && d1 % f.be == 0) { *rows = d0; *cols = d1; }
+        else if (out_len == d1 && in_len == d0 && d0 % f.be == 0) { *rows = d1; *cols = d0; }
+        else
+            return fail(JK_TENSOR_BOUNDS,
+                        "%s: matrix shape [%zu, %zu] does not match output len %zu and %s-aligned input len %zu",
+                        tname(w), d0, d1, out_len, quant_name(quant), in_len);
+    } else {
+        size_t total = num_elements(w);
+        if (in_len == 0 || out_len == 0 || in_len % f.be || out_len * in_len != total)
+            return fail(JK_TENSOR_BOUNDS, "%s: tensor elements %zu do not match output len %zu * input len %zu",
+                        tname(w), total, out_len, in_len);
+        *rows = out_len;
+        *cols = in_len;
+    }
+    if (*rows == 0 || *cols == 0)
+        return fail(JK_TENSOR_BOUNDS, "%s: empty matrix [%zu, %zu]", tname(w), *rows, *cols);
+    size_t need = (*rows * *cols / f.be) * f.bb + trailer_bytes(quant);
+    if (w->byte_len < need)
+        return fail(JK_TENSOR_BOUNDS, "%s: %s buffer length %zu < required %zu", tname(w),
+                    quant_name(quant), w->byte_len, need);
+    return JK_OK;
+}
+
+// validate_matrix_view (repack.rs:1208-1281) with validate_matrix_shape (1172-1206).
+static jk_status validate_matrix_view(const jk_tensor_view *w, size_t rows, size_t cols) {
+    if (rows == 0 || cols == 0)
+        return fail(JK_TENSOR_BOUNDS, "%s: repack dimensions must be non-zero, got [%zu, %zu]", tname(w), rows, cols);
+    const Fmt f = fmt_of(w->quant);
+    if (cols % f.be)
+        return fail(JK_TENSOR_BOUNDS, "%s: cols %zu not a multiple of block size %d", tname(w), cols, f.be);
+    if (w->ndim == 1) {
+        if (rows * cols != w->shape[0])
+            return fail(JK_TENSOR_BOUNDS, "%s: 1D shape %zu != rows * cols %zu", tname(w), w->shape[0], rows * cols);
+    } else if (w->ndim == 2) {
+        size_t d0 = w->shape[0], d1 = w->shape[1];
+        if (!((d0 == rows && d1 == cols) || (d0 == cols && d1 == rows)))
+            return fail(JK_TENSOR_BOUNDS, "%s: shape [%zu, %zu] does not match [%zu, %zu]", tname(w), d0, d1, rows, cols);
+    } else {
+        return fail(JK_TENSOR_BOUNDS, "%s: expected 1D or 2D weight tensor, got %zuD", tname(w), w->ndim);
+    }
+    size_t need = rows * (cols / f.be) * f.bb + trailer_bytes(w->quant);
+    if (w->byte_len < need)
+        return fail(JK_TENSOR_BOUNDS, "%s: buffer length %zu < required %zu", tname(w), w->byte_len, need);
+    return JK_OK;
+}
+
+static float read_trailer_scale(const uint8_t *t, size_t len) {
+    if (len < 4) return 0.0f;
+    float v;
+    memcpy(&v, t, 4);
+    return std::isfinite(v) ? v : 0.0f;  // read_i2_s_trailer_scale, quant.rs:360-366
+}
+
+// Device weight limits: row and block indices are 32-bit inside the kernels.
+static const size_t kMaxRows = (size_t)1 << 30;
+
+}  // namespace jk
+
+using namespace jk;
+
+extern "C" {
+
+const char *jk_last_error(void) { return g_err.c_str(); }
+int jk_abi_version(void) { return JK_ABI_VERSION; }
+
+jk_status jk_init(int device) {
+    JK_HIP(hipSetDevice(device));
+    return JK_OK;
+}
+
+jk_status jk_stream_create(jk_stream *out) {
+    if (!out) return fail(JK_TENSOR_BOUNDS, "null stream out-pointer");
+    hipStream_t s;
+    JK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *out = (jk_stream)s;
+    return JK_OK;
+}
+
+jk_status jk_stream_destroy(jk_stream s) {
+    if (s) JK_HIP(hipStreamDestroy((hipStream_t)s));
+    return JK_OK;
+}
+
+jk_status jk_stream_sync(jk_stream s) {
+    JK_HIP(hipStreamSynchronize((hipStream_t)s));
+    return JK_OK;
+}
+
+jk_status jk_device_alloc(size_t bytes, void **out) {
+    if (!out) return fail(JK_TENSOR_BOUNDS, "null out-pointer");
+    *out = nullptr;
+    if (bytes == 0) return JK_OK;
+    JK_HIP(hipMalloc(out, bytes));
+    return JK_OK;
+}
+
+jk_status jk_device_free(void *p) {
+    if (p) JK_HIP(hipFree(p));
+    return JK_OK;
+}
+
+jk_status jk_copy_to_device(jk_stream s, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return JK_OK;
+    JK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)s));
+    return JK_OK;
+}
+
+jk_status jk_copy_to_host(jk_stream s, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return JK_OK;
+    JK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)s));
+    return JK_OK;
+}
+
+// ------------------------------------------------------------------ weights
+jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, size_t cols,
+                           jk_weight **out) {
+    if (!out) return fail(JK_TENSOR_BOUNDS, "null weight out-pointer");
+    *out = nullptr;
+    if (!w || (!w->bytes && w->byte_len) || (w->ndim && !w->shape))
+        return fail(JK_TENSOR_BOUNDS, "null tensor view");
+    // BlockScaledTileLayout::for_tensor (repack.rs:1308-1333): dense and unsupported
+    // formats are a CapabilityMismatch.
+    if (!fmt_known(w->quant))
+        return fail(JK_CAPABILITY_MISMATCH, "%s: quant type %d is not supported by libjk", tname(w), (int)w->quant);
+    if (rows == 0 && cols == 0) {
+        // RepackedWeight::repack orientation inference (repack.rs:2255-2285).
+        if (w->ndim != 2)
+            return fail(JK_TENSOR_BOUNDS, "%s: RepackedWeight::repack requires a 2D tensor, got %zuD", tname(w), w->ndim);
+        size_t d0 = w->shape[0], d1 = w->shape[1], be = (size_t)fmt_of(w->quant).be;
+        if (d0 % be == 0 && d1 % be != 0) { rows = d1; cols = d0; }
+        else if (d1 % be == 0 && d0 % be != 0) { rows = d0; cols = d1; }
+        else { rows = d1; cols = d0; }
+    }
+    JK_TRY(validate_matrix_view(w, rows, cols));
+    if (rows >= kMaxRows || cols / (size_t)fmt_of(w->quant).be >= kMaxRows)
+        return fail(JK_TENSOR_BOUNDS, "%s: matrix [%zu, %zu] exceeds the device index range", tname(w), rows, cols);
+    const Fmt f = fmt_of(w->quant);
+    const size_t nb = cols / f.be;
+    const size_t payload = rows * nb * f.bb;
+    const size_t plane_bytes = rows * nb * (size_t)f.chunks * 16;
+    const size_t dbytes = f.d_off >= 0 ? rows * nb * 2 : 0;
+    jk_weight *h = new jk_weight();
+    memset(h, 0, sizeof *h);
+    JK_HIP(hipGetDevice(&h->device));
+    hipStream_t st = (hipStream_t)s;
+    uint8_t *staging = nullptr;
+    hipError_t e = hipMalloc(&h->alloc, plane_bytes + dbytes + 256);
+    if (e == hipSuccess) e = hipMalloc(&staging, payload);
+    if (e == hipSuccess) e = hipMemcpyAsync(staging, w->bytes, payload, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) {
+        if (staging) (void)hipFree(staging);
+        if (h->alloc) (void)hipFree(h->alloc);
+        delete h;
+        return hip_fail(e, "jk_weight_upload");
+    }
+    h->dev.planes = (const uint8_t *)h->alloc;
+    h->dev.dplane = dbytes ? (const uint16_t *)((uint8_t *)h->alloc + plane_bytes) : nullptr;
+    h->dev.quant = w->quant;
+    h->dev.rows = (int)rows;
+    h->dev.cols = (int)cols;
+    h->dev.nb = (int)nb;
+    h->dev.tensor_scale = w->quant == JK_I2_S
+                              ? read_trailer_scale((const uint8_t *)w->bytes + payload, w->byte_len - payload)
+                              : 0.0f;
+    h->device_bytes = plane_bytes + dbytes;
+    h->gguf_bytes = payload + trailer_bytes(w->quant);
+    jk_status rs = launch_repack(st, h->dev, staging);
+    // The staging buffer may only be released once the repack kernel has consumed it.
+    hipError_t se = hipStreamSynchronize(st);
+    (void)hipFree(staging);
+    if (rs != JK_OK || se != hipSuccess) {
+        (void)hipFree(h->alloc);
+        delete h;
+        return rs != JK_OK ? rs : hip_fail(se, "jk_weight_upload repack");
+    }
+    *out = h;
+    return JK_OK;
+}
+
+jk_status jk_weight_free(jk_weight *w) {
+    if (!w) return JK_OK;
+    hipError_t e = hipFree(w->alloc);
+    delete w;
+    if (e != hipSuccess) return hip_fail(e, "jk_weight_free");
+    return JK_OK;
+}
+
+jk_status jk_weight_get_info(const jk_weight *w, jk_weight_info *out) {
+    if (!w || !out) return fail(JK_TENSOR_BOUNDS, "null weight handle");
+    out->quant = w->dev.quant;
+    out->rows = (size_t)w->dev.rows;
+    out->cols = (size_t)w->dev.cols;
+    out->device_bytes = w->device_bytes;
+    out->gguf_bytes = w->gguf_bytes;
+    return JK_OK;
+}
+
+jk_status jk_weight_dequantize_rows(jk_stream s, const jk_weight *w, size_t r0, size_t r1, float *out,
+                                    size_t out_len) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "null weight handle");
+    if (r0 >= r1 || r1 > (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "row range %zu..%zu out of bounds for %d rows", r0, r1, w->dev.rows);
+    if (out_len != (r1 - r0) * (size_t)w->dev.cols)
+        return fail(JK_TENSOR_BOUNDS, "output length %zu != %zu rows * %d cols", out_len, r1 - r0, w->dev.cols);
+    if (!out) return fail(JK_TENSOR_BOUNDS, "null output");
+    return launch_dequant_rows((hipStream_t)s, w->dev, (int)r0, (int)r1, out);
+}
+
+// ------------------------------------------------------ activation quantization
+jk_status jk_quantize_row_q8_0(jk_stream s, const float *x, size_t n, jk_block_q8_0 *out, size_t out_blocks) {
+    // validate_activation_quant_slice (quant_q8.rs:111-149)
+    if (n == 0 || n % 32)
+        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_0: input length %zu must be a positive multiple of 32", n);
+    if (out_blocks != n / 32)
+        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_0: output block count %zu != expected %zu", out_blocks, n / 32);
+    if (!x || !out) return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_0: null pointer");
+    return launch_quantize_q8_0((hipStream_t)s, x, n / 32, out);
+}
+
+jk_status jk_quantize_row_q8_k(jk_stream s, const float *x, size_t n, jk_block_q8k *out, size_t out_blocks) {
+    if (n == 0 || n % 256)
+        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: input length %zu must be a positive multiple of 256", n);
+    if (out_blocks != n / 256)
+        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: output block count %zu != expected %zu", out_blocks, n / 256);
+    if (!x || !out) return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: null pointer");
+    return launch_quantize_q8_k((hipStream_t)s, x, n / 256, out);
+}
+
+size_t jk_act_q8_bytes(size_t m, size_t k) {
+    size_t kp = (k + 31) / 32 * 32, kb = kp / 32, kc = kp / 16, sb = (k + 255) / 256;
+    // float arrays first (4-byte aligned), then the i8 values, padded to 256 bytes
+    return 4 * m * (kb + kb + kc + sb) + m * kp + 256;
+}
+
+jk_status jk_act_q8_bind(void *storage, size_t storage_len, size_t m, size_t k, jk_act_q8 *o) {
+    if (!o) return fail(JK_TENSOR_BOUNDS, "null jk_act_q8");
+    if (m == 0 || k == 0)
+        return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: m and k must be non-zero, got [%zu, %zu]", m, k);
+    if (m >= kMaxRows || k >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: [%zu, %zu] too large", m, k);
+    if (!storage || storage_len < jk_act_q8_bytes(m, k))
+        return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: storage %zu < required %zu", storage_len, jk_act_q8_bytes(m, k));
+    if ((uintptr_t)storage % 16)
+        return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: storage must be 16-byte aligned");
+    o->m = m;
+    o->k = k;
+    o->k_padded = (k + 31) / 32 * 32;
+    o->k_blocks32 = o->k_padded / 32;
+    o->k_chunks = o->k_padded / 16;
+    o->sb256 = (k + 255) / 256;
+    float *f = (float *)storage;
+    o->scales = f; f += m * o->k_blocks32;
+    o->sums = f; f += m * o->k_blocks32;
+    o->sums16 = f; f += m * o->k_chunks;
+    o->super256 = f; f += m * o->sb256;
+    uintptr_t q = ((uintptr_t)f + 255) & ~(uintptr_t)255;
+    o->qs = (int8_t *)q;
+    return JK_OK;
+}
+
+jk_status jk_quantize_act_q8(jk_stream s, const float *x, size_t m, size_t k, const jk_act_q8 *act) {
+    // QuantizedActQ8::quantize_into (repack.rs:542-568)
+    if (!act) return fail(JK_TENSOR_BOUNDS, "null jk_act_q8");
+    if (m == 0 || k == 0)
+        return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: m and k must be non-zero, got [%zu, %zu]", m, k);
+    if (act->m != m || act->k != k)
+        return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: buffer bound for [%zu, %zu], got [%zu, %zu]", act->m, act->k, m, k);
+    if (!x) return fail(JK_TENSOR_BOUNDS, "QuantizedActQ8: null input");
+    return launch_quantize_act_q8((hipStream_t)s, x, *act);
+}
+
+jk_status jk_subln_quantize_absmax_i8(jk_stream s, const float *x, const float *norm_w, size_t m, size_t k,
+                                      float eps, int8_t *q, float *scales) {
+    // lib.rs:1048-1061: empty input is a TensorBoundsError
+    if (m == 0 || k == 0) return fail(JK_TENSOR_BOUNDS, "subln: dimension mismatch: m=%zu, k=%zu", m, k);
+    if (!x || !norm_w || !q || !scales) return fail(JK_TENSOR_BOUNDS, "subln: null pointer");
+    if (k >= kMaxRows || m >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "subln: [%zu, %zu] too large", m, k);
+    return launch_absmax_i8((hipStream_t)s, x, norm_w, m, k, eps, q, scales);
+}
+
+jk_status jk_quantize_absmax_i8(jk_stream s, const float *x, size_t m, size_t k, int8_t *q, float *scales) {
+    if (m == 0 || k == 0) return fail(JK_TENSOR_BOUNDS, "absmax: dimension mismatch: m=%zu, k=%zu", m, k);
+    if (!x || !q || !scales) return fail(JK_TENSOR_BOUNDS, "absmax: null pointer");
+    if (k >= kMaxRows || m >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "absmax: [%zu, %zu] too large", m, k);
+    return launch_absmax_i8((hipStream_t)s, x, nullptr, m, k, 0.0f, q, scales);
+}
+
+// --------------------------------------------------------------- quant_q8 GEMV
+static jk_status gemv_check(const jk_weight *w, int quant, const void *x, size_t nx, const float *y,
+                            size_t r0, size_t r1, const char *name) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "%s: null weight handle", name);
+    if (quant && w->dev.quant != quant)
+        return fail(JK_TENSOR_BOUNDS, "%s: expected %s quant type, got %s", name, quant_name(quant),
+                    quant_name(w->dev.quant));
+    if (w->dev.quant == JK_I2_S)
+        return fail(JK_CAPABILITY_MISMATCH, "%s: I2_S has no quant_q8 GEMV", name);
+    // check_q8_block_len (quant_q8.rs:1562-1578)
+    if (nx != (size_t)w->dev.nb)
+        return fail(JK_TENSOR_BOUNDS, "%s: x_blocks len %zu != expected %d", name, nx, w->dev.nb);
+    if (r0 > r1 || r1 > (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "%s: row range %zu..%zu out of bounds for %d rows", name, r0, r1, w->dev.rows);
+    if (!x || (!y && r1 > r0)) return fail(JK_TENSOR_BOUNDS, "%s: null pointer", name);
+    return JK_OK;
+}
+
+static jk_status gemv_full(jk_stream s, const jk_weight *w, int quant, const void *x, size_t nx, float *y,
+                           size_t y_len, const char *name) {
+    JK_TRY(gemv_check(w, quant, x, nx, y, 0, w ? (size_t)w->dev.rows : 0, name));
+    if (y_len != (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "%s: output len %zu != rows %d", name, y_len, w->dev.rows);
+    return launch_gemv_q8((hipStream_t)s, w->dev, x, y, 0, w->dev.rows);
+}
+
+jk_status jk_gemv_q4_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_Q4_0, x, nx, y, n, "gemv_q4_0_q8_0");
+}
+jk_status jk_gemv_q8_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_Q8_0, x, nx, y, n, "gemv_q8_0_q8_0");
+}
+jk_status jk_gemv_q4_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_Q4_K, x, nx, y, n, "gemv_q4_k_q8_k");
+}
+jk_status jk_gemv_q6_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_Q6_K, x, nx, y, n, "gemv_q6_k_q8_k");
+}
+jk_status jk_gemv_tq2_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_TQ2_0, x, nx, y, n, "gemv_tq2_0_q8_k");
+}
+
+jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t nx, float *y, size_t r0, size_t r1) {
+    JK_TRY(gemv_check(w, 0, x, nx, y, r0, r1, "gemv_q8_rows"));
+    if (r0 == r1) return JK_OK;
+    return launch_gemv_q8((hipStream_t)s, w->dev, x, y, (int)r0, (int)r1);
+}
+
+// -------------------------------------------------------------- vec_dot (f32)
+jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "vec_dot: null weight handle");
+    int q = w->dev.quant;
+    if (q == JK_TQ2_0) return fail(JK_CAPABILITY_MISMATCH, "vec_dot: TQ2_0 has no f32-activation matvec");
+    if (n != (size_t)w->dev.cols || y_len != (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "vec_dot: matrix [%d, %d] does not match output len %zu and input len %zu",
+                    w->dev.rows, w->dev.cols, y_len, n);
+    if (!x || !y) return fail(JK_TENSOR_BOUNDS, "vec_dot: null pointer");
+    return launch_vec_dot_f32((hipStream_t)s, w->dev, x, y);
+}
+
+// ------------------------------------------------------------ repacked GEMM
+jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
+                           size_t r0, size_t r1) {
+    // execute_gemm_repacked_rows (repack.rs:2725-2778)
+    if (!w || !act) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null argument");
+    if (act->k != (size_t)w->dev.cols)
+        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: activation k %zu != weight cols %d", act->k, w->dev.cols);
+    if (r0 > r1 || r1 > (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: row range %zu..%zu out of bounds for %d rows", r0, r1, w->dev.rows);
+    if (y_len != act->m * (r1 - r0))
+        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: output len %zu != %zu * %zu", y_len, act->m, r1 - r0);
+    if (r1 == r0) return JK_OK;
+    if (!y) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null output");
+    return launch_gemm_repacked((hipStream_t)s, w->dev, *act, y, (int)r0, (int)r1);
+}
+
+jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
+                           size_t r0, size_t r1) {
+    if (act && act->m != 1)
+        return fail(JK_TENSOR_BOUNDS, "gemv_repacked requires act.m() == 1, got %zu", act->m);
+    return jk_gemm_repacked(s, w, act, y, y_len, r0, r1);
+}
+
+// ---------------------------------------------------------------- BitLinear
+jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
+                          size_t k, float *y, size_t y_len) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "bitlinear: null weight handle");
+    int q = w->dev.quant;
+    // validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
+    if (q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
+        return fail(JK_TENSOR_BOUNDS, "bitlinear: unsupported quant type %s", quant_name(q));
+    if (m == 0 || k != (size_t)w->dev.cols || y_len != m * (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "bitlinear: weights [%d, %d] do not match m=%zu k=%zu out=%zu", w->dev.rows,
+                    w->dev.cols, m, k, y_len);
+    if (m >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "bitlinear: m=%zu too large", m);
+    if (!act || !act_scales || !y) return fail(JK_TENSOR_BOUNDS, "bitlinear: null pointer");
+    return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
+}
+
+}  // extern "C"

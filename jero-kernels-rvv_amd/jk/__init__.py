@@ -1,0 +1,376 @@
+"""Python host mirror of the jero-kernels-rvv quantized-matmul API over libjk.so.
+
+The functions keep the reference crate's names and argument meaning (quant_q8.rs,
+quant.rs, repack.rs, ime.rs, lib.rs); errors raise the reference's two K3Error kinds.
+All compute runs in libjk.so (hand-written HIP for gfx950); this module only marshals
+arguments. A missing libjk.so is an ImportError-grade failure, never a fallback.
+
+Two tiers, as in include/jk.h:
+  * host tier   -- numpy in, numpy out, synchronous (``gemv_q4_k_q8_k(out, view, x)``);
+  * device tier -- ``Weight`` handles plus device pointers (``int`` or any object with
+                   ``data_ptr()``, e.g. a torch tensor) on a HIP stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PACKAGE_DIR = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(PACKAGE_DIR, "libjk.so")
+HEADER_PATH = os.path.join(os.path.dirname(PACKAGE_DIR), "include", "jk.h")
+
+# ---------------------------------------------------------------- formats
+Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = 2, 8, 12, 14, 35, 36
+QUANT_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K_M", Q6_K: "Q6_K", TQ2_0: "TQ2_0", I2_S: "I2_S"}
+BLOCK_ELEMENTS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256, TQ2_0: 256, I2_S: 128}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210, TQ2_0: 66, I2_S: 32}
+TRAILER_BYTES = {I2_S: 32}
+
+# BlockQ8_0 (quant_q8.rs:37-44) and BlockQ8K (62-72), #[repr(C)] byte layouts.
+BLOCK_Q8_0 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
+BLOCK_Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+assert BLOCK_Q8_0.itemsize == 36 and BLOCK_Q8K.itemsize == 292
+
+OK, TENSOR_BOUNDS, CAPABILITY_MISMATCH, DEVICE_ERROR = 0, 1, 2, 3
+
+
+class K3Error(RuntimeError):
+    """Base of the errors the reference path returns."""
+
+
+class TensorBoundsError(K3Error):
+    """K3Error::TensorBoundsError: shape, length, range or quant-type mismatch."""
+
+
+class CapabilityMismatch(K3Error):
+    """K3Error::CapabilityMismatch: format not supported by the entry point."""
+
+
+class DeviceError(K3Error):
+    """HIP runtime failure (no reference counterpart)."""
+
+
+_ERRORS = {TENSOR_BOUNDS: TensorBoundsError, CAPABILITY_MISMATCH: CapabilityMismatch, DEVICE_ERROR: DeviceError}
+
+# ---------------------------------------------------------------- ctypes
+_sz = C.c_size_t
+_vp = C.c_void_p
+
+
+class TensorViewC(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("quant", C.c_int32), ("shape", C.POINTER(_sz)), ("ndim", _sz),
+                ("bytes", _vp), ("byte_len", _sz)]
+
+
+class ActQ8C(C.Structure):
+    _fields_ = [("m", _sz), ("k", _sz), ("k_padded", _sz), ("k_blocks32", _sz), ("k_chunks", _sz), ("sb256", _sz),
+                ("qs", _vp), ("scales", _vp), ("sums", _vp), ("sums16", _vp), ("super256", _vp)]
+
+
+class WeightInfoC(C.Structure):
+    _fields_ = [("quant", C.c_int32), ("rows", _sz), ("cols", _sz), ("device_bytes", _sz), ("gguf_bytes", _sz)]
+
+
+_lib_handle = None
+
+
+def lib() -> C.CDLL:
+    """Loads libjk.so (built in-tree by ``make -C jero-kernels-rvv_amd``)."""
+    global _lib_handle
+    if _lib_handle is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"libjk.so not built: run `make -C {PACKAGE_DIR}` (expected {LIB_PATH})")
+        h = C.CDLL(LIB_PATH)
+        h.jk_last_error.restype = C.c_char_p
+        h.jk_act_q8_bytes.restype = _sz
+        h.jk_act_q8_bytes.argtypes = [_sz, _sz]
+        _lib_handle = h
+    return _lib_handle
+
+
+def header_symbols() -> list[str]:
+    """Every function name declared in include/jk.h."""
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"\b(jk_[a-z0-9_]+)\s*\(", text)))
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        msg = lib().jk_last_error().decode(errors="replace")
+        raise _ERRORS.get(status, K3Error)(msg)
+
+
+def _ptr(x) -> int:
+    """Device or host address of an int, numpy array or torch-like tensor."""
+    if x is None:
+        return 0
+    if isinstance(x, int):
+        return x
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    return int(x.data_ptr())
+
+
+class TensorView:
+    """jero_core::TensorView fields the path reads: name, quant, shape, bytes."""
+
+    def __init__(self, name: str, quant: int, shape, data):
+        self.name = name
+        self.quant = int(quant)
+        self.shape = tuple(int(s) for s in shape)
+        self.data = np.ascontiguousarray(np.frombuffer(memoryview(data), dtype=np.uint8)
+                                         if not isinstance(data, np.ndarray) else data.view(np.uint8).reshape(-1))
+        self._name_b = name.encode()
+        self._shape_c = (_sz * max(1, len(self.shape)))(*self.shape)
+
+    def c(self) -> TensorViewC:
+        return TensorViewC(self._name_b, self.quant, C.cast(self._shape_c, C.POINTER(_sz)), len(self.shape),
+                           self.data.ctypes.data, self.data.nbytes)
+
+
+# ---------------------------------------------------------------- host tier
+def _f32(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def quantize_row_q8_0(x) -> np.ndarray:
+    """quantize_row_q8_0 (quant_q8.rs:395): f32[n] -> BlockQ8_0[n / 32]."""
+    x = _f32(x).reshape(-1)
+    out = np.zeros(x.size // 32 if x.size % 32 == 0 else 0, dtype=BLOCK_Q8_0)
+    _check(lib().jk_host_quantize_row_q8_0(_vp(x.ctypes.data), _sz(x.size), _vp(out.ctypes.data), _sz(out.size)))
+    return out
+
+
+def quantize_row_q8_k(x) -> np.ndarray:
+    """quantize_row_q8_k (quant_q8.rs:576): f32[n] -> BlockQ8K[n / 256]."""
+    x = _f32(x).reshape(-1)
+    out = np.zeros(x.size // 256 if x.size % 256 == 0 else 0, dtype=BLOCK_Q8K)
+    _check(lib().jk_host_quantize_row_q8_k(_vp(x.ctypes.data), _sz(x.size), _vp(out.ctypes.data), _sz(out.size)))
+    return out
+
+
+def _vec_dot_row(fn: str, w_blocks, x_blocks) -> float:
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x_blocks)
+    out = C.c_float(0.0)
+    _check(getattr(lib(), fn)(_vp(w.ctypes.data), _sz(w.size), _vp(x.ctypes.data), _sz(x.size), C.byref(out)))
+    return out.value
+
+
+def vec_dot_q4_0_q8_0(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:1463"""
+    return _vec_dot_row("jk_host_vec_dot_q4_0_q8_0", w_blocks, x_blocks)
+
+
+def vec_dot_q8_0_q8_0(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:1493"""
+    return _vec_dot_row("jk_host_vec_dot_q8_0_q8_0", w_blocks, x_blocks)
+
+
+def vec_dot_q4_k_q8_k(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:3019"""
+    return _vec_dot_row("jk_host_vec_dot_q4_k_q8_k", w_blocks, x_blocks)
+
+
+def vec_dot_q6_k_q8_k(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:3056"""
+    return _vec_dot_row("jk_host_vec_dot_q6_k_q8_k", w_blocks, x_blocks)
+
+
+def vec_dot_tq2_0_q8_k(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:3086"""
+    return _vec_dot_row("jk_host_vec_dot_tq2_0_q8_k", w_blocks, x_blocks)
+
+
+def _gemv(fn: str, out: np.ndarray, weights: TensorView, x_blocks) -> None:
+    x = np.ascontiguousarray(x_blocks)
+    v = weights.c()
+    _check(getattr(lib(), fn)(_vp(out.ctypes.data), _sz(out.size), C.byref(v), _vp(x.ctypes.data), _sz(x.size)))
+
+
+def gemv_q4_0_q8_0(out, weights, x_blocks):
+    """quant_q8.rs:1586 -- fills out[rows]."""
+    _gemv("jk_host_gemv_q4_0_q8_0", out, weights, x_blocks)
+
+
+def gemv_q8_0_q8_0(out, weights, x_blocks):
+    """quant_q8.rs:1670"""
+    _gemv("jk_host_gemv_q8_0_q8_0", out, weights, x_blocks)
+
+
+def gemv_q4_k_q8_k(out, weights, x_blocks):
+    """quant_q8.rs:3101"""
+    _gemv("jk_host_gemv_q4_k_q8_k", out, weights, x_blocks)
+
+
+def gemv_q6_k_q8_k(out, weights, x_blocks):
+    """quant_q8.rs:3189"""
+    _gemv("jk_host_gemv_q6_k_q8_k", out, weights, x_blocks)
+
+
+def gemv_tq2_0_q8_k(out, weights, x_blocks):
+    """quant_q8.rs:3250"""
+    _gemv("jk_host_gemv_tq2_0_q8_k", out, weights, x_blocks)
+
+
+def _vec_dot_f32(fn: str, out: np.ndarray, weights: TensorView, inp) -> None:
+    x = _f32(inp).reshape(-1)
+    v = weights.c()
+    _check(getattr(lib(), fn)(_vp(out.ctypes.data), _sz(out.size), C.byref(v), _vp(x.ctypes.data), _sz(x.size)))
+
+
+def vec_dot_q4_0(out, weights, inp):
+    """quant.rs:1458"""
+    _vec_dot_f32("jk_host_vec_dot_q4_0", out, weights, inp)
+
+
+def vec_dot_q8_0(out, weights, inp):
+    """quant.rs:1069"""
+    _vec_dot_f32("jk_host_vec_dot_q8_0", out, weights, inp)
+
+
+def vec_dot_q6_k(out, weights, inp):
+    """quant.rs:1089"""
+    _vec_dot_f32("jk_host_vec_dot_q6_k", out, weights, inp)
+
+
+def vec_dot_q4_k_m(out, weights, inp):
+    """VectorKernel::vec_dot_q4_k_m (lib.rs:157)"""
+    _vec_dot_f32("jk_host_vec_dot_q4_k_m", out, weights, inp)
+
+
+def vec_dot_i2_s(out, weights, inp):
+    """quant.rs:2199"""
+    _vec_dot_f32("jk_host_vec_dot_i2_s", out, weights, inp)
+
+
+def dequantize_tensor_row(weights: TensorView, row: int, out: np.ndarray) -> None:
+    """dequantize_tensor_row / dequantize_token_row (quant.rs:2492, 2580)."""
+    v = weights.c()
+    _check(lib().jk_host_dequantize_tensor_row(C.byref(v), _sz(row), _vp(out.ctypes.data), _sz(out.size)))
+
+
+def bitlinear_i8(out: np.ndarray, weights: TensorView, act_i8, act_scale: float) -> None:
+    """bitlinear_i8_rvv (ime.rs:882)."""
+    a = np.ascontiguousarray(act_i8, dtype=np.int8).reshape(-1)
+    v = weights.c()
+    _check(lib().jk_host_bitlinear_i8(_vp(out.ctypes.data), _sz(out.size), C.byref(v), _vp(a.ctypes.data),
+                                      _sz(a.size), C.c_float(act_scale)))
+
+
+# ---------------------------------------------------------------- device tier
+def init(device: int = 0) -> None:
+    _check(lib().jk_init(C.c_int(device)))
+
+
+def sync(stream=None) -> None:
+    _check(lib().jk_stream_sync(_vp(stream or 0)))
+
+
+class Weight:
+    """Device-resident weight (RepackedWeight::from_tensor, repack.rs:2288)."""
+
+    def __init__(self, view: TensorView, rows: int = 0, cols: int = 0, stream=None):
+        h = _vp()
+        v = view.c()
+        _check(lib().jk_weight_upload(_vp(stream or 0), C.byref(v), _sz(rows), _sz(cols), C.byref(h)))
+        self._h = h
+        info = WeightInfoC()
+        _check(lib().jk_weight_get_info(h, C.byref(info)))
+        self.quant, self.rows, self.cols = info.quant, info.rows, info.cols
+        self.device_bytes, self.gguf_bytes = info.device_bytes, info.gguf_bytes
+
+    @property
+    def handle(self):
+        return self._h
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            lib().jk_weight_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def act_q8_bytes(m: int, k: int) -> int:
+    return int(lib().jk_act_q8_bytes(_sz(m), _sz(k)))
+
+
+def act_q8_bind(storage, storage_len: int, m: int, k: int) -> ActQ8C:
+    a = ActQ8C()
+    _check(lib().jk_act_q8_bind(_vp(_ptr(storage)), _sz(storage_len), _sz(m), _sz(k), C.byref(a)))
+    return a
+
+
+def dev_quantize_row_q8_0(x, n, out, out_blocks, stream=None):
+    _check(lib().jk_quantize_row_q8_0(_vp(stream or 0), _vp(_ptr(x)), _sz(n), _vp(_ptr(out)), _sz(out_blocks)))
+
+
+def dev_quantize_row_q8_k(x, n, out, out_blocks, stream=None):
+    _check(lib().jk_quantize_row_q8_k(_vp(stream or 0), _vp(_ptr(x)), _sz(n), _vp(_ptr(out)), _sz(out_blocks)))
+
+
+def dev_quantize_act_q8(x, m, k, act: ActQ8C, stream=None):
+    _check(lib().jk_quantize_act_q8(_vp(stream or 0), _vp(_ptr(x)), _sz(m), _sz(k), C.byref(act)))
+
+
+def dev_subln_quantize_absmax_i8(x, norm_w, m, k, eps, q, scales, stream=None):
+    _check(lib().jk_subln_quantize_absmax_i8(_vp(stream or 0), _vp(_ptr(x)), _vp(_ptr(norm_w)), _sz(m), _sz(k),
+                                             C.c_float(eps), _vp(_ptr(q)), _vp(_ptr(scales))))
+
+
+def dev_quantize_absmax_i8(x, m, k, q, scales, stream=None):
+    _check(lib().jk_quantize_absmax_i8(_vp(stream or 0), _vp(_ptr(x)), _sz(m), _sz(k), _vp(_ptr(q)),
+                                       _vp(_ptr(scales))))
+
+
+_GEMV_FN = {Q4_0: "jk_gemv_q4_0_q8_0", Q8_0: "jk_gemv_q8_0_q8_0", Q4_K: "jk_gemv_q4_k_q8_k",
+            Q6_K: "jk_gemv_q6_k_q8_k", TQ2_0: "jk_gemv_tq2_0_q8_k"}
+
+
+def dev_gemv_q8(w: Weight, x, nx, y, y_len, stream=None, fn: str | None = None):
+    name = fn or _GEMV_FN.get(w.quant, "jk_gemv_q4_0_q8_0")
+    _check(getattr(lib(), name)(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(nx), _vp(_ptr(y)), _sz(y_len)))
+
+
+def dev_gemv_q8_rows(w: Weight, x, nx, y, r0, r1, stream=None):
+    _check(lib().jk_gemv_q8_rows(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(nx), _vp(_ptr(y)), _sz(r0), _sz(r1)))
+
+
+def dev_vec_dot_f32(w: Weight, x, n, y, y_len, stream=None):
+    _check(lib().jk_vec_dot_f32(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(n), _vp(_ptr(y)), _sz(y_len)))
+
+
+def dev_gemm_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
+    _check(lib().jk_gemm_repacked(_vp(stream or 0), w.handle, C.byref(act), _vp(_ptr(y)), _sz(y_len), _sz(r0),
+                                  _sz(r1)))
+
+
+def dev_gemv_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
+    _check(lib().jk_gemv_repacked(_vp(stream or 0), w.handle, C.byref(act), _vp(_ptr(y)), _sz(y_len), _sz(r0),
+                                  _sz(r1)))
+
+
+def dev_bitlinear_i8(w: Weight, act, act_scales, m, k, y, y_len, stream=None):
+    _check(lib().jk_bitlinear_i8(_vp(stream or 0), w.handle, _vp(_ptr(act)), _vp(_ptr(act_scales)), _sz(m), _sz(k),
+                                 _vp(_ptr(y)), _sz(y_len)))
+
+
+def dev_dequantize_rows(w: Weight, r0, r1, out, out_len, stream=None):
+    _check(lib().jk_weight_dequantize_rows(_vp(stream or 0), w.handle, _sz(r0), _sz(r1), _vp(_ptr(out)),
+                                           _sz(out_len)))
+
+
+def host_gemm_repacked_f32(out: np.ndarray, w: Weight, inp, m: int, r0: int, r1: int) -> None:
+    """gemm_repacked_f32_rows (repack.rs:4143)."""
+    x = _f32(inp).reshape(-1)
+    _check(lib().jk_host_gemm_repacked_f32(_vp(out.ctypes.data), _sz(out.size), w.handle, _vp(x.ctypes.data), _sz(m),
+                                           _sz(r0), _sz(r1)))

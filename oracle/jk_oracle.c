@@ -1,0 +1,929 @@
+/*
+ * jk_oracle.c -- CPU restatement of the jero-kernels-rvv portable scalar fallback
+ * for the quantized-matmul path. TEST INFRASTRUCTURE ONLY: the parity checker and
+ * the timed CPU baseline; never part of the product library.
+ *
+ * Citations are file:line in the reference crate (src/...). Build with
+ * -ffp-contract=off so that every `a * b + c` of the reference rounds twice.
+ */
+#include "jk_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------- */
+/* Format tables: quant.rs:19-91, ime.rs:27-37, lib.rs:128-132                */
+/* ------------------------------------------------------------------------- */
+size_t or_block_elements(int q) {
+    switch (q) {
+    case OR_Q4_0: case OR_Q8_0: return 32;
+    case OR_Q4_K: case OR_Q6_K: case OR_TQ2_0: return 256;
+    case OR_I2_S: return 128;
+    default: return 0;
+    }
+}
+
+size_t or_block_bytes(int q) {
+    switch (q) {
+    case OR_Q4_0: return 18;
+    case OR_Q8_0: return 34;
+    case OR_Q4_K: return 144;
+    case OR_Q6_K: return 210;
+    case OR_TQ2_0: return 66;
+    case OR_I2_S: return 32;
+    default: return 0;
+    }
+}
+
+/* I2_S carries a 32-byte tensor-wide scale trailer (quant.rs:89-91). */
+size_t or_scale_trailer_bytes(int q) { return q == OR_I2_S ? 32 : 0; }
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* Rust `sum: f32 = iter.sum()` folds from -0.0; `let mut acc = 0.0` starts at +0.0. */
+static float neg_zero(void) { return -0.0f; }
+
+/* Rust `x.round().clamp(lo, hi) as i8`: NaN clamps to NaN and `NaN as i8` is 0. */
+static int8_t rust_round_clamp_i8(float v, float lo, float hi) {
+    float r = roundf(v);
+    if (isnan(r)) return 0;
+    if (r < lo) r = lo;
+    if (r > hi) r = hi;
+    return (int8_t)r;
+}
+
+/* ------------------------------------------------------------------------- */
+/* f16 decode: lib.rs:676-717                                                 */
+/* ------------------------------------------------------------------------- */
+float or_f16_to_f32_ieee(uint16_t bits) {
+    uint32_t sign = (bits >> 15) & 1u, exp = (bits >> 10) & 0x1Fu, mant = bits & 0x3FFu;
+    uint32_t out;
+    if (exp == 0) {
+        if (mant == 0) {
+            out = sign << 31;
+        } else {
+            uint32_t m = mant, e = 127u - 14u;
+            while ((m & 0x400u) == 0) { m <<= 1; e -= 1; }
+            m &= 0x3FFu;
+            out = (sign << 31) | (e << 23) | (m << 13);
+        }
+    } else if (exp == 0x1F) {
+        out = mant == 0 ? ((sign << 31) | 0x7F800000u) : ((sign << 31) | 0x7FC00000u | (mant << 13));
+    } else {
+        out = (sign << 31) | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &out, 4);
+    return f;
+}
+
+float or_f16_to_f32_finite(uint16_t bits) {
+    float v = or_f16_to_f32_ieee(bits);
+    return isfinite(v) ? v : 0.0f;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Block dequantization                                                       */
+/* ------------------------------------------------------------------------- */
+
+/* quant.rs:550-568 */
+void or_dequantize_q4_0_block(const uint8_t *blk, float *out) {
+    float d = or_f16_to_f32_finite(rd16(blk));
+    if (d == 0.0f) { for (int i = 0; i < 32; i++) out[i] = 0.0f; return; }
+    for (int i = 0; i < 16; i++) {
+        uint8_t b = blk[2 + i];
+        out[i] = d * (float)((int)(b & 0x0F) - 8);
+        out[i + 16] = d * (float)((int)((b >> 4) & 0x0F) - 8);
+    }
+}
+
+/* quant.rs:571-588 */
+void or_dequantize_q8_0_block(const uint8_t *blk, float *out) {
+    float d = or_f16_to_f32_finite(rd16(blk));
+    if (d == 0.0f) { for (int i = 0; i < 32; i++) out[i] = 0.0f; return; }
+    for (int i = 0; i < 32; i++) out[i] = d * (float)(int8_t)blk[2 + i];
+}
+
+/* quant_q8.rs:1818-1830 (same table as lib.rs:736-745 and repack.rs:1158-1170) */
+static void unpack_k4_scales_mins(const uint8_t *s, uint8_t sc[8], uint8_t m[8]) {
+    for (int j = 0; j < 4; j++) {
+        sc[j] = s[j] & 0x3F;
+        m[j] = s[j + 4] & 0x3F;
+    }
+    for (int j = 4; j < 8; j++) {
+        sc[j] = (uint8_t)((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+        m[j] = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* lib.rs:720-766 (no zero-scale short cut; d1*q - m1 rounds twice) */
+void or_dequantize_q4_k_block(const uint8_t *blk, float *out) {
+    float d = or_f16_to_f32_finite(rd16(blk));
+    float dmin = or_f16_to_f32_finite(rd16(blk + 2));
+    uint8_t sc[8], m[8];
+    unpack_k4_scales_mins(blk + 4, sc, m);
+    const uint8_t *qs = blk + 16;
+    for (int c = 0; c < 4; c++) {
+        float d1 = d * (float)sc[2 * c], m1 = dmin * (float)m[2 * c];
+        float d2 = d * (float)sc[2 * c + 1], m2 = dmin * (float)m[2 * c + 1];
+        for (int l = 0; l < 32; l++) out[64 * c + l] = d1 * (float)(qs[32 * c + l] & 0x0F) - m1;
+        for (int l = 0; l < 32; l++) out[64 * c + 32 + l] = d2 * (float)(qs[32 * c + l] >> 4) - m2;
+    }
+}
+
+/* quant.rs:594-648: out = (d * sc) * q evaluated left to right */
+void or_dequantize_q6_k_block(const uint8_t *blk, float *out) {
+    float d = or_f16_to_f32_finite(rd16(blk + 208));
+    if (d == 0.0f) { for (int i = 0; i < 256; i++) out[i] = 0.0f; return; }
+    const uint8_t *ql = blk, *qh = blk + 128, *sc = blk + 192;
+    for (int h = 0; h < 2; h++) {
+        int n = 128 * h;
+        const uint8_t *L = ql + 64 * h, *H = qh + 32 * h;
+        const int8_t *S = (const int8_t *)(sc + 8 * h);
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16;
+            int q1 = (int)((L[l] & 0x0F) | ((H[l] & 3) << 4)) - 32;
+            int q2 = (int)((L[l + 32] & 0x0F) | (((H[l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)((L[l] >> 4) | (((H[l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)((L[l + 32] >> 4) | (((H[l] >> 6) & 3) << 4)) - 32;
+            out[n + l] = d * (float)S[is] * (float)q1;
+            out[n + l + 32] = d * (float)S[is + 2] * (float)q2;
+            out[n + l + 64] = d * (float)S[is + 4] * (float)q3;
+            out[n + l + 96] = d * (float)S[is + 6] * (float)q4;
+        }
+    }
+}
+
+/* ime.rs:636-658: crate layout, d first, element 4i+j = bits 2j of qs[i] */
+float or_unpack_tq2_0_block_i8(const uint8_t *blk, int8_t *out) {
+    float s = or_f16_to_f32_finite(rd16(blk));
+    for (int i = 0; i < 64; i++) {
+        uint8_t b = blk[2 + i];
+        out[4 * i] = (int8_t)((b & 3) - 1);
+        out[4 * i + 1] = (int8_t)(((b >> 2) & 3) - 1);
+        out[4 * i + 2] = (int8_t)(((b >> 4) & 3) - 1);
+        out[4 * i + 3] = (int8_t)(((b >> 6) & 3) - 1);
+    }
+    return s;
+}
+
+/* quant.rs:370-377 */
+void or_unpack_i2_s_block_i8(const uint8_t *blk, int8_t *out) {
+    for (int g = 0; g < 32; g++) {
+        uint8_t b = blk[g];
+        out[g] = (int8_t)(((b >> 6) & 3) - 1);
+        out[32 + g] = (int8_t)(((b >> 4) & 3) - 1);
+        out[64 + g] = (int8_t)(((b >> 2) & 3) - 1);
+        out[96 + g] = (int8_t)((b & 3) - 1);
+    }
+}
+
+/* quant.rs:94-102 (scale_i8_into_f32) */
+static void scale_i8_into_f32(float scale, const int8_t *q, float *out, int n) {
+    if (scale == 0.0f) { for (int i = 0; i < n; i++) out[i] = 0.0f; return; }
+    for (int i = 0; i < n; i++) out[i] = scale * (float)q[i];
+}
+
+/* quant.rs:380-387 */
+void or_dequantize_i2_s_block(const uint8_t *blk, float scale, float *out) {
+    int8_t q[128];
+    or_unpack_i2_s_block_i8(blk, q);
+    scale_i8_into_f32(scale, q, out, 128);
+}
+
+/* quant.rs:360-366 */
+float or_read_i2_s_trailer_scale(const uint8_t *t, size_t len) {
+    if (len < 4) return 0.0f;
+    float v;
+    memcpy(&v, t, 4);
+    return isfinite(v) ? v : 0.0f;
+}
+
+/* One block of any path format to f32 (quant.rs:2272-2392 dispatch arms). */
+static void dequant_block_any(int q, const uint8_t *blk, float i2s_scale, float *out) {
+    switch (q) {
+    case OR_Q4_0: or_dequantize_q4_0_block(blk, out); break;
+    case OR_Q8_0: or_dequantize_q8_0_block(blk, out); break;
+    case OR_Q4_K: or_dequantize_q4_k_block(blk, out); break;
+    case OR_Q6_K: or_dequantize_q6_k_block(blk, out); break;
+    case OR_TQ2_0: { /* quant.rs:2369-2378 */
+        int8_t t[256];
+        float d = or_unpack_tq2_0_block_i8(blk, t);
+        scale_i8_into_f32(d, t, out, 256);
+        break;
+    }
+    case OR_I2_S: or_dequantize_i2_s_block(blk, i2s_scale, out); break;
+    default: break;
+    }
+}
+
+static int known_quant(int q) { return or_block_elements(q) != 0; }
+
+/* quant.rs:2403-2483 */
+int or_dequantize_row_bytes(int quant, const uint8_t *row, size_t row_len, size_t n_cols,
+                            float *out, size_t out_len) {
+    if (n_cols == 0 || out_len != n_cols) return OR_TENSOR_BOUNDS;
+    if (!known_quant(quant)) return OR_CAPABILITY_MISMATCH;
+    size_t be = or_block_elements(quant), bb = or_block_bytes(quant);
+    if (n_cols % be) return OR_TENSOR_BOUNDS;
+    size_t packed = (n_cols / be) * bb;
+    if (row_len != packed + or_scale_trailer_bytes(quant)) return OR_TENSOR_BOUNDS;
+    float s = quant == OR_I2_S ? or_read_i2_s_trailer_scale(row + packed, row_len - packed) : 1.0f;
+    for (size_t b = 0; b < n_cols / be; b++) dequant_block_any(quant, row + b * bb, s, out + b * be);
+    return OR_OK;
+}
+
+static size_t num_elements(const or_tensor_view *w) {
+    size_t n = 1;
+    for (size_t i = 0; i < w->ndim; i++) n *= w->shape[i];
+    return w->ndim ? n : 0;
+}
+
+/* quant.rs:2492-2568 with validate_token_row_geometry quant.rs:1749-1808 */
+int or_dequantize_tensor_row(const or_tensor_view *w, size_t row, float *out, size_t out_len) {
+    if (!known_quant(w->quant)) return OR_CAPABILITY_MISMATCH;
+    size_t cols = out_len;
+    if (cols == 0) return OR_TENSOR_BOUNDS;
+    size_t total = num_elements(w);
+    if (total == 0 || total % cols) return OR_TENSOR_BOUNDS;
+    size_t nrows = total / cols;
+    if (w->ndim == 2 && !((w->shape[0] == cols && w->shape[1] == nrows) ||
+                          (w->shape[1] == cols && w->shape[0] == nrows)))
+        return OR_TENSOR_BOUNDS;
+    if (row >= nrows) return OR_TENSOR_BOUNDS;
+    size_t be = or_block_elements(w->quant), bb = or_block_bytes(w->quant);
+    if (cols % be) return OR_TENSOR_BOUNDS;
+    size_t row_bytes = (cols / be) * bb, payload = nrows * row_bytes;
+    if (w->byte_len < payload + or_scale_trailer_bytes(w->quant)) return OR_TENSOR_BOUNDS;
+    float s = w->quant == OR_I2_S ? or_read_i2_s_trailer_scale(w->bytes + payload, w->byte_len - payload)
+                                  : 1.0f;
+    const uint8_t *r = w->bytes + row * row_bytes;
+    for (size_t b = 0; b < cols / be; b++) dequant_block_any(w->quant, r + b * bb, s, out + b * be);
+    return OR_OK;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Activation quantization                                                    */
+/* ------------------------------------------------------------------------- */
+
+/* quant_q8.rs:102-108 */
+static int8_t round_scaled_to_i8(float v, float inv) {
+    if (!isfinite(v)) return 0;
+    return rust_round_clamp_i8(v * inv, -127.0f, 127.0f);
+}
+
+/* quant_q8.rs:203-219; amax is a fold of f32::max over |finite x| from 0.0 */
+static void quantize_block_q8_0(const float *x, or_block_q8_0 *b) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++)
+        if (isfinite(x[i])) amax = fmaxf(amax, fabsf(x[i]));
+    if (amax == 0.0f || !isfinite(amax)) { memset(b, 0, sizeof *b); return; }
+    float inv = 127.0f / amax;
+    b->d = amax / 127.0f;
+    for (int i = 0; i < 32; i++) b->qs[i] = round_scaled_to_i8(x[i], inv);
+}
+
+/* quant_q8.rs:111-149 (validate_activation_input / _quant_slice) */
+int or_quantize_row_q8_0(const float *x, size_t n, or_block_q8_0 *out, size_t out_len) {
+    if (n == 0 || n % 32) return OR_TENSOR_BOUNDS;
+    if (out_len != n / 32) return OR_TENSOR_BOUNDS;
+    for (size_t b = 0; b < n / 32; b++) quantize_block_q8_0(x + 32 * b, out + b);
+    return OR_OK;
+}
+
+/* quant_q8.rs:447-475 */
+static void quantize_block_q8_k(const float *x, or_block_q8k *b) {
+    float amax = 0.0f;
+    for (int i = 0; i < 256; i++)
+        if (isfinite(x[i])) amax = fmaxf(amax, fabsf(x[i]));
+    if (amax == 0.0f || !isfinite(amax)) { memset(b, 0, sizeof *b); return; }
+    float inv = 127.0f / amax;
+    b->d = amax / 127.0f;
+    for (int s = 0; s < 16; s++) {
+        int16_t sum = 0;
+        for (int i = 0; i < 16; i++) {
+            int8_t q = round_scaled_to_i8(x[16 * s + i], inv);
+            b->qs[16 * s + i] = q;
+            sum = (int16_t)(sum + q);
+        }
+        b->bsums[s] = sum;
+    }
+}
+
+/* quant_q8.rs:576-594 */
+int or_quantize_row_q8_k(const float *x, size_t n, or_block_q8k *out, size_t out_len) {
+    if (n == 0 || n % 256) return OR_TENSOR_BOUNDS;
+    if (out_len != n / 256) return OR_TENSOR_BOUNDS;
+    for (size_t b = 0; b < n / 256; b++) quantize_block_q8_k(x + 256 * b, out + b);
+    return OR_OK;
+}
+
+/* repack.rs:175-204: sequential f32 sum from +0.0; zero threshold absmax < 1e-30 */
+static void quantize_block32(const float *src, int8_t *q, float *scale, float *sum_out) {
+    float clean[32], absmax = 0.0f, sum = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        float v = isfinite(src[i]) ? src[i] : 0.0f;
+        clean[i] = v;
+        sum += v;
+        float a = fabsf(v);
+        if (a > absmax) absmax = a;
+    }
+    *sum_out = sum;
+    if (absmax < 1e-30f) {
+        memset(q, 0, 32);
+        *scale = 0.0f;
+        return;
+    }
+    float inv = 127.0f / absmax;
+    *scale = absmax / 127.0f;
+    for (int i = 0; i < 32; i++) q[i] = rust_round_clamp_i8(clean[i] * inv, -127.0f, 127.0f);
+}
+
+size_t or_act_q8_bytes(size_t m, size_t k) {
+    size_t kp = (k + 31) / 32 * 32, kb = kp / 32, kc = kp / 16, sb = (k + 255) / 256;
+    return m * kp + 4 * m * (kb + kb + kc + sb);
+}
+
+/* QuantizedActQ8::quantize_into, repack.rs:542-650 (logical row-major form) */
+int or_quantize_act_q8(const float *act, size_t m, size_t k, void *storage, size_t storage_len,
+                       or_act_q8 *o) {
+    if (m == 0 || k == 0) return OR_TENSOR_BOUNDS;
+    if (storage_len < or_act_q8_bytes(m, k)) return OR_TENSOR_BOUNDS;
+    o->m = m; o->k = k;
+    o->k_padded = (k + 31) / 32 * 32;
+    o->k_blocks32 = o->k_padded / 32;
+    o->k_chunks = o->k_padded / 16;
+    o->sb256 = (k + 255) / 256;
+    float *f = (float *)storage;
+    o->scales = f; f += m * o->k_blocks32;
+    o->sums = f; f += m * o->k_blocks32;
+    o->sums16 = f; f += m * o->k_chunks;
+    o->super256 = f; f += m * o->sb256;
+    o->qs = (int8_t *)f;
+    float *row_f32 = malloc(o->k_padded * sizeof(float));
+    if (!row_f32) return OR_TENSOR_BOUNDS;
+    for (size_t r = 0; r < m; r++) {
+        const float *src = act + r * k;
+        for (size_t i = 0; i < o->k_padded; i++)
+            row_f32[i] = i < k ? (isfinite(src[i]) ? src[i] : 0.0f) : 0.0f;
+        for (size_t i = 0; i < o->sb256; i++) o->super256[r * o->sb256 + i] = 0.0f;
+        /* quantize_row_f32_to_q8_32_scalar, repack.rs:376-400: zero-padded tail */
+        for (size_t b = 0; b < o->k_blocks32; b++) {
+            float buf[32];
+            for (int i = 0; i < 32; i++) {
+                size_t idx = 32 * b + i;
+                buf[i] = idx < k ? src[idx] : 0.0f;
+            }
+            float sc, sm;
+            quantize_block32(buf, o->qs + r * o->k_padded + 32 * b, &sc, &sm);
+            o->scales[r * o->k_blocks32 + b] = sc;
+            o->sums[r * o->k_blocks32 + b] = sm;
+            size_t sbi = (32 * b) / 256;
+            if (sbi < o->sb256 && sc > o->super256[r * o->sb256 + sbi]) o->super256[r * o->sb256 + sbi] = sc;
+        }
+        /* x_sums_16: `.iter().copied().sum()` over the sanitized f32 row (repack.rs:644-645) */
+        for (size_t c = 0; c < o->k_chunks; c++) {
+            float s = neg_zero();
+            for (int i = 0; i < 16; i++) s += row_f32[16 * c + i];
+            o->sums16[r * o->k_chunks + c] = s;
+        }
+    }
+    free(row_f32);
+    return OR_OK;
+}
+
+/* Shared tail of lib.rs:1072-1098 on already-normalized values. */
+static float absmax_quantize_tail(int8_t *out, const float *xn, size_t len) {
+    float max_val = 0.0f;
+    for (size_t i = 0; i < len; i++) {
+        float a = fabsf(xn[i]);
+        if (a > max_val) max_val = a;
+    }
+    if (isnan(max_val) || max_val < 1e-12f) {
+        memset(out, 0, len);
+        return 1.0f / 127.0f;
+    }
+    float scale = max_val / 127.0f;
+    for (size_t i = 0; i < len; i++) out[i] = rust_round_clamp_i8(xn[i] / scale, -128.0f, 127.0f);
+    return scale;
+}
+
+/* lib.rs:1042-1101 */
+int or_subln_quantize_absmax_i8(int8_t *out, const float *in, const float *w, size_t len,
+                                float eps, float *scale_out) {
+    if (len == 0) return OR_TENSOR_BOUNDS;
+    float sum_sq = 0.0f; /* dot_product_f32_scalar, lib.rs:770-778 */
+    for (size_t i = 0; i < len; i++) sum_sq += in[i] * in[i];
+    float mean_sq = sum_sq / (float)len;
+    float inv_rms = 1.0f / sqrtf(mean_sq + eps);
+    float *xn = malloc(len * sizeof(float));
+    if (!xn) return OR_TENSOR_BOUNDS;
+    for (size_t i = 0; i < len; i++) xn[i] = in[i] * inv_rms * w[i];
+    *scale_out = absmax_quantize_tail(out, xn, len);
+    free(xn);
+    return OR_OK;
+}
+
+/* Per-token absmax quantizer without the RMSNorm step: lib.rs:1072-1098 applied to
+ * x_norm = input (identical to the subln recipe whenever inv_rms == 1 and w == 1). */
+int or_quantize_absmax_i8(int8_t *out, const float *in, size_t len, float *scale_out) {
+    if (len == 0) return OR_TENSOR_BOUNDS;
+    *scale_out = absmax_quantize_tail(out, in, len);
+    return OR_OK;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Validators                                                                 */
+/* ------------------------------------------------------------------------- */
+
+/* Orientation rule shared by validate_quant_matvec_dimensions (quant.rs:1810-1894),
+ * validate_q4_0/q8_0/q6_k_dimensions (quant.rs:762-892, 1315-1394) and
+ * validate_q4_k_m_dimensions (lib.rs:1195-1260): [rows, cols] or GGUF [cols, rows]. */
+static int orient(const or_tensor_view *w, int quant, size_t out_len, size_t in_len,
+                  size_t *rows, size_t *cols) {
+    if (w->quant != quant) return OR_TENSOR_BOUNDS;
+    if (w->ndim == 0) return OR_TENSOR_BOUNDS;
+    size_t be = or_block_elements(quant);
+    if (w->ndim == 2) {
+        size_t d0 = w->shape[0], d1 = w->shape[1];
+        if (out_len == d0 && in_len == d1 && d1 % be == 0) { *rows = d0; *cols = d1; }
+        else if (out_len == d1 && in_len == d0 && d0 % be == 0) { *rows = d1; *cols = d0; }
+        else return OR_TENSOR_BOUNDS;
+    } else {
+        size_t total = num_elements(w);
+        if (in_len == 0 || out_len == 0 || in_len % be || out_len * in_len != total) return OR_TENSOR_BOUNDS;
+        *rows = out_len; *cols = in_len;
+    }
+    /* Byte-length check (quant.rs:1881-1891). The Q8_0 / Q6_K / Q4_K validators leave it
+     * to the slice bound, which panics; here every format fails closed instead. */
+    if (*cols == 0 || *rows == 0) return OR_TENSOR_BOUNDS;
+    size_t need = (*rows * *cols / be) * or_block_bytes(quant) + or_scale_trailer_bytes(quant);
+    if (w->byte_len < need) return OR_TENSOR_BOUNDS;
+    return OR_OK;
+}
+
+/* ------------------------------------------------------------------------- */
+/* quant_q8 integer block dots                                                */
+/* ------------------------------------------------------------------------- */
+
+/* quant_q8.rs:672-684 */
+static float dot_q4_0_q8_0_block(const uint8_t *w, const or_block_q8_0 *x) {
+    float dw = or_f16_to_f32_finite(rd16(w));
+    if (dw == 0.0f || x->d == 0.0f) return 0.0f;
+    int32_t sumi = 0;
+    for (int i = 0; i < 16; i++) {
+        uint8_t b = w[2 + i];
+        sumi += ((int)(b & 0x0F) - 8) * x->qs[i] + ((int)((b >> 4) & 0x0F) - 8) * x->qs[i + 16];
+    }
+    return (float)sumi * (dw * x->d);
+}
+
+/* quant_q8.rs:707-717 */
+static float dot_q8_0_q8_0_block(const uint8_t *w, const or_block_q8_0 *x) {
+    float dw = or_f16_to_f32_finite(rd16(w));
+    if (dw == 0.0f || x->d == 0.0f) return 0.0f;
+    int32_t sumi = 0;
+    for (int i = 0; i < 32; i++) sumi += (int8_t)w[2 + i] * x->qs[i];
+    return (float)sumi * (dw * x->d);
+}
+
+/* quant_q8.rs:1834-1862 */
+static float dot_q4_k_q8_k_block(const uint8_t *w, const or_block_q8k *x) {
+    float d = or_f16_to_f32_finite(rd16(w)), dmin = or_f16_to_f32_finite(rd16(w + 2));
+    if ((d == 0.0f && dmin == 0.0f) || x->d == 0.0f) return 0.0f;
+    uint8_t sc[8], m[8];
+    unpack_k4_scales_mins(w + 4, sc, m);
+    const uint8_t *qs = w + 16;
+    int32_t sumi = 0, sum_mins = 0;
+    for (int c = 0; c < 4; c++) {
+        int32_t lo = 0, hi = 0;
+        for (int l = 0; l < 32; l++) {
+            uint8_t b = qs[32 * c + l];
+            lo += (b & 0x0F) * x->qs[64 * c + l];
+            hi += (b >> 4) * x->qs[64 * c + 32 + l];
+        }
+        sumi += sc[2 * c] * lo + sc[2 * c + 1] * hi;
+        int32_t bl = x->bsums[4 * c] + x->bsums[4 * c + 1];
+        int32_t bh = x->bsums[4 * c + 2] + x->bsums[4 * c + 3];
+        sum_mins += m[2 * c] * bl + m[2 * c + 1] * bh;
+    }
+    return (d * x->d) * (float)sumi - (dmin * x->d) * (float)sum_mins;
+}
+
+/* quant_q8.rs:1903-1942 */
+static float dot_q6_k_q8_k_block(const uint8_t *w, const or_block_q8k *x) {
+    float d = or_f16_to_f32_finite(rd16(w + 208));
+    if (d == 0.0f || x->d == 0.0f) return 0.0f;
+    const uint8_t *ql = w, *qh = w + 128;
+    const int8_t *sc = (const int8_t *)(w + 192);
+    int32_t sumi = 0;
+    for (int h = 0; h < 2; h++) {
+        int n = 128 * h;
+        for (int is = 0; is < 2; is++) {
+            int32_t s1 = 0, s2 = 0, s3 = 0, s4 = 0;
+            for (int l = 16 * is; l < 16 * is + 16; l++) {
+                uint8_t bl = ql[64 * h + l], bh = ql[64 * h + l + 32], hb = qh[32 * h + l];
+                int q1 = (int)((bl & 0x0F) | ((hb & 3) << 4)) - 32;
+                int q2 = (int)((bh & 0x0F) | (((hb >> 2) & 3) << 4)) - 32;
+                int q3 = (int)((bl >> 4) | (((hb >> 4) & 3) << 4)) - 32;
+                int q4 = (int)((bh >> 4) | (((hb >> 6) & 3) << 4)) - 32;
+                s1 += q1 * x->qs[n + l];
+                s2 += q2 * x->qs[n + l + 32];
+                s3 += q3 * x->qs[n + l + 64];
+                s4 += q4 * x->qs[n + l + 96];
+            }
+            sumi += sc[8 * h + is] * s1 + sc[8 * h + is + 2] * s2 + sc[8 * h + is + 4] * s3 +
+                    sc[8 * h + is + 6] * s4;
+        }
+    }
+    return (d * x->d) * (float)sumi;
+}
+
+/* quant_q8.rs:1992-2003 with dot_i8_scalar ime.rs:490-496 */
+static float dot_tq2_0_q8_k_block(const uint8_t *w, const or_block_q8k *x) {
+    if (x->d == 0.0f) return 0.0f;
+    int8_t t[256];
+    float dw = or_unpack_tq2_0_block_i8(w, t);
+    if (dw == 0.0f) return 0.0f;
+    int32_t dot = 0;
+    for (int i = 0; i < 256; i++) dot += t[i] * x->qs[i];
+    return (float)dot * (dw * x->d);
+}
+
+typedef float (*blockdot_fn)(const uint8_t *, const void *);
+
+static float bd_q4_0(const uint8_t *w, const void *x) { return dot_q4_0_q8_0_block(w, x); }
+static float bd_q8_0(const uint8_t *w, const void *x) { return dot_q8_0_q8_0_block(w, x); }
+static float bd_q4_k(const uint8_t *w, const void *x) { return dot_q4_k_q8_k_block(w, x); }
+static float bd_q6_k(const uint8_t *w, const void *x) { return dot_q6_k_q8_k_block(w, x); }
+static float bd_tq2_0(const uint8_t *w, const void *x) { return dot_tq2_0_q8_k_block(w, x); }
+
+static blockdot_fn blockdot_for(int q, size_t *xsz) {
+    switch (q) {
+    case OR_Q4_0: *xsz = sizeof(or_block_q8_0); return bd_q4_0;
+    case OR_Q8_0: *xsz = sizeof(or_block_q8_0); return bd_q8_0;
+    case OR_Q4_K: *xsz = sizeof(or_block_q8k); return bd_q4_k;
+    case OR_Q6_K: *xsz = sizeof(or_block_q8k); return bd_q6_k;
+    case OR_TQ2_0: *xsz = sizeof(or_block_q8k); return bd_tq2_0;
+    default: return 0;
+    }
+}
+
+/* Row drivers dot_*_row (quant_q8.rs:1217-1238, 2815-2830, 2902-2915, 2987-2993):
+ * `.map(block_dot).sum()` -> fold from -0.0 in block order. */
+static float row_sum_neg0(blockdot_fn f, const uint8_t *w, size_t bb, const uint8_t *x, size_t xsz,
+                          size_t nb) {
+    float acc = neg_zero();
+    for (size_t b = 0; b < nb; b++) acc += f(w + b * bb, x + b * xsz);
+    return acc;
+}
+
+/* validate_q8_block_row_bytes, quant_q8.rs:644-664 */
+static int vec_dot_rowblocks(int q, const uint8_t *w, size_t w_len, const void *x, size_t nx,
+                             float *out) {
+    size_t xsz, bb = or_block_bytes(q);
+    blockdot_fn f = blockdot_for(q, &xsz);
+    if (nx == 0 || w_len != nx * bb) return OR_TENSOR_BOUNDS;
+    *out = row_sum_neg0(f, w, bb, x, xsz, nx);
+    return OR_OK;
+}
+
+/* quant_q8.rs:1463 */
+int or_vec_dot_q4_0_q8_0(const uint8_t *w, size_t w_len, const or_block_q8_0 *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_Q4_0, w, w_len, x, nx, out);
+}
+/* quant_q8.rs:1493 */
+int or_vec_dot_q8_0_q8_0(const uint8_t *w, size_t w_len, const or_block_q8_0 *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_Q8_0, w, w_len, x, nx, out);
+}
+/* quant_q8.rs:3019 */
+int or_vec_dot_q4_k_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_Q4_K, w, w_len, x, nx, out);
+}
+/* quant_q8.rs:3056 */
+int or_vec_dot_q6_k_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_Q6_K, w, w_len, x, nx, out);
+}
+/* quant_q8.rs:3086 */
+int or_vec_dot_tq2_0_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_TQ2_0, w, w_len, x, nx, out);
+}
+
+/* run_4row_chunked_gemv (quant_q8.rs:1510-1560) with accumulate = false:
+ * rows below (rows / 4) * 4 use the 4-row kernels (acc = [0.0; 4], += per block),
+ * the tail rows use the 1-row `.sum()` driver. */
+int or_gemv_rows(int quant, float *out, const uint8_t *w, size_t rows, size_t cols, const void *x,
+                 size_t r0, size_t r1) {
+    size_t xsz, bb = or_block_bytes(quant), nb = cols / or_block_elements(quant);
+    blockdot_fn f = blockdot_for(quant, &xsz);
+    if (!f) return OR_CAPABILITY_MISMATCH;
+    size_t rows4 = rows / 4 * 4, stride = nb * bb;
+    for (size_t r = r0; r < r1; r++) {
+        const uint8_t *wr = w + r * stride;
+        if (r < rows4) {
+            float acc = 0.0f;
+            for (size_t b = 0; b < nb; b++) acc += f(wr + b * bb, (const uint8_t *)x + b * xsz);
+            out[r - r0] = acc;
+        } else {
+            out[r - r0] = row_sum_neg0(f, wr, bb, x, xsz, nb);
+        }
+    }
+    return OR_OK;
+}
+
+/* gemv_* entry points: cols = x_blocks.len() * block_elements, then the format's
+ * validator and check_q8_block_len (quant_q8.rs:1562-1578). */
+static int gemv_entry(int quant, float *out, size_t out_len, const or_tensor_view *w,
+                      const void *x, size_t nx) {
+    size_t rows, cols;
+    int st = orient(w, quant, out_len, nx * or_block_elements(quant), &rows, &cols);
+    if (st) return st;
+    if (nx != cols / or_block_elements(quant)) return OR_TENSOR_BOUNDS;
+    return or_gemv_rows(quant, out, w->bytes, rows, cols, x, 0, rows);
+}
+
+/* quant_q8.rs:1586-1605 */
+int or_gemv_q4_0_q8_0(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8_0 *x, size_t nx) {
+    return gemv_entry(OR_Q4_0, out, out_len, w, x, nx);
+}
+/* quant_q8.rs:1670-1689 */
+int or_gemv_q8_0_q8_0(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8_0 *x, size_t nx) {
+    return gemv_entry(OR_Q8_0, out, out_len, w, x, nx);
+}
+/* quant_q8.rs:3101-3123 */
+int or_gemv_q4_k_q8_k(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8k *x, size_t nx) {
+    return gemv_entry(OR_Q4_K, out, out_len, w, x, nx);
+}
+/* quant_q8.rs:3189-3211 */
+int or_gemv_q6_k_q8_k(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8k *x, size_t nx) {
+    return gemv_entry(OR_Q6_K, out, out_len, w, x, nx);
+}
+/* quant_q8.rs:3250-3273 */
+int or_gemv_tq2_0_q8_k(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8k *x, size_t nx) {
+    return gemv_entry(OR_TQ2_0, out, out_len, w, x, nx);
+}
+
+/* ------------------------------------------------------------------------- */
+/* f32-activation matvec: dequantize block, dot_product_f32_scalar, row sum   */
+/* ------------------------------------------------------------------------- */
+
+/* vec_dot_q4_0_scalar quant.rs:1401-1436, vec_dot_q8_0_scalar 899-934,
+ * vec_dot_q6_k_scalar 1012-1047, vec_dot_q4_k_m_scalar lib.rs:1268-1303,
+ * vec_dot_i2_s quant.rs:2199-2240 (zero trailer scale -> row 0.0). */
+static int vec_dot_f32_entry(int quant, float *out, size_t out_len, const or_tensor_view *w,
+                             const float *in, size_t in_len) {
+    size_t rows, cols;
+    int st = orient(w, quant, out_len, in_len, &rows, &cols);
+    if (st) return st;
+    size_t be = or_block_elements(quant), bb = or_block_bytes(quant), nb = cols / be;
+    float s = 1.0f;
+    if (quant == OR_I2_S) {
+        size_t payload = rows * nb * bb;
+        s = or_read_i2_s_trailer_scale(w->bytes + payload, w->byte_len - payload);
+    }
+    float buf[256];
+    for (size_t r = 0; r < rows; r++) {
+        if (quant == OR_I2_S && s == 0.0f) { out[r] = 0.0f; continue; }
+        float row_sum = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            dequant_block_any(quant, w->bytes + (r * nb + b) * bb, s, buf);
+            float sum = 0.0f; /* lib.rs:770-778 */
+            for (size_t i = 0; i < be; i++) sum += buf[i] * in[b * be + i];
+            row_sum += sum;
+        }
+        out[r] = row_sum;
+    }
+    return OR_OK;
+}
+
+int or_vec_dot_q4_0(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q4_0, out, out_len, w, in, in_len);
+}
+int or_vec_dot_q8_0(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q8_0, out, out_len, w, in, in_len);
+}
+int or_vec_dot_q6_k(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q6_K, out, out_len, w, in, in_len);
+}
+int or_vec_dot_q4_k_m(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q4_K, out, out_len, w, in, in_len);
+}
+int or_vec_dot_i2_s(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_I2_S, out, out_len, w, in, in_len);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Repacked block-scaled i8 weights and GEMM                                  */
+/* ------------------------------------------------------------------------- */
+
+/* validate_matrix_view (repack.rs:1208-1281) + validate_matrix_shape (1172-1206). */
+static int validate_matrix_view(const or_tensor_view *w, size_t rows, size_t cols) {
+    if (rows == 0 || cols == 0) return OR_TENSOR_BOUNDS;
+    size_t be = or_block_elements(w->quant);
+    if (cols % be) return OR_TENSOR_BOUNDS;
+    if (w->ndim == 1) {
+        if (rows * cols != w->shape[0]) return OR_TENSOR_BOUNDS;
+    } else if (w->ndim == 2) {
+        size_t d0 = w->shape[0], d1 = w->shape[1];
+        if (!((d0 == rows && d1 == cols) || (d0 == cols && d1 == rows))) return OR_TENSOR_BOUNDS;
+    } else {
+        return OR_TENSOR_BOUNDS;
+    }
+    size_t need = rows * (cols / be) * or_block_bytes(w->quant) + or_scale_trailer_bytes(w->quant);
+    if (w->byte_len < need) return OR_TENSOR_BOUNDS;
+    return OR_OK;
+}
+
+/* BlockScaledTileLayout::from_validated_dims (repack.rs:1334-1366) and the per-format
+ * arms of repack_block_scaled_range_into_i8 (repack.rs:1724-2103), written to a
+ * logical row-major layout: q[rows][cols], scales/mins[rows][scale_groups]. */
+int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t *q,
+                      float *scales, float *mins, size_t *sg_out, int *has_mins_out, int *cps_out) {
+    if (!known_quant(w->quant)) return OR_CAPABILITY_MISMATCH;
+    int st = validate_matrix_view(w, rows, cols);
+    if (st) return st;
+    int cps = w->quant == OR_Q6_K ? 1 : 2;
+    size_t k_padded = (cols + 31) / 32 * 32, sg = k_padded / 16 / cps;
+    int has_mins = w->quant == OR_Q4_K;
+    if (sg_out) *sg_out = sg;
+    if (has_mins_out) *has_mins_out = has_mins;
+    if (cps_out) *cps_out = cps;
+    if (!q) return OR_OK;
+    size_t be = or_block_elements(w->quant), bb = or_block_bytes(w->quant), nb = cols / be;
+    size_t row_bytes = nb * bb;
+    float i2s = 0.0f;
+    if (w->quant == OR_I2_S)
+        i2s = or_read_i2_s_trailer_scale(w->bytes + rows * row_bytes, w->byte_len - rows * row_bytes);
+    memset(q, 0, rows * k_padded);
+    for (size_t i = 0; i < rows * sg; i++) scales[i] = 0.0f;
+    if (has_mins && mins) for (size_t i = 0; i < rows * sg; i++) mins[i] = 0.0f;
+    for (size_t r = 0; r < rows; r++) {
+        const uint8_t *rr = w->bytes + r * row_bytes;
+        int8_t *qr = q + r * k_padded;
+        float *sr = scales + r * sg;
+        float *mr = has_mins ? mins + r * sg : 0;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t *blk = rr + b * bb;
+            switch (w->quant) {
+            case OR_Q8_0: { /* repack.rs:1766-1781 */
+                float d = or_f16_to_f32_finite(rd16(blk));
+                sr[b] = d;
+                if (d != 0.0f) for (int i = 0; i < 32; i++) qr[32 * b + i] = (int8_t)blk[2 + i];
+                break;
+            }
+            case OR_Q4_0: { /* repack.rs:1782-1813 */
+                float d = or_f16_to_f32_finite(rd16(blk));
+                sr[b] = d;
+                if (d != 0.0f)
+                    for (int i = 0; i < 16; i++) {
+                        qr[32 * b + i] = (int8_t)((blk[2 + i] & 0x0F) - 8);
+                        qr[32 * b + i + 16] = (int8_t)(((blk[2 + i] >> 4) & 0x0F) - 8);
+                    }
+                break;
+            }
+            case OR_Q4_K: { /* repack.rs:1912-1955 */
+                float d = or_f16_to_f32_finite(rd16(blk)), dmin = or_f16_to_f32_finite(rd16(blk + 2));
+                uint8_t sc[8], m[8];
+                unpack_k4_scales_mins(blk + 4, sc, m);
+                for (int c = 0; c < 4; c++) {
+                    size_t g0 = 8 * b + 2 * c;
+                    sr[g0] = d * (float)sc[2 * c];
+                    mr[g0] = dmin * (float)m[2 * c];
+                    sr[g0 + 1] = d * (float)sc[2 * c + 1];
+                    mr[g0 + 1] = dmin * (float)m[2 * c + 1];
+                    for (int l = 0; l < 32; l++) {
+                        qr[256 * b + 64 * c + l] = (int8_t)(blk[16 + 32 * c + l] & 0x0F);
+                        qr[256 * b + 64 * c + 32 + l] = (int8_t)(blk[16 + 32 * c + l] >> 4);
+                    }
+                }
+                break;
+            }
+            case OR_Q6_K: { /* repack.rs:2003-2046 */
+                float d = or_f16_to_f32_finite(rd16(blk + 208));
+                for (int s = 0; s < 16; s++) sr[16 * b + s] = d * (float)(int8_t)blk[192 + s];
+                if (d != 0.0f) {
+                    const uint8_t *ql = blk, *qh = blk + 128;
+                    for (int h = 0; h < 2; h++)
+                        for (int l = 0; l < 32; l++) {
+                            uint8_t bl = ql[64 * h + l], bh = ql[64 * h + l + 32], hb = qh[32 * h + l];
+                            int8_t *o = qr + 256 * b + 128 * h;
+                            o[l] = (int8_t)(((bl & 0x0F) | ((hb & 3) << 4)) - 32);
+                            o[l + 32] = (int8_t)(((bh & 0x0F) | (((hb >> 2) & 3) << 4)) - 32);
+                            o[l + 64] = (int8_t)(((bl >> 4) | (((hb >> 4) & 3) << 4)) - 32);
+                            o[l + 96] = (int8_t)(((bh >> 4) | (((hb >> 6) & 3) << 4)) - 32);
+                        }
+                }
+                break;
+            }
+            case OR_TQ2_0: { /* repack.rs:2061-2075: trits always written */
+                float d = or_unpack_tq2_0_block_i8(blk, qr + 256 * b);
+                for (int s = 0; s < 8; s++) sr[8 * b + s] = d;
+                break;
+            }
+            case OR_I2_S: { /* repack.rs:2076-2092 */
+                int8_t t[128];
+                or_unpack_i2_s_block_i8(blk, t);
+                for (int s = 0; s < 4; s++) sr[4 * b + s] = i2s;
+                if (i2s != 0.0f) memcpy(qr + 128 * b, t, 128);
+                break;
+            }
+            }
+        }
+    }
+    return OR_OK;
+}
+
+/* execute_gemm_repacked_rows (repack.rs:2718-3042) on the scalar arm with
+ * tile_dot_scalar_rows (ime.rs:127-148) and accumulate_scaled_tile_scalar
+ * (repack.rs:3045-3093): acc starts at 0.0 and adds one term per scale group in order. */
+int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t rows, size_t cols,
+                     const or_act_q8 *act, size_t r0, size_t r1) {
+    size_t sg;
+    int has_mins, cps;
+    int st = or_repack_logical(w, rows, cols, 0, 0, 0, &sg, &has_mins, &cps);
+    if (st) return st;
+    if (act->k != cols) return OR_TENSOR_BOUNDS;
+    if (r0 > r1 || r1 > rows) return OR_TENSOR_BOUNDS;
+    size_t m = act->m, sub = r1 - r0;
+    if (out_len != m * sub) return OR_TENSOR_BOUNDS;
+    if (sub == 0) return OR_OK;
+    size_t kp = (cols + 31) / 32 * 32;
+    int8_t *q = malloc(rows * kp);
+    float *sc = malloc(rows * sg * sizeof(float));
+    float *mn = has_mins ? malloc(rows * sg * sizeof(float)) : 0;
+    if (!q || !sc || (has_mins && !mn)) { free(q); free(sc); free(mn); return OR_TENSOR_BOUNDS; }
+    or_repack_logical(w, rows, cols, q, sc, mn, 0, 0, 0);
+    size_t gl = 16 * (size_t)cps;
+    for (size_t i = 0; i < m; i++) {
+        const int8_t *xq = act->qs + i * act->k_padded;
+        for (size_t r = r0; r < r1; r++) {
+            const int8_t *wq = q + r * kp;
+            float acc = 0.0f;
+            for (size_t g = 0; g < sg; g++) {
+                int32_t c = 0;
+                for (size_t k = g * gl; k < (g + 1) * gl; k++) c += xq[k] * wq[k];
+                size_t b32 = cps == 2 ? g : g / 2;
+                float xs = act->scales[i * act->k_blocks32 + b32];
+                float ws = sc[r * sg + g];
+                if (has_mins) {
+                    float xsm = cps == 2 ? act->sums[i * act->k_blocks32 + b32] : act->sums16[i * act->k_chunks + g];
+                    acc += (float)c * (xs * ws) - xsm * mn[r * sg + g];
+                } else {
+                    acc += (float)c * (xs * ws);
+                }
+            }
+            out[i * sub + (r - r0)] = acc;
+        }
+    }
+    free(q); free(sc); free(mn);
+    return OR_OK;
+}
+
+/* ------------------------------------------------------------------------- */
+/* BitLinear: bitlinear_i8_rvv (ime.rs:882-938)                               */
+/* ------------------------------------------------------------------------- */
+
+/* validate_bitlinear_dimensions (ime.rs:660-763); TQ1_0 is outside this path. */
+int or_bitlinear_i8(float *out, size_t out_len, const or_tensor_view *w, const int8_t *act,
+                    size_t act_len, float act_scale) {
+    int q = w->quant;
+    if (q != OR_TQ2_0 && q != OR_Q8_0 && q != OR_I2_S) return OR_TENSOR_BOUNDS;
+    if (w->ndim == 0) return OR_TENSOR_BOUNDS;
+    size_t be = or_block_elements(q), bb = or_block_bytes(q);
+    if (w->ndim == 2) {
+        size_t d0 = w->shape[0], d1 = w->shape[1];
+        if (!((out_len == d0 && act_len == d1 && d1 % be == 0) ||
+              (out_len == d1 && act_len == d0 && d0 % be == 0)))
+            return OR_TENSOR_BOUNDS;
+    } else {
+        size_t total = num_elements(w);
+        if (act_len == 0 || out_len == 0 || act_len % be || out_len * act_len != total) return OR_TENSOR_BOUNDS;
+    }
+    size_t rows = out_len, cols = act_len, nb = cols / be;
+    if (w->byte_len < (rows * cols / be) * bb + or_scale_trailer_bytes(q)) return OR_TENSOR_BOUNDS;
+    float i2s = 0.0f;
+    if (q == OR_I2_S)
+        i2s = or_read_i2_s_trailer_scale(w->bytes + rows * nb * bb, w->byte_len - rows * nb * bb);
+    int8_t wb[256];
+    for (size_t r = 0; r < rows; r++) {
+        float row_sum = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t *blk = w->bytes + (r * nb + b) * bb;
+            float bs; /* unpack_bitlinear_block_i8, ime.rs:792-871 */
+            if (q == OR_TQ2_0) bs = or_unpack_tq2_0_block_i8(blk, wb);
+            else if (q == OR_Q8_0) {
+                bs = or_f16_to_f32_finite(rd16(blk));
+                for (int i = 0; i < 32; i++) wb[i] = (int8_t)blk[2 + i];
+            } else {
+                or_unpack_i2_s_block_i8(blk, wb);
+                bs = i2s;
+            }
+            int32_t dot = 0;
+            for (size_t i = 0; i < be; i++) dot += wb[i] * act[b * be + i];
+            row_sum += (float)dot * (bs * act_scale);
+        }
+        out[r] = row_sum;
+    }
+    return OR_OK;
+}

@@ -1,0 +1,271 @@
+"""ctypes binding of liboracle.so -- the CPU restatement of the reference's scalar path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as the checker
+and by bench.py's cpu_baseline leg. The product path never imports this module.
+Status codes follow the product library: 0 ok, 1 TensorBoundsError, 2 CapabilityMismatch.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+BLOCK_Q8_0 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
+BLOCK_Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+
+_sz, _vp = C.c_size_t, C.c_void_p
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what}: oracle status {status}")
+        self.status = status
+
+
+class _View(C.Structure):
+    _fields_ = [("quant", C.c_int), ("shape", C.POINTER(_sz)), ("ndim", _sz), ("bytes", _vp), ("byte_len", _sz)]
+
+
+class _Act(C.Structure):
+    _fields_ = [("m", _sz), ("k", _sz), ("k_padded", _sz), ("k_blocks32", _sz), ("k_chunks", _sz), ("sb256", _sz),
+                ("qs", _vp), ("scales", _vp), ("sums", _vp), ("sums16", _vp), ("super256", _vp)]
+
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-C", HERE, "-s"], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        h = C.CDLL(LIB_PATH)
+        h.or_f16_to_f32_ieee.restype = C.c_float
+        h.or_f16_to_f32_ieee.argtypes = [C.c_uint16]
+        h.or_f16_to_f32_finite.restype = C.c_float
+        h.or_f16_to_f32_finite.argtypes = [C.c_uint16]
+        h.or_unpack_tq2_0_block_i8.restype = C.c_float
+        h.or_read_i2_s_trailer_scale.restype = C.c_float
+        h.or_act_q8_bytes.restype = _sz
+        h.or_act_q8_bytes.argtypes = [_sz, _sz]
+        _lib = h
+    return _lib
+
+
+def _p(a: np.ndarray) -> _vp:
+    return _vp(a.ctypes.data)
+
+
+class View:
+    """Keeps the shape array and bytes of a TensorView alive for one call."""
+
+    def __init__(self, quant: int, shape, data: np.ndarray):
+        self.data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        self.shape = (_sz * max(1, len(shape)))(*[int(s) for s in shape])
+        self.c = _View(int(quant), C.cast(self.shape, C.POINTER(_sz)), len(shape), self.data.ctypes.data,
+                       self.data.nbytes)
+
+
+def _ok(st: int, what: str) -> None:
+    if st != 0:
+        raise OracleError(st, what)
+
+
+def status_of(fn, *args) -> int:
+    """Runs fn and returns its oracle status (0 when it succeeds)."""
+    try:
+        fn(*args)
+        return 0
+    except OracleError as e:
+        return e.status
+
+
+# ----------------------------------------------------------------- f16 / blocks
+def f16_to_f32_ieee(bits: int) -> float:
+    return lib().or_f16_to_f32_ieee(bits)
+
+
+def f16_to_f32_finite(bits: int) -> float:
+    return lib().or_f16_to_f32_finite(bits)
+
+
+def dequantize_row_bytes(quant: int, row: np.ndarray, n_cols: int) -> np.ndarray:
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    out = np.zeros(n_cols, dtype=np.float32)
+    _ok(lib().or_dequantize_row_bytes(quant, _p(row), _sz(row.size), _sz(n_cols), _p(out), _sz(out.size)),
+        "dequantize_row_bytes")
+    return out
+
+
+def dequantize_tensor_row(quant: int, shape, data: np.ndarray, row: int, cols: int) -> np.ndarray:
+    v = View(quant, shape, data)
+    out = np.zeros(cols, dtype=np.float32)
+    _ok(lib().or_dequantize_tensor_row(C.byref(v.c), _sz(row), _p(out), _sz(cols)), "dequantize_tensor_row")
+    return out
+
+
+def unpack_tq2_0_block_i8(block: np.ndarray):
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(256, dtype=np.int8)
+    s = lib().or_unpack_tq2_0_block_i8(_p(b), _p(out))
+    return s, out
+
+
+def unpack_i2_s_block_i8(block: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(128, dtype=np.int8)
+    lib().or_unpack_i2_s_block_i8(_p(b), _p(out))
+    return out
+
+
+def dequantize_i2_s_block(block: np.ndarray, scale: float) -> np.ndarray:
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(128, dtype=np.float32)
+    lib().or_dequantize_i2_s_block(_p(b), C.c_float(scale), _p(out))
+    return out
+
+
+# ----------------------------------------------------------------- quantizers
+def quantize_row_q8_0(x: np.ndarray, out_len: int | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n = x.size // 32 if out_len is None else out_len
+    out = np.zeros(n, dtype=BLOCK_Q8_0)
+    _ok(lib().or_quantize_row_q8_0(_p(x), _sz(x.size), _p(out), _sz(n)), "quantize_row_q8_0")
+    return out
+
+
+def quantize_row_q8_k(x: np.ndarray, out_len: int | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n = x.size // 256 if out_len is None else out_len
+    out = np.zeros(n, dtype=BLOCK_Q8K)
+    _ok(lib().or_quantize_row_q8_k(_p(x), _sz(x.size), _p(out), _sz(n)), "quantize_row_q8_k")
+    return out
+
+
+class ActQ8:
+    """Logical QuantizedActQ8 contents (numpy views into one storage buffer)."""
+
+    def __init__(self, act: np.ndarray, m: int, k: int):
+        act = np.ascontiguousarray(act, dtype=np.float32).reshape(-1)
+        self.storage = np.zeros(lib().or_act_q8_bytes(m, k), dtype=np.uint8)
+        self.c = _Act()
+        _ok(lib().or_quantize_act_q8(_p(act), _sz(m), _sz(k), _p(self.storage), _sz(self.storage.size),
+                                     C.byref(self.c)), "quantize_act_q8")
+        c = self.c
+        self.m, self.k, self.k_padded = c.m, c.k, c.k_padded
+        self.k_blocks32, self.k_chunks, self.sb256 = c.k_blocks32, c.k_chunks, c.sb256
+        base = self.storage.ctypes.data
+
+        def arr(ptr, dtype, count):
+            off = ptr - base
+            return self.storage[off: off + count * np.dtype(dtype).itemsize].view(dtype)
+
+        self.scales = arr(c.scales, np.float32, m * c.k_blocks32).reshape(m, -1)
+        self.sums = arr(c.sums, np.float32, m * c.k_blocks32).reshape(m, -1)
+        self.sums16 = arr(c.sums16, np.float32, m * c.k_chunks).reshape(m, -1)
+        self.super256 = arr(c.super256, np.float32, m * c.sb256).reshape(m, -1)
+        self.qs = arr(c.qs, np.int8, m * c.k_padded).reshape(m, -1)
+
+
+def subln_quantize_absmax_i8(x: np.ndarray, w: np.ndarray, eps: float):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    q = np.zeros(x.size, dtype=np.int8)
+    s = C.c_float(0)
+    _ok(lib().or_subln_quantize_absmax_i8(_p(q), _p(x), _p(w), _sz(x.size), C.c_float(eps), C.byref(s)), "subln")
+    return q, s.value
+
+
+def quantize_absmax_i8(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.zeros(x.size, dtype=np.int8)
+    s = C.c_float(0)
+    _ok(lib().or_quantize_absmax_i8(_p(q), _p(x), _sz(x.size), C.byref(s)), "absmax")
+    return q, s.value
+
+
+# ----------------------------------------------------------------- quant_q8 path
+_VEC_DOT_Q8 = {2: "or_vec_dot_q4_0_q8_0", 8: "or_vec_dot_q8_0_q8_0", 12: "or_vec_dot_q4_k_q8_k",
+               14: "or_vec_dot_q6_k_q8_k", 35: "or_vec_dot_tq2_0_q8_k"}
+_GEMV_Q8 = {2: "or_gemv_q4_0_q8_0", 8: "or_gemv_q8_0_q8_0", 12: "or_gemv_q4_k_q8_k", 14: "or_gemv_q6_k_q8_k",
+            35: "or_gemv_tq2_0_q8_k"}
+
+
+def vec_dot_q8(quant: int, w_row: np.ndarray, x_blocks: np.ndarray) -> float:
+    w = np.ascontiguousarray(w_row, dtype=np.uint8)
+    x = np.ascontiguousarray(x_blocks)
+    out = C.c_float(0)
+    _ok(getattr(lib(), _VEC_DOT_Q8[quant])(_p(w), _sz(w.size), _p(x), _sz(x.size), C.byref(out)), "vec_dot_q8")
+    return out.value
+
+
+def gemv_q8(quant: int, shape, data: np.ndarray, x_blocks: np.ndarray, out_len: int) -> np.ndarray:
+    v = View(quant, shape, data)
+    x = np.ascontiguousarray(x_blocks)
+    out = np.zeros(out_len, dtype=np.float32)
+    _ok(getattr(lib(), _GEMV_Q8[quant])(_p(out), _sz(out_len), C.byref(v.c), _p(x), _sz(x.size)), "gemv_q8")
+    return out
+
+
+def gemv_rows(quant: int, data: np.ndarray, rows: int, cols: int, x_blocks: np.ndarray, r0: int, r1: int):
+    """Rows [r0, r1) of the quant_q8 GEMV (row-partitioned CPU baseline)."""
+    d = np.ascontiguousarray(data, dtype=np.uint8)
+    x = np.ascontiguousarray(x_blocks)
+    out = np.zeros(r1 - r0, dtype=np.float32)
+    _ok(lib().or_gemv_rows(quant, _p(out), _p(d), _sz(rows), _sz(cols), _p(x), _sz(r0), _sz(r1)), "gemv_rows")
+    return out
+
+
+_VEC_DOT_F32 = {2: "or_vec_dot_q4_0", 8: "or_vec_dot_q8_0", 14: "or_vec_dot_q6_k", 12: "or_vec_dot_q4_k_m",
+                36: "or_vec_dot_i2_s"}
+
+
+def vec_dot_f32(quant: int, shape, data: np.ndarray, x: np.ndarray, out_len: int) -> np.ndarray:
+    v = View(quant, shape, data)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(out_len, dtype=np.float32)
+    _ok(getattr(lib(), _VEC_DOT_F32[quant])(_p(out), _sz(out_len), C.byref(v.c), _p(x), _sz(x.size)),
+        "vec_dot_f32")
+    return out
+
+
+# ----------------------------------------------------------------- repack GEMM
+def repack_logical(quant: int, shape, data: np.ndarray, rows: int, cols: int):
+    v = View(quant, shape, data)
+    sg, hm, cps = _sz(0), C.c_int(0), C.c_int(0)
+    _ok(lib().or_repack_logical(C.byref(v.c), _sz(rows), _sz(cols), None, None, None, C.byref(sg), C.byref(hm),
+                                C.byref(cps)), "repack_logical")
+    kp = (cols + 31) // 32 * 32
+    q = np.zeros((rows, kp), dtype=np.int8)
+    sc = np.zeros((rows, sg.value), dtype=np.float32)
+    mn = np.zeros((rows, sg.value), dtype=np.float32) if hm.value else None
+    _ok(lib().or_repack_logical(C.byref(v.c), _sz(rows), _sz(cols), _p(q), _p(sc),
+                                _p(mn) if mn is not None else None, None, None, None), "repack_logical")
+    return q, sc, mn, cps.value
+
+
+def gemm_repacked(quant: int, shape, data: np.ndarray, rows: int, cols: int, act: ActQ8, r0: int, r1: int):
+    v = View(quant, shape, data)
+    out = np.zeros(act.m * (r1 - r0), dtype=np.float32)
+    _ok(lib().or_gemm_repacked(_p(out), _sz(out.size), C.byref(v.c), _sz(rows), _sz(cols), C.byref(act.c), _sz(r0),
+                               _sz(r1)), "gemm_repacked")
+    return out.reshape(act.m, r1 - r0)
+
+
+# ----------------------------------------------------------------- BitLinear
+def bitlinear_i8(quant: int, shape, data: np.ndarray, act: np.ndarray, act_scale: float, out_len: int):
+    v = View(quant, shape, data)
+    a = np.ascontiguousarray(act, dtype=np.int8).reshape(-1)
+    out = np.zeros(out_len, dtype=np.float32)
+    _ok(lib().or_bitlinear_i8(_p(out), _sz(out_len), C.byref(v.c), _p(a), _sz(a.size), C.c_float(act_scale)),
+        "bitlinear")
+    return out

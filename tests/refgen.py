@@ -1,0 +1,125 @@
+"""Seeded input generators of the reference crate's integration tests, restated in numpy.
+
+The reference synthesizes all test inputs in-test with an LCG
+(s = s * 6364136223846793005 + 1442695040888963407, tests/wave4_quant_gemv_and_argmax.rs:31-36);
+these functions produce inputs of the same construction for the parity tests here.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+M64 = (1 << 64) - 1
+
+
+class Lcg:
+    def __init__(self, seed: int, inc: int = 1442695040888963407):
+        self.s = seed & M64
+        self.inc = inc
+
+    def next(self) -> int:
+        self.s = (self.s * 6364136223846793005 + self.inc) & M64
+        return self.s
+
+    def hi32(self) -> int:
+        return self.next() >> 32
+
+
+def gen_activation(n: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:38-48"""
+    g = Lcg(seed)
+    r = np.array([g.hi32() for _ in range(n)], dtype=np.float64).astype(np.float32) / np.float32(4294967296.0)
+    i = np.arange(n, dtype=np.float32)
+    return ((r - np.float32(0.35)) * np.float32(1.4) + np.sin(i * np.float32(0.013)) * np.float32(0.2)).astype(np.float32)
+
+
+def _u16(v: int):
+    return [v & 0xFF, v >> 8]
+
+
+def fill_q4_0(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:77-96"""
+    nb = cols // 32
+    raw = np.zeros(rows * nb * 18, np.uint8)
+    g = Lcg(seed)
+    scales = [0x3000, 0x3200, 0x3400, 0x3600]
+    for r in range(rows):
+        for b in range(nb):
+            off = (r * nb + b) * 18
+            raw[off:off + 2] = _u16(scales[(r + b) % 4])
+            for j in range(16):
+                lo = (g.next() >> 32) % 16
+                hi = (g.next() >> 40) % 16
+                raw[off + 2 + j] = (hi << 4) | lo
+    return raw
+
+
+def fill_q8_0(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:116-133"""
+    nb = cols // 32
+    raw = np.zeros(rows * nb * 34, np.uint8)
+    g = Lcg(seed)
+    scales = [0x2800, 0x2C00, 0x3000, 0x3200]
+    for r in range(rows):
+        for b in range(nb):
+            off = (r * nb + b) * 34
+            raw[off:off + 2] = _u16(scales[(r + b) % 4])
+            for j in range(32):
+                q = (g.hi32() % 127) - 63
+                raw[off + 2 + j] = q & 0xFF
+    return raw
+
+
+def fill_q4_k(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:135-153"""
+    nb = cols // 256
+    raw = np.zeros(rows * nb * 144, np.uint8)
+    g = Lcg(seed)
+    for blk in range(rows * nb):
+        off = blk * 144
+        raw[off:off + 2] = _u16(0x3000)
+        raw[off + 2:off + 4] = _u16(0x2800)
+        for idx in range(4, 16):
+            raw[off + idx] = g.hi32() % 31 + 1
+        for idx in range(16, 144):
+            raw[off + idx] = g.hi32() & 0xFF
+    return raw
+
+
+def fill_q6_k(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:175-193"""
+    nb = cols // 256
+    raw = np.zeros(rows * nb * 210, np.uint8)
+    g = Lcg(seed)
+    for blk in range(rows * nb):
+        off = blk * 210
+        for idx in range(192):
+            raw[off + idx] = g.hi32() & 0xFF
+        for idx in range(192, 208):
+            raw[off + idx] = ((g.hi32() % 15) - 7) & 0xFF
+        raw[off + 208:off + 210] = _u16(0x3000)
+    return raw
+
+
+def fill_tq2_0(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:210-226"""
+    nb = cols // 256
+    raw = np.zeros(rows * nb * 66, np.uint8)
+    g = Lcg(seed)
+    for blk in range(rows * nb):
+        off = blk * 66
+        raw[off:off + 2] = _u16(0x3400)
+        for idx in range(2, 66):
+            raw[off + idx] = g.hi32() & 0xFF
+    return raw
+
+
+def cosine(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def rel_l2(got, ref) -> float:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(got - ref) / np.linalg.norm(ref))

@@ -1,0 +1,341 @@
+"""GPU parity: every libjk entry point against the oracle on identical seeded inputs.
+
+The bar is bit-exactness for everything (quantizers, dequantization, and the f32 outputs
+of GEMV / vec_dot / GEMM / BitLinear, whose per-block arithmetic and block-order
+accumulation follow the reference exactly). `same_bits` compares float bit patterns,
+so the sign of zero counts; two NaNs count as equal.
+"""
+import numpy as np
+import pytest
+
+import jk
+import oracle as O
+from jk import synth
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = jk.Q4_0, jk.Q8_0, jk.Q4_K, jk.Q6_K, jk.TQ2_0, jk.I2_S
+GEMV_FORMATS = [Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0]
+
+
+def same_bits(a, b) -> bool:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    if a.shape != b.shape:
+        return False
+    eq = a.view(np.uint32) == b.view(np.uint32)
+    return bool(np.all(eq | (np.isnan(a) & np.isnan(b))))
+
+
+def mismatch(a, b) -> str:
+    a, b = np.asarray(a, np.float32).ravel(), np.asarray(b, np.float32).ravel()
+    bad = np.nonzero(a.view(np.uint32) != b.view(np.uint32))[0]
+    if bad.size == 0:
+        return "ok"
+    i = bad[0]
+    return f"{bad.size} mismatches, first at {i}: gpu {a[i]!r} oracle {b[i]!r}"
+
+
+def dev(torch, arr):
+    a = np.ascontiguousarray(arr)
+    return torch.from_numpy(a.view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def empty(torch, nbytes):
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device="cuda")
+
+
+def host(t, dtype, count=None):
+    a = t.cpu().numpy().view(dtype)
+    return a if count is None else a[:count]
+
+
+def x_blocks(quant, x):
+    return O.quantize_row_q8_0(x) if quant in (Q4_0, Q8_0) else O.quantize_row_q8_k(x)
+
+
+def gpu_gemv(torch, w, xq, r0=0, r1=None):
+    r1 = w.rows if r1 is None else r1
+    dx = dev(torch, xq)
+    dy = empty(torch, 4 * (r1 - r0))
+    if r0 == 0 and r1 == w.rows:
+        jk.dev_gemv_q8(w, dx, xq.size, dy, w.rows)
+    else:
+        jk.dev_gemv_q8_rows(w, dx, xq.size, dy, r0, r1)
+    torch.cuda.synchronize()
+    return host(dy, np.float32, r1 - r0)
+
+
+# ------------------------------------------------------------------ quantizers
+@pytest.mark.parametrize("n", [32, 4096, 14336, 32 * 1001])
+def test_quantize_row_q8_0(gpu, n):
+    torch = gpu
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * rng.choice([1e-3, 1, 50], n)).astype(np.float32)
+    x[rng.random(n) < 0.01] = np.nan
+    x[rng.random(n) < 0.01] = np.inf
+    x[:32] = 0.0
+    ref = O.quantize_row_q8_0(x)
+    dy = empty(torch, ref.nbytes)
+    jk.dev_quantize_row_q8_0(dev(torch, x), n, dy, n // 32)
+    torch.cuda.synchronize()
+    got = host(dy, jk.BLOCK_Q8_0, ref.size)
+    assert same_bits(got["d"], ref["d"]) and np.array_equal(got["qs"], ref["qs"])
+
+
+@pytest.mark.parametrize("n", [256, 4096, 14336, 256 * 77])
+def test_quantize_row_q8_k(gpu, n):
+    torch = gpu
+    rng = np.random.default_rng(n + 1)
+    x = (rng.standard_normal(n) * rng.choice([1e-3, 1, 50], n)).astype(np.float32)
+    x[rng.random(n) < 0.01] = -np.inf
+    x[:256] = np.nan
+    ref = O.quantize_row_q8_k(x)
+    dy = empty(torch, ref.nbytes)
+    jk.dev_quantize_row_q8_k(dev(torch, x), n, dy, n // 256)
+    torch.cuda.synchronize()
+    got = host(dy, jk.BLOCK_Q8K, ref.size)
+    assert same_bits(got["d"], ref["d"])
+    assert np.array_equal(got["qs"], ref["qs"]) and np.array_equal(got["bsums"], ref["bsums"])
+
+
+def gpu_act(torch, x, m, k):
+    need = jk.act_q8_bytes(m, k)
+    storage = empty(torch, need)
+    act = jk.act_q8_bind(storage, need, m, k)
+    jk.dev_quantize_act_q8(dev(torch, x), m, k, act)
+    return storage, act
+
+
+@pytest.mark.parametrize("m,k", [(1, 4096), (5, 300), (64, 4096), (3, 40)])
+def test_quantize_act_q8(gpu, m, k):
+    torch = gpu
+    rng = np.random.default_rng(m * k)
+    x = (rng.standard_normal((m, k)) * rng.choice([1e-3, 1, 50], (m, k))).astype(np.float32)
+    x[rng.random((m, k)) < 0.01] = np.nan
+    x[0, :32] = -0.0
+    ref = O.ActQ8(x, m, k)
+    storage, act = gpu_act(torch, x, m, k)
+    torch.cuda.synchronize()
+    base = storage.data_ptr()
+    raw = storage.cpu().numpy()
+
+    def arr(ptr, dtype, count):
+        return raw[ptr - base: ptr - base + count * np.dtype(dtype).itemsize].view(dtype)
+
+    assert np.array_equal(arr(act.qs, np.int8, m * act.k_padded).reshape(m, -1), ref.qs)
+    for name, pa, refv in (("scales", act.scales, ref.scales), ("sums", act.sums, ref.sums),
+                           ("sums16", act.sums16, ref.sums16), ("super256", act.super256, ref.super256)):
+        got = arr(pa, np.float32, refv.size).reshape(refv.shape)
+        assert same_bits(got, refv), (name, mismatch(got, refv))
+
+
+@pytest.mark.parametrize("k", [2560, 6912, 100])
+def test_absmax_quantizers(gpu, k):
+    torch = gpu
+    rng = np.random.default_rng(k)
+    m = 4
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1] = 0.0
+    x[2] *= 1e-14
+    w = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    dq, ds = empty(torch, m * k), empty(torch, 4 * m)
+    jk.dev_subln_quantize_absmax_i8(dev(torch, x), dev(torch, w), m, k, 1e-5, dq, ds)
+    dq2, ds2 = empty(torch, m * k), empty(torch, 4 * m)
+    jk.dev_quantize_absmax_i8(dev(torch, x), m, k, dq2, ds2)
+    torch.cuda.synchronize()
+    for r in range(m):
+        q, s = O.subln_quantize_absmax_i8(x[r], w, 1e-5)
+        assert np.array_equal(host(dq, np.int8, m * k).reshape(m, k)[r], q)
+        assert same_bits(host(ds, np.float32, m)[r:r + 1], np.float32([s]))
+        q2, s2 = O.quantize_absmax_i8(x[r])
+        assert np.array_equal(host(dq2, np.int8, m * k).reshape(m, k)[r], q2)
+        assert same_bits(host(ds2, np.float32, m)[r:r + 1], np.float32([s2]))
+
+
+# ------------------------------------------------------------------ weights
+@pytest.mark.parametrize("quant", [Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S])
+def test_upload_and_dequantize_rows(gpu, quant):
+    torch = gpu
+    rows, cols = 19, 2048
+    raw = synth.random_weights(quant, rows, cols, seed=quant, specials=True)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    assert w.device_bytes == rows * cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[quant]
+    dy = empty(torch, 4 * rows * cols)
+    jk.dev_dequantize_rows(w, 0, rows, dy, rows * cols)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, rows * cols).reshape(rows, cols)
+    for r in range(rows):
+        ref = O.dequantize_tensor_row(quant, [rows, cols], raw, r, cols)
+        assert same_bits(got[r], ref), (r, mismatch(got[r], ref))
+
+
+# ------------------------------------------------------------------ quant_q8 GEMV
+@pytest.mark.parametrize("quant", GEMV_FORMATS)
+@pytest.mark.parametrize("rows,cols", [(1, 256), (3, 512), (5, 4352), (17, 1024), (33, 7168), (64, 2560)])
+def test_gemv_q8_small_shapes(gpu, quant, rows, cols):
+    torch = gpu
+    if cols % jk.BLOCK_ELEMENTS[quant]:
+        pytest.skip("shape not block aligned")
+    raw = synth.random_weights(quant, rows, cols, seed=rows * 7 + quant, specials=True)
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[: jk.BLOCK_ELEMENTS[quant]] = 0.0  # one all-zero activation block
+    xq = x_blocks(quant, x)
+    ref = O.gemv_q8(quant, [rows, cols], raw, xq, rows)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    got = gpu_gemv(torch, w, xq)
+    assert same_bits(got, ref), mismatch(got, ref)
+
+
+@pytest.mark.parametrize("quant", GEMV_FORMATS)
+def test_gemv_q8_row_slices_identical(gpu, quant):
+    torch = gpu
+    rows, cols = 61, 2048
+    raw = synth.gguf_weights(quant, rows, cols, seed=quant)
+    xq = x_blocks(quant, synth.activations(cols, 1))
+    w = jk.Weight(jk.TensorView("w", quant, [cols, rows], raw), rows, cols)
+    full = gpu_gemv(torch, w, xq)
+    assert same_bits(full, O.gemv_q8(quant, [cols, rows], raw, xq, rows))
+    for r0, r1 in ((0, 16), (7, 29), (57, 61), (60, 61)):
+        assert same_bits(gpu_gemv(torch, w, xq, r0, r1), full[r0:r1])
+
+
+CONFIG_MATRICES = [
+    ("C1 Q4_0 4096x4096", Q4_0, 4096, 4096),
+    ("C2 Q8_0 11008x4096", Q8_0, 11008, 4096),
+] + [(f"C3 {n}", q, r, c) for n, q, r, c in synth.LLAMA3_8B_LAYER] + [
+    ("C5 TQ2_0 6912x2560", TQ2_0, 6912, 2560),
+    ("C5 TQ2_0 2560x6912", TQ2_0, 2560, 6912),
+]
+
+
+@pytest.mark.parametrize("name,quant,rows,cols", CONFIG_MATRICES, ids=[c[0] for c in CONFIG_MATRICES])
+def test_gemv_q8_full_config_shapes(gpu, name, quant, rows, cols):
+    torch = gpu
+    raw = synth.gguf_weights(quant, rows, cols, seed=rows + cols + quant)
+    xq = x_blocks(quant, synth.activations(cols, 5))
+    ref = O.gemv_q8(quant, [cols, rows], raw, xq, rows)
+    w = jk.Weight(jk.TensorView(name, quant, [cols, rows], raw), rows, cols)
+    got = gpu_gemv(torch, w, xq)
+    assert same_bits(got, ref), mismatch(got, ref)
+
+
+# ------------------------------------------------------------------ f32 vec_dot
+@pytest.mark.parametrize("quant", [Q4_0, Q8_0, Q4_K, Q6_K, I2_S])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (5, 4352), (33, 4096)])
+def test_vec_dot_f32(gpu, quant, rows, cols):
+    torch = gpu
+    raw = synth.random_weights(quant, rows, cols, seed=rows + quant, specials=True)
+    x = np.random.default_rng(rows).standard_normal(cols).astype(np.float32)
+    ref = O.vec_dot_f32(quant, [rows, cols], raw, x, rows)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    dy = empty(torch, 4 * rows)
+    jk.dev_vec_dot_f32(w, dev(torch, x), cols, dy, rows)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, rows)
+    assert same_bits(got, ref), mismatch(got, ref)
+
+
+def test_vec_dot_i2_s_zero_scale_rows_are_zero(gpu):
+    torch = gpu
+    rows, cols = 6, 256
+    raw = synth.gguf_weights(I2_S, rows, cols, seed=1)
+    raw[-32:-28] = 0  # trailer scale 0.0
+    w = jk.Weight(jk.TensorView("w", I2_S, [rows, cols], raw), rows, cols)
+    dy = empty(torch, 4 * rows)
+    jk.dev_vec_dot_f32(w, dev(torch, np.ones(cols, np.float32)), cols, dy, rows)
+    torch.cuda.synchronize()
+    assert same_bits(host(dy, np.float32, rows), np.zeros(rows, np.float32))
+
+
+# ------------------------------------------------------------------ repacked GEMM
+def gpu_gemm(torch, w, x, m, r0=0, r1=None):
+    r1 = w.rows if r1 is None else r1
+    storage, act = gpu_act(torch, x, m, w.cols)
+    dy = empty(torch, 4 * m * (r1 - r0))
+    jk.dev_gemm_repacked(w, act, dy, m * (r1 - r0), r0, r1)
+    torch.cuda.synchronize()
+    return host(dy, np.float32, m * (r1 - r0)).reshape(m, r1 - r0)
+
+
+@pytest.mark.parametrize("quant", [Q8_0, Q4_0, Q4_K, Q6_K, TQ2_0, I2_S])
+@pytest.mark.parametrize("m,rows,cols", [(1, 37, 512), (5, 64, 256), (70, 100, 1024), (64, 128, 4096)])
+def test_gemm_repacked(gpu, quant, m, rows, cols):
+    torch = gpu
+    raw = synth.random_weights(quant, rows, cols, seed=m + quant, specials=True)
+    x = np.random.default_rng(m + rows).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    got = gpu_gemm(torch, w, x, m)
+    ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, O.ActQ8(x, m, cols), 0, rows)
+    assert same_bits(got, ref), mismatch(got, ref)
+    got_slice = gpu_gemm(torch, w, x, m, 3, rows - 5)
+    assert same_bits(got_slice, ref[:, 3:rows - 5])
+
+
+@pytest.mark.parametrize("m", [64, 512])
+def test_gemm_q8_0_prefill_shape_rows_sample(gpu, m):
+    """C4 prefill shape 14336 x 4096, M tokens: full GPU GEMM, oracle on row windows."""
+    torch = gpu
+    rows, cols = 14336, 4096
+    raw = synth.gguf_weights(Q8_0, rows, cols, seed=4)
+    x = synth.activations((m, cols), 6)
+    w = jk.Weight(jk.TensorView("ffn", Q8_0, [cols, rows], raw), rows, cols)
+    got = gpu_gemm(torch, w, x, m)
+    act = O.ActQ8(x, m, cols)
+    for r0 in (0, 7168, 14336 - 40):
+        ref = O.gemm_repacked(Q8_0, [cols, rows], raw, rows, cols, act, r0, r0 + 40)
+        assert same_bits(got[:, r0:r0 + 40], ref), (r0, mismatch(got[:, r0:r0 + 40], ref))
+
+
+# ------------------------------------------------------------------ BitLinear
+@pytest.mark.parametrize("quant", [TQ2_0, I2_S, Q8_0])
+@pytest.mark.parametrize("m,rows,cols", [(1, 7, 256), (3, 64, 2560), (2, 2560, 6912)])
+def test_bitlinear(gpu, quant, m, rows, cols):
+    torch = gpu
+    raw = synth.gguf_weights(quant, rows, cols, seed=m + quant) if quant != Q8_0 else \
+        synth.random_weights(quant, rows, cols, seed=m, specials=True)
+    rng = np.random.default_rng(rows)
+    a = rng.integers(-128, 128, (m, cols)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    dy = empty(torch, 4 * m * rows)
+    jk.dev_bitlinear_i8(w, dev(torch, a), dev(torch, sc), m, cols, dy, m * rows)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, m * rows).reshape(m, rows)
+    for i in range(m):
+        ref = O.bitlinear_i8(quant, [rows, cols], raw, a[i], float(sc[i]), rows)
+        assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
+
+
+# ------------------------------------------------------------------ host tier
+def test_host_tier_matches_oracle(gpu):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(4096).astype(np.float32)
+    assert np.array_equal(jk.quantize_row_q8_0(x).view(np.uint8), O.quantize_row_q8_0(x).view(np.uint8))
+    assert np.array_equal(jk.quantize_row_q8_k(x).view(np.uint8), O.quantize_row_q8_k(x).view(np.uint8))
+    raw = synth.gguf_weights(Q4_K, 9, 4096, seed=3)
+    xq = O.quantize_row_q8_k(x)
+    out = np.zeros(9, np.float32)
+    jk.gemv_q4_k_q8_k(out, jk.TensorView("w", Q4_K, [4096, 9], raw), xq)
+    assert same_bits(out, O.gemv_q8(Q4_K, [4096, 9], raw, xq, 9))
+    v = jk.vec_dot_q4_k_q8_k(raw[:16 * 144], xq)
+    assert same_bits(np.float32([v]), np.float32([O.vec_dot_q8(Q4_K, raw[:16 * 144], xq)]))
+    f = np.zeros(9, np.float32)
+    jk.vec_dot_q4_k_m(f, jk.TensorView("w", Q4_K, [4096, 9], raw), x)
+    assert same_bits(f, O.vec_dot_f32(Q4_K, [4096, 9], raw, x, 9))
+    row = np.zeros(4096, np.float32)
+    jk.dequantize_tensor_row(jk.TensorView("w", Q4_K, [4096, 9], raw), 4, row)
+    assert same_bits(row, O.dequantize_tensor_row(Q4_K, [4096, 9], raw, 4, 4096))
+    tq = synth.gguf_weights(TQ2_0, 5, 512, seed=1)
+    a = rng.integers(-128, 128, 512).astype(np.int8)
+    bl = np.zeros(5, np.float32)
+    jk.bitlinear_i8(bl, jk.TensorView("w", TQ2_0, [5, 512], tq), a, 0.02)
+    assert same_bits(bl, O.bitlinear_i8(TQ2_0, [5, 512], tq, a, 0.02, 5))
+    w8 = synth.gguf_weights(Q8_0, 40, 1024, seed=2)
+    w = jk.Weight(jk.TensorView("w", Q8_0, [40, 1024], w8), 40, 1024)
+    xs = rng.standard_normal((3, 1024)).astype(np.float32)
+    g = np.zeros(3 * 30, np.float32)
+    jk.host_gemm_repacked_f32(g, w, xs, 3, 5, 35)
+    ref = O.gemm_repacked(Q8_0, [40, 1024], w8, 40, 1024, O.ActQ8(xs, 3, 1024), 5, 35)
+    assert same_bits(g.reshape(3, 30), ref)
