@@ -3,13 +3,14 @@
 Headline (``value``): batch-1 decode GEMV throughput over Llama-3-8B layer shapes, in GB/s
 of algorithmic bytes (GGUF weight bytes + Q8_K activation blocks + f32 outputs). One step
 is one token's decode pass over ``--layers`` layers of distinct weights (32 = the whole
-Llama-3-8B stack, 4.4 GB, far larger than the 256 MB Infinity Cache): per layer the
-activations are quantized to Q8_K on the device (4 quantizations) and the seven GEMVs run
-(Q/K/V/O 4096-wide and gate/up 14336x4096 in Q4_K, down 4096x14336 in Q6_K). The step is
-captured once in a HIP graph and replayed.
+Llama-3-8B stack, 4.4 GB, far larger than the 256 MB Infinity Cache). Per layer the seven
+GEMVs (Q/K/V/O 4096-wide and gate/up 14336x4096 in Q4_K, down 4096x14336 in Q6_K) run in
+dependency order as four grouped launches -- {Q,K,V}, {O}, {gate,up}, {down} -- each
+quantizing its f32 activation to Q8_K on the device (bit-exact quantize_row_q8_k). The
+step is captured once in a HIP graph and replayed.
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel (Q4_K GEMV at the 14336x4096 gate/up shape), timed per
+  roofline      the dominant launch (grouped Q4_K gate+up GEMV, 2 x 14336x4096), timed per
                 launch with HIP events on the launch stream, against 8 TB/s HBM;
   gemm_q8_0     Q8_0 prefill GEMM 14336x4096 at 512 tokens (QuantizedActQ8 quantization +
                 int8-MFMA GEMM), in int8 TOPS against the 5.0 POPS dense int8 peak;
@@ -61,6 +62,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--gemm-m", type=int, default=512)
     ap.add_argument("--no-graph", action="store_true", help="launch the step eagerly instead of a HIP graph")
+    ap.add_argument("--down", choices=("fused", "split"), default="split",
+                    help="ffn_down activation: quantized inside the GEMV launch, or by its own launch")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -99,28 +102,40 @@ def main() -> int:
     log(f"layer algorithmic bytes {layer_bytes}, device weights {weight_dev_bytes / 1e9:.2f} GB")
 
     gen = torch.Generator(device="cpu").manual_seed(1234)
-    x_in = torch.randn(4096, generator=gen).to(dev)
-    a_in = torch.randn(4096, generator=gen).to(dev)
-    h_in = torch.randn(14336, generator=gen).to(dev)
-    q4096 = torch.empty(16 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
-    qa4096 = torch.empty_like(q4096)
-    q14336 = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
+    acts = {"x": torch.randn(4096, generator=gen).to(dev), "attn": torch.randn(4096, generator=gen).to(dev),
+            "ffn_in": torch.randn(4096, generator=gen).to(dev), "h": torch.randn(14336, generator=gen).to(dev)}
+    h_q8 = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
     outs = {name: torch.empty(rows, dtype=torch.float32, device=dev)
             for name, _, rows, _ in synth.LLAMA3_8B_LAYER}
+    # The layer's GEMVs in dependency order: each stage is one grouped launch whose
+    # activation is quantized to Q8_K inside the launch. ffn_down (K = 14336) takes its
+    # activation pre-quantized by a quantize_row_q8_k launch with --down split.
+    STAGES = [("qkv", ("attn_q", "attn_k", "attn_v"), "x"), ("attn_output", ("attn_output",), "attn"),
+              ("ffn_gate_up", ("ffn_gate", "ffn_up"), "ffn_in"), ("ffn_down", ("ffn_down",), "h")]
+    layer_jobs = []
+    for L in layers:
+        m = {name: (rows, w) for name, quant, rows, cols, w in L.mats}
+        per = []
+        for stage, names, act in STAGES:
+            if stage == "ffn_down" and args.down == "split":
+                jobs = [(m[n][1], h_q8, None, outs[n], 0, m[n][0]) for n in names]
+            else:
+                jobs = [(m[n][1], None, acts[act], outs[n], 0, m[n][0]) for n in names]
+            per.append((stage, jk.gemv_jobs(jobs), len(jobs)))
+        layer_jobs.append(per)
+    lib = jk.lib()
+
+    def launch_stage(stage, arr, n, stream):
+        if stage == "ffn_down" and args.down == "split":
+            jk.dev_quantize_row_q8_k(acts["h"], 14336, h_q8, 56, stream)
+        st = lib.jk_gemv_q8_batch(jk._vp(stream), arr, jk._sz(n))
+        if st != 0:
+            raise jk.K3Error(lib.jk_last_error().decode())
 
     def run_layers(stream):
-        for L in layers:
-            m = {name: (quant, rows, cols, w) for name, quant, rows, cols, w in L.mats}
-            jk.dev_quantize_row_q8_k(x_in, 4096, q4096, 16, stream)
-            for name in ("attn_q", "attn_k", "attn_v"):
-                jk.dev_gemv_q8(m[name][3], q4096, 16, outs[name], m[name][1], stream)
-            jk.dev_quantize_row_q8_k(a_in, 4096, qa4096, 16, stream)
-            jk.dev_gemv_q8(m["attn_output"][3], qa4096, 16, outs["attn_output"], 4096, stream)
-            jk.dev_quantize_row_q8_k(x_in, 4096, q4096, 16, stream)
-            for name in ("ffn_gate", "ffn_up"):
-                jk.dev_gemv_q8(m[name][3], q4096, 16, outs[name], m[name][1], stream)
-            jk.dev_quantize_row_q8_k(h_in, 14336, q14336, 56, stream)
-            jk.dev_gemv_q8(m["ffn_down"][3], q14336, 56, outs["ffn_down"], 4096, stream)
+        for per in layer_jobs:
+            for stage, arr, n in per:
+                launch_stage(stage, arr, n, stream)
 
     graph = None
     if not args.no_graph:
@@ -157,32 +172,32 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step (wall {wall * 1e3 / args.steps:.4f} ms/step)")
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Per-launch decomposition (events around each GEMV launch, eager) for the layer table.
+    # Per-stage decomposition: HIP events around each stage launch (eager, one layer after
+    # another so every launch streams weights not touched by the previous one).
     s = torch.cuda.current_stream().cuda_stream
-    per_mat = {}
-    for name, quant, rows, cols in synth.LLAMA3_8B_LAYER:
-        xq, nx = (q14336, 56) if cols == 14336 else (q4096, 16)
-        jk.dev_quantize_row_q8_k(h_in if cols == 14336 else x_in, cols, xq, nx, s)
+    mat_bytes = {name: gemv_bytes(q, r, c, jk) for name, q, r, c in synth.LLAMA3_8B_LAYER}
+    per_stage = {}
+    for si, (stage, names, _) in enumerate(STAGES):
         evs = []
         for rep in range(2):
-            for L in layers:
-                w = next(m[4] for m in L.mats if m[0] == name)
+            for per in layer_jobs:
+                _, arr, n = per[si]
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
-                jk.dev_gemv_q8(w, xq, nx, outs[name], rows, s)
+                launch_stage(stage, arr, n, s)
                 e1.record()
                 evs.append((e0, e1))
         torch.cuda.synchronize()
         dur_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in evs[len(layers):]]))  # second pass
-        b = gemv_bytes(quant, rows, cols, jk)
-        per_mat[name] = {"quant": jk.QUANT_NAMES[quant], "rows": rows, "cols": cols, "bytes": b,
-                         "us": round(dur_us, 3), "gbs": round(b / (dur_us * 1e-6) / 1e9, 1)}
-        log(f"  {name:12s} {rows}x{cols} {jk.QUANT_NAMES[quant]}: {dur_us:.2f} us, {per_mat[name]['gbs']} GB/s")
-    dom = per_mat["ffn_gate"]
+        b = sum(mat_bytes[n] for n in names)
+        per_stage[stage] = {"matrices": list(names), "bytes": b, "us": round(dur_us, 3),
+                            "gbs": round(b / (dur_us * 1e-6) / 1e9, 1)}
+        log(f"  {stage:12s} {b:>10d} B: {dur_us:.2f} us, {per_stage[stage]['gbs']} GB/s")
+    dom = per_stage["ffn_gate_up"]
     roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gemv_q8_kernel<Q4_K> (ffn_gate 14336x4096)", "avg_launch_us": dom["us"],
-                "bytes_per_launch": dom["bytes"]}
+                "kernel": "gemv_q8_group_kernel<Q4_K,16,f32> (ffn_gate + ffn_up, 2 x 14336x4096)",
+                "avg_launch_us": dom["us"], "bytes_per_launch": dom["bytes"]}
 
     # ------------------------------------------------------------ prefill GEMM (Q8_0)
     gemm = None
@@ -260,10 +275,11 @@ def main() -> int:
                                "down Q6_K, activations Q8_K (quantized on device each layer)",
                    "layers": args.layers, "hidden": 4096, "ffn": 14336, "kv_rows": 1024,
                    "bytes_per_step": step_bytes, "launch": "eager" if graph is None else "hip_graph",
+                   "launches_per_layer": 4 + (args.down == "split"), "down_activation": args.down,
                    "parallelism": "single_gpu"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "decode_tok_s_equiv": round(1e3 / ms_per_step * args.layers / 32, 1),
-        "roofline": roofline, "per_matrix": per_mat, "gemm_q8_0": gemm, "cpu_baseline": cpu,
+        "roofline": roofline, "per_stage": per_stage, "gemm_q8_0": gemm, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
     return 0

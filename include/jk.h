@@ -168,6 +168,27 @@ jk_status jk_gemv_tq2_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k
 jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t nx, float *y,
                           size_t row_begin, size_t row_end);
 
+/* Grouped quant_q8 GEMV: one launch evaluates several independent products of one
+ * weight format (e.g. a layer's Q/K/V projections, or gate and up). Each job is a
+ * gemv_* call of the five above over rows [row_begin, row_end) of its weight, writing
+ * y[row - row_begin]; its activation is either caller blocks (x_q8: BlockQ8_0 for
+ * Q4_0/Q8_0, BlockQ8K for Q4_K/Q6_K/TQ2_0) or f32 values (x_f32) that the launch
+ * quantizes with quantize_row_q8_0 / quantize_row_q8_k (quant_q8.rs:395, 576) -- results
+ * are identical either way. Jobs of different formats are split into separate launches.
+ * No single reference function corresponds: this is the reference's per-matrix sequence
+ * (quantize_row_q8_k, then gemv_q4_k_q8_k per matrix) batched into one launch. */
+typedef struct jk_gemv_job {
+    const jk_weight *w;
+    const void *x_q8;
+    const float *x_f32;
+    float *y;
+    size_t row_begin, row_end;
+} jk_gemv_job;
+jk_status jk_gemv_q8_batch(jk_stream s, const jk_gemv_job *jobs, size_t njobs);
+/* quantize_row_q8_0 / quantize_row_q8_k (quant_q8.rs:395, 576) of x followed by the
+ * matching gemv_* (quant_q8.rs:1586-3273) in one launch: y[rows] from f32 x[cols]. */
+jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len);
+
 /* ------------------------------------------ f32-activation matvec (vec_dot) */
 /* vec_dot_q4_0 (quant.rs:1458), vec_dot_q8_0 (1069), vec_dot_q6_k (1089),
  * VectorKernel::vec_dot_q4_k_m (lib.rs:157, scalar impl 1268-1303), vec_dot_i2_s

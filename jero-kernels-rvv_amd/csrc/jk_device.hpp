@@ -53,10 +53,99 @@ __device__ __forceinline__ float ld_dscale(const WeightDev &w, int r, int b) {
     return f16_finite(w.dplane[(size_t)r * (size_t)w.nb + (size_t)b]);
 }
 
+// Byte i of a dword, and dword i of a 16-byte chunk.
+__device__ __forceinline__ int byte_of(uint32_t v, int i) { return (int)((v >> (8 * i)) & 255u); }
+
+__device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 // Bytewise a - k for bytes that may borrow (k < 128 per byte): result bytes are the
 // two's-complement i8 values of (byte - k).
 __device__ __forceinline__ int bytes_sub(uint32_t a, uint32_t k) {
     return (int)(((a | 0x80808080u) - k) ^ 0x80808080u);
+}
+
+// Rust `v.round().clamp(lo, hi) as i8`: round half away from zero, NaN -> 0.
+__device__ __forceinline__ int rust_round_clamp_i8(float v, float lo, float hi) {
+    float r = roundf(v);
+    if (__builtin_isnan(r)) return 0;
+    r = r < lo ? lo : r;
+    r = r > hi ? hi : r;
+    return (int)r;
+}
+
+// round_scaled_to_i8 (quant_q8.rs:102-108)
+__device__ __forceinline__ int round_scaled_to_i8(float v, float inv) {
+    if (!__builtin_isfinite(v)) return 0;
+    return rust_round_clamp_i8(v * inv, -127.0f, 127.0f);
+}
+
+// DPP lane permutations (GFX9 encodings), all lanes of the row taking part:
+// quad_perm [1,0,3,2] = lane ^ 1, quad_perm [2,3,0,1] = lane ^ 2, row_half_mirror
+// (lane i <-> 7 - i within 8), row_mirror (lane i <-> 15 - i within 16).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
+// Maximum / sum over aligned groups of 4, 8 or 16 lanes; every lane of a group gets it.
+__device__ __forceinline__ float max8_dpp(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    return fmaxf(v, dpp_f<kDppHalfMirror>(v));
+}
+__device__ __forceinline__ int sum4_dpp(int v) {
+    v += dpp_i<kDppXor1>(v);
+    return v + dpp_i<kDppXor2>(v);
+}
+__device__ __forceinline__ int sum8_dpp(int v) {
+    v = sum4_dpp(v);
+    return v + dpp_i<kDppHalfMirror>(v);
+}
+
+// Maximum over the whole wave (all lanes active), returned wave-uniform.
+__device__ __forceinline__ float wave_max64_dpp(float v) {
+    v = max8_dpp(v);
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float e = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, e));
+}
+// Sum over the whole wave (all lanes active), returned wave-uniform.
+__device__ __forceinline__ int wave_sum64_dpp(int v) {
+    v = sum8_dpp(v);
+    v += dpp_i<kDppMirror>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
+
+template <int W>
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
+    return v;
+}
+
+// Ordered workgroup barrier for LDS traffic only: outstanding global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Makes this wave's LDS writes visible to the other lanes of the same wave.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
 }  // namespace jk

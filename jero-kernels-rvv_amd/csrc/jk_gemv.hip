@@ -1,4 +1,4 @@
-// jk_gemv.hip -- batch-1 matrix-vector kernels on the plane layout.
+// jk_gemv.hip -- f32-activation matvec (vec_dot_*) and BitLinear kernels on the plane layout.
 //
 // Work mapping (all kernels here): a workgroup of 256 lanes covers 16 output rows;
 // each 16-lane DPP row of a wave owns one output row and lane p of it processes
@@ -13,189 +13,6 @@
 #include "jk_device.hpp"
 
 namespace jk {
-
-// ---------------------------------------------------------------- quant_q8 block values
-
-// dot_q4_0_q8_0_block_scalar (quant_q8.rs:672-684)
-__device__ __forceinline__ float bv_q4_0(const WeightDev &w, int r, int b, const jk_block_q8_0 *xb) {
-    const uint4 q = ld_chunk(w, 0, r, b);
-    const float dw = ld_dscale(w, r, b);
-    const float xd = xb->d;
-    const int *xi = reinterpret_cast<const int *>(xb->qs);
-    int xv[8];
-    for (int i = 0; i < 8; ++i) xv[i] = xi[i];
-    if (dw == 0.0f || xd == 0.0f) return 0.0f;
-    const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
-    int s = 0, sx = 0;
-    for (int i = 0; i < 4; ++i) {
-        s = dot4((int)(qq[i] & 0x0F0F0F0Fu), xv[i], s);
-        s = dot4((int)((qq[i] >> 4) & 0x0F0F0F0Fu), xv[4 + i], s);
-    }
-    for (int i = 0; i < 8; ++i) sx = dot4(xv[i], 0x01010101, sx);
-    s -= 8 * sx;  // nibbles are stored biased by +8
-    return (float)s * (dw * xd);
-}
-
-// dot_q8_0_q8_0_block_scalar (quant_q8.rs:707-717)
-__device__ __forceinline__ float bv_q8_0(const WeightDev &w, int r, int b, const jk_block_q8_0 *xb) {
-    const uint4 q0 = ld_chunk(w, 0, r, b), q1 = ld_chunk(w, 1, r, b);
-    const float dw = ld_dscale(w, r, b);
-    const float xd = xb->d;
-    const int *xi = reinterpret_cast<const int *>(xb->qs);
-    int xv[8];
-    for (int i = 0; i < 8; ++i) xv[i] = xi[i];
-    if (dw == 0.0f || xd == 0.0f) return 0.0f;
-    const uint32_t qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    int s = 0;
-    for (int i = 0; i < 8; ++i) s = dot4((int)qq[i], xv[i], s);
-    return (float)s * (dw * xd);
-}
-
-__device__ __forceinline__ int byte_of(uint32_t v, int i) { return (int)((v >> (8 * i)) & 255u); }
-
-// dot_q4_k_q8_k_block_scalar (quant_q8.rs:1834-1862); scale/min table unpack_q4_q5_k_scales_mins
-// (quant_q8.rs:1818-1830) evaluated four bytes at a time.
-__device__ __forceinline__ float bv_q4_k(const WeightDev &w, int r, int b, const jk_block_q8k *xb) {
-    const uint4 h = ld_chunk(w, 0, r, b);
-    uint4 q[8];
-    for (int c = 0; c < 8; ++c) q[c] = ld_chunk(w, 1 + c, r, b);
-    const float xd = xb->d;
-    const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
-    if ((d == 0.0f && dmin == 0.0f) || xd == 0.0f) return 0.0f;
-    const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
-    const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
-    const uint32_t m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
-    const int *xq = reinterpret_cast<const int *>(xb->qs);
-    int sumi = 0, sum_mins = 0;
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t wd[8] = {q[2 * c].x, q[2 * c].y, q[2 * c].z, q[2 * c].w,
-                                q[2 * c + 1].x, q[2 * c + 1].y, q[2 * c + 1].z, q[2 * c + 1].w};
-        int lo = 0, hi = 0;
-        for (int i = 0; i < 8; ++i) {
-            lo = dot4((int)(wd[i] & 0x0F0F0F0Fu), xq[16 * c + i], lo);
-            hi = dot4((int)((wd[i] >> 4) & 0x0F0F0F0Fu), xq[16 * c + 8 + i], hi);
-        }
-        const uint32_t scv = c < 2 ? sc_lo : sc_hi, mv = c < 2 ? m_lo : m_hi;
-        const int j = (2 * c) & 3;
-        sumi += byte_of(scv, j) * lo + byte_of(scv, j + 1) * hi;
-        const int bl = (int)xb->bsums[4 * c] + (int)xb->bsums[4 * c + 1];
-        const int bh = (int)xb->bsums[4 * c + 2] + (int)xb->bsums[4 * c + 3];
-        sum_mins += byte_of(mv, j) * bl + byte_of(mv, j + 1) * bh;
-    }
-    return (d * xd) * (float)sumi - (dmin * xd) * (float)sum_mins;
-}
-
-__device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-
-// dot_q6_k_q8_k_block_scalar (quant_q8.rs:1903-1942): per 16-element group j the sum of
-// (q - 32) * x is formed as sum(q * x) - 32 * sum(x), with sum(x) taken from the quants.
-__device__ __forceinline__ float bv_q6_k(const WeightDev &w, int r, int b, const jk_block_q8k *xb) {
-    uint4 ql[8], qh[4];
-    for (int c = 0; c < 8; ++c) ql[c] = ld_chunk(w, c, r, b);
-    for (int c = 0; c < 4; ++c) qh[c] = ld_chunk(w, 8 + c, r, b);
-    const uint4 scv = ld_chunk(w, 12, r, b);
-    const float d = ld_dscale(w, r, b);
-    const float xd = xb->d;
-    if (d == 0.0f || xd == 0.0f) return 0.0f;
-    const int *xq = reinterpret_cast<const int *>(xb->qs);
-    int S[16], X[16];
-    for (int j = 0; j < 16; ++j) { S[j] = 0; X[j] = 0; }
-    for (int h = 0; h < 2; ++h)
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t L = comp(ql[(16 * h + t) >> 2], t & 3);
-            const uint32_t H = comp(ql[(16 * h + 8 + t) >> 2], t & 3);
-            const uint32_t Q = comp(qh[(8 * h + t) >> 2], t & 3);
-            const int g = 8 * h + (t >> 2);
-            const int q1 = (int)((L & 0x0F0F0F0Fu) | ((Q & 0x03030303u) << 4));
-            const int q2 = (int)((H & 0x0F0F0F0Fu) | (((Q >> 2) & 0x03030303u) << 4));
-            const int q3 = (int)(((L >> 4) & 0x0F0F0F0Fu) | (((Q >> 4) & 0x03030303u) << 4));
-            const int q4 = (int)(((H >> 4) & 0x0F0F0F0Fu) | (((Q >> 6) & 0x03030303u) << 4));
-            const int x1 = xq[32 * h + t], x2 = xq[32 * h + 8 + t], x3 = xq[32 * h + 16 + t], x4 = xq[32 * h + 24 + t];
-            S[g] = dot4(q1, x1, S[g]);
-            S[g + 2] = dot4(q2, x2, S[g + 2]);
-            S[g + 4] = dot4(q3, x3, S[g + 4]);
-            S[g + 6] = dot4(q4, x4, S[g + 6]);
-            X[g] = dot4(x1, 0x01010101, X[g]);
-            X[g + 2] = dot4(x2, 0x01010101, X[g + 2]);
-            X[g + 4] = dot4(x3, 0x01010101, X[g + 4]);
-            X[g + 6] = dot4(x4, 0x01010101, X[g + 6]);
-        }
-    int sumi = 0;
-    for (int j = 0; j < 16; ++j) {
-        const int sc = (int)(int8_t)(comp(scv, j >> 2) >> (8 * (j & 3)));
-        sumi += sc * (S[j] - 32 * X[j]);
-    }
-    return (d * xd) * (float)sumi;
-}
-
-// dot_tq2_0_q8_k_block_scalar (quant_q8.rs:1992-2003): sum((t - 1) * x) = sum(t * x) - sum(x).
-__device__ __forceinline__ float bv_tq2_0(const WeightDev &w, int r, int b, const jk_block_q8k *xb) {
-    uint4 q[4];
-    for (int c = 0; c < 4; ++c) q[c] = ld_chunk(w, c, r, b);
-    const float dw = ld_dscale(w, r, b);
-    const float xd = xb->d;
-    if (xd == 0.0f || dw == 0.0f) return 0.0f;
-    const int *xq = reinterpret_cast<const int *>(xb->qs);
-    int s = 0, sx = 0;
-    for (int k = 0; k < 16; ++k) {
-        const uint32_t wv = comp(q[k >> 2], k & 3);
-        for (int j = 0; j < 4; ++j) {
-            const int xv = xq[4 * k + j];
-            s = dot4((int)((wv >> (2 * j)) & 0x03030303u), xv, s);
-            sx = dot4(xv, 0x01010101, sx);
-        }
-    }
-    return (float)(s - sx) * (dw * xd);
-}
-
-template <int Q>
-__device__ __forceinline__ float q8_block_value(const WeightDev &w, int r, int b, const void *x) {
-    if constexpr (Q == JK_Q4_0) return bv_q4_0(w, r, b, static_cast<const jk_block_q8_0 *>(x) + b);
-    if constexpr (Q == JK_Q8_0) return bv_q8_0(w, r, b, static_cast<const jk_block_q8_0 *>(x) + b);
-    if constexpr (Q == JK_Q4_K) return bv_q4_k(w, r, b, static_cast<const jk_block_q8k *>(x) + b);
-    if constexpr (Q == JK_Q6_K) return bv_q6_k(w, r, b, static_cast<const jk_block_q8k *>(x) + b);
-    if constexpr (Q == JK_TQ2_0) return bv_tq2_0(w, r, b, static_cast<const jk_block_q8k *>(x) + b);
-    return 0.0f;
-}
-
-// gemv_* (quant_q8.rs:1586-3273) through run_4row_chunked_gemv (1510-1560): rows below
-// (rows / 4) * 4 accumulate from +0.0 (4-row kernels), the tail rows from -0.0 (the
-// 1-row kernels' `.sum()`).
-template <int Q>
-__global__ __launch_bounds__(256) void gemv_q8_kernel(WeightDev w, const void *__restrict__ x,
-                                                      float *__restrict__ y, int r0, int r1) {
-    const int p = threadIdx.x & 15;
-    const int row = r0 + (int)((blockIdx.x * 256u + threadIdx.x) >> 4);
-    const bool active = row < r1;
-    const int r = active ? row : r0;
-    const int rows4 = (w.rows >> 2) << 2;
-    float acc = r < rows4 ? 0.0f : -0.0f;
-    const int nb = w.nb;
-    const int iters = (nb + 15) >> 4;
-    for (int it = 0; it < iters; ++it) {
-        const int g = min(16, nb - 16 * it);
-        float v = 0.0f;
-        if (p < g) v = q8_block_value<Q>(w, r, 16 * it + p, x);
-        acc = chain_add(acc, v, g);
-    }
-    const int g_last = nb - 16 * (iters - 1);
-    if (active && p == g_last - 1) y[row - r0] = acc;
-}
-
-jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1) {
-    const dim3 grid((unsigned)((r1 - r0 + 15) / 16)), block(256);
-    switch (w.quant) {
-    case JK_Q4_0: hipLaunchKernelGGL(gemv_q8_kernel<JK_Q4_0>, grid, block, 0, s, w, x, y, r0, r1); break;
-    case JK_Q8_0: hipLaunchKernelGGL(gemv_q8_kernel<JK_Q8_0>, grid, block, 0, s, w, x, y, r0, r1); break;
-    case JK_Q4_K: hipLaunchKernelGGL(gemv_q8_kernel<JK_Q4_K>, grid, block, 0, s, w, x, y, r0, r1); break;
-    case JK_Q6_K: hipLaunchKernelGGL(gemv_q8_kernel<JK_Q6_K>, grid, block, 0, s, w, x, y, r0, r1); break;
-    case JK_TQ2_0: hipLaunchKernelGGL(gemv_q8_kernel<JK_TQ2_0>, grid, block, 0, s, w, x, y, r0, r1); break;
-    default: return fail(JK_CAPABILITY_MISMATCH, "gemv: unsupported quant %d", w.quant);
-    }
-    return check_launch("gemv_q8_kernel");
-}
 
 // ----------------------------------------------------------- f32-activation block values
 // Each returns dot_product_f32_scalar(dequantized block, x block) (lib.rs:770-778): one

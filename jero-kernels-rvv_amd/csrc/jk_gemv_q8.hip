@@ -1,0 +1,873 @@
+// jk_gemv_q8.hip -- batch-1 quant_q8 GEMV (Q4_0/Q8_0 x Q8_0, Q4_K/Q6_K/TQ2_0 x Q8_K).
+//
+// One launch serves a group of up to kMaxGemvJobs independent matrix-vector products of
+// one weight format (e.g. the Q, K and V projections of a layer, or gate and up). Each
+// workgroup owns a slice of output rows of one job and:
+//   1. issues the 128-bit non-temporal loads of its first weight blocks,
+//   2. stages the job's activation vector in LDS -- either quantizing f32 input with the
+//      quantize_row_q8_0 / quantize_row_q8_k recipes (bit-exact) or copying caller
+//      blocks -- while those loads are in flight,
+//   3. evaluates every (row, block) with the reference's per-block arithmetic (integer
+//      dot + f32 epilogue) and folds the block values of a row in block order.
+// Lane mapping: LPR lanes per output row (16: one DPP row, 64: one wave); lane p takes
+// blocks p, p + LPR, ... of its row. With LPR = 16 the ordered fold is chain_add over
+// the DPP row; with LPR = 64 the wave's block values go through LDS and lane 0 adds
+// them in order. Either way a row's result equals the reference's sequential
+// block-order f32 sum bit for bit (run_4row_chunked_gemv, quant_q8.rs:1510-1560).
+#include <limits.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "jk_device.hpp"
+
+namespace jk {
+
+// ------------------------------------------------------------ activation accessors
+// Q8_K block staged in LDS: qs[256] @0, bsums i16[16] @256 (as given), d f32 @288,
+// per-16 sums of qs i16[16] @304 (recomputed from qs): 336 bytes, a multiple of 16 whose
+// dword stride (84) puts the 16-byte reads of 16 consecutive blocks on distinct banks.
+constexpr int kXkBytes = 336;
+// Q8_0 block staged in LDS: qs[32] @0, d f32 @32, sum of qs i32 @36: 48 bytes.
+constexpr int kX0Bytes = 48;
+
+struct XkLds {
+    const uint8_t *p;
+    __device__ int q(int i) const { return reinterpret_cast<const int *>(p)[i]; }
+    __device__ int bsum(int j) const { return reinterpret_cast<const int16_t *>(p + 256)[j]; }
+    __device__ float d() const { return *reinterpret_cast<const float *>(p + 288); }
+    __device__ int s16(int j) const { return reinterpret_cast<const int16_t *>(p + 304)[j]; }
+};
+
+struct XkGlb {
+    const jk_block_q8k *b;
+    __device__ int q(int i) const { return reinterpret_cast<const int *>(b->qs)[i]; }
+    __device__ int bsum(int j) const { return b->bsums[j]; }
+    __device__ float d() const { return b->d; }
+    __device__ int s16(int j) const {
+        int s = 0;
+        for (int i = 0; i < 4; ++i) s = dot4(q(4 * j + i), 0x01010101, s);
+        return s;
+    }
+};
+
+struct X0Lds {
+    const uint8_t *p;
+    __device__ int q(int i) const { return reinterpret_cast<const int *>(p)[i]; }
+    __device__ float d() const { return *reinterpret_cast<const float *>(p + 32); }
+    __device__ int sum() const { return *reinterpret_cast<const int *>(p + 36); }
+};
+
+struct X0Glb {
+    const jk_block_q8_0 *b;
+    __device__ int q(int i) const { return reinterpret_cast<const int *>(b->qs)[i]; }
+    __device__ float d() const { return b->d; }
+    __device__ int sum() const {
+        int s = 0;
+        for (int i = 0; i < 8; ++i) s = dot4(q(i), 0x01010101, s);
+        return s;
+    }
+};
+
+template <int Q> struct QTraits {
+    static constexpr bool K = Q == JK_Q4_K || Q == JK_Q6_K || Q == JK_TQ2_0;  // Q8_K activations
+    static constexpr int XB = K ? kXkBytes : kX0Bytes;                        // LDS bytes per block
+    static constexpr int XE = K ? 256 : 32;                                   // elements per block
+    static constexpr int C = fmt_of(Q).chunks;                                // 16-byte weight chunks
+    static constexpr bool D = fmt_of(Q).d_off >= 0;                           // scale in the d-plane
+    // blocks per lane per batch: about 64-144 weight bytes per lane per batch (two
+    // batches are in flight per wave)
+    static constexpr int U = C >= 4 ? 1 : C == 2 ? 2 : 4;
+};
+
+template <int Q> struct WReg {
+    uint4 c[QTraits<Q>::C];
+    uint32_t d;
+};
+
+// Loads block b of row r with 128-bit non-temporal loads. xo (0 or 16) is XORed into
+// every byte address: 16 keeps each access inside its own 128-byte line but makes it a
+// distinct load (dummy loads that must not be merged with the real ones).
+template <int Q>
+__device__ __forceinline__ void wload(WReg<Q> &o, const WeightDev &w, int r, int b, unsigned xo = 0) {
+#pragma unroll
+    for (int c = 0; c < QTraits<Q>::C; ++c) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(chunk_ptr(w, c, r, b)) ^ xo;
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(a));
+        o.c[c] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    if constexpr (QTraits<Q>::D)
+        o.d = *reinterpret_cast<const uint16_t *>(
+            reinterpret_cast<uintptr_t>(w.dplane + (size_t)r * (size_t)w.nb + (size_t)b) ^ (xo >> 3));
+}
+
+// ------------------------------------------------------------------ block values
+// dot_q4_0_q8_0_block_scalar (quant_q8.rs:672-684): nibbles are stored biased by +8, so
+// sum((n - 8) * x) = sum(n * x) - 8 * sum(x), exactly.
+template <class X>
+__device__ __forceinline__ float val_q4_0(const WReg<JK_Q4_0> &wr, const X &x) {
+    const float dw = f16_finite(wr.d);
+    const float xd = x.d();
+    if (dw == 0.0f || xd == 0.0f) return 0.0f;
+    const uint4 q = wr.c[0];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s = dot4((int)(comp(q, i) & 0x0F0F0F0Fu), x.q(i), s);
+        s = dot4((int)((comp(q, i) >> 4) & 0x0F0F0F0Fu), x.q(4 + i), s);
+    }
+    s -= 8 * x.sum();
+    return (float)s * (dw * xd);
+}
+
+// dot_q8_0_q8_0_block_scalar (quant_q8.rs:707-717)
+template <class X>
+__device__ __forceinline__ float val_q8_0(const WReg<JK_Q8_0> &wr, const X &x) {
+    const float dw = f16_finite(wr.d);
+    const float xd = x.d();
+    if (dw == 0.0f || xd == 0.0f) return 0.0f;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = dot4((int)comp(wr.c[i >> 2], i & 3), x.q(i), s);
+    return (float)s * (dw * xd);
+}
+
+// dot_q4_k_q8_k_block_scalar (quant_q8.rs:1834-1862) with the scale/min table of
+// unpack_q4_q5_k_scales_mins (quant_q8.rs:1818-1830) evaluated four bytes at a time.
+template <class X>
+__device__ __forceinline__ float val_q4_k(const WReg<JK_Q4_K> &wr, const X &x) {
+    const uint4 h = wr.c[0];
+    const float xd = x.d();
+    const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
+    if ((d == 0.0f && dmin == 0.0f) || xd == 0.0f) return 0.0f;
+    const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    int sumi = 0, sum_mins = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint4 qa = wr.c[1 + 2 * c], qb = wr.c[2 + 2 * c];
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t wd = comp(i < 4 ? qa : qb, i & 3);
+            lo = dot4((int)(wd & 0x0F0F0F0Fu), x.q(16 * c + i), lo);
+            hi = dot4((int)((wd >> 4) & 0x0F0F0F0Fu), x.q(16 * c + 8 + i), hi);
+        }
+        const uint32_t scv = c < 2 ? sc_lo : sc_hi, mv = c < 2 ? m_lo : m_hi;
+        const int j = (2 * c) & 3;
+        sumi += byte_of(scv, j) * lo + byte_of(scv, j + 1) * hi;
+        const int bl = x.bsum(4 * c) + x.bsum(4 * c + 1);
+        const int bh = x.bsum(4 * c + 2) + x.bsum(4 * c + 3);
+        sum_mins += byte_of(mv, j) * bl + byte_of(mv, j + 1) * bh;
+        // one 64-element chunk of activations in registers at a time
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return (d * xd) * (float)sumi - (dmin * xd) * (float)sum_mins;
+}
+
+// dot_q6_k_q8_k_block_scalar (quant_q8.rs:1903-1942): per 16-element group j,
+// sum((q - 32) * x) = sum(q * x) - 32 * sum(x), with sum(x) from the recomputed sums.
+template <class X>
+__device__ __forceinline__ float val_q6_k(const WReg<JK_Q6_K> &wr, const X &x) {
+    const float d = f16_finite(wr.d);
+    const float xd = x.d();
+    if (d == 0.0f || xd == 0.0f) return 0.0f;
+    int S[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) S[j] = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t L = comp(wr.c[(16 * h + t) >> 2], t & 3);
+            const uint32_t H = comp(wr.c[(16 * h + 8 + t) >> 2], t & 3);
+            const uint32_t Qh = comp(wr.c[8 + ((8 * h + t) >> 2)], t & 3);
+            const int g = 8 * h + (t >> 2);
+            const int q1 = (int)((L & 0x0F0F0F0Fu) | ((Qh & 0x03030303u) << 4));
+            const int q2 = (int)((H & 0x0F0F0F0Fu) | (((Qh >> 2) & 0x03030303u) << 4));
+            const int q3 = (int)(((L >> 4) & 0x0F0F0F0Fu) | (((Qh >> 4) & 0x03030303u) << 4));
+            const int q4 = (int)(((H >> 4) & 0x0F0F0F0Fu) | (((Qh >> 6) & 0x03030303u) << 4));
+            S[g] = dot4(q1, x.q(32 * h + t), S[g]);
+            S[g + 2] = dot4(q2, x.q(32 * h + 8 + t), S[g + 2]);
+            S[g + 4] = dot4(q3, x.q(32 * h + 16 + t), S[g + 4]);
+            S[g + 6] = dot4(q4, x.q(32 * h + 24 + t), S[g + 6]);
+        }
+    const uint4 scv = wr.c[12];
+    int sumi = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int sc = (int)(int8_t)(comp(scv, j >> 2) >> (8 * (j & 3)));
+        sumi += sc * (S[j] - 32 * x.s16(j));
+    }
+    return (d * xd) * (float)sumi;
+}
+
+// dot_tq2_0_q8_k_block_scalar (quant_q8.rs:1992-2003): sum((t - 1) * x) = sum(t * x) - sum(x).
+// The device dword holds element 4j+i of activation dword j in bits 2j of byte i.
+template <class X>
+__device__ __forceinline__ float val_tq2_0(const WReg<JK_TQ2_0> &wr, const X &x) {
+    const float dw = f16_finite(wr.d);
+    const float xd = x.d();
+    if (xd == 0.0f || dw == 0.0f) return 0.0f;
+    int s = 0, sx = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t wv = comp(wr.c[k >> 2], k & 3);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s = dot4((int)((wv >> (2 * j)) & 0x03030303u), x.q(4 * k + j), s);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sx += x.s16(j);
+    return (float)(s - sx) * (dw * xd);
+}
+
+template <int Q, class X>
+__device__ __forceinline__ float block_value(const WReg<Q> &wr, const X &x) {
+    if constexpr (Q == JK_Q4_0) return val_q4_0(wr, x);
+    else if constexpr (Q == JK_Q8_0) return val_q8_0(wr, x);
+    else if constexpr (Q == JK_Q4_K) return val_q4_k(wr, x);
+    else if constexpr (Q == JK_Q6_K) return val_q6_k(wr, x);
+    else return val_tq2_0(wr, x);
+}
+
+// ------------------------------------------------------------------ LDS staging
+// The activation is read into registers in rounds of ROUND dwords per workgroup, before
+// any weight load of the CU (see the kernel): vector memory returns data in issue order,
+// so activation loads queued behind weight loads would wait for the weight stream. With
+// NW waves per workgroup, thread t holds dwords (or float4s) t + 64*NW*i of a round.
+template <int NW, bool F32> struct XRegs {
+    // dwords per thread per round: a 4096-wide f32 activation (16 KB) in one round; caller
+    // blocks are 4x smaller
+    static constexpr int N = F32 && NW <= 4 ? 16 : 8;
+    static constexpr int ROUND = 64 * NW * N;
+    uint32_t v[N];
+};
+
+// Round r of an f32 activation of n4 float4s (clamped, unconditional loads: entries past
+// the end are never staged).
+template <int NW>
+__device__ __forceinline__ void xload_f32(XRegs<NW, true> &xr, const float *__restrict__ x, int n4, int r) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll
+    for (int i = 0; i < XRegs<NW, true>::N / 4; ++i) {
+        const float4 v = x4[min(r * (XRegs<NW, true>::ROUND / 4) + (int)threadIdx.x + 64 * NW * i, n4 - 1)];
+        xr.v[4 * i] = __float_as_uint(v.x);
+        xr.v[4 * i + 1] = __float_as_uint(v.y);
+        xr.v[4 * i + 2] = __float_as_uint(v.z);
+        xr.v[4 * i + 3] = __float_as_uint(v.w);
+    }
+}
+
+// Round r of caller blocks (ndw dwords), clamped and unconditional as above.
+template <int NW>
+__device__ __forceinline__ void xload_raw(XRegs<NW, false> &xr, const uint32_t *__restrict__ x, int ndw, int r) {
+#pragma unroll
+    for (int i = 0; i < XRegs<NW, false>::N; ++i) xr.v[i] = x[min(r * XRegs<NW, false>::ROUND + (int)threadIdx.x + 64 * NW * i, ndw - 1)];
+}
+
+// Rust `(x * inv).round().clamp(-127.0, 127.0) as i8` for finite x (round_scaled_to_i8,
+// quant_q8.rs:102-108): round-half-away-from-zero as trunc(t + copysign(0.5 - 2^-25, t)),
+// exact for |t| < 2^23 and saturating beyond, a med3 clamp, and NaN -> 0 (t is NaN only
+// when a subnormal block maximum makes inv infinite and x is 0).
+__device__ __forceinline__ int quant_i8(float x, float inv) {
+    const float t = x * inv;
+    const float h = __uint_as_float((__float_as_uint(t) & 0x80000000u) | 0x3EFFFFFFu);  // +-(0.5 - 2^-25)
+    const int q = (int)__builtin_amdgcn_fmed3f(__builtin_truncf(t + h), -127.0f, 127.0f);
+    return t == t ? q : 0;
+}
+
+__device__ __forceinline__ uint32_t pack4(const int (&q)[4]) {
+    return (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+           ((uint32_t)q[3] << 24);
+}
+
+// quantize_block_q8_k_scalar (quant_q8.rs:447-475) of one block by one wave, lane l holding
+// elements 4l..4l+3 (non-finite elements count as 0, as there); bsums[j] is the sum of
+// lanes 4j..4j+3.
+__device__ __forceinline__ void quantize_q8_k_wave(float (&v)[4], uint8_t *dst, int l) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_isfinite(v[i]) ? v[i] : 0.0f;
+    const float amax = wave_max64_dpp(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    const bool zero = amax == 0.0f;  // amax is finite here
+    const float inv = zero ? 0.0f : 127.0f / amax;
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = quant_i8(v[i], inv);
+    const int part = sum4_dpp(q[0] + q[1] + q[2] + q[3]);
+    reinterpret_cast<uint32_t *>(dst)[l] = pack4(q);
+    if ((l & 3) == 0) {
+        reinterpret_cast<int16_t *>(dst + 256)[l >> 2] = (int16_t)part;
+        reinterpret_cast<int16_t *>(dst + 304)[l >> 2] = (int16_t)part;
+    }
+    if (l == 0) *reinterpret_cast<float *>(dst + 288) = zero ? 0.0f : amax / 127.0f;
+}
+
+// quantize_block_q8_0_scalar (quant_q8.rs:203-219) of one block by 8 lanes, lane l (of 8)
+// holding elements 4l..4l+3.
+__device__ __forceinline__ void quantize_q8_0_lanes(float (&v)[4], uint8_t *dst, int l) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_isfinite(v[i]) ? v[i] : 0.0f;
+    const float amax = max8_dpp(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    const bool zero = amax == 0.0f;
+    const float inv = zero ? 0.0f : 127.0f / amax;
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = quant_i8(v[i], inv);
+    const int s = sum8_dpp(q[0] + q[1] + q[2] + q[3]);
+    reinterpret_cast<uint32_t *>(dst)[l] = pack4(q);
+    if (l == 0) {
+        *reinterpret_cast<float *>(dst + 32) = zero ? 0.0f : amax / 127.0f;
+        *reinterpret_cast<int *>(dst + 36) = s;
+    }
+}
+
+// Quantizes round r of f32 activations (registers) into the staged LDS blocks.
+template <int Q, int NW>
+__device__ __forceinline__ void xstage_f32(const XRegs<NW, true> &xr, int nb, int r, uint8_t *s_x) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < XRegs<NW, true>::N / 4; ++i) {
+        float v[4] = {__uint_as_float(xr.v[4 * i]), __uint_as_float(xr.v[4 * i + 1]), __uint_as_float(xr.v[4 * i + 2]),
+                      __uint_as_float(xr.v[4 * i + 3])};
+        const int f = r * (XRegs<NW, true>::ROUND / 4) + tid + 64 * NW * i;
+        if constexpr (QTraits<Q>::K) {
+            const int blk = f >> 6;  // uniform over the wave
+            if (blk < nb) quantize_q8_k_wave(v, s_x + blk * kXkBytes, tid & 63);
+        } else {
+            const int blk = f >> 3;  // uniform over 8 lanes
+            if (blk < nb) quantize_q8_0_lanes(v, s_x + blk * kX0Bytes, tid & 7);
+        }
+    }
+}
+
+// Scatters round r of caller blocks (BlockQ8K: d, qs[64], bsums[8] dwords; BlockQ8_0: d,
+// qs[8]) into the staged LDS layout.
+template <int Q, int NW>
+__device__ __forceinline__ void xstage_raw(const XRegs<NW, false> &xr, int ndw, int r, uint8_t *s_x) {
+    constexpr bool K = QTraits<Q>::K;
+    constexpr int DW = K ? 73 : 9, STEP = 64 * NW;
+    // block / word of slot 0, then advanced by STEP dwords per slot without dividing
+    const int k0 = r * XRegs<NW, false>::ROUND + (int)threadIdx.x;
+    int blk = k0 / DW, wd = k0 - blk * DW;
+#pragma unroll
+    for (int i = 0; i < XRegs<NW, false>::N; ++i) {
+        const int k = k0 + STEP * i;
+        if (i > 0) {
+            blk += STEP / DW;
+            wd += STEP % DW;
+            if (wd >= DW) {
+                wd -= DW;
+                ++blk;
+            }
+        }
+        if (k < ndw) {
+            uint8_t *dst = s_x + blk * QTraits<Q>::XB;
+            int off;
+            if (K) off = wd == 0 ? 288 : wd <= 64 ? 4 * (wd - 1) : 256 + 4 * (wd - 65);
+            else off = wd == 0 ? 32 : 4 * (wd - 1);
+            *reinterpret_cast<uint32_t *>(dst + off) = xr.v[i];
+        }
+        if ((i & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bounds the live address temporaries
+    }
+}
+
+// Sums of the staged caller quants: per-16 sums (Q8_K) or the block sum (Q8_0).
+template <int Q, int NW>
+__device__ __forceinline__ void xstage_sums(int nb, uint8_t *s_x) {
+    if constexpr (QTraits<Q>::K) {
+        for (int it = threadIdx.x; it < nb * 16; it += 64 * NW) {
+            uint8_t *dst = s_x + (it >> 4) * kXkBytes;
+            const int j = it & 15;
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s = dot4(reinterpret_cast<const int *>(dst)[4 * j + i], 0x01010101, s);
+            reinterpret_cast<int16_t *>(dst + 304)[j] = (int16_t)s;
+        }
+    } else {
+        for (int it = threadIdx.x; it < nb; it += 64 * NW) {
+            uint8_t *dst = s_x + it * kX0Bytes;
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = dot4(reinterpret_cast<const int *>(dst)[i], 0x01010101, s);
+            *reinterpret_cast<int *>(dst + 36) = s;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ ordered fold
+// LPR == 64: the wave's g block values are added in order by lane 0 (acc lives in lane 0).
+__device__ __forceinline__ float fold_wave(float acc, float v, int g, float *red) {
+    const int l = threadIdx.x & 63;
+    red[l] = v;
+    wave_lds_sync();
+    if (l == 0)
+        for (int i = 0; i < g; ++i) acc += red[i];
+    wave_lds_sync();
+    return acc;
+}
+
+// The two halves of activation staging, around the weight loads issued between them.
+// begin: round 0 into registers, then a barrier that puts every activation load of the
+// workgroup ahead of its weight loads (it waits for no data).
+template <int Q, bool F32, int NW>
+__device__ __forceinline__ void stage_begin(XRegs<NW, F32> &xr, const GemvJob &job, int nb) {
+    using T = QTraits<Q>;
+    if constexpr (F32) xload_f32<NW>(xr, job.xf, nb * T::XE / 4, 0);
+    else xload_raw<NW>(xr, static_cast<const uint32_t *>(job.xq), nb * (T::K ? 73 : 9), 0);
+    lds_barrier();
+}
+// finish: every round into the staged LDS layout (rounds after the first wait behind the
+// weight loads), then the sums of caller blocks.
+template <int Q, bool F32, int NW>
+__device__ __forceinline__ void stage_finish(XRegs<NW, F32> &xr, const GemvJob &job, int nb, uint8_t *s_x) {
+    using T = QTraits<Q>;
+    constexpr int RD = XRegs<NW, F32>::ROUND;
+    const int n4 = nb * T::XE / 4;         // f32 input: float4 count
+    const int ndw = nb * (T::K ? 73 : 9);  // caller blocks: dword count
+    const int nrounds = F32 ? (n4 + RD / 4 - 1) / (RD / 4) : (ndw + RD - 1) / RD;
+    for (int rr = 0; rr < nrounds; ++rr) {
+        if (rr > 0) {
+            if constexpr (F32) xload_f32<NW>(xr, job.xf, n4, rr);
+            else xload_raw<NW>(xr, static_cast<const uint32_t *>(job.xq), ndw, rr);
+        }
+        if constexpr (F32) xstage_f32<Q, NW>(xr, nb, rr, s_x);
+        else xstage_raw<Q, NW>(xr, ndw, rr, s_x);
+    }
+    lds_barrier();
+    if constexpr (!F32) {
+        xstage_sums<Q, NW>(nb, s_x);
+        lds_barrier();
+    }
+}
+
+// Job of workgroup blockIdx.x (jobs are ordered by first workgroup; unused wg0 entries
+// hold INT_MAX).
+__device__ __forceinline__ int job_of_block(const GemvGroup &grp) {
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGemvJobs; ++i) j += (int)blockIdx.x >= grp.wg0[i];
+    return j;
+}
+
+// ------------------------------------------------------------------ kernel
+// Work unit of a wave: RPU output rows (4 with LPR 16, 1 with LPR 64) over all their
+// blocks, walked in batches of U blocks per lane. A wave takes units u, u + S, u + 2S, ...
+// (S = waves of its job), in pairs of batches whose loads are issued together.
+template <int Q, int LPR>
+struct Walker {
+    using T = QTraits<Q>;
+    static constexpr int RPU = 64 / LPR;
+    int nb, nit, units, stride, r0, r1, rows4, sub, p;
+
+    __device__ __forceinline__ void next(int &u, int &it0) const {
+        it0 += T::U;
+        if (it0 >= nit) {
+            it0 = 0;
+            u += stride;
+        }
+    }
+    __device__ __forceinline__ int row_of(int u) const { return r0 + u * RPU + sub; }
+
+    // Batch (u, it0), or with dummy set, a distinct re-read of the same lines.
+    __device__ __forceinline__ void load(WReg<Q> (&wr)[T::U], const WeightDev &w, int u, int it0,
+                                         bool dummy = false) const {
+        const int row = row_of(u);
+        const int r = row < r1 ? row : r0;
+#pragma unroll
+        for (int k = 0; k < T::U; ++k) wload<Q>(wr[k], w, r, min((it0 + k) * LPR + p, nb - 1), dummy ? 16u : 0u);
+    }
+
+    // Folds batch (u, it0) into acc in block order. At the unit's last batch every lane
+    // parks acc in its LDS slot of the unit (slot[k * 64 + lane], k = the wave's unit
+    // ordinal): a global store here would sit in a lane-divergent branch between the
+    // loads, and the compiler then has to drain all outstanding loads at every wait.
+    template <class Red>
+    __device__ __forceinline__ float run(const WReg<Q> (&wr)[T::U], int u, int it0, float acc, const uint8_t *s_x,
+                                         float *slot, int k0, Red *red) const {
+        const int row = row_of(u);
+        const int r = row < r1 ? row : r0;
+        if (it0 == 0) acc = r < rows4 ? 0.0f : -0.0f;
+        float v[T::U];
+#pragma unroll
+        for (int k = 0; k < T::U; ++k) {
+            const int b = (it0 + k) * LPR + p;
+            v[k] = 0.0f;
+            if (b < nb) {
+                if constexpr (T::K) v[k] = block_value<Q>(wr[k], XkLds{s_x + b * T::XB});
+                else v[k] = block_value<Q>(wr[k], X0Lds{s_x + b * T::XB});
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < T::U; ++k) {
+            if (it0 + k < nit) {
+                const int g = min(LPR, nb - (it0 + k) * LPR);
+                if constexpr (LPR == 16) acc = chain_add(acc, v[k], g);
+                else acc = fold_wave(acc, v[k], g, red);
+            }
+        }
+        if (it0 + T::U >= nit) slot[((u - k0) / stride) * 64 + (threadIdx.x & 63)] = acc;
+        return acc;
+    }
+
+    // Lane that holds a row's result after the fold.
+    __device__ __forceinline__ int writer() const { return LPR == 16 ? nb - LPR * (nit - 1) - 1 : 0; }
+};
+
+// Register budget: 4 waves per SIMD (<= 128 VGPRs) for Q4_K / Q4_0 / Q8_0 / TQ2_0, 2 for
+// Q6_K. Waves per workgroup (NW): a "full" workgroup fills a CU at that budget (16 or 8
+// waves), so the activation is staged once per CU; launches with too few row units to
+// give every CU a full workgroup use 4-wave workgroups instead.
+template <int Q> constexpr int kWavesPerSimd = Q == JK_Q6_K ? 2 : 4;
+template <int Q> constexpr int kFullWaves = 4 * kWavesPerSimd<Q>;
+
+template <int Q, int LPR, bool F32, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<Q>))) void
+gemv_q8_group_kernel(GemvGroup grp) {
+    using T = QTraits<Q>;
+    extern __shared__ __align__(16) uint8_t s_x[];
+    __shared__ float s_red[LPR == 64 ? NW : 1][64];
+
+    const GemvJob &job = grp.job[job_of_block(grp)];
+    const WeightDev &w = job.w;
+
+    // wave index as a scalar: the unit loop below must be wave-uniform control flow
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    Walker<Q, LPR> wk;
+    wk.nb = w.nb;
+    wk.nit = (w.nb + LPR - 1) / LPR;
+    wk.units = (job.r1 - job.r0 + Walker<Q, LPR>::RPU - 1) / Walker<Q, LPR>::RPU;
+    wk.stride = job.nwg * NW;
+    wk.r0 = job.r0;
+    wk.r1 = job.r1;
+    wk.rows4 = (w.rows >> 2) << 2;
+    wk.sub = lane / LPR;
+    wk.p = lane % LPR;
+
+    // 1. first round of the activation into registers (see stage_begin)
+    const int nb = w.nb;
+    XRegs<NW, F32> xr;
+    stage_begin<Q, F32, NW>(xr, job, nb);
+
+    // 2. the first pair of weight batches. Loads are issued unconditionally -- a load that
+    //    may or may not have been issued would make every later wait drain all outstanding
+    //    loads. A batch position past the last unit re-reads batch A's own addresses (lines
+    //    already requested), so the dummy loads neither add traffic nor pile onto one row;
+    //    a wave without any unit reads a row of its own index.
+    int ua = ((int)blockIdx.x - job.wg0) * NW + wave, ia = 0;
+    int ub = ua, ib = ia;
+    wk.next(ub, ib);
+    WReg<Q> A[T::U], B[T::U];
+    const int ua_ld = ua < wk.units ? ua : ua % wk.units;
+    wk.load(A, w, ua_ld, ia);
+    {
+        const bool bd = ub >= wk.units;  // wave-uniform
+        wk.load(B, w, bd ? ua_ld : ub, bd ? ia : ib, bd);
+    }
+
+    // 3. activation vector into the staged LDS layout
+    stage_finish<Q, F32, NW>(xr, job, nb, s_x);
+
+    // 4. batches in order, in pairs: both loads of a pair are issued before either batch
+    //    is evaluated, and nothing is outstanding across the loop's back-edge, so every
+    //    wait below is exact (for the decode shapes a wave has at most one pair).
+    float acc = 0.0f;
+    float *red = s_red[LPR == 64 ? wave : 0];
+    float *slot = reinterpret_cast<float *>(s_x + grp.out_off) + wave * grp.upw * 64;
+    const int u0 = ua;
+    while (ua < wk.units) {
+        acc = wk.run(A, ua, ia, acc, s_x, slot, u0, red);
+        if (ub < wk.units) acc = wk.run(B, ub, ib, acc, s_x, slot, u0, red);
+        ua = ub;
+        ia = ib;
+        wk.next(ua, ia);
+        if (ua >= wk.units) break;
+        ub = ua;
+        ib = ia;
+        wk.next(ub, ib);
+        wk.load(A, w, ua, ia);
+        const bool bd = ub >= wk.units;
+        wk.load(B, w, bd ? ua : ub, bd ? ia : ib, bd);
+    }
+
+    // 5. results out of the LDS slots
+    wave_lds_sync();
+    const int wr_lane = wk.writer();
+    for (int u = u0, k = 0; u < wk.units; u += wk.stride, ++k) {
+        const int row = wk.row_of(u);
+        if (row < wk.r1 && wk.p == wr_lane) job.y[row - wk.r0] = slot[k * 64 + lane];
+    }
+}
+
+// ------------------------------------------------------------------ fast kernel
+// Straight-line variant for launches whose rows fit in one batch per unit (nit <= UF):
+// each wave owns QPW consecutive units, issues all their weight loads up front, evaluates
+// them and keeps the results in registers until one store pass at the end. Without a loop
+// the compiler keeps every load where it is written and every wait exact.
+template <int Q> constexpr int kFastU = Q == JK_Q4_0 || Q == JK_Q8_0 ? 8 : Q == JK_TQ2_0 ? 2 : 1;
+template <int Q> constexpr bool kFastPair = Q != JK_Q8_0;  // QPW = 2 fits the register budget
+
+template <int Q, int LPR, bool F32, int NW, int QPW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<Q>))) void
+gemv_q8_fast_kernel(GemvGroup grp) {
+    using T = QTraits<Q>;
+    constexpr int RPU = 64 / LPR, UF = kFastU<Q>;
+    extern __shared__ __align__(16) uint8_t s_x[];
+    __shared__ float s_red[LPR == 64 ? NW : 1][64];
+
+    const GemvJob &job = grp.job[job_of_block(grp)];
+    const WeightDev &w = job.w;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int sub = lane / LPR, p = lane % LPR;
+    const int nb = w.nb, nit = (nb + LPR - 1) / LPR;  // nit <= UF
+    const int r0 = job.r0, r1 = job.r1;
+    const int units = (r1 - r0 + RPU - 1) / RPU;
+    const int base = (((int)blockIdx.x - job.wg0) * NW + wave) * QPW;  // first unit of the wave
+
+    // 1. activation round 0, then every weight load of the wave. A unit past the end
+    //    re-reads a valid unit's lines at distinct addresses (xor 16): the loads stay
+    //    unconditional, add no traffic and are never merged with the real ones.
+    XRegs<NW, F32> xr;
+    stage_begin<Q, F32, NW>(xr, job, nb);
+    WReg<Q> W[QPW][UF];
+    const int ufb = base < units ? base : base % units;
+#pragma unroll
+    for (int q = 0; q < QPW; ++q) {
+        const bool dummy = base + q >= units;
+        const int row = r0 + (dummy ? ufb : base + q) * RPU + sub;
+        const int r = min(row, r1 - 1);
+#pragma unroll
+        for (int k = 0; k < UF; ++k) wload<Q>(W[q][k], w, r, min(k * LPR + p, nb - 1), dummy ? 16u : 0u);
+    }
+
+    // 2. activation vector into the staged LDS layout
+    stage_finish<Q, F32, NW>(xr, job, nb, s_x);
+
+    // 3. block values folded in block order; results stay in registers
+    const int rows4 = (w.rows >> 2) << 2;
+    float *red = s_red[LPR == 64 ? wave : 0];
+    float out[QPW];
+#pragma unroll
+    for (int q = 0; q < QPW; ++q) {
+        const int row = r0 + (base + q) * RPU + sub;
+        float acc = row < rows4 ? 0.0f : -0.0f;
+        float v[UF];
+#pragma unroll
+        for (int k = 0; k < UF; ++k) {
+            const int b = k * LPR + p;
+            v[k] = 0.0f;
+            if (b < nb) {
+                if constexpr (T::K) v[k] = block_value<Q>(W[q][k], XkLds{s_x + b * T::XB});
+                else v[k] = block_value<Q>(W[q][k], X0Lds{s_x + b * T::XB});
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < UF; ++k) {
+            if (k < nit) {
+                const int g = min(LPR, nb - k * LPR);
+                if constexpr (LPR == 16) acc = chain_add(acc, v[k], g);
+                else acc = fold_wave(acc, v[k], g, red);
+            }
+        }
+        out[q] = acc;
+    }
+
+    // 4. stores
+    const int writer = LPR == 16 ? nb - LPR * (nit - 1) - 1 : 0;
+#pragma unroll
+    for (int q = 0; q < QPW; ++q) {
+        const int row = r0 + (base + q) * RPU + sub;
+        if (base + q < units && row < r1 && p == writer) job.y[row - r0] = out[q];
+    }
+}
+
+// ------------------------------------------------------------------ global-x fallback
+// Activations read from global memory (matrices whose activation exceeds the LDS budget).
+template <int Q>
+__global__ __launch_bounds__(256) void gemv_q8_global_kernel(WeightDev w, const void *__restrict__ x,
+                                                             float *__restrict__ y, int r0, int r1) {
+    const int p = threadIdx.x & 15;
+    const int row = r0 + (int)((blockIdx.x * 256u + threadIdx.x) >> 4);
+    const bool active = row < r1;
+    const int r = active ? row : r0;
+    const int rows4 = (w.rows >> 2) << 2;
+    float acc = r < rows4 ? 0.0f : -0.0f;
+    const int nb = w.nb;
+    const int iters = (nb + 15) >> 4;
+    for (int it = 0; it < iters; ++it) {
+        const int g = min(16, nb - 16 * it);
+        const int b = 16 * it + p;
+        float v = 0.0f;
+        if (p < g) {
+            WReg<Q> wr;
+            wload<Q>(wr, w, r, b);
+            if constexpr (QTraits<Q>::K) v = block_value<Q>(wr, XkGlb{static_cast<const jk_block_q8k *>(x) + b});
+            else v = block_value<Q>(wr, X0Glb{static_cast<const jk_block_q8_0 *>(x) + b});
+        }
+        acc = chain_add(acc, v, g);
+    }
+    const int g_last = nb - 16 * (iters - 1);
+    if (active && p == g_last - 1) y[row - r0] = acc;
+}
+
+// ------------------------------------------------------------------ launchers
+constexpr int kMaxLdsX = 60 * 1024;  // staged activation; static LDS stays within the 64 KB default
+
+// Resident workgroups per CU of a kernel at a given dynamic LDS size (queried once).
+template <class K>
+static int resident_per_cu(K kernel, size_t lds, int threads) {
+    static std::mutex mu;
+    static std::map<std::pair<const void *, size_t>, int> cache;
+    const std::pair<const void *, size_t> key{reinterpret_cast<const void *>(kernel), lds};
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) n = 1;
+    cache[key] = n;
+    return n;
+}
+
+static int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+template <int Q, int LPR, bool F32, int NW>
+static jk_status launch_group_run(hipStream_t s, GemvGroup &g, size_t lds) {
+    // (lds: the staged activation; the result slots are appended below)
+    constexpr int RPU = 64 / LPR;
+    auto kern = gemv_q8_group_kernel<Q, LPR, F32, NW>;
+    // Size the grid to one resident round: each wave then walks ceil(units / waves) units.
+    const int cap_waves = resident_per_cu(kern, lds, 64 * NW) * cu_count() * NW;
+    long total = 0;
+    for (int i = 0; i < g.njobs; ++i) total += (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
+    // (at most 16 units per wave: bigger jobs get more than one round of workgroups)
+    const int upw = (int)std::min<long>(16, (total + cap_waves - 1) / cap_waves);
+    g.upw = upw;
+    g.out_off = (int)((lds + 15) / 16 * 16);
+    lds = (size_t)g.out_off + (size_t)NW * upw * 64 * sizeof(float);
+    int wgs = 0;
+    for (int i = 0; i < g.njobs; ++i) {
+        const int units = (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
+        g.job[i].wg0 = g.wg0[i] = wgs;
+        g.job[i].nwg = (units + NW * upw - 1) / (NW * upw);
+        wgs += g.job[i].nwg;
+    }
+    for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
+    hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * NW), lds, s, g);
+    return check_launch("gemv_q8_group_kernel");
+}
+
+template <int Q, int LPR, bool F32, int NW, int QPW>
+static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds) {
+    constexpr int RPU = 64 / LPR;
+    int wgs = 0;
+    for (int i = 0; i < g.njobs; ++i) {
+        const int units = (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
+        g.job[i].wg0 = g.wg0[i] = wgs;
+        g.job[i].nwg = (units + NW * QPW - 1) / (NW * QPW);
+        wgs += g.job[i].nwg;
+    }
+    for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
+    hipLaunchKernelGGL((gemv_q8_fast_kernel<Q, LPR, F32, NW, QPW>), dim3((unsigned)wgs), dim3(64 * NW), lds, s, g);
+    return check_launch("gemv_q8_fast_kernel");
+}
+
+// Fast-kernel launch: full workgroups when every CU gets one, two units per wave when one
+// unit per wave would need more than one resident round.
+template <int Q, int LPR, bool F32>
+static jk_status launch_fast(hipStream_t s, GemvGroup &g, size_t lds) {
+    constexpr int RPU = 64 / LPR, FW = kFullWaves<Q>;
+    long units = 0;
+    for (int i = 0; i < g.njobs; ++i) units += (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
+    const long ncu = cu_count();
+    if (units < ncu * FW) return launch_fast_run<Q, LPR, F32, 4, 1>(s, g, lds);
+    const long cap = (long)resident_per_cu(gemv_q8_fast_kernel<Q, LPR, F32, FW, 1>, lds, 64 * FW) * ncu * FW;
+    if constexpr (kFastPair<Q>)
+        if (units > cap) return launch_fast_run<Q, LPR, F32, FW, 2>(s, g, lds);
+    return launch_fast_run<Q, LPR, F32, FW, 1>(s, g, lds);
+}
+
+template <int Q>
+static jk_status launch_group_q(hipStream_t s, const GemvJob *jobs, int n) {
+    using T = QTraits<Q>;
+    int max_nb = 0;
+    for (int i = 0; i < n; ++i) max_nb = max(max_nb, jobs[i].w.nb);
+    const size_t lds = (size_t)max_nb * T::XB;
+    if (lds > (size_t)kMaxLdsX) {
+        for (int i = 0; i < n; ++i) {
+            const GemvJob &j = jobs[i];
+            if (j.xf) return fail(JK_CAPABILITY_MISMATCH, "gemv: f32 activations need K <= %d",
+                                  kMaxLdsX / T::XB * T::XE);
+            hipLaunchKernelGGL(gemv_q8_global_kernel<Q>, dim3((unsigned)((j.r1 - j.r0 + 15) / 16)), dim3(256), 0, s,
+                               j.w, j.xq, j.y, j.r0, j.r1);
+            JK_TRY(check_launch("gemv_q8_global_kernel"));
+        }
+        return JK_OK;
+    }
+    const bool wide = T::K && max_nb > 32;  // one wave per row for long K-quant rows
+    // one launch per run of jobs with the same activation kind (f32 or caller blocks)
+    int base = 0;
+    while (base < n) {
+        const bool f32 = jobs[base].xf != nullptr;
+        GemvGroup g;
+        memset(&g, 0, sizeof g);
+        while (base < n && g.njobs < kMaxGemvJobs && (jobs[base].xf != nullptr) == f32) g.job[g.njobs++] = jobs[base++];
+        const int lpr = wide ? 64 : 16;
+        if ((max_nb + lpr - 1) / lpr <= kFastU<Q>) {
+            if (wide && f32) JK_TRY((launch_fast<Q, 64, true>(s, g, lds)));
+            else if (wide) JK_TRY((launch_fast<Q, 64, false>(s, g, lds)));
+            else if (f32) JK_TRY((launch_fast<Q, 16, true>(s, g, lds)));
+            else JK_TRY((launch_fast<Q, 16, false>(s, g, lds)));
+            continue;
+        }
+        // full workgroups when every CU gets at least one
+        const int rpu = wide ? 1 : 4;
+        long units = 0;
+        for (int i = 0; i < g.njobs; ++i) units += (g.job[i].r1 - g.job[i].r0 + rpu - 1) / rpu;
+        const bool full = units >= (long)cu_count() * kFullWaves<Q>;
+        constexpr int FW = kFullWaves<Q>;
+        if (wide && f32) JK_TRY(full ? (launch_group_run<Q, 64, true, FW>(s, g, lds)) : (launch_group_run<Q, 64, true, 4>(s, g, lds)));
+        else if (wide) JK_TRY(full ? (launch_group_run<Q, 64, false, FW>(s, g, lds)) : (launch_group_run<Q, 64, false, 4>(s, g, lds)));
+        else if (f32) JK_TRY(full ? (launch_group_run<Q, 16, true, FW>(s, g, lds)) : (launch_group_run<Q, 16, true, 4>(s, g, lds)));
+        else JK_TRY(full ? (launch_group_run<Q, 16, false, FW>(s, g, lds)) : (launch_group_run<Q, 16, false, 4>(s, g, lds)));
+    }
+    return JK_OK;
+}
+
+// All jobs share one weight format and have r1 > r0 (checked by the callers).
+jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n) {
+    if (n <= 0) return JK_OK;
+    switch (jobs[0].w.quant) {
+    case JK_Q4_0: return launch_group_q<JK_Q4_0>(s, jobs, n);
+    case JK_Q8_0: return launch_group_q<JK_Q8_0>(s, jobs, n);
+    case JK_Q4_K: return launch_group_q<JK_Q4_K>(s, jobs, n);
+    case JK_Q6_K: return launch_group_q<JK_Q6_K>(s, jobs, n);
+    case JK_TQ2_0: return launch_group_q<JK_TQ2_0>(s, jobs, n);
+    default: return fail(JK_CAPABILITY_MISMATCH, "gemv: unsupported quant %d", jobs[0].w.quant);
+    }
+}
+
+jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1) {
+    GemvJob j;
+    memset(&j, 0, sizeof j);
+    j.w = w;
+    j.xq = x;
+    j.y = y;
+    j.r0 = r0;
+    j.r1 = r1;
+    return launch_gemv_group(s, &j, 1);
+}
+
+}  // namespace jk

@@ -63,6 +63,26 @@ struct WeightDev {
     int nb;
 };
 
+// One product of a grouped quant_q8 GEMV launch: y[row - r0] for rows [r0, r1) of w,
+// against pre-quantized activation blocks xq or f32 activations xf (quantized in the
+// launch). wg0 / nwg are the job's first workgroup and workgroup count, filled in by the
+// launcher.
+constexpr int kMaxGemvJobs = 8;
+struct GemvJob {
+    WeightDev w;
+    const void *xq;
+    const float *xf;
+    float *y;
+    int r0, r1, wg0, nwg;
+};
+struct GemvGroup {
+    int wg0[kMaxGemvJobs];  // first workgroup of each job (one scalar load for the lookup)
+    GemvJob job[kMaxGemvJobs];
+    int njobs;
+    int upw;      // units per wave (upper bound), sizes the per-wave result slots in LDS
+    int out_off;  // byte offset of the result slots in dynamic LDS
+};
+
 }  // namespace jk
 
 struct jk_weight {
@@ -108,6 +128,7 @@ jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 
 jk_status launch_absmax_i8(hipStream_t s, const float *x, const float *norm_w, size_t m, size_t k,
                            float eps, int8_t *q, float *scales);
 jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1);
+jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n);
 jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y);
 jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act,
                            const float *act_scales, int m, float *y);

@@ -7,27 +7,6 @@
 
 namespace jk {
 
-// Rust `v.round().clamp(lo, hi) as i8`: round half away from zero, NaN -> 0.
-__device__ __forceinline__ int rust_round_clamp_i8(float v, float lo, float hi) {
-    float r = roundf(v);
-    if (__builtin_isnan(r)) return 0;
-    r = r < lo ? lo : r;
-    r = r > hi ? hi : r;
-    return (int)r;
-}
-
-// round_scaled_to_i8 (quant_q8.rs:102-108)
-__device__ __forceinline__ int round_scaled_to_i8(float v, float inv) {
-    if (!__builtin_isfinite(v)) return 0;
-    return rust_round_clamp_i8(v * inv, -127.0f, 127.0f);
-}
-
-template <int W>
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
-    return v;
-}
-
 // quantize_block_q8_0_scalar (quant_q8.rs:203-219): 32 lanes per block, one element each.
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, size_t nblocks,
                                                             jk_block_q8_0 *__restrict__ out) {

@@ -409,6 +409,68 @@ jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t
     return launch_gemv_q8((hipStream_t)s, w->dev, x, y, (int)r0, (int)r1);
 }
 
+// Validation shared by the grouped / fused GEMV entries (no reference counterpart for the
+// grouping itself; each job follows gemv_* validation, check_q8_block_len quant_q8.rs:1562).
+static jk_status gemv_job_check(const jk_gemv_job *j, size_t i, GemvJob *out) {
+    const jk_weight *w = j->w;
+    if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: null weight handle", i);
+    const int q = w->dev.quant;
+    if (q != JK_Q4_0 && q != JK_Q8_0 && q != JK_Q4_K && q != JK_Q6_K && q != JK_TQ2_0)
+        return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_batch: job %zu: %s has no quant_q8 GEMV", i, quant_name(q));
+    if ((j->x_q8 == nullptr) == (j->x_f32 == nullptr))
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: exactly one of x_q8 and x_f32 must be set", i);
+    if ((uintptr_t)j->x_q8 % 4 || (uintptr_t)j->x_f32 % 16)
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: x_q8 must be 4-byte and x_f32 16-byte aligned", i);
+    if (j->row_begin > j->row_end || j->row_end > (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: row range %zu..%zu out of bounds for %d rows", i,
+                    j->row_begin, j->row_end, w->dev.rows);
+    if (!j->y && j->row_end > j->row_begin) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: null output", i);
+    memset(out, 0, sizeof *out);
+    out->w = w->dev;
+    out->xq = j->x_q8;
+    out->xf = j->x_f32;
+    out->y = j->y;
+    out->r0 = (int)j->row_begin;
+    out->r1 = (int)j->row_end;
+    return JK_OK;
+}
+
+jk_status jk_gemv_q8_batch(jk_stream s, const jk_gemv_job *jobs, size_t njobs) {
+    if (njobs == 0) return JK_OK;
+    if (!jobs) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: null job array");
+    // validate everything before launching anything (fail closed)
+    for (size_t i = 0; i < njobs; ++i) {
+        GemvJob tmp;
+        JK_TRY(gemv_job_check(&jobs[i], i, &tmp));
+    }
+    // launch runs of consecutive non-empty jobs that share a weight format
+    GemvJob run[kMaxGemvJobs];
+    int n = 0, quant = 0;
+    for (size_t i = 0; i < njobs; ++i) {
+        GemvJob gj;
+        JK_TRY(gemv_job_check(&jobs[i], i, &gj));
+        if (gj.r1 == gj.r0) continue;
+        if (n == kMaxGemvJobs || (n > 0 && gj.w.quant != quant)) {
+            JK_TRY(launch_gemv_group((hipStream_t)s, run, n));
+            n = 0;
+        }
+        quant = gj.w.quant;
+        run[n++] = gj;
+    }
+    return launch_gemv_group((hipStream_t)s, run, n);
+}
+
+jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: null weight handle");
+    if (n != (size_t)w->dev.cols)
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: input len %zu != cols %d", n, w->dev.cols);
+    if (y_len != (size_t)w->dev.rows)
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: output len %zu != rows %d", y_len, w->dev.rows);
+    if (!x) return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: null input");
+    jk_gemv_job j = {w, nullptr, x, y, 0, (size_t)w->dev.rows};
+    return jk_gemv_q8_batch(s, &j, 1);
+}
+
 // -------------------------------------------------------------- vec_dot (f32)
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
     if (!w) return fail(JK_TENSOR_BOUNDS, "vec_dot: null weight handle");

@@ -71,6 +71,10 @@ class ActQ8C(C.Structure):
                 ("qs", _vp), ("scales", _vp), ("sums", _vp), ("sums16", _vp), ("super256", _vp)]
 
 
+class GemvJobC(C.Structure):
+    _fields_ = [("w", _vp), ("x_q8", _vp), ("x_f32", _vp), ("y", _vp), ("row_begin", _sz), ("row_end", _sz)]
+
+
 class WeightInfoC(C.Structure):
     _fields_ = [("quant", C.c_int32), ("rows", _sz), ("cols", _sz), ("device_bytes", _sz), ("gguf_bytes", _sz)]
 
@@ -343,6 +347,27 @@ def dev_gemv_q8(w: Weight, x, nx, y, y_len, stream=None, fn: str | None = None):
 
 def dev_gemv_q8_rows(w: Weight, x, nx, y, r0, r1, stream=None):
     _check(lib().jk_gemv_q8_rows(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(nx), _vp(_ptr(y)), _sz(r0), _sz(r1)))
+
+
+def dev_gemv_q8_f32(w: Weight, x, n, y, y_len, stream=None):
+    """quantize_row_q8_0/q8_k of f32 x and the matching gemv_* in one launch."""
+    _check(lib().jk_gemv_q8_f32(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(n), _vp(_ptr(y)), _sz(y_len)))
+
+
+def gemv_jobs(jobs) -> C.Array:
+    """ctypes array of jk_gemv_job from (weight, x_q8, x_f32, y, row_begin, row_end) tuples."""
+    arr = (GemvJobC * max(1, len(jobs)))()
+    for i, (w, xq, xf, y, r0, r1) in enumerate(jobs):
+        arr[i] = GemvJobC(w.handle.value if isinstance(w, Weight) else w, _ptr(xq) or None, _ptr(xf) or None,
+                          _ptr(y) or None, r0, r1)
+    return arr
+
+
+def dev_gemv_q8_batch(jobs, stream=None):
+    """Grouped quant_q8 GEMV over (weight, x_q8, x_f32, y, row_begin, row_end) tuples."""
+    arr = jobs if isinstance(jobs, C.Array) else gemv_jobs(jobs)
+    n = len(jobs)
+    _check(lib().jk_gemv_q8_batch(_vp(stream or 0), arr, _sz(n)))
 
 
 def dev_vec_dot_f32(w: Weight, x, n, y, y_len, stream=None):

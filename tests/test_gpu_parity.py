@@ -221,6 +221,124 @@ def test_gemv_q8_full_config_shapes(gpu, name, quant, rows, cols):
     assert same_bits(got, ref), mismatch(got, ref)
 
 
+# ------------------------------------------------- fused-quantize and grouped GEMV
+def gpu_gemv_f32(torch, w, x):
+    dx = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    dy = empty(torch, 4 * w.rows)
+    jk.dev_gemv_q8_f32(w, dx, x.size, dy, w.rows)
+    torch.cuda.synchronize()
+    return host(dy, np.float32, w.rows)
+
+
+# K values cover one and several staging rounds, LPR 16 and 64 (K-quants with > 32
+# blocks), and a K-quant row long enough for two 64-block iterations.
+FUSED_SHAPES = [(1, 256), (5, 4352), (37, 4096), (33, 7168), (17, 8448), (9, 14336), (4, 17920), (3, 32000)]
+
+
+@pytest.mark.parametrize("quant", GEMV_FORMATS)
+@pytest.mark.parametrize("rows,cols", FUSED_SHAPES)
+def test_gemv_q8_f32_fused_quantize(gpu, quant, rows, cols):
+    """quantize_row_q8_* + gemv_* fused in one launch == oracle quantize + gemv, bit for bit."""
+    torch = gpu
+    if cols % jk.BLOCK_ELEMENTS[quant]:
+        pytest.skip("shape not block aligned")
+    raw = synth.random_weights(quant, rows, cols, seed=rows * 11 + quant, specials=True)
+    rng = np.random.default_rng(cols + rows)
+    x = (rng.standard_normal(cols) * rng.choice([1e-3, 1.0, 40.0], cols)).astype(np.float32)
+    x[: jk.BLOCK_ELEMENTS[quant]] = 0.0
+    x[rng.random(cols) < 0.005] = np.nan
+    x[rng.random(cols) < 0.005] = -np.inf
+    if cols >= 512:  # a block whose maximum is subnormal: 127 / amax overflows to inf
+        x[256:512] = (rng.standard_normal(256) * 1e-40).astype(np.float32)
+        x[256:512:7] = 0.0
+    ref = O.gemv_q8(quant, [rows, cols], raw, x_blocks(quant, x), rows)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    got = gpu_gemv_f32(torch, w, x)
+    assert same_bits(got, ref), mismatch(got, ref)
+
+
+@pytest.mark.parametrize("quant,cols", [(Q4_K, 256 * 57), (Q6_K, 256 * 200), (Q8_0, 32 * 500), (Q4_0, 32 * 1500)])
+def test_gemv_q8_long_rows_caller_blocks(gpu, quant, cols):
+    """Caller blocks over several staging rounds, and past the LDS budget (global path)."""
+    torch = gpu
+    rows = 5
+    raw = synth.random_weights(quant, rows, cols, seed=cols, specials=True)
+    xq = x_blocks(quant, synth.activations(cols, 3))
+    ref = O.gemv_q8(quant, [rows, cols], raw, xq, rows)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    got = gpu_gemv(torch, w, xq)
+    assert same_bits(got, ref), mismatch(got, ref)
+
+
+def test_gemv_q8_caller_q8k_with_inconsistent_bsums(gpu):
+    """Q6_K / TQ2_0 dots use the quants themselves, Q4_K uses bsums as given (quant_q8.rs:1834-2003)."""
+    torch = gpu
+    rows, cols = 7, 1024
+    x = O.quantize_row_q8_k(synth.activations(cols, 9))
+    x["bsums"] = np.random.default_rng(1).integers(-3000, 3000, x["bsums"].shape, dtype=np.int16)
+    for quant in (Q4_K, Q6_K, TQ2_0):
+        raw = synth.gguf_weights(quant, rows, cols, seed=quant)
+        ref = O.gemv_q8(quant, [rows, cols], raw, x, rows)
+        w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+        got = gpu_gemv(torch, w, x)
+        assert same_bits(got, ref), (quant, mismatch(got, ref))
+
+
+def test_gemv_q8_batch_mixed_jobs(gpu):
+    """One grouped call == the per-matrix calls: shared and distinct activations, f32 and
+    caller blocks, row slices, an empty job and two weight formats (split launches)."""
+    torch = gpu
+    specs = [(Q4_K, 96, 4096), (Q4_K, 24, 4096), (Q4_K, 40, 4096), (Q6_K, 33, 14336), (Q4_0, 50, 4096),
+             (Q4_K, 64, 4096)]
+    xs = {c: synth.activations(c, c) for c in (4096, 14336)}
+    dxf = {c: torch.from_numpy(xs[c]).cuda() for c in xs}
+    dq = {}
+    jobs, expect, outs = [], [], []
+    for i, (quant, rows, cols) in enumerate(specs):
+        raw = synth.gguf_weights(quant, rows, cols, seed=50 + i)
+        w = jk.Weight(jk.TensorView(f"w{i}", quant, [rows, cols], raw), rows, cols)
+        xq = x_blocks(quant, xs[cols])
+        key = (quant in (Q4_0, Q8_0), cols)
+        if key not in dq:
+            dq[key] = dev(torch, xq)
+        full = O.gemv_q8(quant, [rows, cols], raw, xq, rows)
+        r0, r1 = (3, rows - 5) if i % 2 else (0, rows)
+        if i == 5:
+            r0 = r1 = 10  # empty job
+        y = empty(torch, 4 * max(1, r1 - r0))
+        use_f32 = i % 3 != 1
+        jobs.append((w, None if use_f32 else dq[key], dxf[cols] if use_f32 else None, y, r0, r1))
+        expect.append(full[r0:r1])
+        outs.append((y, r1 - r0))
+    jk.dev_gemv_q8_batch(jobs)
+    torch.cuda.synchronize()
+    for (y, n), ref in zip(outs, expect):
+        if n:
+            got = host(y, np.float32, n)
+            assert same_bits(got, ref), mismatch(got, ref)
+
+
+def test_gemv_q8_batch_validation(gpu):
+    torch = gpu
+    raw = synth.gguf_weights(Q4_K, 4, 256, seed=1)
+    w = jk.Weight(jk.TensorView("w", Q4_K, [4, 256], raw), 4, 256)
+    wi = jk.Weight(jk.TensorView("wi", I2_S, [4, 128], synth.gguf_weights(I2_S, 4, 128, seed=2)), 4, 128)
+    x = torch.zeros(256, dtype=torch.float32, device="cuda")
+    y = torch.zeros(4, dtype=torch.float32, device="cuda")
+    with pytest.raises(jk.TensorBoundsError):  # neither activation
+        jk.dev_gemv_q8_batch([(w, None, None, y, 0, 4)])
+    with pytest.raises(jk.TensorBoundsError):  # both activations
+        jk.dev_gemv_q8_batch([(w, x, x, y, 0, 4)])
+    with pytest.raises(jk.TensorBoundsError):  # rows out of range
+        jk.dev_gemv_q8_batch([(w, None, x, y, 0, 5)])
+    with pytest.raises(jk.TensorBoundsError):  # misaligned f32 activation
+        jk.dev_gemv_q8_batch([(w, None, x.data_ptr() + 4, y, 0, 4)])
+    with pytest.raises(jk.CapabilityMismatch):  # I2_S has no quant_q8 GEMV
+        jk.dev_gemv_q8_batch([(wi, None, x, y, 0, 4)])
+    with pytest.raises(jk.TensorBoundsError):
+        jk.dev_gemv_q8_f32(w, x, 255, y, 4)
+
+
 # ------------------------------------------------------------------ f32 vec_dot
 @pytest.mark.parametrize("quant", [Q4_0, Q8_0, Q4_K, Q6_K, I2_S])
 @pytest.mark.parametrize("rows,cols", [(1, 256), (5, 4352), (33, 4096)])
