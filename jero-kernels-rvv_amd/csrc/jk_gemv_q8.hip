@@ -91,17 +91,21 @@ template <int Q> struct WReg {
 // Loads block b of row r with 128-bit non-temporal loads. xo (0 or 16) is XORed into
 // every byte address: 16 keeps each access inside its own 128-byte line but makes it a
 // distinct load (dummy loads that must not be merged with the real ones).
+// Addresses are a wave-uniform plane base plus one 32-bit per-lane offset shared by all
+// chunks (planes hold fewer than 2^28 blocks, checked at upload).
 template <int Q>
 __device__ __forceinline__ void wload(WReg<Q> &o, const WeightDev &w, int r, int b, unsigned xo = 0) {
+    const uint32_t blk = (uint32_t)r * (uint32_t)w.nb + (uint32_t)b;
+    const uint32_t off = (blk << 4) ^ xo;
+    const size_t pstride = (size_t)w.rows * (size_t)w.nb * 16;
 #pragma unroll
     for (int c = 0; c < QTraits<Q>::C; ++c) {
-        const uintptr_t a = reinterpret_cast<uintptr_t>(chunk_ptr(w, c, r, b)) ^ xo;
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(a));
+        const uint8_t *plane = w.planes + (size_t)c * pstride;
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(plane + off));
         o.c[c] = make_uint4(v.x, v.y, v.z, v.w);
     }
     if constexpr (QTraits<Q>::D)
-        o.d = *reinterpret_cast<const uint16_t *>(
-            reinterpret_cast<uintptr_t>(w.dplane + (size_t)r * (size_t)w.nb + (size_t)b) ^ (xo >> 3));
+        o.d = *reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(w.dplane) + ((blk << 1) ^ (xo >> 3)));
 }
 
 // ------------------------------------------------------------------ block values
@@ -604,7 +608,8 @@ gemv_q8_group_kernel(GemvGroup grp) {
 
 // ------------------------------------------------------------------ fast kernel
 // Straight-line variant for launches whose rows fit in one batch per unit (nit <= UF):
-// each wave owns QPW consecutive units, issues all their weight loads up front, evaluates
+// workgroup g of a job owns units [g * upg, (g + 1) * upg) and wave w of it units
+// g * upg + w + NW * q (q < QPW); a wave issues all its weight loads up front, evaluates
 // them and keeps the results in registers until one store pass at the end. Without a loop
 // the compiler keeps every load where it is written and every wait exact.
 template <int Q> constexpr int kFastU = Q == JK_Q4_0 || Q == JK_Q8_0 ? 8 : Q == JK_TQ2_0 ? 2 : 1;
@@ -624,8 +629,9 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     const int sub = lane / LPR, p = lane % LPR;
     const int nb = w.nb, nit = (nb + LPR - 1) / LPR;  // nit <= UF
     const int r0 = job.r0, r1 = job.r1;
-    const int units = (r1 - r0 + RPU - 1) / RPU;
-    const int base = (((int)blockIdx.x - job.wg0) * NW + wave) * QPW;  // first unit of the wave
+    const int g0 = ((int)blockIdx.x - job.wg0) * job.upg;
+    const int units = min((r1 - r0 + RPU - 1) / RPU, g0 + job.upg);  // end of this workgroup's units
+    const int base = g0 + wave;                                          // unit q: base + NW * q
 
     // 1. activation round 0, then every weight load of the wave. A unit past the end
     //    re-reads a valid unit's lines at distinct addresses (xor 16): the loads stay
@@ -633,11 +639,11 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     XRegs<NW, F32> xr;
     stage_begin<Q, F32, NW>(xr, job, nb);
     WReg<Q> W[QPW][UF];
-    const int ufb = base < units ? base : base % units;
+    const int ufb = base < units ? base : g0;  // a valid unit of the workgroup
 #pragma unroll
     for (int q = 0; q < QPW; ++q) {
-        const bool dummy = base + q >= units;
-        const int row = r0 + (dummy ? ufb : base + q) * RPU + sub;
+        const bool dummy = base + NW * q >= units;
+        const int row = r0 + (dummy ? ufb : base + NW * q) * RPU + sub;
         const int r = min(row, r1 - 1);
 #pragma unroll
         for (int k = 0; k < UF; ++k) wload<Q>(W[q][k], w, r, min(k * LPR + p, nb - 1), dummy ? 16u : 0u);
@@ -652,7 +658,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     float out[QPW];
 #pragma unroll
     for (int q = 0; q < QPW; ++q) {
-        const int row = r0 + (base + q) * RPU + sub;
+        const int row = r0 + (base + NW * q) * RPU + sub;
         float acc = row < rows4 ? 0.0f : -0.0f;
         float v[UF];
 #pragma unroll
@@ -679,8 +685,8 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     const int writer = LPR == 16 ? nb - LPR * (nit - 1) - 1 : 0;
 #pragma unroll
     for (int q = 0; q < QPW; ++q) {
-        const int row = r0 + (base + q) * RPU + sub;
-        if (base + q < units && row < r1 && p == writer) job.y[row - r0] = out[q];
+        const int row = r0 + (base + NW * q) * RPU + sub;
+        if (base + NW * q < units && row < r1 && p == writer) job.y[row - r0] = out[q];
     }
 }
 
@@ -770,13 +776,14 @@ static jk_status launch_group_run(hipStream_t s, GemvGroup &g, size_t lds) {
 }
 
 template <int Q, int LPR, bool F32, int NW, int QPW>
-static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds) {
+static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds, int upg) {
     constexpr int RPU = 64 / LPR;
     int wgs = 0;
     for (int i = 0; i < g.njobs; ++i) {
         const int units = (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
         g.job[i].wg0 = g.wg0[i] = wgs;
-        g.job[i].nwg = (units + NW * QPW - 1) / (NW * QPW);
+        g.job[i].upg = upg;
+        g.job[i].nwg = (units + upg - 1) / upg;
         wgs += g.job[i].nwg;
     }
     for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
@@ -784,19 +791,21 @@ static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds) {
     return check_launch("gemv_q8_fast_kernel");
 }
 
-// Fast-kernel launch: full workgroups when every CU gets one, two units per wave when one
-// unit per wave would need more than one resident round.
+// Fast-kernel launch: about one workgroup per CU, each with upg = ceil(units / CUs) units,
+// in the smallest workgroup shape (waves x units per wave) that covers upg; bigger
+// launches use the largest shape and more than one workgroup per CU.
 template <int Q, int LPR, bool F32>
 static jk_status launch_fast(hipStream_t s, GemvGroup &g, size_t lds) {
     constexpr int RPU = 64 / LPR, FW = kFullWaves<Q>;
     long units = 0;
     for (int i = 0; i < g.njobs; ++i) units += (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
     const long ncu = cu_count();
-    if (units < ncu * FW) return launch_fast_run<Q, LPR, F32, 4, 1>(s, g, lds);
-    const long cap = (long)resident_per_cu(gemv_q8_fast_kernel<Q, LPR, F32, FW, 1>, lds, 64 * FW) * ncu * FW;
-    if constexpr (kFastPair<Q>)
-        if (units > cap) return launch_fast_run<Q, LPR, F32, FW, 2>(s, g, lds);
-    return launch_fast_run<Q, LPR, F32, FW, 1>(s, g, lds);
+    const int upg = (int)std::max<long>(1, (units + ncu - 1) / ncu);
+    if (upg <= 4) return launch_fast_run<Q, LPR, F32, 4, 1>(s, g, lds, upg);
+    if (upg <= 8) return launch_fast_run<Q, LPR, F32, 8, 1>(s, g, lds, upg);
+    if (FW == 16 && upg <= 16) return launch_fast_run<Q, LPR, F32, FW, 1>(s, g, lds, upg);
+    if constexpr (kFastPair<Q>) return launch_fast_run<Q, LPR, F32, FW, 2>(s, g, lds, std::min(upg, 2 * FW));
+    return launch_fast_run<Q, LPR, F32, FW, 1>(s, g, lds, std::min(upg, FW));
 }
 
 template <int Q>

@@ -74,6 +74,8 @@ struct GemvJob {
     const float *xf;
     float *y;
     int r0, r1, wg0, nwg;
+    int upg;  // units per workgroup (fast kernel)
+    int pad;
 };
 struct GemvGroup {
     int wg0[kMaxGemvJobs];  // first workgroup of each job (one scalar load for the lookup)

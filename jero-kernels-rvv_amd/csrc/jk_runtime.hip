@@ -209,7 +209,8 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
         else { rows = d1; cols = d0; }
     }
     JK_TRY(validate_matrix_view(w, rows, cols));
-    if (rows >= kMaxRows || cols / (size_t)fmt_of(w->quant).be >= kMaxRows)
+    if (rows >= kMaxRows || cols / (size_t)fmt_of(w->quant).be >= kMaxRows ||
+        rows * (cols / (size_t)fmt_of(w->quant).be) >= ((size_t)1 << 28))
         return fail(JK_TENSOR_BOUNDS, "%s: matrix [%zu, %zu] exceeds the device index range", tname(w), rows, cols);
     const Fmt f = fmt_of(w->quant);
     const size_t nb = cols / f.be;
