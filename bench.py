@@ -172,35 +172,50 @@ def main() -> int:
     log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step (wall {wall * 1e3 / args.steps:.4f} ms/step)")
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Per-stage decomposition: HIP events around each stage launch (eager, one layer after
-    # another so every launch streams weights not touched by the previous one).
-    s = torch.cuda.current_stream().cuda_stream
+    # Per-stage decomposition: each stage's launches for all layers captured back to back in
+    # a HIP graph (distinct weights, so every launch streams from HBM), replayed with HIP
+    # events on the capturing stream around the replays; per-launch time = elapsed /
+    # (replays x layers). This includes the graph's inter-launch gap, which a kernel trace
+    # does not.
     mat_bytes = {name: gemv_bytes(q, r, c, jk) for name, q, r, c in synth.LLAMA3_8B_LAYER}
     per_stage = {}
+    reps = 5
     for si, (stage, names, _) in enumerate(STAGES):
-        evs = []
-        for rep in range(2):
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
             for per in layer_jobs:
-                _, arr, n = per[si]
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                launch_stage(stage, arr, n, s)
-                e1.record()
-                evs.append((e0, e1))
+                launch_stage(stage, per[si][1], per[si][2], side.cuda_stream)
+        torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        dur_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in evs[len(layers):]]))  # second pass
+        with torch.cuda.graph(g):
+            cs = torch.cuda.current_stream().cuda_stream
+            for per in layer_jobs:
+                launch_stage(stage, per[si][1], per[si][2], cs)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        dur_us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
         b = sum(mat_bytes[n] for n in names)
         per_stage[stage] = {"matrices": list(names), "bytes": b, "us": round(dur_us, 3),
                             "gbs": round(b / (dur_us * 1e-6) / 1e9, 1)}
-        log(f"  {stage:12s} {b:>10d} B: {dur_us:.2f} us, {per_stage[stage]['gbs']} GB/s")
+        log(f"  {stage:12s} {b:>10d} B: {dur_us:.2f} us/launch, {per_stage[stage]['gbs']} GB/s")
+        del g
     dom = per_stage["ffn_gate_up"]
     roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gemv_q8_group_kernel<Q4_K,16,f32> (ffn_gate + ffn_up, 2 x 14336x4096)",
+                "kernel": "gemv_q8_fast_kernel<Q4_K> (ffn_gate + ffn_up, 2 x 14336x4096, f32 activation)",
                 "avg_launch_us": dom["us"], "bytes_per_launch": dom["bytes"]}
 
     # ------------------------------------------------------------ prefill GEMM (Q8_0)
     gemm = None
+    s = torch.cuda.current_stream().cuda_stream
     if args.gemm_m > 0:
         M, N, K = args.gemm_m, 14336, 4096
         ncopies = 10

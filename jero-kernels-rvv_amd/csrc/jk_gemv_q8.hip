@@ -243,22 +243,23 @@ __device__ __forceinline__ float block_value(const WReg<Q> &wr, const X &x) {
 // any weight load of the CU (see the kernel): vector memory returns data in issue order,
 // so activation loads queued behind weight loads would wait for the weight stream. With
 // NW waves per workgroup, thread t holds dwords (or float4s) t + 64*NW*i of a round.
-template <int NW, bool F32> struct XRegs {
-    // dwords per thread per round: a 4096-wide f32 activation (16 KB) in one round; caller
-    // blocks are 4x smaller
-    static constexpr int N = F32 && NW <= 4 ? 16 : 8;
+template <int NW, bool F32, int Q> struct XRegs {
+    // dwords per thread per round: a 4096-wide f32 activation (16 KB) in one round, and for
+    // Q6_K (whose register budget is 2 waves per SIMD) a 14336-wide one; caller blocks are
+    // 4x smaller
+    static constexpr int N = F32 && Q == JK_Q6_K ? (NW <= 4 ? 64 : 32) : F32 && NW <= 4 ? 16 : 8;
     static constexpr int ROUND = 64 * NW * N;
     uint32_t v[N];
 };
 
 // Round r of an f32 activation of n4 float4s (clamped, unconditional loads: entries past
 // the end are never staged).
-template <int NW>
-__device__ __forceinline__ void xload_f32(XRegs<NW, true> &xr, const float *__restrict__ x, int n4, int r) {
+template <int NW, int Q>
+__device__ __forceinline__ void xload_f32(XRegs<NW, true, Q> &xr, const float *__restrict__ x, int n4, int r) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
 #pragma unroll
-    for (int i = 0; i < XRegs<NW, true>::N / 4; ++i) {
-        const float4 v = x4[min(r * (XRegs<NW, true>::ROUND / 4) + (int)threadIdx.x + 64 * NW * i, n4 - 1)];
+    for (int i = 0; i < XRegs<NW, true, Q>::N / 4; ++i) {
+        const float4 v = x4[min(r * (XRegs<NW, true, Q>::ROUND / 4) + (int)threadIdx.x + 64 * NW * i, n4 - 1)];
         xr.v[4 * i] = __float_as_uint(v.x);
         xr.v[4 * i + 1] = __float_as_uint(v.y);
         xr.v[4 * i + 2] = __float_as_uint(v.z);
@@ -267,10 +268,10 @@ __device__ __forceinline__ void xload_f32(XRegs<NW, true> &xr, const float *__re
 }
 
 // Round r of caller blocks (ndw dwords), clamped and unconditional as above.
-template <int NW>
-__device__ __forceinline__ void xload_raw(XRegs<NW, false> &xr, const uint32_t *__restrict__ x, int ndw, int r) {
+template <int NW, int Q>
+__device__ __forceinline__ void xload_raw(XRegs<NW, false, Q> &xr, const uint32_t *__restrict__ x, int ndw, int r) {
 #pragma unroll
-    for (int i = 0; i < XRegs<NW, false>::N; ++i) xr.v[i] = x[min(r * XRegs<NW, false>::ROUND + (int)threadIdx.x + 64 * NW * i, ndw - 1)];
+    for (int i = 0; i < XRegs<NW, false, Q>::N; ++i) xr.v[i] = x[min(r * XRegs<NW, false, Q>::ROUND + (int)threadIdx.x + 64 * NW * i, ndw - 1)];
 }
 
 // Rust `(x * inv).round().clamp(-127.0, 127.0) as i8` for finite x (round_scaled_to_i8,
@@ -331,13 +332,13 @@ __device__ __forceinline__ void quantize_q8_0_lanes(float (&v)[4], uint8_t *dst,
 
 // Quantizes round r of f32 activations (registers) into the staged LDS blocks.
 template <int Q, int NW>
-__device__ __forceinline__ void xstage_f32(const XRegs<NW, true> &xr, int nb, int r, uint8_t *s_x) {
+__device__ __forceinline__ void xstage_f32(const XRegs<NW, true, Q> &xr, int nb, int r, uint8_t *s_x) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < XRegs<NW, true>::N / 4; ++i) {
+    for (int i = 0; i < XRegs<NW, true, Q>::N / 4; ++i) {
         float v[4] = {__uint_as_float(xr.v[4 * i]), __uint_as_float(xr.v[4 * i + 1]), __uint_as_float(xr.v[4 * i + 2]),
                       __uint_as_float(xr.v[4 * i + 3])};
-        const int f = r * (XRegs<NW, true>::ROUND / 4) + tid + 64 * NW * i;
+        const int f = r * (XRegs<NW, true, Q>::ROUND / 4) + tid + 64 * NW * i;
         if constexpr (QTraits<Q>::K) {
             const int blk = f >> 6;  // uniform over the wave
             if (blk < nb) quantize_q8_k_wave(v, s_x + blk * kXkBytes, tid & 63);
@@ -351,14 +352,14 @@ __device__ __forceinline__ void xstage_f32(const XRegs<NW, true> &xr, int nb, in
 // Scatters round r of caller blocks (BlockQ8K: d, qs[64], bsums[8] dwords; BlockQ8_0: d,
 // qs[8]) into the staged LDS layout.
 template <int Q, int NW>
-__device__ __forceinline__ void xstage_raw(const XRegs<NW, false> &xr, int ndw, int r, uint8_t *s_x) {
+__device__ __forceinline__ void xstage_raw(const XRegs<NW, false, Q> &xr, int ndw, int r, uint8_t *s_x) {
     constexpr bool K = QTraits<Q>::K;
     constexpr int DW = K ? 73 : 9, STEP = 64 * NW;
     // block / word of slot 0, then advanced by STEP dwords per slot without dividing
-    const int k0 = r * XRegs<NW, false>::ROUND + (int)threadIdx.x;
+    const int k0 = r * XRegs<NW, false, Q>::ROUND + (int)threadIdx.x;
     int blk = k0 / DW, wd = k0 - blk * DW;
 #pragma unroll
-    for (int i = 0; i < XRegs<NW, false>::N; ++i) {
+    for (int i = 0; i < XRegs<NW, false, Q>::N; ++i) {
         const int k = k0 + STEP * i;
         if (i > 0) {
             blk += STEP / DW;
@@ -418,25 +419,25 @@ __device__ __forceinline__ float fold_wave(float acc, float v, int g, float *red
 // begin: round 0 into registers, then a barrier that puts every activation load of the
 // workgroup ahead of its weight loads (it waits for no data).
 template <int Q, bool F32, int NW>
-__device__ __forceinline__ void stage_begin(XRegs<NW, F32> &xr, const GemvJob &job, int nb) {
+__device__ __forceinline__ void stage_begin(XRegs<NW, F32, Q> &xr, const GemvJob &job, int nb) {
     using T = QTraits<Q>;
-    if constexpr (F32) xload_f32<NW>(xr, job.xf, nb * T::XE / 4, 0);
-    else xload_raw<NW>(xr, static_cast<const uint32_t *>(job.xq), nb * (T::K ? 73 : 9), 0);
+    if constexpr (F32) xload_f32<NW, Q>(xr, job.xf, nb * T::XE / 4, 0);
+    else xload_raw<NW, Q>(xr, static_cast<const uint32_t *>(job.xq), nb * (T::K ? 73 : 9), 0);
     lds_barrier();
 }
 // finish: every round into the staged LDS layout (rounds after the first wait behind the
 // weight loads), then the sums of caller blocks.
 template <int Q, bool F32, int NW>
-__device__ __forceinline__ void stage_finish(XRegs<NW, F32> &xr, const GemvJob &job, int nb, uint8_t *s_x) {
+__device__ __forceinline__ void stage_finish(XRegs<NW, F32, Q> &xr, const GemvJob &job, int nb, uint8_t *s_x) {
     using T = QTraits<Q>;
-    constexpr int RD = XRegs<NW, F32>::ROUND;
+    constexpr int RD = XRegs<NW, F32, Q>::ROUND;
     const int n4 = nb * T::XE / 4;         // f32 input: float4 count
     const int ndw = nb * (T::K ? 73 : 9);  // caller blocks: dword count
     const int nrounds = F32 ? (n4 + RD / 4 - 1) / (RD / 4) : (ndw + RD - 1) / RD;
     for (int rr = 0; rr < nrounds; ++rr) {
         if (rr > 0) {
-            if constexpr (F32) xload_f32<NW>(xr, job.xf, n4, rr);
-            else xload_raw<NW>(xr, static_cast<const uint32_t *>(job.xq), ndw, rr);
+            if constexpr (F32) xload_f32<NW, Q>(xr, job.xf, n4, rr);
+            else xload_raw<NW, Q>(xr, static_cast<const uint32_t *>(job.xq), ndw, rr);
         }
         if constexpr (F32) xstage_f32<Q, NW>(xr, nb, rr, s_x);
         else xstage_raw<Q, NW>(xr, ndw, rr, s_x);
@@ -553,7 +554,7 @@ gemv_q8_group_kernel(GemvGroup grp) {
 
     // 1. first round of the activation into registers (see stage_begin)
     const int nb = w.nb;
-    XRegs<NW, F32> xr;
+    XRegs<NW, F32, Q> xr;
     stage_begin<Q, F32, NW>(xr, job, nb);
 
     // 2. the first pair of weight batches. Loads are issued unconditionally -- a load that
@@ -613,7 +614,6 @@ gemv_q8_group_kernel(GemvGroup grp) {
 // them and keeps the results in registers until one store pass at the end. Without a loop
 // the compiler keeps every load where it is written and every wait exact.
 template <int Q> constexpr int kFastU = Q == JK_Q4_0 || Q == JK_Q8_0 ? 8 : Q == JK_TQ2_0 ? 2 : 1;
-template <int Q> constexpr bool kFastPair = Q != JK_Q8_0;  // QPW = 2 fits the register budget
 
 template <int Q, int LPR, bool F32, int NW, int QPW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<Q>))) void
@@ -636,7 +636,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     // 1. activation round 0, then every weight load of the wave. A unit past the end
     //    re-reads a valid unit's lines at distinct addresses (xor 16): the loads stay
     //    unconditional, add no traffic and are never merged with the real ones.
-    XRegs<NW, F32> xr;
+    XRegs<NW, F32, Q> xr;
     stage_begin<Q, F32, NW>(xr, job, nb);
     WReg<Q> W[QPW][UF];
     const int ufb = base < units ? base : g0;  // a valid unit of the workgroup
@@ -791,21 +791,20 @@ static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds, int up
     return check_launch("gemv_q8_fast_kernel");
 }
 
-// Fast-kernel launch: about one workgroup per CU, each with upg = ceil(units / CUs) units,
-// in the smallest workgroup shape (waves x units per wave) that covers upg; bigger
-// launches use the largest shape and more than one workgroup per CU.
+// Fast-kernel launch. Measured on MI355X: 8-wave workgroups with one unit per wave (about
+// 3.5 workgroups per CU for the gate + up launch) beat one 16-wave workgroup per CU and
+// two units per wave -- workgroups that start and stage their activation at different
+// times keep the memory pipeline fuller. Launches with at most 4 units per CU use 4-wave
+// workgroups, one per CU.
 template <int Q, int LPR, bool F32>
 static jk_status launch_fast(hipStream_t s, GemvGroup &g, size_t lds) {
-    constexpr int RPU = 64 / LPR, FW = kFullWaves<Q>;
+    constexpr int RPU = 64 / LPR;
     long units = 0;
     for (int i = 0; i < g.njobs; ++i) units += (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
     const long ncu = cu_count();
     const int upg = (int)std::max<long>(1, (units + ncu - 1) / ncu);
     if (upg <= 4) return launch_fast_run<Q, LPR, F32, 4, 1>(s, g, lds, upg);
-    if (upg <= 8) return launch_fast_run<Q, LPR, F32, 8, 1>(s, g, lds, upg);
-    if (FW == 16 && upg <= 16) return launch_fast_run<Q, LPR, F32, FW, 1>(s, g, lds, upg);
-    if constexpr (kFastPair<Q>) return launch_fast_run<Q, LPR, F32, FW, 2>(s, g, lds, std::min(upg, 2 * FW));
-    return launch_fast_run<Q, LPR, F32, FW, 1>(s, g, lds, std::min(upg, FW));
+    return launch_fast_run<Q, LPR, F32, 8, 1>(s, g, lds, 8);
 }
 
 template <int Q>
