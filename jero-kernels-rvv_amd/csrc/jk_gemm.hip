@@ -1,16 +1,20 @@
 // jk_gemm.hip -- prefill GEMM on int8 MFMA for the repacked (block-scaled i8) model.
 //
-// out[m][n] = sum over scale groups g, in order, starting from 0.0:
+// out[m][n] = sum over scale groups g, in K order, starting from 0.0:
 //     acc += f32(sum_k xq[m][k] * wq[n][k]) * (xs[m][b32(g)] * ws[n][g])  [- xsum * wm]
 // (execute_gemm_repacked_rows, repack.rs:2718-3042, accumulate_scaled_tile_scalar
-// 3045-3093). One MFMA covers exactly one scale group (32 elements with
-// v_mfma_i32_32x32x32_i8, 16 with v_mfma_i32_32x32x16_i8 for Q6_K), so the integer
-// partial of every group is exact and the f32 epilogue runs per group in K order:
-// each output keeps the reference's arithmetic and order, bit for bit.
+// 3045-3093). One MFMA covers exactly one scale group (v_mfma_i32_32x32x32_i8 for the
+// 32-element groups, v_mfma_i32_32x32x16_i8 for Q6_K's 16-element groups), so every
+// group's integer partial is exact and the f32 epilogue runs per group in K order: each
+// output keeps the reference's arithmetic and order, bit for bit.
 //
-// Tiling: a 256-lane workgroup computes a 64 (M) x 64 (N) output tile as 2 x 2 waves of
-// 32 x 32. Weight fragments are unpacked from the plane layout straight into MFMA
-// operand registers; activation scales of a K stage are staged through LDS.
+// Tiling: a workgroup of 4 waves computes a 128 (weight rows) x 64 (tokens) tile, each
+// wave 64 x 32 as two 32x32 MFMA tiles. K advances in chunks of 256 elements (8 steps of
+// 32; one super-block of the 256-element formats): while the 8 steps of a chunk are
+// evaluated from LDS, the next chunk's weights (unpacked from the plane layout to i8),
+// activations and scales are loaded into registers -- each pair of threads reads whole
+// 128-byte lines of a row -- and written to LDS after a barrier. LDS rows are padded from
+// 256 to 272 bytes so the 16-byte fragment reads of 16 lanes land on distinct banks.
 #include "jk_device.hpp"
 
 namespace jk {
@@ -18,155 +22,286 @@ namespace jk {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Scale-group geometry of the repacked layout (BlockScaledTileLayout, repack.rs:1334-1366).
+constexpr int kTN = 128;   // weight rows per workgroup
+constexpr int kTM = 64;    // tokens per workgroup
+constexpr int kKC = 256;   // K elements per chunk
+constexpr int kRowB = 272; // padded LDS bytes per 256-byte row
+
 template <int Q> struct GemmFmt {
     static constexpr int GK = Q == JK_Q6_K ? 16 : 32;  // elements per scale group
     static constexpr bool MINS = Q == JK_Q4_K;
+    static constexpr int NG = 128 / GK;                 // scale groups per half chunk
 };
 
-// B operand of one lane for group g and k-half h: 16 (GK 32) or 8 (GK 16) weights of row n as
-// i8, plus the group's weight scale ws and min wm (repack_block_scaled_range_into_i8,
-// repack.rs:1724-2103, per format).
+struct GemmChunk {
+    uint8_t a[kTN * kRowB];  // weights, i8, [row][k]
+    uint8_t b[kTM * kRowB];  // activations, i8, [token][k]
+    float ws[16][kTN];       // weight scale per scale group of the chunk
+    float wm[8][kTN];        // weight min per 32-group (Q4_K)
+    float xs[8][kTM];        // activation scale per 32-block
+    float xm[8][kTM];        // activation sum per 32-block (Q4_K)
+};
+
+// Half h (elements 128h .. 128h+127) of chunk kc of weight row n as 128 i8 values (q[i]:
+// elements 128h + 16i ..), with repack_block_scaled_range_into_i8's values
+// (repack.rs:1724-2103), and the weight scale / min of each of its scale groups. Blocks
+// past the row end (a partial last chunk) are read clamped and never used.
 template <int Q>
-__device__ __forceinline__ void load_b(const WeightDev &w, int n, int g, int h, v4i &bq, long &bq8, float &ws,
-                                       float &wm) {
-    if constexpr (Q == JK_Q8_0) {
-        const uint4 v = ld_chunk(w, h, n, g);
-        bq = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        ws = ld_dscale(w, n, g);
-    } else if constexpr (Q == JK_Q4_0) {
-        const uint4 v = ld_chunk(w, 0, n, g);
-        const int sh = 4 * h;
-        bq = v4i{bytes_sub((v.x >> sh) & 0x0F0F0F0Fu, 0x08080808u), bytes_sub((v.y >> sh) & 0x0F0F0F0Fu, 0x08080808u),
-                 bytes_sub((v.z >> sh) & 0x0F0F0F0Fu, 0x08080808u), bytes_sub((v.w >> sh) & 0x0F0F0F0Fu, 0x08080808u)};
-        ws = ld_dscale(w, n, g);
-    } else if constexpr (Q == JK_Q4_K) {
-        const int b = g >> 3, s = g & 7, c = s >> 1;
-        const uint4 hd = ld_chunk(w, 0, n, b);
-        const uint4 v = ld_chunk(w, 1 + 2 * c + h, n, b);
-        const int sh = 4 * (s & 1);
-        bq = v4i{(int)((v.x >> sh) & 0x0F0F0F0Fu), (int)((v.y >> sh) & 0x0F0F0F0Fu), (int)((v.z >> sh) & 0x0F0F0F0Fu),
-                 (int)((v.w >> sh) & 0x0F0F0F0Fu)};
-        const float d = f16_finite(hd.x & 0xFFFFu), dmin = f16_finite(hd.x >> 16);
-        // unpack_k4_scales_mins (repack.rs:1158-1170) for sub-block s
-        const uint32_t sc_lo = hd.y & 0x3F3F3F3Fu, m_lo = hd.z & 0x3F3F3F3Fu;
-        const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
-        const uint32_t m_hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-        const uint32_t scv = s < 4 ? sc_lo : sc_hi, mv = s < 4 ? m_lo : m_hi;
-        ws = d * (float)((scv >> (8 * (s & 3))) & 255u);
-        wm = dmin * (float)((mv >> (8 * (s & 3))) & 255u);
-    } else if constexpr (Q == JK_Q6_K) {
-        const int b = g >> 4, j = g & 15;
-        const int h6 = j >> 3, quarter = (j & 7) >> 1, is = j & 1;
-        const int l0 = 16 * is + 8 * h;  // first of this lane's 8 elements inside the 32-run
-        const int lbyte = 64 * h6 + l0 + ((quarter & 1) ? 32 : 0), qbyte = 32 * h6 + l0;
-        const uint4 lv = ld_chunk(w, lbyte >> 4, n, b), qv = ld_chunk(w, 8 + (qbyte >> 4), n, b);
-        const int li = (lbyte & 15) >> 2, qi = (qbyte & 15) >> 2;
-        uint32_t L[2] = {li == 0 ? lv.x : li == 2 ? lv.z : lv.x, li == 0 ? lv.y : li == 2 ? lv.w : lv.y};
-        uint32_t H[2] = {qi == 0 ? qv.x : qi == 2 ? qv.z : qv.x, qi == 0 ? qv.y : qi == 2 ? qv.w : qv.y};
-        const int lsh = quarter < 2 ? 0 : 4, hsh = 2 * quarter;
-        int q2[2];
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t v6 = ((L[i] >> lsh) & 0x0F0F0F0Fu) | (((H[i] >> hsh) & 0x03030303u) << 4);
-            q2[i] = bytes_sub(v6, 0x20202020u);
+__device__ __forceinline__ void chunk_w(const WeightDev &w, int n, int kc, int h, uint4 (&q)[8], float (&ws)[8],
+                                        float (&wm)[4]) {
+    const int nb = w.nb;
+    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b = min(8 * kc + 4 * h + i, nb - 1);
+            ws[i] = ld_dscale(w, n, b);
+            if constexpr (Q == JK_Q8_0) {
+                q[2 * i] = ld_chunk(w, 0, n, b);
+                q[2 * i + 1] = ld_chunk(w, 1, n, b);
+            } else {
+                const uint4 v = ld_chunk(w, 0, n, b);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int sh = 4 * hh;
+                    q[2 * i + hh] = make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x0F0F0F0Fu, 0x08080808u),
+                                               (uint32_t)bytes_sub((v.y >> sh) & 0x0F0F0F0Fu, 0x08080808u),
+                                               (uint32_t)bytes_sub((v.z >> sh) & 0x0F0F0F0Fu, 0x08080808u),
+                                               (uint32_t)bytes_sub((v.w >> sh) & 0x0F0F0F0Fu, 0x08080808u));
+                }
+            }
         }
-        bq8 = (long)(((unsigned long)(uint32_t)q2[1] << 32) | (uint32_t)q2[0]);
-        const uint4 scv = ld_chunk(w, 12, n, b);
-        const uint32_t sd = j < 4 ? scv.x : j < 8 ? scv.y : j < 12 ? scv.z : scv.w;
-        ws = ld_dscale(w, n, b) * (float)(int8_t)(sd >> (8 * (j & 3)));
+    } else if constexpr (Q == JK_Q4_K) {
+        // unpack_k4_scales_mins (repack.rs:1158-1170); qs chunk pair (2c, 2c+1) holds
+        // elements 64c .. 64c+63 (low nibbles first)
+        const uint4 hd = ld_chunk(w, 0, n, kc);
+        const float d = f16_finite(hd.x & 0xFFFFu), dmin = f16_finite(hd.x >> 16);
+        const uint32_t sc = h == 0 ? (hd.y & 0x3F3F3F3Fu) : ((hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u));
+        const uint32_t mv = h == 0 ? (hd.z & 0x3F3F3F3Fu) : (((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            ws[t] = d * (float)((sc >> (8 * t)) & 255u);
+            wm[t] = dmin * (float)((mv >> (8 * t)) & 255u);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint4 v0 = ld_chunk(w, 1 + 2 * (2 * h + c), n, kc), v1 = ld_chunk(w, 2 + 2 * (2 * h + c), n, kc);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int sh = 4 * hh;
+                q[4 * c + 2 * hh] = make_uint4((v0.x >> sh) & 0x0F0F0F0Fu, (v0.y >> sh) & 0x0F0F0F0Fu,
+                                               (v0.z >> sh) & 0x0F0F0F0Fu, (v0.w >> sh) & 0x0F0F0F0Fu);
+                q[4 * c + 2 * hh + 1] = make_uint4((v1.x >> sh) & 0x0F0F0F0Fu, (v1.y >> sh) & 0x0F0F0F0Fu,
+                                                   (v1.z >> sh) & 0x0F0F0F0Fu, (v1.w >> sh) & 0x0F0F0F0Fu);
+            }
+        }
+    } else if constexpr (Q == JK_Q6_K) {
+        // dequantize_q6_k_block's element order (quant.rs:594-648): half h6 = h; 16-group
+        // j = 8h + 2*quarter + is covers ql bytes 64h + 16is + 32(quarter&1) and qh bytes
+        // 32h + 16is, low/high nibble and 2-bit field by quarter
+        const uint4 scv = ld_chunk(w, 12, n, kc);
+        const float d = ld_dscale(w, n, kc);
+        uint4 ql[4], qh[2];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ql[c] = ld_chunk(w, 4 * h + c, n, kc);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) qh[c] = ld_chunk(w, 8 + 2 * h + c, n, kc);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int quarter = g >> 1, is = g & 1, j = 8 * h + g;
+            ws[g] = d * (float)(int8_t)(comp(scv, j >> 2) >> (8 * (j & 3)));
+            const uint4 lv = ql[is + 2 * (quarter & 1)], hv = qh[is];
+            const int lsh = quarter < 2 ? 0 : 4, hsh = 2 * quarter;
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t v6 = ((comp(lv, i) >> lsh) & 0x0F0F0F0Fu) | (((comp(hv, i) >> hsh) & 0x03030303u) << 4);
+                o[i] = (uint32_t)bytes_sub(v6, 0x20202020u);
+            }
+            q[g] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
     } else if constexpr (Q == JK_TQ2_0) {
-        const int b = g >> 3, s = g & 7, k = 2 * s + h;
-        const uint4 v = ld_chunk(w, k >> 2, n, b);
-        const uint32_t wv = (k & 3) == 0 ? v.x : (k & 3) == 1 ? v.y : (k & 3) == 2 ? v.z : v.w;
-        bq = v4i{bytes_sub(wv & 0x03030303u, 0x01010101u), bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
-                 bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u), bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u)};
-        ws = ld_dscale(w, n, b);
-    } else if constexpr (Q == JK_I2_S) {
-        const int b = g >> 2, s = g & 3, sh = 6 - 2 * s;
-        const uint4 v = ld_chunk(w, h, n, b);
-        bq = v4i{bytes_sub((v.x >> sh) & 0x03030303u, 0x01010101u), bytes_sub((v.y >> sh) & 0x03030303u, 0x01010101u),
-                 bytes_sub((v.z >> sh) & 0x03030303u, 0x01010101u), bytes_sub((v.w >> sh) & 0x03030303u, 0x01010101u)};
-        ws = w.tensor_scale;
+        const float d = ld_dscale(w, n, kc);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ws[t] = d;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint4 v = ld_chunk(w, 2 * h + c, n, kc);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t wv = comp(v, k);
+                q[4 * c + k] = make_uint4((uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
+                                          (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
+                                          (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
+                                          (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u));
+            }
+        }
+    } else {  // JK_I2_S: chunk = blocks 2kc, 2kc+1; half h = block 2kc+h, group t = 2-bit field
+        const int b = min(2 * kc + h, nb - 1);
+        const uint4 v0 = ld_chunk(w, 0, n, b), v1 = ld_chunk(w, 1, n, b);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            ws[t] = w.tensor_scale;
+            const int sh = 6 - 2 * t;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint4 v = c ? v1 : v0;
+                q[2 * t + c] = make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x03030303u, 0x01010101u),
+                                          (uint32_t)bytes_sub((v.y >> sh) & 0x03030303u, 0x01010101u),
+                                          (uint32_t)bytes_sub((v.z >> sh) & 0x03030303u, 0x01010101u),
+                                          (uint32_t)bytes_sub((v.w >> sh) & 0x03030303u, 0x01010101u));
+            }
+        }
     }
 }
 
-constexpr int kStageGroups = 8;  // scale groups per LDS stage of activation scales
+// Registers of one chunk's staging. Thread t stages weight row t / 2, half t % 2, and
+// activation token t / 4, quarter t % 4 (k 64 * (t % 4) ..), with that token's scales
+// (and sums) of steps 2 * (t % 4) and 2 * (t % 4) + 1.
+struct ChunkRegs {
+    uint4 wq[8];
+    float ws[8], wm[4];
+    uint4 xq[4];
+    float xs[2], xm[2];
+};
+
+template <int Q>
+__device__ __forceinline__ void chunk_load(ChunkRegs &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1,
+                                           int m0, int M, int kc) {
+    const int t = threadIdx.x;
+    const int n = min(n0 + (t >> 1), r1 - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.wm[i] = 0.0f;
+    chunk_w<Q>(w, n, kc, t & 1, r.wq, r.ws, r.wm);
+    const int m = min(m0 + (t >> 2), M - 1), qq = t & 3;
+    const int8_t *row = a.qs + (size_t)m * a.k_padded;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int k = kKC * kc + 64 * qq + 16 * i;
+        if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
+        r.xq[i] = *reinterpret_cast<const uint4 *>(row + k);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int b = min(8 * kc + 2 * qq + i, (int)a.k_blocks32 - 1);
+        r.xs[i] = a.scales[(size_t)m * a.k_blocks32 + b];
+        r.xm[i] = GemmFmt<Q>::MINS ? a.sums[(size_t)m * a.k_blocks32 + b] : 0.0f;
+    }
+}
+
+template <int Q>
+__device__ __forceinline__ void chunk_store(const ChunkRegs &r, GemmChunk &c) {
+    using F = GemmFmt<Q>;
+    const int t = threadIdx.x, row = t >> 1, h = t & 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(c.a + row * kRowB + 128 * h + 16 * i) = r.wq[i];
+#pragma unroll
+    for (int g = 0; g < F::NG; ++g) c.ws[F::NG * h + g][row] = r.ws[g];
+    if constexpr (F::MINS)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) c.wm[4 * h + g][row] = r.wm[g];
+    const int tok = t >> 2, qq = t & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4 *>(c.b + tok * kRowB + 64 * qq + 16 * i) = r.xq[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        c.xs[2 * qq + i][tok] = r.xs[i];
+        if constexpr (F::MINS) c.xm[2 * qq + i][tok] = r.xm[i];
+    }
+}
 
 template <int Q>
 __global__ __launch_bounds__(256) void gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
                                                             int r0, int r1) {
     using F = GemmFmt<Q>;
-    __shared__ float s_xs[kStageGroups][64];
-    __shared__ float s_xm[F::MINS ? kStageGroups : 1][64];
+    __shared__ __align__(16) GemmChunk cs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm_i = wave & 1, wn_i = wave >> 1;
-    const int m_base = blockIdx.y * 64, n_base = r0 + blockIdx.x * 64;
+    const int wn = wave & 1, wmi = wave >> 1;  // wave tile: rows 64 * wn .., tokens 32 * wmi ..
+    const int n0 = r0 + blockIdx.x * kTN, m0 = blockIdx.y * kTM;
     const int M = (int)a.m;
-    const int h = lane >> 5;
-    // operand rows of this lane (clamped for loads; masked on store)
-    const int am = min(m_base + 32 * wm_i + (lane & 31), M - 1);
-    const int bn = min(n_base + 32 * wn_i + (lane & 31), r1 - 1);
-    const int ngroups = (w.cols + F::GK - 1) / F::GK;
-    float acc[16];
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-    const int8_t *arow = a.qs + (size_t)am * a.k_padded;
-    for (int g0 = 0; g0 < ngroups; g0 += kStageGroups) {
-        __syncthreads();
-        // stage xs (and x sums) for 64 rows x kStageGroups groups; element (g, row) at [g][row]
-        for (int idx = threadIdx.x; idx < kStageGroups * 64; idx += 256) {
-            const int gg = idx >> 6, row = idx & 63;
-            const int g = g0 + gg;
-            const int mrow = min(m_base + row, M - 1);
-            float xs = 0.0f, xm = 0.0f;
-            if (g < ngroups) {
-                const int b32 = F::GK == 32 ? g : g >> 1;
-                xs = a.scales[(size_t)mrow * a.k_blocks32 + b32];
-                if constexpr (F::MINS) xm = a.sums[(size_t)mrow * a.k_blocks32 + b32];
+    const int steps = w.cols / 32;
+    const int nchunks = (steps + 7) / 8;
+    const int hl = lane >> 5, jl = lane & 31;
+    const int tok = 32 * wmi + jl;
+
+    float acc[2][16];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
+
+    ChunkRegs rg;
+    chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
+    chunk_store<Q>(rg, cs);
+    __syncthreads();
+    for (int kc = 0; kc < nchunks; ++kc) {
+        const bool more = kc + 1 < nchunks;
+        if (more) chunk_load<Q>(rg, w, a, n0, r1, m0, M, kc + 1);
+        const int nst = min(8, steps - 8 * kc);
+        for (int st = 0; st < nst; ++st) {
+            const float xs = cs.xs[st][tok];
+            const float xsum = F::MINS ? cs.xm[st][tok] : 0.0f;
+#pragma unroll
+            for (int gg = 0; gg < 32 / F::GK; ++gg) {
+                v16i c[2];
+                if constexpr (F::GK == 32) {
+                    const v4i bq = *reinterpret_cast<const v4i *>(cs.b + tok * kRowB + 32 * st + 16 * hl);
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        const v4i aq =
+                            *reinterpret_cast<const v4i *>(cs.a + (64 * wn + 32 * nt + jl) * kRowB + 32 * st + 16 * hl);
+                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+                    }
+                } else {
+                    const long bq = *reinterpret_cast<const long *>(cs.b + tok * kRowB + 32 * st + 16 * gg + 8 * hl);
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        const long aq = *reinterpret_cast<const long *>(cs.a + (64 * wn + 32 * nt + jl) * kRowB +
+                                                                        32 * st + 16 * gg + 8 * hl);
+                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, bq, v16i{0}, 0, 0, 0);
+                    }
+                }
+                // C layout: lane holds token column jl, weight rows 8 * (v / 4) + 4 * hl + v % 4
+                const int g = (32 / F::GK) * st + gg;
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int rl = 64 * wn + 32 * nt + 8 * q + 4 * hl;
+                        const float4 ws4 = *reinterpret_cast<const float4 *>(&cs.ws[g][rl]);
+                        float4 wm4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                        if constexpr (F::MINS) wm4 = *reinterpret_cast<const float4 *>(&cs.wm[st][rl]);
+                        const float wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, wmv[4] = {wm4.x, wm4.y, wm4.z, wm4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float t = (float)c[nt][4 * q + e] * (xs * wsv[e]);
+                            if constexpr (F::MINS) acc[nt][4 * q + e] += t - xsum * wmv[e];
+                            else acc[nt][4 * q + e] += t;
+                        }
+                    }
             }
-            s_xs[gg][row] = xs;
-            if constexpr (F::MINS) s_xm[gg][row] = xm;
         }
-        __syncthreads();
-        const int gend = min(kStageGroups, ngroups - g0);
-        for (int gg = 0; gg < gend; ++gg) {
-            const int g = g0 + gg;
-            v16i c;
-            float ws = 0.0f, wmn = 0.0f;
-            if constexpr (F::GK == 32) {
-                const uint4 av = *reinterpret_cast<const uint4 *>(arow + 32 * g + 16 * h);
-                const v4i aq = v4i{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
-                v4i bq;
-                long unused;
-                load_b<Q>(w, bn, g, h, bq, unused, ws, wmn);
-                c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
-            } else {
-                const long aq = *reinterpret_cast<const long *>(arow + 16 * g + 8 * h);
-                v4i unused;
-                long bq;
-                load_b<Q>(w, bn, g, h, unused, bq, ws, wmn);
-                c = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, bq, v16i{0}, 0, 0, 0);
-            }
-            // C layout: lane holds column n = lane % 32, rows 8 * (i / 4) + 4 * h + i % 4
-            for (int i = 0; i < 16; ++i) {
-                const int ml = 32 * wm_i + 8 * (i >> 2) + 4 * h + (i & 3);
-                const float t = (float)c[i] * (s_xs[gg][ml] * ws);
-                if constexpr (F::MINS) acc[i] += t - s_xm[gg][ml] * wmn;
-                else acc[i] += t;
-            }
+        if (more) {
+            __syncthreads();
+            chunk_store<Q>(rg, cs);
+            __syncthreads();
         }
     }
-    const int n = n_base + 32 * wn_i + (lane & 31);
-    if (n < r1) {
-        const size_t sub = (size_t)(r1 - r0);
-        for (int i = 0; i < 16; ++i) {
-            const int m = m_base + 32 * wm_i + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (m < M) y[(size_t)m * sub + (size_t)(n - r0)] = acc[i];
-        }
+
+    const int m = m0 + tok;
+    if (m < M) {
+        const size_t ld = (size_t)(r1 - r0);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int n = n0 + 64 * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
+                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = acc[nt][v];
+            }
     }
 }
 
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    const dim3 grid((unsigned)((r1 - r0 + 63) / 64), (unsigned)((a.m + 63) / 64)), block(256);
+    const dim3 grid((unsigned)((r1 - r0 + kTN - 1) / kTN), (unsigned)((a.m + kTM - 1) / kTM)), block(256);
     switch (w.quant) {
     case JK_Q8_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q8_0>, grid, block, 0, s, w, a, y, r0, r1); break;
     case JK_Q4_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q4_0>, grid, block, 0, s, w, a, y, r0, r1); break;
