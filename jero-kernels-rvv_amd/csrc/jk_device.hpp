@@ -10,10 +10,11 @@ namespace jk {
 
 // f16_to_f32_finite (lib.rs:676-717): exact decode, NaN/Inf -> +0.0, signed zero kept.
 __device__ __forceinline__ float f16_finite(uint32_t h) {
+    // straight-line selects: no branch that would wait on the load feeding h
     const uint32_t e = (h >> 10) & 31u, m = h & 1023u, s = (h & 0x8000u) << 16;
-    if (e == 31u) return 0.0f;
-    if (e == 0u) return __uint_as_float(s | __float_as_uint((float)m * 0x1p-24f));
-    return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+    const float sub = __uint_as_float(s | __float_as_uint((float)m * 0x1p-24f));
+    const float nrm = __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+    return e == 31u ? 0.0f : (e == 0u ? sub : nrm);
 }
 
 // Signed 4 x i8 dot product accumulated into c (v_dot4_i32_i8).
