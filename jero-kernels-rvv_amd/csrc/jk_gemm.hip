@@ -8,22 +8,26 @@
 // group's integer partial is exact and the f32 epilogue runs per group in K order: each
 // output keeps the reference's arithmetic and order, bit for bit.
 //
-// Tiling: a workgroup of 4 waves computes a 128 (weight rows) x 64 (tokens) tile, each
+// Tiling: a workgroup of 8 waves computes a 128 (weight rows) x 128 (tokens) tile, each
 // wave 64 x 32 as two 32x32 MFMA tiles. K advances in chunks of 256 elements (8 steps of
-// 32; one super-block of the 256-element formats): while the 8 steps of a chunk are
-// evaluated from LDS, the next chunk's weights (unpacked from the plane layout to i8),
-// activations and scales are loaded into registers -- each pair of threads reads whole
-// 128-byte lines of a row -- and written to LDS after a barrier. LDS rows are padded from
-// 256 to 272 bytes so the 16-byte fragment reads of 16 lanes land on distinct banks.
+// 32; one super-block of the 256-element formats). While the 8 steps of a chunk are
+// evaluated from LDS, the next chunk is loaded into registers -- waves 0-3 load the weight
+// tile, waves 4-7 the activation tile, each with line-wide coalesced reads -- and after a
+// barrier it is unpacked to i8 and written to LDS. LDS rows are padded from 256 to 272
+// bytes so the 16-byte fragment reads of 16 lanes land on distinct banks.
+#include <utility>
+
 #include "jk_device.hpp"
 
 namespace jk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kTN = 128;   // weight rows per workgroup
-constexpr int kTM = 64;    // tokens per workgroup
+constexpr int kTM = 128;   // tokens per workgroup
+constexpr int kThreads = 512;
 constexpr int kKC = 256;   // K elements per chunk
 constexpr int kRowB = 272; // padded LDS bytes per 256-byte row
 
@@ -42,6 +46,16 @@ struct GemmChunk {
     float xm[8][kTM];        // activation sum per 32-block (Q4_K)
 };
 
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): register arrays
+// indexed by it get constant indices from the start, not only after loop unrolling.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F> __device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // One 16-byte global load without the streaming hint: a weight tile is read once per
 // token tile, so its lines are meant to stay in L2 for the neighbouring workgroups.
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -59,22 +73,23 @@ __device__ __forceinline__ const uint8_t *plane_ptr(const WeightDev &w, int c, i
 //   32 (i % 4) + t / 8 of plane i / 4. Scales: row t / 2, blocks 8kc + 4 (t % 2) ..
 //  K-quants, TQ2_0, I2_S: 16 or 32 bytes per (plane, row) and chunk; thread t takes row
 //   t / 2 and the half t % 2 of the chunk's elements (128h .. 128h+127).
-template <int Q> struct RawW {
-    static constexpr int NV = Q == JK_Q8_0 ? 8 : Q == JK_Q4_0 ? 4 : Q == JK_Q4_K ? 5 : Q == JK_Q6_K ? 7 : 2;
-    static constexpr int ND = Q == JK_Q8_0 || Q == JK_Q4_0 ? 4 : 1;
-    uint4 v[NV];
-    uint32_t d[ND];
+//  Activations (waves 4-7, t = thread - 256): load i covers token 16i + t / 16, piece
+//   t % 16 of its 256-byte row; scales (and sums) of token t / 2, steps 4 (t % 2) ...
+// Both roles use the same registers: v / d hold whichever tile the wave stages.
+struct Stage {
+    uint4 v[8];
+    uint32_t d[8];
 };
 
 // Blocks past the row end (a partial last chunk) are read clamped and never used; rows
 // past r1 are read clamped to r1 - 1 and never stored.
 template <int Q>
-__device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, RawW<Q> &r) {
+__device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage &r) {
     const int nb = w.nb, t = threadIdx.x;
     if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
         const int b = min(8 * kc + (t & 7), nb - 1);
 #pragma unroll
-        for (int i = 0; i < RawW<Q>::NV; ++i) {
+        for (int i = 0; i < (Q == JK_Q8_0 ? 8 : 4); ++i) {
             const int n = min(n0 + 32 * (i & 3) + (t >> 3), r1 - 1);
             r.v[i] = ldg16(plane_ptr(w, i >> 2, n, b));
         }
@@ -114,7 +129,7 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
 // with repack_block_scaled_range_into_i8's values (repack.rs:1724-2103), and the weight
 // scale / min of each of its scale groups.
 template <int Q>
-__device__ __forceinline__ void chunk_w_unpack(const WeightDev &w, const RawW<Q> &r, int h, uint4 (&q)[8],
+__device__ __forceinline__ void chunk_w_unpack(const WeightDev &w, const Stage &r, int h, uint4 (&q)[8],
                                                float (&ws)[8], float (&wm)[4]) {
     if constexpr (Q == JK_Q4_K) {
         // unpack_k4_scales_mins (repack.rs:1158-1170); qs chunk pair (2c, 2c+1) holds
@@ -193,51 +208,64 @@ __device__ __forceinline__ void chunk_w_unpack(const WeightDev &w, const RawW<Q>
     }
 }
 
-// Registers of one chunk's staging. Thread t stages weight row t / 2, half t % 2, and
-// activation token t / 4, quarter t % 4 (k 64 * (t % 4) ..), with that token's scales
-// (and sums) of steps 2 * (t % 4) and 2 * (t % 4) + 1.
-template <int Q> struct ChunkRegs {
-    RawW<Q> w;
-    uint4 xq[4];
-    float xs[2], xm[2];
-};
-
-// Activations: 64 tokens x 256 bytes, 16 consecutive lanes per token row (load i: token
-// 16i + t / 16, piece t % 16); scales (and sums) of token t / 4, steps 2 (t % 4) + {0, 1}.
 template <int Q>
-__device__ __forceinline__ void chunk_load(ChunkRegs<Q> &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1,
-                                           int m0, int M, int kc) {
-    const int t = threadIdx.x;
-    chunk_w_load<Q>(w, n0, r1, kc, r.w);
-    int k = kKC * kc + 16 * (t & 15);
-    if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = min(m0 + 16 * i + (t >> 4), M - 1);
-        r.xq[i] = ldg16(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + k);
-    }
-    const int m = min(m0 + (t >> 2), M - 1), qq = t & 3;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int b = min(8 * kc + 2 * qq + i, (int)a.k_blocks32 - 1);
-        r.xs[i] = a.scales[(size_t)m * a.k_blocks32 + b];
-        r.xm[i] = GemmFmt<Q>::MINS ? a.sums[(size_t)m * a.k_blocks32 + b] : 0.0f;
-    }
+__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage &r);
+
+// Global loads of chunk kc into the staging registers of this thread's role.
+template <int Q>
+__device__ __forceinline__ void chunk_load(Stage &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1, int m0,
+                                           int M, int kc) {
+    // two one-sided branches rather than if / else: the roles' final register writes must
+    // not be merged into one store with a selected address (which forces a stack copy)
+    if (threadIdx.x < 256) chunk_w_load<Q>(w, n0, r1, kc, r);
+    if (threadIdx.x >= 256) chunk_x_load<Q>(a, m0, M, kc, r);
 }
 
+// Activation role: thread t = threadIdx.x - 256 of waves 4-7.
 template <int Q>
-__device__ __forceinline__ void chunk_store(const WeightDev &w, const ChunkRegs<Q> &r, GemmChunk &c) {
+__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage &r) {
+    const int t = threadIdx.x - 256;
+    int k = kKC * kc + 16 * (t & 15);
+    if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
+    static_for<8>([&](auto i) {
+        const int m = min(m0 + 16 * i + (t >> 4), M - 1);
+        r.v[i] = ldg16(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + k);
+    });
+    const int m = min(m0 + (t >> 1), M - 1);
+    static_for<4>([&](auto j) {
+        const int b = min(8 * kc + 4 * (t & 1) + j, (int)a.k_blocks32 - 1);
+        r.d[j] = __float_as_uint(a.scales[(size_t)m * a.k_blocks32 + b]);
+        r.d[4 + j] = GemmFmt<Q>::MINS ? __float_as_uint(a.sums[(size_t)m * a.k_blocks32 + b]) : 0u;
+    });
+}
+
+// Unpack the staging registers and write them to the chunk's LDS tiles.
+template <int Q>
+__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, GemmChunk &c) {
     using F = GemmFmt<Q>;
+    if (threadIdx.x >= 256) {
+        const int t = threadIdx.x - 256;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<uint4 *>(c.b + (16 * i + (t >> 4)) * kRowB + 16 * (t & 15)) = r.v[i];
+        const int tok = t >> 1, g0 = 4 * (t & 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c.xs[g0 + j][tok] = __uint_as_float(r.d[j]);
+            if constexpr (F::MINS) c.xm[g0 + j][tok] = __uint_as_float(r.d[4 + j]);
+        }
+        return;
+    }
     const int t = threadIdx.x;
     if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
         const int piece = t & 7;
 #pragma unroll
-        for (int i = 0; i < RawW<Q>::NV; ++i) {
+        for (int i = 0; i < (Q == JK_Q8_0 ? 8 : 4); ++i) {
             uint8_t *dst = c.a + (32 * (i & 3) + (t >> 3)) * kRowB + 32 * piece;
             if constexpr (Q == JK_Q8_0) {
-                *reinterpret_cast<uint4 *>(dst + 16 * (i >> 2)) = r.w.v[i];
+                *reinterpret_cast<uint4 *>(dst + 16 * (i >> 2)) = r.v[i];
             } else {
-                const uint4 v = r.w.v[i];
+                const uint4 v = r.v[i];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const int sh = 4 * hh;
@@ -251,12 +279,12 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const ChunkRegs<
         }
         const int row = t >> 1, h = t & 1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) c.ws[4 * h + j][row] = f16_finite(r.w.d[j]);
+        for (int j = 0; j < 4; ++j) c.ws[4 * h + j][row] = f16_finite(r.d[j]);
     } else {
         const int row = t >> 1, h = t & 1;
         uint4 q[8];
         float ws[8], wm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        chunk_w_unpack<Q>(w, r.w, h, q, ws, wm);
+        chunk_w_unpack<Q>(w, r, h, q, ws, wm);
 #pragma unroll
         for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(c.a + row * kRowB + 128 * h + 16 * i) = q[i];
 #pragma unroll
@@ -265,24 +293,23 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const ChunkRegs<
 #pragma unroll
             for (int g = 0; g < 4; ++g) c.wm[4 * h + g][row] = wm[g];
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4 *>(c.b + (16 * i + (t >> 4)) * kRowB + 16 * (t & 15)) = r.xq[i];
-    const int tok = t >> 2, qq = t & 3;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        c.xs[2 * qq + i][tok] = r.xs[i];
-        if constexpr (F::MINS) c.xm[2 * qq + i][tok] = r.xm[i];
-    }
 }
 
 template <int Q>
-__global__ __launch_bounds__(256) void gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
+__global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
                                                             int r0, int r1) {
     using F = GemmFmt<Q>;
     __shared__ __align__(16) GemmChunk cs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave & 1, wmi = wave >> 1;  // wave tile: rows 64 * wn .., tokens 32 * wmi ..
-    const int n0 = r0 + blockIdx.x * kTN, m0 = blockIdx.y * kTM;
+    // Workgroup i runs on XCD i % 8. Tile order: the token tiles of one weight row tile go
+    // to consecutive workgroups of one XCD, so they run together and share the row tile's
+    // weights in that XCD's L2; row tiles are dealt round-robin over the XCDs.
+    const int ntn = (r1 - r0 + kTN - 1) / kTN, ntm = ((int)a.m + kTM - 1) / kTM;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;  // padding workgroups of the last round-robin group
+    const int n0 = r0 + tn * kTN, m0 = tm * kTM;
     const int M = (int)a.m;
     const int steps = w.cols / 32;
     const int nchunks = (steps + 7) / 8;
@@ -295,15 +322,14 @@ __global__ __launch_bounds__(256) void gemm_repacked_kernel(WeightDev w, jk_act_
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
 
-    ChunkRegs<Q> rg;
+    Stage rg;
     chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
     chunk_store<Q>(w, rg, cs);
     __syncthreads();
     for (int kc = 0; kc < nchunks; ++kc) {
         const bool more = kc + 1 < nchunks;
         if (more) chunk_load<Q>(rg, w, a, n0, r1, m0, M, kc + 1);
-        const int nst = min(8, steps - 8 * kc);
-        for (int st = 0; st < nst; ++st) {
+        auto step = [&](int st) {
             const float xs = cs.xs[st][tok];
             const float xsum = F::MINS ? cs.xm[st][tok] : 0.0f;
 #pragma unroll
@@ -326,26 +352,29 @@ __global__ __launch_bounds__(256) void gemm_repacked_kernel(WeightDev w, jk_act_
                         c[nt] = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, bq, v16i{0}, 0, 0, 0);
                     }
                 }
-                // C layout: lane holds token column jl, weight rows 8 * (v / 4) + 4 * hl + v % 4
+                // Scale products xs * ws (and xsum * wm) of all 64 x 32 outputs as two 32 x 32
+                // f32 outer products (K = 1, zero accumulator): each is the single rounded f32
+                // product, as a VALU multiply gives, except that -0 comes out +0 -- which the
+                // accumulation cannot observe, as an accumulator that starts at +0.0 never
+                // becomes -0. Lane l supplies the scale of row 64 wn + l (block l / 32 = nt)
+                // and of token tok. Both results share c's layout: lane holds token column
+                // jl, weight rows 8 * (v / 4) + 4 * hl + v % 4 of block nt in element 16 nt + v.
                 const int g = (32 / F::GK) * st + gg;
+                const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][64 * wn + lane], xs, v32f{0}, 0, 0, 0);
+                v32f pm;
+                if constexpr (F::MINS) pm = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.wm[st][64 * wn + lane], xsum, v32f{0}, 0, 0, 0);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int rl = 64 * wn + 32 * nt + 8 * q + 4 * hl;
-                        const float4 ws4 = *reinterpret_cast<const float4 *>(&cs.ws[g][rl]);
-                        float4 wm4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                        if constexpr (F::MINS) wm4 = *reinterpret_cast<const float4 *>(&cs.wm[st][rl]);
-                        const float wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, wmv[4] = {wm4.x, wm4.y, wm4.z, wm4.w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float t = (float)c[nt][4 * q + e] * (xs * wsv[e]);
-                            if constexpr (F::MINS) acc[nt][4 * q + e] += t - xsum * wmv[e];
-                            else acc[nt][4 * q + e] += t;
-                        }
+                    for (int v = 0; v < 16; ++v) {
+                        const float t = (float)c[nt][v] * p[16 * nt + v];
+                        if constexpr (F::MINS) acc[nt][v] += t - pm[16 * nt + v];
+                        else acc[nt][v] += t;
                     }
             }
-        }
+        };
+        const int nst = min(8, steps - 8 * kc);
+        for (int st = 0; st < nst; ++st) step(st);
         if (more) {
             __syncthreads();
             chunk_store<Q>(w, rg, cs);
@@ -367,7 +396,8 @@ __global__ __launch_bounds__(256) void gemm_repacked_kernel(WeightDev w, jk_act_
 }
 
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    const dim3 grid((unsigned)((r1 - r0 + kTN - 1) / kTN), (unsigned)((a.m + kTM - 1) / kTM)), block(256);
+    const size_t ntn = (size_t)(r1 - r0 + kTN - 1) / kTN, ntm = (a.m + kTM - 1) / kTM;
+    const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(kThreads);
     switch (w.quant) {
     case JK_Q8_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q8_0>, grid, block, 0, s, w, a, y, r0, r1); break;
     case JK_Q4_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q4_0>, grid, block, 0, s, w, a, y, r0, r1); break;

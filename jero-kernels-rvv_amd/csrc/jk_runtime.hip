@@ -495,8 +495,11 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
         return fail(JK_TENSOR_BOUNDS, "gemm_repacked: row range %zu..%zu out of bounds for %d rows", r0, r1, w->dev.rows);
     if (y_len != act->m * (r1 - r0))
         return fail(JK_TENSOR_BOUNDS, "gemm_repacked: output len %zu != %zu * %zu", y_len, act->m, r1 - r0);
-    if (r1 == r0) return JK_OK;
+    if (r1 == r0 || act->m == 0) return JK_OK;
     if (!y) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null output");
+    if (act->m > ((size_t)1 << 24))
+        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: %zu tokens exceed the 2^24 per call this device path tiles",
+                    act->m);
     return launch_gemm_repacked((hipStream_t)s, w->dev, *act, y, (int)r0, (int)r1);
 }
 
