@@ -58,6 +58,12 @@ def gemv_bytes(quant, rows, cols, jk) -> int:
     return rows * nb * jk.BLOCK_BYTES[quant] + (cols // 256) * jk.BLOCK_Q8K.itemsize + rows * 4
 
 
+def gemv_bytes_q80(quant, rows, cols, jk) -> int:
+    """Q4_0 / Q8_0 GEMV: weight bytes + BlockQ8_0 activation blocks + f32 outputs."""
+    nb = cols // jk.BLOCK_ELEMENTS[quant]
+    return rows * nb * jk.BLOCK_BYTES[quant] + (cols // 32) * jk.BLOCK_Q8_0.itemsize + rows * 4
+
+
 class Layer:
     """Device weights and buffers of one decode layer."""
 
@@ -79,6 +85,8 @@ def main() -> int:
     ap.add_argument("--gemm-m", type=int, default=512, help="token count of the reported GEMM line (0 = skip)")
     ap.add_argument("--gemm-sweep", default="64,128,2048", help="further token counts timed for the GEMM sweep")
     ap.add_argument("--no-graph", action="store_true", help="launch the step eagerly instead of a HIP graph")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the per-kernel lines of the other workloads (C1, C2, C5, vec_dot f32, quantizers)")
     ap.add_argument("--down", choices=("fused", "split"), default="split",
                     help="ffn_down activation: quantized inside the GEMV launch, or by its own launch")
     args = ap.parse_args()
@@ -292,6 +300,121 @@ def main() -> int:
         for w in gw:
             w.free()
 
+    # ------------------------------------------------------------ other kernels of the path
+    # Each line: one kernel at a configuration's shape, weights rotating over enough device
+    # copies (>= 600 MB) that every launch streams from HBM, launches captured back to back in
+    # a HIP graph and timed with HIP events on the capturing stream (per-launch time includes
+    # the graph's inter-launch gap). Bytes are algorithmic (weight bytes + activation + output).
+    secondary = {}
+    if not args.no_secondary:
+        def graph_us(launch, n, reps=5):
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for i in range(n):
+                    launch(i, side.cuda_stream)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cs = torch.cuda.current_stream().cuda_stream
+                for i in range(n):
+                    launch(i, cs)
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            del g
+            return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+        def copies(quant, rows, cols, seed):
+            data = synth.gguf_weights(quant, rows, cols, seed=seed)
+            n = max(4, int(600e6 // data.nbytes) + 1)
+            return [jk.Weight(jk.TensorView(f"w{i}", quant, (rows, cols), data), rows, cols) for i in range(n)]
+
+        def hbm_line(name, bytes_, us, note):
+            gbs = bytes_ / (us * 1e-6) / 1e9
+            secondary[name] = {"us": round(us, 3), "bytes": int(bytes_), "gbs": round(gbs, 1),
+                               "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm", "workload": note}
+            log(f"  {name:28s} {us:8.2f} us  {gbs:7.1f} GB/s  {note}")
+
+        log("other kernels of the path:")
+        # C1, C2: quant_q8 GEMV with caller Q8_0 blocks
+        for name, quant, rows, cols in (("gemv_q4_0_q8_0 C1", jk.Q4_0, 4096, 4096),
+                                        ("gemv_q8_0_q8_0 C2", jk.Q8_0, 11008, 4096)):
+            ws = copies(quant, rows, cols, 500 + quant)
+            xq = torch.empty(cols // 32 * jk.BLOCK_Q8_0.itemsize, dtype=torch.uint8, device=dev)
+            jk.dev_quantize_row_q8_0(acts["x"], cols, xq, cols // 32)
+            y = torch.empty(rows, dtype=torch.float32, device=dev)
+            us = graph_us(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 32, y, rows, st), len(ws))
+            b = gemv_bytes_q80(quant, rows, cols, jk)
+            hbm_line(name, b, us, f"{rows}x{cols}, Q8_0 activation blocks")
+            for w in ws:
+                w.free()
+        # A8: f32-activation vec_dot (dequantize x f32 dot) at the Q4_K attn shape and Q6_K down
+        for name, quant, rows, cols, xa in (("vec_dot_q4_k_m f32", jk.Q4_K, 4096, 4096, "x"),
+                                            ("vec_dot_q6_k f32", jk.Q6_K, 4096, 14336, "h")):
+            ws = copies(quant, rows, cols, 600 + quant)
+            y = torch.empty(rows, dtype=torch.float32, device=dev)
+            us = graph_us(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts[xa], cols, y, rows, st), len(ws))
+            b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + 4 * cols + 4 * rows
+            hbm_line(name, b, us, f"{rows}x{cols}, f32 activation")
+            for w in ws:
+                w.free()
+        # C5: ternary GEMV (Q8_K caller blocks) and BitLinear at batch 1 and 128
+        for quant, qname in ((jk.TQ2_0, "tq2_0"), (jk.I2_S, "i2_s")):
+            for rows, cols in ((6912, 2560), (2560, 6912)):
+                ws = copies(quant, rows, cols, 700 + rows)
+                wbytes = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant]
+                if quant == jk.TQ2_0:
+                    xq = torch.empty(cols // 256 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
+                    xin = torch.randn(cols, generator=gen).to(dev)
+                    jk.dev_quantize_row_q8_k(xin, cols, xq, cols // 256)
+                    y = torch.empty(rows, dtype=torch.float32, device=dev)
+                    us = graph_us(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 256, y, rows, st), len(ws))
+                    hbm_line(f"gemv_tq2_0_q8_k {rows}x{cols}", wbytes + cols // 256 * 292 + 4 * rows, us,
+                             "C5, Q8_K activation blocks")
+                for m in (1, 128):
+                    xin = torch.randn(m, cols, generator=gen).to(dev)
+                    aq = torch.empty(m * cols, dtype=torch.int8, device=dev)
+                    asc = torch.empty(m, dtype=torch.float32, device=dev)
+                    jk.dev_quantize_absmax_i8(xin, m, cols, aq, asc)
+                    y = torch.empty(m * rows, dtype=torch.float32, device=dev)
+                    us = graph_us(lambda i, st: jk.dev_bitlinear_i8(ws[i % len(ws)], aq, asc, m, cols, y, m * rows, st),
+                                  len(ws))
+                    b = wbytes + m * (cols + 4) + 4 * m * rows
+                    name = f"bitlinear_{qname} {rows}x{cols} M={m}"
+                    if m == 1:
+                        hbm_line(name, b, us, "C5, per-token absmax i8 activation")
+                    else:
+                        tops = 2.0 * m * rows * cols / (us * 1e-6) / 1e12
+                        secondary[name] = {"us": round(us, 3), "tops": round(tops, 2),
+                                           "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                           "gbs": round(b / (us * 1e-6) / 1e9, 1), "bound": "ridge",
+                                           "workload": "C5 at 128 tokens (AI 537-684 op/B, near the ridge)"}
+                        log(f"  {name:28s} {us:8.2f} us  {tops:7.2f} TOPS")
+                for w in ws:
+                    w.free()
+        # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
+        yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
+        us = graph_us(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
+        secondary["quantize_row_q8_k 14336"] = {"us": round(us, 3), "bound": "latency",
+                                                "workload": "ffn_down input, 56 blocks"}
+        log(f"  {'quantize_row_q8_k 14336':28s} {us:8.2f} us")
+        M, K = 512, 4096
+        xin = torch.randn(M, K, generator=gen).to(dev)
+        need = jk.act_q8_bytes(M, K)
+        store = torch.empty(need, dtype=torch.uint8, device=dev)
+        act = jk.act_q8_bind(store, need, M, K)
+        us = graph_us(lambda i, st: jk.dev_quantize_act_q8(xin, M, K, act, st), 32)
+        b = M * K * 4 + M * K + M * (K // 32) * 8
+        hbm_line("quantize_act_q8 512x4096", b, us, "QuantizedActQ8::quantize_into for the prefill GEMM")
+        del xin, store
+
     # ------------------------------------------------------------ CPU baseline (oracle)
     cpu = None
     if args.cpu_seconds > 0:
@@ -331,6 +454,7 @@ def main() -> int:
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "decode_tok_s_equiv": round(1e3 / ms_per_step * args.layers / 32, 1),
         "roofline": roofline, "per_stage": per_stage, "gemm_q8_0": gemm, "gemm_q8_0_sweep": sweep,
+        "secondary": secondary,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -149,4 +149,16 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
+// Ordered fold of one value per lane over a whole wave: lane 0 adds the g values of lanes
+// 0..g-1 in lane order to acc (acc lives in lane 0). red: 64 floats of LDS for this wave.
+__device__ __forceinline__ float fold_wave(float acc, float v, int g, float *red) {
+    const int l = threadIdx.x & 63;
+    red[l] = v;
+    wave_lds_sync();
+    if (l == 0)
+        for (int i = 0; i < g; ++i) acc += red[i];
+    wave_lds_sync();
+    return acc;
+}
+
 }  // namespace jk

@@ -14,132 +14,187 @@
 
 namespace jk {
 
-// ----------------------------------------------------------- f32-activation block values
-// Each returns dot_product_f32_scalar(dequantized block, x block) (lib.rs:770-778): one
-// product and one add per element in element order, starting from +0.0.
+// ----------------------------------------------------------- f32-activation matvec
+// vec_dot_{q4_0,q8_0,q6_k}_scalar (quant.rs:1401-1436, 899-934, 1012-1047),
+// vec_dot_q4_k_m_scalar (lib.rs:1268-1303), vec_dot_i2_s (quant.rs:2199-2240): for each
+// block, dot_product_f32_scalar(dequantized block, x block) (lib.rs:770-778) -- one product
+// and one add per element in element order from +0.0 -- and row_sum (from +0.0) adds the
+// block dots in block order.
+//
+// Mapping: lane p of a row's LPR lanes takes blocks p, p + LPR, ...; a block's element
+// chain runs in the lane, fully unrolled, on the block's bytes held in registers (16-byte
+// plane loads) and the activation staged once per workgroup in LDS (or read through the
+// caches when it does not fit); the block values are folded across lanes in block order.
+template <int Q> struct VdFmt {
+    static constexpr int E = Q == JK_Q4_0 || Q == JK_Q8_0 ? 32 : Q == JK_I2_S ? 128 : 256;  // elements
+    static constexpr int C = Q == JK_Q4_0 ? 1 : Q == JK_Q8_0 || Q == JK_I2_S ? 2 : Q == JK_Q4_K ? 9 : 13;
+    static constexpr bool D = Q == JK_Q4_0 || Q == JK_Q8_0 || Q == JK_Q6_K;  // f16 scale in the d-plane
+};
 
-__device__ float fv_block(const WeightDev &w, int r, int b, const float *__restrict__ x) {
+template <int Q> struct VdBlock {
+    uint4 c[VdFmt<Q>::C];
+    uint32_t d;
+};
+
+template <int Q>
+__device__ __forceinline__ void vd_load(VdBlock<Q> &o, const WeightDev &w, int r, int b) {
+#pragma unroll
+    for (int c = 0; c < VdFmt<Q>::C; ++c) o.c[c] = ld_chunk(w, c, r, b);
+    if constexpr (VdFmt<Q>::D) o.d = w.dplane[(size_t)r * (size_t)w.nb + (size_t)b];
+}
+
+// Byte k (0..15 within chunk c) of the block's chunks.
+template <int Q>
+__device__ __forceinline__ uint32_t vd_byte(const VdBlock<Q> &o, int c, int k) {
+    return (comp(o.c[c], k >> 2) >> (8 * (k & 3))) & 255u;
+}
+
+template <int Q>
+__device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__restrict__ xb, float i2s_scale) {
     float sum = 0.0f;
-    switch (w.quant) {
-    case JK_Q4_0: {  // dequantize_q4_0_block (quant.rs:550-568)
-        const float d = ld_dscale(w, r, b);
-        const uint4 q = ld_chunk(w, 0, r, b);
-        const float *xb = x + 32 * (size_t)b;
+    if constexpr (Q == JK_Q4_0 || Q == JK_Q8_0) {
+        // dequantize_q4_0_block / dequantize_q8_0_block (quant.rs:550-588). The reference
+        // writes +0.0 for d == 0 where d * q gives +-0: no sum observes the difference, since
+        // a sum that starts at +0.0 never becomes -0 under round-to-nearest addition (the
+        // products are finite, so NaN cases are unchanged as well).
+        const float d = f16_finite(o.d);
+#pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const int nib = (int)((comp(q, (i & 15) >> 2) >> (8 * (i & 3) + (i >> 4) * 4)) & 15u);
-            const float wv = d == 0.0f ? 0.0f : d * (float)(nib - 8);
+            int qv;
+            if constexpr (Q == JK_Q4_0) qv = (int)((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) - 8;
+            else qv = (int)(int8_t)vd_byte<Q>(o, i >> 4, i & 15);
+            const float wv = d * (float)qv;
             sum += wv * xb[i];
         }
-        break;
-    }
-    case JK_Q8_0: {  // dequantize_q8_0_block (quant.rs:571-588)
-        const float d = ld_dscale(w, r, b);
-        const uint4 q0 = ld_chunk(w, 0, r, b), q1 = ld_chunk(w, 1, r, b);
-        const float *xb = x + 32 * (size_t)b;
-        for (int i = 0; i < 32; ++i) {
-            const uint32_t dw = comp(i < 16 ? q0 : q1, (i & 15) >> 2);
-            const int qv = (int)(int8_t)(dw >> (8 * (i & 3)));
-            const float wv = d == 0.0f ? 0.0f : d * (float)qv;
-            sum += wv * xb[i];
-        }
-        break;
-    }
-    case JK_Q4_K: {  // dequantize_q4_k_m_block (lib.rs:720-766)
-        const uint4 h = ld_chunk(w, 0, r, b);
+    } else if constexpr (Q == JK_Q4_K) {
+        // dequantize_q4_k_m_block (lib.rs:720-766): y = d1 * q - m1, two roundings
+        const uint4 h = o.c[0];
         const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
         const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
         const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
         const uint32_t m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
-        const float *xb = x + 256 * (size_t)b;
+#pragma unroll
         for (int c = 0; c < 4; ++c) {
             const uint32_t scv = c < 2 ? sc_lo : sc_hi, mv = c < 2 ? m_lo : m_hi;
             const int j = (2 * c) & 3;
-            const float d1 = d * (float)byte_of(scv, j), m1 = dmin * (float)byte_of(mv, j);
-            const float d2 = d * (float)byte_of(scv, j + 1), m2 = dmin * (float)byte_of(mv, j + 1);
-            const uint4 qa = ld_chunk(w, 1 + 2 * c, r, b), qb = ld_chunk(w, 2 + 2 * c, r, b);
-            for (int l = 0; l < 32; ++l) {
-                const uint32_t dw = comp(l < 16 ? qa : qb, (l & 15) >> 2);
-                const float wv = d1 * (float)((dw >> (8 * (l & 3))) & 15u) - m1;
-                sum += wv * xb[64 * c + l];
-            }
-            for (int l = 0; l < 32; ++l) {
-                const uint32_t dw = comp(l < 16 ? qa : qb, (l & 15) >> 2);
-                const float wv = d2 * (float)((dw >> (8 * (l & 3) + 4)) & 15u) - m2;
-                sum += wv * xb[64 * c + 32 + l];
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+                const float d1 = d * (float)byte_of(scv, j + hi), m1 = dmin * (float)byte_of(mv, j + hi);
+#pragma unroll
+                for (int l = 0; l < 32; ++l) {
+                    const uint32_t q = (vd_byte<Q>(o, 1 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u;
+                    const float wv = d1 * (float)q - m1;
+                    sum += wv * xb[64 * c + 32 * hi + l];
+                }
             }
         }
-        break;
-    }
-    case JK_Q6_K: {  // dequantize_q6_k_block (quant.rs:594-648), visited in element order
-        const float d = ld_dscale(w, r, b);
-        const uint4 scv = ld_chunk(w, 12, r, b);
-        const float *xb = x + 256 * (size_t)b;
-        for (int e = 0; e < 256; ++e) {
-            float wv = 0.0f;
-            if (d != 0.0f) {
-                const int h = e >> 7, rr = e & 127, quarter = rr >> 5, l = rr & 31;
-                const int lbyte = 64 * h + l + ((quarter & 1) ? 32 : 0);
-                const int qbyte = 32 * h + l;
-                const uint32_t Lw = comp(ld_chunk(w, lbyte >> 4, r, b), (lbyte & 15) >> 2);
-                const uint32_t Qw = comp(ld_chunk(w, 8 + (qbyte >> 4), r, b), (qbyte & 15) >> 2);
-                const int L = (int)((Lw >> (8 * (lbyte & 3))) & 255u);
-                const int Q = (int)((Qw >> (8 * (qbyte & 3))) & 255u);
-                const int lo = quarter < 2 ? (L & 15) : (L >> 4);
-                const int q = (lo | (((Q >> (2 * quarter)) & 3) << 4)) - 32;
-                const int sb = 8 * h + (l >> 4) + 2 * quarter;
-                const float sc = (float)(int8_t)(comp(scv, sb >> 2) >> (8 * (sb & 3)));
-                wv = d * sc * (float)q;
+    } else if constexpr (Q == JK_Q6_K) {
+        // dequantize_q6_k_block (quant.rs:594-648) visited in element order: (d * sc) * q
+        // (its d == 0 -> +0.0 case needs no select, as for Q4_0 above)
+        const float d = f16_finite(o.d);
+        float dsc[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dsc[j] = d * (float)(int8_t)vd_byte<Q>(o, 12, j);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int quarter = 0; quarter < 4; ++quarter) {
+#pragma unroll
+                for (int l = 0; l < 32; ++l) {
+                    const int lbyte = 64 * h + l + ((quarter & 1) ? 32 : 0), qbyte = 32 * h + l;
+                    // each field straight from its source dword (no shared byte temporaries)
+                    const uint32_t lo = (comp(o.c[lbyte >> 4], (lbyte & 15) >> 2) >> (8 * (lbyte & 3) + (quarter < 2 ? 0 : 4))) & 15u;
+                    const uint32_t hi2 = (comp(o.c[8 + (qbyte >> 4)], (qbyte & 15) >> 2) >> (8 * (qbyte & 3) + 2 * quarter)) & 3u;
+                    const int q = (int)(lo | (hi2 << 4)) - 32;
+                    const float wv = dsc[8 * h + (l >> 4) + 2 * quarter] * (float)q;
+                    sum += wv * xb[128 * h + 32 * quarter + l];
+                }
+                // the chain is serial: an empty asm with a memory clobber keeps the next 32
+                // activation reads from being hoisted ahead of this group (bounded live range)
+                __asm__ volatile("" ::: "memory");
             }
-            sum += wv * xb[e];
-        }
-        break;
-    }
-    case JK_I2_S: {  // dequantize_i2_s_block (quant.rs:380-387), scale == 0 handled by the caller
-        const float sc = w.tensor_scale;
-        const uint4 q0 = ld_chunk(w, 0, r, b), q1 = ld_chunk(w, 1, r, b);
-        const float *xb = x + 128 * (size_t)b;
+    } else {  // JK_I2_S: dequantize_i2_s_block (quant.rs:380-387), (scale * t) * x
+#pragma unroll
         for (int e = 0; e < 128; ++e) {
             const int grp = e >> 5, g = e & 31;
-            const uint32_t dw = comp(g < 16 ? q0 : q1, (g & 15) >> 2);
-            const int byte = (int)((dw >> (8 * (g & 3))) & 255u);
-            const int t = ((byte >> (6 - 2 * grp)) & 3) - 1;
-            sum += (sc * (float)t) * xb[e];
+            const int t = (int)((vd_byte<Q>(o, g >> 4, g & 15) >> (6 - 2 * grp)) & 3u) - 1;
+            sum += (i2s_scale * (float)t) * xb[e];
         }
-        break;
-    }
-    default: break;
     }
     return sum;
 }
 
-// vec_dot_{q4_0,q8_0,q6_k}_scalar (quant.rs:1401-1436, 899-934, 1012-1047),
-// vec_dot_q4_k_m_scalar (lib.rs:1268-1303), vec_dot_i2_s (quant.rs:2199-2240):
-// row_sum starts at +0.0 and adds each block's dot in block order.
-__global__ __launch_bounds__(256) void vec_dot_f32_kernel(WeightDev w, const float *__restrict__ x,
-                                                          float *__restrict__ y) {
-    const int p = threadIdx.x & 15;
-    const int row = (int)((blockIdx.x * 256u + threadIdx.x) >> 4);
-    const bool active = row < w.rows;
-    const int r = active ? row : 0;
-    if (w.quant == JK_I2_S && w.tensor_scale == 0.0f) {
-        if (active && p == 0) y[row] = 0.0f;
+constexpr int kVdWaves = 8;
+constexpr int kVdLdsMax = 60 * 1024;  // staged activation bytes
+
+template <int Q, int LPR, bool XL>
+__global__ __launch_bounds__(64 * kVdWaves) void vec_dot_f32_kernel(WeightDev w, const float *__restrict__ x,
+                                                                     float *__restrict__ y) {
+    constexpr int RPW = 64 / LPR, E = VdFmt<Q>::E;
+    extern __shared__ __align__(16) float s_xf[];
+    __shared__ float s_red[LPR == 64 ? kVdWaves : 1][64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int sub = lane / LPR, p = lane % LPR;
+    const int row = ((int)blockIdx.x * kVdWaves + wave) * RPW + sub;
+    const int r = min(row, w.rows - 1);
+    const int nb = w.nb, iters = (nb + LPR - 1) / LPR;
+    if (Q == JK_I2_S && w.tensor_scale == 0.0f) {  // zero trailer scale: all outputs 0 (quant.rs:2219)
+        if (row < w.rows && p == 0) y[row] = 0.0f;
         return;
     }
-    float acc = 0.0f;
-    const int nb = w.nb, iters = (nb + 15) >> 4;
-    for (int it = 0; it < iters; ++it) {
-        const int g = min(16, nb - 16 * it);
-        float v = 0.0f;
-        if (p < g) v = fv_block(w, r, 16 * it + p, x);
-        acc = chain_add(acc, v, g);
+    VdBlock<Q> blk;
+    vd_load<Q>(blk, w, r, min(p, nb - 1));
+    // Staged blocks are padded by 16 bytes (XS floats apart) so that the 16-byte reads of
+    // 16 lanes, each in its own block, fall on distinct LDS banks.
+    constexpr int XS = XL ? E + 4 : E;
+    const float *xs = x;
+    if constexpr (XL) {
+        const int n4 = w.cols / 4;
+        for (int i = tid; i < n4; i += 64 * kVdWaves)
+            reinterpret_cast<float4 *>(s_xf)[i + i / (E / 4)] = reinterpret_cast<const float4 *>(x)[i];
+        __syncthreads();
+        xs = s_xf;
     }
-    const int g_last = nb - 16 * (iters - 1);
-    if (active && p == g_last - 1) y[row] = acc;
+    float *red = s_red[LPR == 64 ? wave : 0];
+    float acc = 0.0f;
+    for (int it = 0; it < iters; ++it) {
+        const int b = it * LPR + p;
+        if (it > 0) vd_load<Q>(blk, w, r, min(b, nb - 1));
+        const float v = b < nb ? vd_block<Q>(blk, xs + (size_t)XS * min(b, nb - 1), w.tensor_scale) : 0.0f;
+        const int g = min(LPR, nb - it * LPR);
+        if constexpr (LPR == 16) acc = chain_add(acc, v, g);
+        else acc = fold_wave(acc, v, g, red);
+    }
+    const int writer = LPR == 16 ? nb - LPR * (iters - 1) - 1 : 0;
+    if (row < w.rows && p == writer) y[row] = acc;
+}
+
+template <int Q>
+static jk_status launch_vd(hipStream_t s, const WeightDev &w, const float *x, float *y) {
+    const size_t lds_need = (size_t)w.nb * (VdFmt<Q>::E + 4) * 4;  // padded blocks
+    const bool xl = lds_need <= (size_t)kVdLdsMax;
+    const size_t lds = xl ? lds_need : 0;
+    if (w.nb > 32) {
+        const dim3 grid((unsigned)((w.rows + kVdWaves - 1) / kVdWaves));
+        if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, true>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
+        else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, false>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
+    } else {
+        const dim3 grid((unsigned)((w.rows + 4 * kVdWaves - 1) / (4 * kVdWaves)));
+        if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 16, true>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
+        else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 16, false>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
+    }
+    return check_launch("vec_dot_f32_kernel");
 }
 
 jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y) {
-    hipLaunchKernelGGL(vec_dot_f32_kernel, dim3((unsigned)((w.rows + 15) / 16)), dim3(256), 0, s, w, x, y);
-    return check_launch("vec_dot_f32_kernel");
+    switch (w.quant) {
+    case JK_Q4_0: return launch_vd<JK_Q4_0>(s, w, x, y);
+    case JK_Q8_0: return launch_vd<JK_Q8_0>(s, w, x, y);
+    case JK_Q4_K: return launch_vd<JK_Q4_K>(s, w, x, y);
+    case JK_Q6_K: return launch_vd<JK_Q6_K>(s, w, x, y);
+    case JK_I2_S: return launch_vd<JK_I2_S>(s, w, x, y);
+    default: return fail(JK_CAPABILITY_MISMATCH, "vec_dot_f32: unsupported quant %d", w.quant);
+    }
 }
 
 // ------------------------------------------------------------------------ BitLinear

@@ -403,18 +403,6 @@ __device__ __forceinline__ void xstage_sums(int nb, uint8_t *s_x) {
     }
 }
 
-// ------------------------------------------------------------------ ordered fold
-// LPR == 64: the wave's g block values are added in order by lane 0 (acc lives in lane 0).
-__device__ __forceinline__ float fold_wave(float acc, float v, int g, float *red) {
-    const int l = threadIdx.x & 63;
-    red[l] = v;
-    wave_lds_sync();
-    if (l == 0)
-        for (int i = 0; i < g; ++i) acc += red[i];
-    wave_lds_sync();
-    return acc;
-}
-
 // The two halves of activation staging, around the weight loads issued between them.
 // begin: round 0 into registers, then a barrier that puts every activation load of the
 // workgroup ahead of its weight loads (it waits for no data).
@@ -633,31 +621,35 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     const int units = min((r1 - r0 + RPU - 1) / RPU, g0 + job.upg);  // end of this workgroup's units
     const int base = g0 + wave;                                          // unit q: base + NW * q
 
-    // 1. activation round 0, then every weight load of the wave. A unit past the end
-    //    re-reads a valid unit's lines at distinct addresses (xor 16): the loads stay
-    //    unconditional, add no traffic and are never merged with the real ones.
+    // 1. activation round 0, then the weight loads of the wave's first two units. A unit
+    //    past the end re-reads a valid unit's lines at distinct addresses (xor 16): the
+    //    loads stay unconditional, add no traffic and are never merged with the real ones.
     XRegs<NW, F32, Q> xr;
     stage_begin<Q, F32, NW>(xr, job, nb);
-    WReg<Q> W[QPW][UF];
     const int ufb = base < units ? base : g0;  // a valid unit of the workgroup
-#pragma unroll
-    for (int q = 0; q < QPW; ++q) {
+    WReg<Q> W[QPW > 1 ? 2 : 1][UF];
+    auto load_unit = [&](int q, WReg<Q>(&dst)[UF]) {
         const bool dummy = base + NW * q >= units;
         const int row = r0 + (dummy ? ufb : base + NW * q) * RPU + sub;
         const int r = min(row, r1 - 1);
 #pragma unroll
-        for (int k = 0; k < UF; ++k) wload<Q>(W[q][k], w, r, min(k * LPR + p, nb - 1), dummy ? 16u : 0u);
-    }
+        for (int k = 0; k < UF; ++k) wload<Q>(dst[k], w, r, min(k * LPR + p, nb - 1), dummy ? 16u : 0u);
+    };
+    load_unit(0, W[0]);
+    if constexpr (QPW > 1) load_unit(1, W[1]);
 
     // 2. activation vector into the staged LDS layout
     stage_finish<Q, F32, NW>(xr, job, nb, s_x);
 
-    // 3. block values folded in block order; results stay in registers
+    // 3. units in order, two in flight: unit q is folded while unit q + 1 loads, then unit
+    //    q + 2 is issued into the buffer just consumed. Block values fold in block order;
+    //    results stay in registers.
     const int rows4 = (w.rows >> 2) << 2;
     float *red = s_red[LPR == 64 ? wave : 0];
     float out[QPW];
 #pragma unroll
     for (int q = 0; q < QPW; ++q) {
+        const WReg<Q>(&Wq)[UF] = W[q & (QPW > 1 ? 1 : 0)];
         const int row = r0 + (base + NW * q) * RPU + sub;
         float acc = row < rows4 ? 0.0f : -0.0f;
         float v[UF];
@@ -666,8 +658,8 @@ gemv_q8_fast_kernel(GemvGroup grp) {
             const int b = k * LPR + p;
             v[k] = 0.0f;
             if (b < nb) {
-                if constexpr (T::K) v[k] = block_value<Q>(W[q][k], XkLds{s_x + b * T::XB});
-                else v[k] = block_value<Q>(W[q][k], X0Lds{s_x + b * T::XB});
+                if constexpr (T::K) v[k] = block_value<Q>(Wq[k], XkLds{s_x + b * T::XB});
+                else v[k] = block_value<Q>(Wq[k], X0Lds{s_x + b * T::XB});
             }
         }
 #pragma unroll
@@ -679,6 +671,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
             }
         }
         out[q] = acc;
+        if (q + 2 < QPW) load_unit(q + 2, W[q & 1]);
     }
 
     // 4. stores
