@@ -15,6 +15,8 @@
 // tile, waves 4-7 the activation tile, each with line-wide coalesced reads -- and after a
 // barrier it is unpacked to i8 and written to LDS. LDS rows are padded from 256 to 272
 // bytes so the 16-byte fragment reads of 16 lanes land on distinct banks.
+#include <string.h>
+
 #include <utility>
 
 #include "jk_device.hpp"
@@ -295,10 +297,15 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, 
     }
 }
 
-template <int Q>
+// GB: 32-element steps per scale block. 1 for the repacked GEMM (per-32 activation scales,
+// one epilogue per step); for BitLinear (one scale per token and per weight block: 256
+// elements for TQ2_0, 128 for I2_S, 32 for Q8_0) the block's MFMAs accumulate in i32 and the
+// epilogue runs once per block.
+template <int Q, int GB = 1>
 __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
                                                             int r0, int r1) {
     using F = GemmFmt<Q>;
+    static_assert(GB == 1 || F::GK == 32, "block accumulation needs 32-element steps");
     __shared__ __align__(16) GemmChunk cs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave & 1, wmi = wave >> 1;  // wave tile: rows 64 * wn .., tokens 32 * wmi ..
@@ -322,6 +329,7 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
 
+    v16i cacc[2] = {v16i{0}, v16i{0}};  // i32 partials of the current scale block (GB > 1)
     Stage rg;
     chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
     chunk_store<Q>(w, rg, cs);
@@ -341,7 +349,13 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
                     for (int nt = 0; nt < 2; ++nt) {
                         const v4i aq =
                             *reinterpret_cast<const v4i *>(cs.a + (64 * wn + 32 * nt + jl) * kRowB + 32 * st + 16 * hl);
-                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+                        if constexpr (GB == 1) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+                        else c[nt] = cacc[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, cacc[nt], 0, 0, 0);
+                    }
+                    if constexpr (GB > 1) {
+                        if (st % GB != GB - 1) continue;  // block not complete: no epilogue yet
+                        cacc[0] = v16i{0};
+                        cacc[1] = v16i{0};
                     }
                 } else {
                     const long bq = *reinterpret_cast<const long *>(cs.b + tok * kRowB + 32 * st + 16 * gg + 8 * hl);
@@ -393,6 +407,29 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
                 if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = acc[nt][v];
             }
     }
+}
+
+// bitlinear_i8_rvv (ime.rs:882-938) for m tokens on int8 MFMA: the activation rows act[m][k]
+// are read as the GEMM's quantized rows (row stride k) and the per-token scale as a single
+// "per-32" scale column (k_blocks32 = 1, every block index clamps to it).
+jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales, int m,
+                                float *y) {
+    jk_act_q8 a;
+    memset(&a, 0, sizeof a);
+    a.m = (size_t)m;
+    a.k = a.k_padded = (size_t)w.cols;
+    a.k_blocks32 = 1;
+    a.qs = const_cast<int8_t *>(act);
+    a.scales = const_cast<float *>(act_scales);
+    const size_t ntn = (size_t)(w.rows + kTN - 1) / kTN, ntm = ((size_t)m + kTM - 1) / kTM;
+    const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(kThreads);
+    switch (w.quant) {
+    case JK_TQ2_0: hipLaunchKernelGGL((gemm_repacked_kernel<JK_TQ2_0, 8>), grid, block, 0, s, w, a, y, 0, w.rows); break;
+    case JK_I2_S: hipLaunchKernelGGL((gemm_repacked_kernel<JK_I2_S, 4>), grid, block, 0, s, w, a, y, 0, w.rows); break;
+    case JK_Q8_0: hipLaunchKernelGGL((gemm_repacked_kernel<JK_Q8_0, 1>), grid, block, 0, s, w, a, y, 0, w.rows); break;
+    default: return fail(JK_CAPABILITY_MISMATCH, "bitlinear: unsupported quant %d", w.quant);
+    }
+    return check_launch("gemm_repacked_kernel (bitlinear)");
 }
 
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {

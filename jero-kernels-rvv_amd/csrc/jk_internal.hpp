@@ -132,6 +132,10 @@ jk_status launch_absmax_i8(hipStream_t s, const float *x, const float *norm_w, s
 jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1);
 jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n);
 jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y);
+// Token count from which jk_bitlinear_i8 uses the MFMA GEMM path.
+constexpr int kBitlinearMfmaMinTokens = 16;
+jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales, int m,
+                                float *y);
 jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act,
                            const float *act_scales, int m, float *y);
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y,

@@ -523,6 +523,8 @@ jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, co
                     w->dev.cols, m, k, y_len);
     if (m >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "bitlinear: m=%zu too large", m);
     if (!act || !act_scales || !y) return fail(JK_TENSOR_BOUNDS, "bitlinear: null pointer");
+    // batches of tokens run as an int8-MFMA GEMM (same per-block arithmetic and block order)
+    if (m >= (size_t)kBitlinearMfmaMinTokens) return launch_bitlinear_mfma((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
     return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
 }
 

@@ -408,7 +408,9 @@ def test_gemm_q8_0_prefill_shape_rows_sample(gpu, m):
 
 # ------------------------------------------------------------------ BitLinear
 @pytest.mark.parametrize("quant", [TQ2_0, I2_S, Q8_0])
-@pytest.mark.parametrize("m,rows,cols", [(1, 7, 256), (3, 64, 2560), (2, 2560, 6912)])
+@pytest.mark.parametrize("m,rows,cols", [(1, 7, 256), (3, 64, 2560), (2, 2560, 6912),
+                                         # token batches take the int8-MFMA path
+                                         (16, 300, 2560), (37, 129, 768), (128, 2560, 6912), (128, 6912, 2560)])
 def test_bitlinear(gpu, quant, m, rows, cols):
     torch = gpu
     raw = synth.gguf_weights(quant, rows, cols, seed=m + quant) if quant != Q8_0 else \
