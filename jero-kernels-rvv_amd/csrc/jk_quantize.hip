@@ -69,71 +69,87 @@ jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk
     return check_launch("quantize_q8_k_kernel");
 }
 
-// QuantizedActQ8::quantize_into (repack.rs:542-650) for one (row, 32-block) per thread:
-// quantize_block32_scalar (repack.rs:175-204) with its sequential +0.0-started sum, and
-// the two x_sums_16 entries of the block as Rust `.sum()` folds (from -0.0).
-__global__ __launch_bounds__(256) void quantize_act_q8_kernel(const float *__restrict__ x, jk_act_q8 a) {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= a.m * a.k_blocks32) return;
-    const size_t row = idx / a.k_blocks32, b = idx % a.k_blocks32;
-    const float *src = x + row * a.k;
-    float clean[32];
-    float absmax = 0.0f, sum = 0.0f;
-    for (int i = 0; i < 32; ++i) {
-        const size_t e = b * 32 + i;
-        const float v = e < a.k ? src[e] : 0.0f;
-        clean[i] = __builtin_isfinite(v) ? v : 0.0f;
-        sum += clean[i];
-        const float av = fabsf(clean[i]);
-        if (av > absmax) absmax = av;
+// Ordered f32 fold of N consecutive lanes (N = 4 or 8) that hold four values each, in
+// element order: lane j of the group computes (((prev + v0) + v1) + v2) + v3 where prev is
+// lane j-1's result (init for j == 0). After N steps lane N-1 holds the group's fold.
+template <int N>
+__device__ __forceinline__ float lane_chain(const float (&v)[4], float init) {
+    const int j = (int)(threadIdx.x & (N - 1));
+    float run = init;
+#pragma unroll
+    for (int step = 0; step < N; ++step) {
+        const float prev = __shfl_up(run, 1, N);  // lane j - 1 of the group (lane 0 keeps its own)
+        const float base = j == 0 ? init : prev;
+        const float r = (((base + v[0]) + v[1]) + v[2]) + v[3];
+        run = j == step ? r : run;
     }
-    uint32_t packed[8];
-    float scale = 0.0f;
-    if (absmax < 1e-30f) {
-        for (int i = 0; i < 8; ++i) packed[i] = 0;
-    } else {
-        const float inv = 127.0f / absmax;
-        scale = absmax / 127.0f;
-        for (int i = 0; i < 8; ++i) {
-            uint32_t p = 0;
-            for (int j = 0; j < 4; ++j)
-                p |= (uint32_t)(rust_round_clamp_i8(clean[4 * i + j] * inv, -127.0f, 127.0f) & 255) << (8 * j);
-            packed[i] = p;
-        }
-    }
-    uint4 *dq = reinterpret_cast<uint4 *>(a.qs + row * a.k_padded + b * 32);
-    dq[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    dq[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-    a.scales[row * a.k_blocks32 + b] = scale;
-    a.sums[row * a.k_blocks32 + b] = sum;
-    for (int h = 0; h < 2; ++h) {
-        float s16 = -0.0f;
-        for (int i = 0; i < 16; ++i) s16 += clean[16 * h + i];
-        a.sums16[row * a.k_chunks + 2 * b + h] = s16;
-    }
+    return run;
 }
 
-// super_scales_256 (repack.rs:612-621): max of the block scales of each 256-superblock,
-// starting from 0.0.
-__global__ __launch_bounds__(256) void act_super_kernel(jk_act_q8 a) {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= a.m * a.sb256) return;
-    const size_t row = idx / a.sb256, sb = idx % a.sb256;
-    float mx = 0.0f;
-    for (size_t b = sb * 8; b < sb * 8 + 8 && b < a.k_blocks32; ++b) {
-        const float sc = a.scales[row * a.k_blocks32 + b];
-        if (sc > mx) mx = sc;
+// QuantizedActQ8::quantize_into (repack.rs:542-650): one wave per (row, 256-element
+// superblock), lane l holding elements 4l..4l+3 (coalesced loads), 8 lanes per 32-block.
+// Per block, quantize_block32_scalar (repack.rs:175-204): non-finite -> 0, absmax over the
+// block (zero block below 1e-30), scale = absmax / 127, q = round(x * 127 / absmax) clamped
+// to +-127, and the sequential sum from +0.0; the two x_sums_16 entries are Rust `.sum()`
+// folds from -0.0; super_scales_256 (repack.rs:612-621) is the max of the superblock's
+// block scales from 0.0. Elements past k (the zero-padded tail) take part as +0.0.
+template <bool V4>
+__global__ __launch_bounds__(256) void quantize_act_q8_kernel(const float *__restrict__ x, jk_act_q8 a) {
+    const size_t wv = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (wv >= a.m * a.sb256) return;  // wave-uniform
+    const int l = (int)(threadIdx.x & 63);
+    const size_t row = wv / a.sb256, sb = wv % a.sb256;
+    const size_t e0 = sb * 256 + 4 * (size_t)l;
+    const float *src = x + row * a.k;
+    float v[4];
+    if constexpr (V4) {
+        if (e0 + 3 < a.k) {
+            const float4 f = *reinterpret_cast<const float4 *>(src + e0);
+            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = e0 + i < a.k ? src[e0 + i] : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = e0 + i < a.k ? src[e0 + i] : 0.0f;
     }
-    a.super256[idx] = mx;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_isfinite(v[i]) ? v[i] : 0.0f;
+    const float absmax = max8_dpp(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    const bool zero = absmax < 1e-30f;
+    const float inv = zero ? 0.0f : 127.0f / absmax;
+    const float scale = zero ? 0.0f : absmax / 127.0f;
+    uint32_t packed = 0;
+    if (!zero) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) packed |= (uint32_t)(rust_round_clamp_i8(v[i] * inv, -127.0f, 127.0f) & 255) << (8 * i);
+    }
+    const float sum = lane_chain<8>(v, 0.0f);
+    const float s16 = lane_chain<4>(v, -0.0f);
+    // superblock max of the block scales (lanes 8b hold block b's scale), from 0.0
+    float mx = fmaxf(0.0f, scale);
+    mx = fmaxf(mx, __shfl_xor(mx, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+
+    const size_t b = sb * 8 + (size_t)(l >> 3);
+    if (b < a.k_blocks32) {
+        *reinterpret_cast<uint32_t *>(a.qs + row * a.k_padded + e0) = packed;
+        const int j = l & 7;
+        if (j == 0) a.scales[row * a.k_blocks32 + b] = scale;
+        if (j == 7) a.sums[row * a.k_blocks32 + b] = sum;
+        if ((l & 3) == 3) a.sums16[row * a.k_chunks + 2 * b + (j >> 2)] = s16;
+    }
+    if (l == 0) a.super256[row * a.sb256 + sb] = mx;
 }
 
 jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 &a) {
-    const size_t n = a.m * a.k_blocks32;
-    hipLaunchKernelGGL(quantize_act_q8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, a);
-    JK_TRY(check_launch("quantize_act_q8_kernel"));
-    const size_t n2 = a.m * a.sb256;
-    hipLaunchKernelGGL(act_super_kernel, dim3((unsigned)((n2 + 255) / 256)), dim3(256), 0, s, a);
-    return check_launch("act_super_kernel");
+    const size_t waves = a.m * a.sb256;
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if ((a.k & 3) == 0 && ((uintptr_t)x & 15) == 0) hipLaunchKernelGGL(quantize_act_q8_kernel<true>, grid, block, 0, s, x, a);
+    else hipLaunchKernelGGL(quantize_act_q8_kernel<false>, grid, block, 0, s, x, a);
+    return check_launch("quantize_act_q8_kernel");
 }
 
 // subln_quantize_absmax_i8 (lib.rs:1042-1101) per row; norm_w == nullptr gives the same
