@@ -107,7 +107,7 @@ def gpu_act(torch, x, m, k):
     return storage, act
 
 
-@pytest.mark.parametrize("m,k", [(1, 4096), (5, 300), (64, 4096), (3, 40)])
+@pytest.mark.parametrize("m,k", [(1, 4096), (5, 300), (64, 4096), (3, 40), (2, 101), (7, 259)])
 def test_quantize_act_q8(gpu, m, k):
     torch = gpu
     rng = np.random.default_rng(m * k)
