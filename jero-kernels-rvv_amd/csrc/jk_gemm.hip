@@ -8,13 +8,14 @@
 // group's integer partial is exact and the f32 epilogue runs per group in K order: each
 // output keeps the reference's arithmetic and order, bit for bit.
 //
-// Tiling: a workgroup of 8 waves computes a 128 (weight rows) x 128 (tokens) tile, each
-// wave 64 x 32 as two 32x32 MFMA tiles. K advances in chunks of 256 elements (8 steps of
-// 32; one super-block of the 256-element formats). While the 8 steps of a chunk are
-// evaluated from LDS, the next chunk is loaded into registers -- waves 0-3 load the weight
-// tile, waves 4-7 the activation tile, each with line-wide coalesced reads -- and after a
-// barrier it is unpacked to i8 and written to LDS. LDS rows are padded from 256 to 272
-// bytes so the 16-byte fragment reads of 16 lanes land on distinct banks.
+// Tiling: a workgroup of 4 waves computes a 128 (weight rows) x 64 (tokens) tile, each wave
+// 64 x 32 as two 32x32 MFMA tiles. K advances in chunks of 128 elements (4 steps of 32; half
+// a super-block of the 256-element formats). While the 4 steps of a chunk are evaluated
+// from LDS, the next chunk is loaded into registers with coalesced reads -- every thread a
+// share of both tiles -- and after a barrier it is unpacked to i8 and written to LDS. LDS rows are padded from 128 to 144 bytes so the 16-byte fragment
+// reads of 16 lanes land on distinct banks. A workgroup needs 35 KB of LDS and at most 168
+// VGPRs per lane, so three workgroups share a CU: while one waits at its barrier or on its
+// loads, the others compute.
 #include <string.h>
 
 #include <utility>
@@ -27,25 +28,26 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-constexpr int kTN = 128;   // weight rows per workgroup
-constexpr int kTM = 128;   // tokens per workgroup
-constexpr int kThreads = 512;
-constexpr int kKC = 256;   // K elements per chunk
-constexpr int kRowB = 272; // padded LDS bytes per 256-byte row
+constexpr int kTN = 128;      // weight rows per workgroup
+constexpr int kTM = 64;       // tokens per workgroup
+constexpr int kThreads = 256;
+constexpr int kKC = 128;      // K elements per chunk
+constexpr int kSteps = 4;     // 32-element steps per chunk
+constexpr int kRowB = 144;    // padded LDS bytes per 128-byte row
 
 template <int Q> struct GemmFmt {
     static constexpr int GK = Q == JK_Q6_K ? 16 : 32;  // elements per scale group
     static constexpr bool MINS = Q == JK_Q4_K;
-    static constexpr int NG = 128 / GK;                 // scale groups per half chunk
+    static constexpr int NG = 128 / GK;                 // scale groups per chunk
 };
 
 struct GemmChunk {
     uint8_t a[kTN * kRowB];  // weights, i8, [row][k]
     uint8_t b[kTM * kRowB];  // activations, i8, [token][k]
-    float ws[16][kTN];       // weight scale per scale group of the chunk
-    float wm[8][kTN];        // weight min per 32-group (Q4_K)
-    float xs[8][kTM];        // activation scale per 32-block
-    float xm[8][kTM];        // activation sum per 32-block (Q4_K)
+    float ws[8][kTN];        // weight scale per scale group of the chunk
+    float wm[4][kTN];        // weight min per 32-group (Q4_K)
+    float xs[4][kTM];        // activation scale per 32-block
+    float xm[4][kTM];        // activation sum per 32-block (Q4_K)
 };
 
 // f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): register arrays
@@ -69,18 +71,21 @@ __device__ __forceinline__ const uint8_t *plane_ptr(const WeightDev &w, int c, i
 // Raw bytes of one thread's share of a chunk, exactly as stored in the plane layout, plus
 // raw f16 scales. Loading and unpacking are separate so that every global load of a chunk
 // is in flight while the previous chunk is evaluated; nothing between the loads depends on
-// a loaded value.
-//  Q8_0 / Q4_0: a chunk is 8 blocks, 128 contiguous bytes per (plane, row): 8 consecutive
-//   lanes read one such line (piece t % 8 = block 8kc + t % 8), load i covers rows
-//   32 (i % 4) + t / 8 of plane i / 4. Scales: row t / 2, blocks 8kc + 4 (t % 2) ..
-//  K-quants, TQ2_0, I2_S: 16 or 32 bytes per (plane, row) and chunk; thread t takes row
-//   t / 2 and the half t % 2 of the chunk's elements (128h .. 128h+127).
-//  Activations (waves 4-7, t = thread - 256): load i covers token 16i + t / 16, piece
-//   t % 16 of its 256-byte row; scales (and sums) of token t / 2, steps 4 (t % 2) ...
-// Both roles use the same registers: v / d hold whichever tile the wave stages.
+// a loaded value. Every thread stages part of both tiles, so the four waves (one per SIMD)
+// carry the same load and unpack work.
+//  Q8_0 / Q4_0: a chunk is 4 blocks, 64 contiguous bytes per (plane, row); 4 consecutive
+//   lanes read one such segment (piece t % 4 = block 4kc + t % 4), load i covers rows
+//   t / 4 + 64 (i % 2) of plane i / 2. Scales: row t / 2, blocks 4kc + 2 (t % 2) ...
+//  K-quants, TQ2_0 (256-element blocks): chunk kc is half h = kc % 2 of block kc / 2;
+//   I2_S (128-element blocks): chunk kc is block kc. Thread t takes row t / 2 and part
+//   j = t % 2 of the chunk's planes.
+//  Activations: load i covers token t / 8 + 32i, piece t % 8 of its 128-byte row; scale
+//   (and sum) of token t / 4, block 4kc + t % 4.
 struct Stage {
-    uint4 v[8];
-    uint32_t d[8];
+    uint4 w[4];      // weight plane bytes
+    uint32_t wd[2];  // weight f16 scales (Q8_0 / Q4_0: two blocks; Q6_K, TQ2_0: d)
+    uint4 x[2];      // activation bytes
+    uint32_t xd[2];  // activation scale, sum (Q4_K)
 };
 
 // Blocks past the row end (a partial last chunk) are read clamped and never used; rows
@@ -89,211 +94,163 @@ template <int Q>
 __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage &r) {
     const int nb = w.nb, t = threadIdx.x;
     if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
-        const int b = min(8 * kc + (t & 7), nb - 1);
+        const int b = min(4 * kc + (t & 3), nb - 1);
 #pragma unroll
-        for (int i = 0; i < (Q == JK_Q8_0 ? 8 : 4); ++i) {
-            const int n = min(n0 + 32 * (i & 3) + (t >> 3), r1 - 1);
-            r.v[i] = ldg16(plane_ptr(w, i >> 2, n, b));
+        for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
+            const int n = min(n0 + (t >> 2) + 64 * (i & 1), r1 - 1);
+            r.w[i] = ldg16(plane_ptr(w, i >> 1, n, b));
         }
-        const int n = min(n0 + (t >> 1), r1 - 1);
-        const size_t srow = (size_t)n * (size_t)nb;
+        const size_t srow = (size_t)min(n0 + (t >> 1), r1 - 1) * (size_t)nb;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r.d[j] = w.dplane[srow + (size_t)min(8 * kc + 4 * (t & 1) + j, nb - 1)];
+        for (int j = 0; j < 2; ++j) r.wd[j] = w.dplane[srow + (size_t)min(4 * kc + 2 * (t & 1) + j, nb - 1)];
     } else {
-        const int n = min(n0 + (t >> 1), r1 - 1), h = t & 1;
+        const int n = min(n0 + (t >> 1), r1 - 1), j = t & 1;
+        if constexpr (Q == JK_I2_S) {
+            r.w[0] = ldg16(plane_ptr(w, j, n, min(kc, nb - 1)));
+            return;
+        }
+        const int h = kc & 1, b = kc >> 1;
         if constexpr (Q == JK_Q4_K) {
-            r.v[0] = ldg16(plane_ptr(w, 0, n, kc));  // d, dmin, 12 packed 6-bit scales / mins
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                r.v[1 + 2 * c] = ldg16(plane_ptr(w, 1 + 2 * (2 * h + c), n, kc));
-                r.v[2 + 2 * c] = ldg16(plane_ptr(w, 2 + 2 * (2 * h + c), n, kc));
-            }
+            r.w[0] = ldg16(plane_ptr(w, 0, n, b));  // d, dmin, 12 packed 6-bit scales / mins
+            r.w[1] = ldg16(plane_ptr(w, 1 + 2 * (2 * h + j), n, b));
+            r.w[2] = ldg16(plane_ptr(w, 2 + 2 * (2 * h + j), n, b));
         } else if constexpr (Q == JK_Q6_K) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) r.v[c] = ldg16(plane_ptr(w, 4 * h + c, n, kc));      // ql
-#pragma unroll
-            for (int c = 0; c < 2; ++c) r.v[4 + c] = ldg16(plane_ptr(w, 8 + 2 * h + c, n, kc));  // qh
-            r.v[6] = ldg16(plane_ptr(w, 12, n, kc));                                          // i8 scales
-            r.d[0] = w.dplane[(size_t)n * (size_t)nb + (size_t)kc];
-        } else if constexpr (Q == JK_TQ2_0) {
-#pragma unroll
-            for (int c = 0; c < 2; ++c) r.v[c] = ldg16(plane_ptr(w, 2 * h + c, n, kc));
-            r.d[0] = w.dplane[(size_t)n * (size_t)nb + (size_t)kc];
-        } else {  // JK_I2_S: chunk = blocks 2kc, 2kc + 1; half h = block 2kc + h
-            const int b = min(2 * kc + h, nb - 1);
-#pragma unroll
-            for (int c = 0; c < 2; ++c) r.v[c] = ldg16(plane_ptr(w, c, n, b));
+            r.w[0] = ldg16(plane_ptr(w, 4 * h + j, n, b));      // ql, quarters 0 and 2
+            r.w[1] = ldg16(plane_ptr(w, 4 * h + j + 2, n, b));  // ql, quarters 1 and 3
+            r.w[2] = ldg16(plane_ptr(w, 8 + 2 * h + j, n, b));  // qh
+            r.w[3] = ldg16(plane_ptr(w, 12, n, b));             // i8 scales
+            r.wd[0] = w.dplane[(size_t)n * (size_t)nb + (size_t)b];
+        } else {  // JK_TQ2_0
+            r.w[0] = ldg16(plane_ptr(w, 2 * h + j, n, b));
+            r.wd[0] = w.dplane[(size_t)n * (size_t)nb + (size_t)b];
         }
     }
 }
 
-// The loaded half of the per-row formats as 128 i8 values (q[i]: elements 128h + 16i ..)
-// with repack_block_scaled_range_into_i8's values (repack.rs:1724-2103), and the weight
-// scale / min of each of its scale groups.
 template <int Q>
-__device__ __forceinline__ void chunk_w_unpack(const WeightDev &w, const Stage &r, int h, uint4 (&q)[8],
-                                               float (&ws)[8], float (&wm)[4]) {
+__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage &r) {
+    const int t = threadIdx.x;
+    int k = kKC * kc + 16 * (t & 7);
+    if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = min(m0 + (t >> 3) + 32 * i, M - 1);
+        r.x[i] = ldg16(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + k);
+    }
+    const size_t sidx = (size_t)min(m0 + (t >> 2), M - 1) * a.k_blocks32 + (size_t)min(4 * kc + (t & 3), (int)a.k_blocks32 - 1);
+    r.xd[0] = __float_as_uint(a.scales[sidx]);
+    r.xd[1] = GemmFmt<Q>::MINS ? __float_as_uint(a.sums[sidx]) : 0u;
+}
+
+// Global loads of chunk kc into this thread's staging registers.
+template <int Q>
+__device__ __forceinline__ void chunk_load(Stage &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1, int m0,
+                                           int M, int kc) {
+    chunk_w_load<Q>(w, n0, r1, kc, r);
+    chunk_x_load<Q>(a, m0, M, kc, r);
+}
+
+__device__ __forceinline__ uint4 nib4(uint4 v, int sh, uint32_t bias) {
+    return make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x0F0F0F0Fu, bias), (uint32_t)bytes_sub((v.y >> sh) & 0x0F0F0F0Fu, bias),
+                      (uint32_t)bytes_sub((v.z >> sh) & 0x0F0F0F0Fu, bias), (uint32_t)bytes_sub((v.w >> sh) & 0x0F0F0F0Fu, bias));
+}
+__device__ __forceinline__ uint4 crumb4(uint4 v, int sh) {
+    return make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x03030303u, 0x01010101u),
+                      (uint32_t)bytes_sub((v.y >> sh) & 0x03030303u, 0x01010101u),
+                      (uint32_t)bytes_sub((v.z >> sh) & 0x03030303u, 0x01010101u),
+                      (uint32_t)bytes_sub((v.w >> sh) & 0x03030303u, 0x01010101u));
+}
+
+// Unpack the staging registers to i8 with repack_block_scaled_range_into_i8's values
+// (repack.rs:1724-2103) and write them, with the scale (and min) of each scale group, to
+// the chunk's LDS tiles.
+template <int Q>
+__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, GemmChunk &c, int kc) {
+    const int t = threadIdx.x;
+    {  // activations
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            *reinterpret_cast<uint4 *>(c.b + ((t >> 3) + 32 * i) * kRowB + 16 * (t & 7)) = r.x[i];
+        c.xs[t & 3][t >> 2] = __uint_as_float(r.xd[0]);
+        if constexpr (GemmFmt<Q>::MINS) c.xm[t & 3][t >> 2] = __uint_as_float(r.xd[1]);
+    }
+    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
+        const int piece = t & 3;
+#pragma unroll
+        for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
+            uint8_t *dst = c.a + ((t >> 2) + 64 * (i & 1)) * kRowB + 32 * piece;
+            if constexpr (Q == JK_Q8_0) {
+                *reinterpret_cast<uint4 *>(dst + 16 * (i >> 1)) = r.w[i];
+            } else {
+                *reinterpret_cast<uint4 *>(dst) = nib4(r.w[i], 0, 0x08080808u);
+                *reinterpret_cast<uint4 *>(dst + 16) = nib4(r.w[i], 4, 0x08080808u);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) c.ws[2 * (t & 1) + j][t >> 1] = f16_finite(r.wd[j]);
+        return;
+    }
+    const int row = t >> 1, j = t & 1, h = kc & 1;
+    uint8_t *dst = c.a + row * kRowB;
     if constexpr (Q == JK_Q4_K) {
-        // unpack_k4_scales_mins (repack.rs:1158-1170); qs chunk pair (2c, 2c+1) holds
-        // elements 64c .. 64c+63 (low nibbles first)
-        const uint4 hd = r.v[0];
+        // unpack_k4_scales_mins (repack.rs:1158-1170); qs planes (1 + 2c', 2 + 2c') of
+        // super-block quarter c' = 2h + j hold elements 64j .. 64j + 63 of the half: low
+        // nibbles of both planes, then high nibbles
+        const uint4 hd = r.w[0];
         const float d = f16_finite(hd.x & 0xFFFFu), dmin = f16_finite(hd.x >> 16);
         const uint32_t sc = h == 0 ? (hd.y & 0x3F3F3F3Fu) : ((hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u));
         const uint32_t mv = h == 0 ? (hd.z & 0x3F3F3F3Fu) : (((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u));
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            ws[t] = d * (float)((sc >> (8 * t)) & 255u);
-            wm[t] = dmin * (float)((mv >> (8 * t)) & 255u);
+        for (int e = 0; e < 2; ++e) {
+            const int g = 2 * j + e;
+            c.ws[g][row] = d * (float)((sc >> (8 * g)) & 255u);
+            c.wm[g][row] = dmin * (float)((mv >> (8 * g)) & 255u);
         }
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const uint4 v0 = r.v[1 + 2 * c], v1 = r.v[2 + 2 * c];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int sh = 4 * hh;
-                q[4 * c + 2 * hh] = make_uint4((v0.x >> sh) & 0x0F0F0F0Fu, (v0.y >> sh) & 0x0F0F0F0Fu,
-                                               (v0.z >> sh) & 0x0F0F0F0Fu, (v0.w >> sh) & 0x0F0F0F0Fu);
-                q[4 * c + 2 * hh + 1] = make_uint4((v1.x >> sh) & 0x0F0F0F0Fu, (v1.y >> sh) & 0x0F0F0F0Fu,
-                                                   (v1.z >> sh) & 0x0F0F0F0Fu, (v1.w >> sh) & 0x0F0F0F0Fu);
-            }
+        for (int hh = 0; hh < 2; ++hh) {
+            *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh) = nib4(r.w[1], 4 * hh, 0u);
+            *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh + 16) = nib4(r.w[2], 4 * hh, 0u);
         }
     } else if constexpr (Q == JK_Q6_K) {
-        // dequantize_q6_k_block's element order (quant.rs:594-648): 16-group g of half h
-        // (quarter g / 2, is = g % 2) takes ql bytes 16is + 32(quarter & 1) of the half, qh
-        // bytes 16is, the low / high nibble and 2-bit field by quarter, scale 8h + g
-        const float d = f16_finite(r.d[0]);
-        const uint4 scv = r.v[6];
+        // dequantize_q6_k_block's element order (quant.rs:594-648): 16-group g = j + 2 qq of
+        // half h (quarter qq) takes ql bytes 16j + 32(qq % 2) of the half, qh bytes 16j, the
+        // low / high nibble and 2-bit field by quarter, scale 8h + g
+        const float d = f16_finite(r.wd[0]);
+        const uint4 scv = r.w[3], hv = r.w[2];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            const int quarter = g >> 1, is = g & 1, j = 8 * h + g;
-            ws[g] = d * (float)(int8_t)(comp(scv, j >> 2) >> (8 * (j & 3)));
-            const uint4 lv = r.v[is + 2 * (quarter & 1)], hv = r.v[4 + is];
-            const int lsh = quarter < 2 ? 0 : 4, hsh = 2 * quarter;
+        for (int qq = 0; qq < 4; ++qq) {
+            const int g = j + 2 * qq, js = 8 * h + g;
+            c.ws[g][row] = d * (float)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
+            const uint4 lv = r.w[qq & 1];
+            const int lsh = qq < 2 ? 0 : 4, hsh = 2 * qq;
             uint32_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t v6 = ((comp(lv, i) >> lsh) & 0x0F0F0F0Fu) | (((comp(hv, i) >> hsh) & 0x03030303u) << 4);
                 o[i] = (uint32_t)bytes_sub(v6, 0x20202020u);
             }
-            q[g] = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4 *>(dst + 16 * g) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     } else if constexpr (Q == JK_TQ2_0) {
-        const float d = f16_finite(r.d[0]);
+        // plane 2h + j: its dword k holds elements 64j + 16k .. 64j + 16k + 15, the 2-bit
+        // fields of each byte in order
+        const float d = f16_finite(r.wd[0]);
+        c.ws[2 * j][row] = d;
+        c.ws[2 * j + 1][row] = d;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) ws[t] = d;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const uint4 v = r.v[c];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t wv = comp(v, k);
-                q[4 * c + k] = make_uint4((uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
-                                          (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
-                                          (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
-                                          (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u));
-            }
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t wv = comp(r.w[0], k);
+            *reinterpret_cast<uint4 *>(dst + 64 * j + 16 * k) =
+                make_uint4((uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
+                           (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
+                           (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
+                           (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u));
         }
-    } else {  // JK_I2_S: group t = 2-bit field t (shift 6 - 2t) of both chunks
+    } else {  // JK_I2_S: 32-group g is 2-bit field g (shift 6 - 2g) of planes 0 (first 16) and 1
+        c.ws[2 * j][row] = w.tensor_scale;
+        c.ws[2 * j + 1][row] = w.tensor_scale;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            ws[t] = w.tensor_scale;
-            const int sh = 6 - 2 * t;
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const uint4 v = r.v[c];
-                q[2 * t + c] = make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x03030303u, 0x01010101u),
-                                          (uint32_t)bytes_sub((v.y >> sh) & 0x03030303u, 0x01010101u),
-                                          (uint32_t)bytes_sub((v.z >> sh) & 0x03030303u, 0x01010101u),
-                                          (uint32_t)bytes_sub((v.w >> sh) & 0x03030303u, 0x01010101u));
-            }
-        }
-    }
-}
-
-template <int Q>
-__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage &r);
-
-// Global loads of chunk kc into the staging registers of this thread's role.
-template <int Q>
-__device__ __forceinline__ void chunk_load(Stage &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1, int m0,
-                                           int M, int kc) {
-    // two one-sided branches rather than if / else: the roles' final register writes must
-    // not be merged into one store with a selected address (which forces a stack copy)
-    if (threadIdx.x < 256) chunk_w_load<Q>(w, n0, r1, kc, r);
-    if (threadIdx.x >= 256) chunk_x_load<Q>(a, m0, M, kc, r);
-}
-
-// Activation role: thread t = threadIdx.x - 256 of waves 4-7.
-template <int Q>
-__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage &r) {
-    const int t = threadIdx.x - 256;
-    int k = kKC * kc + 16 * (t & 15);
-    if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
-    static_for<8>([&](auto i) {
-        const int m = min(m0 + 16 * i + (t >> 4), M - 1);
-        r.v[i] = ldg16(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + k);
-    });
-    const int m = min(m0 + (t >> 1), M - 1);
-    static_for<4>([&](auto j) {
-        const int b = min(8 * kc + 4 * (t & 1) + j, (int)a.k_blocks32 - 1);
-        r.d[j] = __float_as_uint(a.scales[(size_t)m * a.k_blocks32 + b]);
-        r.d[4 + j] = GemmFmt<Q>::MINS ? __float_as_uint(a.sums[(size_t)m * a.k_blocks32 + b]) : 0u;
-    });
-}
-
-// Unpack the staging registers and write them to the chunk's LDS tiles.
-template <int Q>
-__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, GemmChunk &c) {
-    using F = GemmFmt<Q>;
-    if (threadIdx.x >= 256) {
-        const int t = threadIdx.x - 256;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<uint4 *>(c.b + (16 * i + (t >> 4)) * kRowB + 16 * (t & 15)) = r.v[i];
-        const int tok = t >> 1, g0 = 4 * (t & 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            c.xs[g0 + j][tok] = __uint_as_float(r.d[j]);
-            if constexpr (F::MINS) c.xm[g0 + j][tok] = __uint_as_float(r.d[4 + j]);
-        }
-        return;
-    }
-    const int t = threadIdx.x;
-    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
-        const int piece = t & 7;
-#pragma unroll
-        for (int i = 0; i < (Q == JK_Q8_0 ? 8 : 4); ++i) {
-            uint8_t *dst = c.a + (32 * (i & 3) + (t >> 3)) * kRowB + 32 * piece;
-            if constexpr (Q == JK_Q8_0) {
-                *reinterpret_cast<uint4 *>(dst + 16 * (i >> 2)) = r.v[i];
-            } else {
-                const uint4 v = r.v[i];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int sh = 4 * hh;
-                    *reinterpret_cast<uint4 *>(dst + 16 * hh) =
-                        make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x0F0F0F0Fu, 0x08080808u),
-                                   (uint32_t)bytes_sub((v.y >> sh) & 0x0F0F0F0Fu, 0x08080808u),
-                                   (uint32_t)bytes_sub((v.z >> sh) & 0x0F0F0F0Fu, 0x08080808u),
-                                   (uint32_t)bytes_sub((v.w >> sh) & 0x0F0F0F0Fu, 0x08080808u));
-                }
-            }
-        }
-        const int row = t >> 1, h = t & 1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) c.ws[4 * h + j][row] = f16_finite(r.d[j]);
-    } else {
-        const int row = t >> 1, h = t & 1;
-        uint4 q[8];
-        float ws[8], wm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        chunk_w_unpack<Q>(w, r, h, q, ws, wm);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(c.a + row * kRowB + 128 * h + 16 * i) = q[i];
-#pragma unroll
-        for (int g = 0; g < F::NG; ++g) c.ws[F::NG * h + g][row] = ws[g];
-        if constexpr (F::MINS)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) c.wm[4 * h + g][row] = wm[g];
+        for (int g = 0; g < 4; ++g) *reinterpret_cast<uint4 *>(dst + 32 * g + 16 * j) = crumb4(r.w[0], 6 - 2 * g);
     }
 }
 
@@ -302,8 +259,8 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, 
 // elements for TQ2_0, 128 for I2_S, 32 for Q8_0) the block's MFMAs accumulate in i32 and the
 // epilogue runs once per block.
 template <int Q, int GB = 1>
-__global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
-                                                            int r0, int r1) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void gemm_repacked_kernel(
+    WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
     using F = GemmFmt<Q>;
     static_assert(GB == 1 || F::GK == 32, "block accumulation needs 32-element steps");
     __shared__ __align__(16) GemmChunk cs;
@@ -319,7 +276,7 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
     const int n0 = r0 + tn * kTN, m0 = tm * kTM;
     const int M = (int)a.m;
     const int steps = w.cols / 32;
-    const int nchunks = (steps + 7) / 8;
+    const int nchunks = (steps + kSteps - 1) / kSteps;
     const int hl = lane >> 5, jl = lane & 31;
     const int tok = 32 * wmi + jl;
 
@@ -332,7 +289,7 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
     v16i cacc[2] = {v16i{0}, v16i{0}};  // i32 partials of the current scale block (GB > 1)
     Stage rg;
     chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
-    chunk_store<Q>(w, rg, cs);
+    chunk_store<Q>(w, rg, cs, 0);
     __syncthreads();
     for (int kc = 0; kc < nchunks; ++kc) {
         const bool more = kc + 1 < nchunks;
@@ -353,7 +310,7 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
                         else c[nt] = cacc[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, cacc[nt], 0, 0, 0);
                     }
                     if constexpr (GB > 1) {
-                        if (st % GB != GB - 1) continue;  // block not complete: no epilogue yet
+                        if ((kSteps * kc + st) % GB != GB - 1) continue;  // block not complete: no epilogue yet
                         cacc[0] = v16i{0};
                         cacc[1] = v16i{0};
                     }
@@ -371,8 +328,8 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
                 // product, as a VALU multiply gives, except that -0 comes out +0 -- which the
                 // accumulation cannot observe, as an accumulator that starts at +0.0 never
                 // becomes -0. Lane l supplies the scale of row 64 wn + l (block l / 32 = nt)
-                // and of token tok. Both results share c's layout: lane holds token column
-                // jl, weight rows 8 * (v / 4) + 4 * hl + v % 4 of block nt in element 16 nt + v.
+                // and of token tok. Both results share c's layout: lane holds token column jl,
+                // weight rows 8 * (v / 4) + 4 * hl + v % 4 of block nt in element 16 nt + v.
                 const int g = (32 / F::GK) * st + gg;
                 const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][64 * wn + lane], xs, v32f{0}, 0, 0, 0);
                 v32f pm;
@@ -387,11 +344,11 @@ __global__ __launch_bounds__(512) void gemm_repacked_kernel(WeightDev w, jk_act_
                     }
             }
         };
-        const int nst = min(8, steps - 8 * kc);
+        const int nst = min(kSteps, steps - kSteps * kc);
         for (int st = 0; st < nst; ++st) step(st);
         if (more) {
             __syncthreads();
-            chunk_store<Q>(w, rg, cs);
+            chunk_store<Q>(w, rg, cs, kc + 1);
             __syncthreads();
         }
     }
