@@ -8,17 +8,17 @@
 // group's integer partial is exact and the f32 epilogue runs per group in K order: each
 // output keeps the reference's arithmetic and order, bit for bit.
 //
-// Tiling: a workgroup of 4 waves computes a 128 (weight rows) x 64 (tokens) tile, each wave
-// 64 x 32 as two 32x32 MFMA tiles. K advances in chunks of 128 elements (4 steps of 32; half
-// a super-block of the 256-element formats). While the 4 steps of a chunk are evaluated
-// from LDS, the next chunk is loaded into registers with coalesced reads -- every thread a
-// share of both tiles -- and after a barrier it is unpacked to i8 and written to LDS. LDS rows are padded from 128 to 144 bytes so the 16-byte fragment
-// reads of 16 lanes land on distinct banks. A workgroup needs 35 KB of LDS and at most 168
-// VGPRs per lane, so three workgroups share a CU: while one waits at its barrier or on its
-// loads, the others compute.
+// Tiling: a workgroup computes a TN (weight rows) x TM (tokens) tile with 2 TN threads, two
+// per weight row when staging. Each wave computes up to 64 x 32 outputs as 32x32 MFMA tiles.
+// K advances in chunks of 128 elements (4 steps of 32; half a super-block of the
+// 256-element formats). While the 4 steps of a chunk are evaluated from LDS, the next chunk
+// is loaded into registers with coalesced reads -- every thread a share of both tiles -- and
+// after a barrier it is unpacked to i8 and written to LDS. LDS rows are padded from 128 to
+// 144 bytes so the 16-byte fragment reads of 16 lanes land on distinct banks.
+// Tile shapes: 128 x 64 (4 waves, 35 KB of LDS, <= 168 VGPRs: three workgroups per CU, so
+// while one waits at its barrier or on its loads the others compute) for large launches;
+// 64 x 64 (2 waves) and 32 x 32 (1 wave) when the large tiles would leave CUs idle.
 #include <string.h>
-
-#include <utility>
 
 #include "jk_device.hpp"
 
@@ -28,9 +28,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-constexpr int kTN = 128;      // weight rows per workgroup
-constexpr int kTM = 64;       // tokens per workgroup
-constexpr int kThreads = 256;
 constexpr int kKC = 128;      // K elements per chunk
 constexpr int kSteps = 4;     // 32-element steps per chunk
 constexpr int kRowB = 144;    // padded LDS bytes per 128-byte row
@@ -41,24 +38,26 @@ template <int Q> struct GemmFmt {
     static constexpr int NG = 128 / GK;                 // scale groups per chunk
 };
 
-struct GemmChunk {
-    uint8_t a[kTN * kRowB];  // weights, i8, [row][k]
-    uint8_t b[kTM * kRowB];  // activations, i8, [token][k]
-    float ws[8][kTN];        // weight scale per scale group of the chunk
-    float wm[4][kTN];        // weight min per 32-group (Q4_K)
-    float xs[4][kTM];        // activation scale per 32-block
-    float xm[4][kTM];        // activation sum per 32-block (Q4_K)
+template <int TN, int TM> struct Tile {
+    static constexpr int THREADS = 2 * TN;        // two staging threads per weight row
+    static constexpr int WAVES = THREADS / 64;
+    static constexpr int RW = TN < 64 ? TN : 64;  // weight rows per wave
+    static constexpr int NT = RW / 32;            // 32-row MFMA blocks per wave
+    static constexpr int WR = TN / RW;            // waves along the rows
+    static constexpr int XL = 8 * TM / THREADS;   // activation loads per thread and chunk
+    static constexpr int XS = 4 * TM / THREADS;   // activation scales per thread and chunk
+    static constexpr int WPE = TN == 128 ? 3 : 2;  // waves per SIMD the register budget allows
+    static_assert(WR * (TM / 32) == WAVES && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
 };
 
-// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): register arrays
-// indexed by it get constant indices from the start, not only after loop unrolling.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F> __device__ __forceinline__ void static_for(F &&f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
+template <int TN, int TM> struct GemmChunk {
+    uint8_t a[TN * kRowB];  // weights, i8, [row][k]
+    uint8_t b[TM * kRowB];  // activations, i8, [token][k]
+    float ws[8][TN];        // weight scale per scale group of the chunk
+    float wm[4][TN];        // weight min per 32-group (Q4_K)
+    float xs[4][TM];        // activation scale per 32-block
+    float xm[4][TM];        // activation sum per 32-block (Q4_K)
+};
 
 // One 16-byte global load without the streaming hint: a weight tile is read once per
 // token tile, so its lines are meant to stay in L2 for the neighbouring workgroups.
@@ -75,29 +74,29 @@ __device__ __forceinline__ const uint8_t *plane_ptr(const WeightDev &w, int c, i
 // carry the same load and unpack work.
 //  Q8_0 / Q4_0: a chunk is 4 blocks, 64 contiguous bytes per (plane, row); 4 consecutive
 //   lanes read one such segment (piece t % 4 = block 4kc + t % 4), load i covers rows
-//   t / 4 + 64 (i % 2) of plane i / 2. Scales: row t / 2, blocks 4kc + 2 (t % 2) ...
+//   t / 4 + TN/2 (i % 2) of plane i / 2. Scales: row t / 2, blocks 4kc + 2 (t % 2) ...
 //  K-quants, TQ2_0 (256-element blocks): chunk kc is half h = kc % 2 of block kc / 2;
 //   I2_S (128-element blocks): chunk kc is block kc. Thread t takes row t / 2 and part
 //   j = t % 2 of the chunk's planes.
-//  Activations: load i covers token t / 8 + 32i, piece t % 8 of its 128-byte row; scale
-//   (and sum) of token t / 4, block 4kc + t % 4.
-struct Stage {
-    uint4 w[4];      // weight plane bytes
-    uint32_t wd[2];  // weight f16 scales (Q8_0 / Q4_0: two blocks; Q6_K, TQ2_0: d)
-    uint4 x[2];      // activation bytes
-    uint32_t xd[2];  // activation scale, sum (Q4_K)
+//  Activations: load i covers token t / 8 + (threads / 8) i, piece t % 8 of its 128-byte
+//   row; scale j (and sum) of entry e = XS t + j: token e / 4, block 4kc + e % 4.
+template <int TN, int TM> struct Stage {
+    uint4 w[4];                         // weight plane bytes
+    uint32_t wd[2];                     // weight f16 scales (Q8_0 / Q4_0: two blocks; Q6_K, TQ2_0: d)
+    uint4 x[Tile<TN, TM>::XL];          // activation bytes
+    uint32_t xd[2][Tile<TN, TM>::XS];   // activation scale, sum (Q4_K)
 };
 
 // Blocks past the row end (a partial last chunk) are read clamped and never used; rows
 // past r1 are read clamped to r1 - 1 and never stored.
-template <int Q>
-__device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage &r) {
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage<TN, TM> &r) {
     const int nb = w.nb, t = threadIdx.x;
     if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
         const int b = min(4 * kc + (t & 3), nb - 1);
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
-            const int n = min(n0 + (t >> 2) + 64 * (i & 1), r1 - 1);
+            const int n = min(n0 + (t >> 2) + TN / 2 * (i & 1), r1 - 1);
             r.w[i] = ldg16(plane_ptr(w, i >> 1, n, b));
         }
         const size_t srow = (size_t)min(n0 + (t >> 1), r1 - 1) * (size_t)nb;
@@ -127,25 +126,31 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
     }
 }
 
-template <int Q>
-__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage &r) {
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage<TN, TM> &r) {
+    using T = Tile<TN, TM>;
     const int t = threadIdx.x;
     int k = kKC * kc + 16 * (t & 7);
     if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int m = min(m0 + (t >> 3) + 32 * i, M - 1);
+    for (int i = 0; i < T::XL; ++i) {
+        const int m = min(m0 + (t >> 3) + T::THREADS / 8 * i, M - 1);
         r.x[i] = ldg16(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + k);
     }
-    const size_t sidx = (size_t)min(m0 + (t >> 2), M - 1) * a.k_blocks32 + (size_t)min(4 * kc + (t & 3), (int)a.k_blocks32 - 1);
-    r.xd[0] = __float_as_uint(a.scales[sidx]);
-    r.xd[1] = GemmFmt<Q>::MINS ? __float_as_uint(a.sums[sidx]) : 0u;
+#pragma unroll
+    for (int j = 0; j < T::XS; ++j) {
+        const int e = T::XS * t + j;
+        const size_t sidx =
+            (size_t)min(m0 + (e >> 2), M - 1) * a.k_blocks32 + (size_t)min(4 * kc + (e & 3), (int)a.k_blocks32 - 1);
+        r.xd[0][j] = __float_as_uint(a.scales[sidx]);
+        r.xd[1][j] = GemmFmt<Q>::MINS ? __float_as_uint(a.sums[sidx]) : 0u;
+    }
 }
 
 // Global loads of chunk kc into this thread's staging registers.
-template <int Q>
-__device__ __forceinline__ void chunk_load(Stage &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1, int m0,
-                                           int M, int kc) {
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void chunk_load(Stage<TN, TM> &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1,
+                                           int m0, int M, int kc) {
     chunk_w_load<Q>(w, n0, r1, kc, r);
     chunk_x_load<Q>(a, m0, M, kc, r);
 }
@@ -164,21 +169,26 @@ __device__ __forceinline__ uint4 crumb4(uint4 v, int sh) {
 // Unpack the staging registers to i8 with repack_block_scaled_range_into_i8's values
 // (repack.rs:1724-2103) and write them, with the scale (and min) of each scale group, to
 // the chunk's LDS tiles.
-template <int Q>
-__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, GemmChunk &c, int kc) {
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, TM> &r, GemmChunk<TN, TM> &c, int kc) {
+    using T = Tile<TN, TM>;
     const int t = threadIdx.x;
     {  // activations
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            *reinterpret_cast<uint4 *>(c.b + ((t >> 3) + 32 * i) * kRowB + 16 * (t & 7)) = r.x[i];
-        c.xs[t & 3][t >> 2] = __uint_as_float(r.xd[0]);
-        if constexpr (GemmFmt<Q>::MINS) c.xm[t & 3][t >> 2] = __uint_as_float(r.xd[1]);
+        for (int i = 0; i < T::XL; ++i)
+            *reinterpret_cast<uint4 *>(c.b + ((t >> 3) + T::THREADS / 8 * i) * kRowB + 16 * (t & 7)) = r.x[i];
+#pragma unroll
+        for (int j = 0; j < T::XS; ++j) {
+            const int e = T::XS * t + j;
+            c.xs[e & 3][e >> 2] = __uint_as_float(r.xd[0][j]);
+            if constexpr (GemmFmt<Q>::MINS) c.xm[e & 3][e >> 2] = __uint_as_float(r.xd[1][j]);
+        }
     }
     if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
         const int piece = t & 3;
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
-            uint8_t *dst = c.a + ((t >> 2) + 64 * (i & 1)) * kRowB + 32 * piece;
+            uint8_t *dst = c.a + ((t >> 2) + TN / 2 * (i & 1)) * kRowB + 32 * piece;
             if constexpr (Q == JK_Q8_0) {
                 *reinterpret_cast<uint4 *>(dst + 16 * (i >> 1)) = r.w[i];
             } else {
@@ -258,94 +268,106 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage &r, 
 // one epilogue per step); for BitLinear (one scale per token and per weight block: 256
 // elements for TQ2_0, 128 for I2_S, 32 for Q8_0) the block's MFMAs accumulate in i32 and the
 // epilogue runs once per block.
-template <int Q, int GB = 1>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void gemm_repacked_kernel(
-    WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+template <int Q, int GB, int TN, int TM>
+__global__ __launch_bounds__(2 * TN) __attribute__((amdgpu_waves_per_eu(Tile<TN, TM>::WPE))) void
+gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
     using F = GemmFmt<Q>;
+    using T = Tile<TN, TM>;
+    constexpr int NT = T::NT, RW = T::RW;
     static_assert(GB == 1 || F::GK == 32, "block accumulation needs 32-element steps");
-    __shared__ __align__(16) GemmChunk cs;
+    __shared__ __align__(16) GemmChunk<TN, TM> cs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wn = wave & 1, wmi = wave >> 1;  // wave tile: rows 64 * wn .., tokens 32 * wmi ..
+    const int wn = wave % T::WR, wmi = wave / T::WR;  // wave tile: rows RW * wn .., tokens 32 * wmi ..
     // Workgroup i runs on XCD i % 8. Tile order: the token tiles of one weight row tile go
     // to consecutive workgroups of one XCD, so they run together and share the row tile's
     // weights in that XCD's L2; row tiles are dealt round-robin over the XCDs.
-    const int ntn = (r1 - r0 + kTN - 1) / kTN, ntm = ((int)a.m + kTM - 1) / kTM;
+    const int ntn = (r1 - r0 + TN - 1) / TN, ntm = ((int)a.m + TM - 1) / TM;
     const int wg = (int)blockIdx.x, local = wg >> 3;
     const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
     if (tn >= ntn) return;  // padding workgroups of the last round-robin group
-    const int n0 = r0 + tn * kTN, m0 = tm * kTM;
+    const int n0 = r0 + tn * TN, m0 = tm * TM;
     const int M = (int)a.m;
     const int steps = w.cols / 32;
     const int nchunks = (steps + kSteps - 1) / kSteps;
     const int hl = lane >> 5, jl = lane & 31;
     const int tok = 32 * wmi + jl;
 
-    float acc[2][16];
+    float acc[NT][16];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
 
-    v16i cacc[2] = {v16i{0}, v16i{0}};  // i32 partials of the current scale block (GB > 1)
-    Stage rg;
+    v16i cacc[NT];  // i32 partials of the current scale block (GB > 1)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) cacc[nt] = v16i{0};
+    // the scale-product MFMA covers two 32-row blocks; lane l supplies row RW wn + srow
+    const int srow = RW * wn + (NT == 2 ? lane : jl);
+    // chunk kc from LDS
+    auto step = [&](int kc, int st) {
+        const float xs = cs.xs[st][tok];
+        const float xsum = F::MINS ? cs.xm[st][tok] : 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < 32 / F::GK; ++gg) {
+            v16i c[NT];
+            if constexpr (F::GK == 32) {
+                const v4i bq = *reinterpret_cast<const v4i *>(cs.b + tok * kRowB + 32 * st + 16 * hl);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const v4i aq =
+                        *reinterpret_cast<const v4i *>(cs.a + (RW * wn + 32 * nt + jl) * kRowB + 32 * st + 16 * hl);
+                    if constexpr (GB == 1) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+                    else c[nt] = cacc[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, cacc[nt], 0, 0, 0);
+                }
+                if constexpr (GB > 1) {
+                    if ((kSteps * kc + st) % GB != GB - 1) continue;  // block not complete: no epilogue yet
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) cacc[nt] = v16i{0};
+                }
+            } else {
+                const long bq = *reinterpret_cast<const long *>(cs.b + tok * kRowB + 32 * st + 16 * gg + 8 * hl);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const long aq = *reinterpret_cast<const long *>(cs.a + (RW * wn + 32 * nt + jl) * kRowB +
+                                                                    32 * st + 16 * gg + 8 * hl);
+                    c[nt] = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, bq, v16i{0}, 0, 0, 0);
+                }
+            }
+            // Scale products xs * ws (and xsum * wm) of all 64 x 32 outputs as two 32 x 32
+            // f32 outer products (K = 1, zero accumulator): each is the single rounded f32
+            // product, as a VALU multiply gives, except that -0 comes out +0 -- which the
+            // accumulation cannot observe, as an accumulator that starts at +0.0 never
+            // becomes -0. Lane l supplies the scale of row srow (block l / 32 = nt; with
+            // one block per wave both halves repeat it) and of token tok. Both results share
+            // c's layout: lane holds token column jl, weight rows 8 * (v / 4) + 4 * hl + v % 4
+            // of block nt in element 16 nt + v.
+            const int g = (32 / F::GK) * st + gg;
+            const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][srow], xs, v32f{0}, 0, 0, 0);
+            v32f pm;
+            if constexpr (F::MINS) pm = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.wm[st][srow], xsum, v32f{0}, 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float t = (float)c[nt][v] * p[16 * nt + v];
+                    if constexpr (F::MINS) acc[nt][v] += t - pm[16 * nt + v];
+                    else acc[nt][v] += t;
+                }
+        }
+    };
+    auto compute = [&](int kc) {
+        const int nst = min(kSteps, steps - kSteps * kc);
+        for (int st = 0; st < nst; ++st) step(kc, st);
+    };
+
+    Stage<TN, TM> rg;
     chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
     chunk_store<Q>(w, rg, cs, 0);
     __syncthreads();
     for (int kc = 0; kc < nchunks; ++kc) {
         const bool more = kc + 1 < nchunks;
         if (more) chunk_load<Q>(rg, w, a, n0, r1, m0, M, kc + 1);
-        auto step = [&](int st) {
-            const float xs = cs.xs[st][tok];
-            const float xsum = F::MINS ? cs.xm[st][tok] : 0.0f;
-#pragma unroll
-            for (int gg = 0; gg < 32 / F::GK; ++gg) {
-                v16i c[2];
-                if constexpr (F::GK == 32) {
-                    const v4i bq = *reinterpret_cast<const v4i *>(cs.b + tok * kRowB + 32 * st + 16 * hl);
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
-                        const v4i aq =
-                            *reinterpret_cast<const v4i *>(cs.a + (64 * wn + 32 * nt + jl) * kRowB + 32 * st + 16 * hl);
-                        if constexpr (GB == 1) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
-                        else c[nt] = cacc[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, cacc[nt], 0, 0, 0);
-                    }
-                    if constexpr (GB > 1) {
-                        if ((kSteps * kc + st) % GB != GB - 1) continue;  // block not complete: no epilogue yet
-                        cacc[0] = v16i{0};
-                        cacc[1] = v16i{0};
-                    }
-                } else {
-                    const long bq = *reinterpret_cast<const long *>(cs.b + tok * kRowB + 32 * st + 16 * gg + 8 * hl);
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
-                        const long aq = *reinterpret_cast<const long *>(cs.a + (64 * wn + 32 * nt + jl) * kRowB +
-                                                                        32 * st + 16 * gg + 8 * hl);
-                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x16_i8(aq, bq, v16i{0}, 0, 0, 0);
-                    }
-                }
-                // Scale products xs * ws (and xsum * wm) of all 64 x 32 outputs as two 32 x 32
-                // f32 outer products (K = 1, zero accumulator): each is the single rounded f32
-                // product, as a VALU multiply gives, except that -0 comes out +0 -- which the
-                // accumulation cannot observe, as an accumulator that starts at +0.0 never
-                // becomes -0. Lane l supplies the scale of row 64 wn + l (block l / 32 = nt)
-                // and of token tok. Both results share c's layout: lane holds token column jl,
-                // weight rows 8 * (v / 4) + 4 * hl + v % 4 of block nt in element 16 nt + v.
-                const int g = (32 / F::GK) * st + gg;
-                const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][64 * wn + lane], xs, v32f{0}, 0, 0, 0);
-                v32f pm;
-                if constexpr (F::MINS) pm = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.wm[st][64 * wn + lane], xsum, v32f{0}, 0, 0, 0);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const float t = (float)c[nt][v] * p[16 * nt + v];
-                        if constexpr (F::MINS) acc[nt][v] += t - pm[16 * nt + v];
-                        else acc[nt][v] += t;
-                    }
-            }
-        };
-        const int nst = min(kSteps, steps - kSteps * kc);
-        for (int st = 0; st < nst; ++st) step(st);
+        compute(kc);
         if (more) {
             __syncthreads();
             chunk_store<Q>(w, rg, cs, kc + 1);
@@ -357,13 +379,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     if (m < M) {
         const size_t ld = (size_t)(r1 - r0);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int n = n0 + 64 * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
+                const int n = n0 + RW * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
                 if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = acc[nt][v];
             }
     }
+}
+
+static long cu_count() {
+    static long n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        n = hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+                ? v
+                : 256;
+    }
+    return n;
+}
+
+// Tile shape of a launch: the largest tile that still gives every CU two workgroups.
+static int gemm_tile(long rows, long m) {
+    const long ncu = cu_count();
+    auto tiles = [&](long tn, long tm) { return (rows + tn - 1) / tn * ((m + tm - 1) / tm); };
+    if (tiles(128, 64) >= 2 * ncu) return 0;
+    if (tiles(64, 64) >= 2 * ncu) return 1;
+    return 2;
+}
+
+template <int Q, int GB, int TN, int TM>
+static void launch_tile(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    const size_t ntn = (size_t)(r1 - r0 + TN - 1) / TN, ntm = (a.m + TM - 1) / TM;
+    const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(Tile<TN, TM>::THREADS);
+    hipLaunchKernelGGL((gemm_repacked_kernel<Q, GB, TN, TM>), grid, block, 0, s, w, a, y, r0, r1);
+}
+
+template <int Q, int GB>
+static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    switch (gemm_tile(r1 - r0, (long)a.m)) {
+    case 0: launch_tile<Q, GB, 128, 64>(s, w, a, y, r0, r1); break;
+    case 1: launch_tile<Q, GB, 64, 64>(s, w, a, y, r0, r1); break;
+    default: launch_tile<Q, GB, 32, 32>(s, w, a, y, r0, r1); break;
+    }
+    return check_launch("gemm_repacked_kernel");
 }
 
 // bitlinear_i8_rvv (ime.rs:882-938) for m tokens on int8 MFMA: the activation rows act[m][k]
@@ -378,30 +438,24 @@ jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t 
     a.k_blocks32 = 1;
     a.qs = const_cast<int8_t *>(act);
     a.scales = const_cast<float *>(act_scales);
-    const size_t ntn = (size_t)(w.rows + kTN - 1) / kTN, ntm = ((size_t)m + kTM - 1) / kTM;
-    const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(kThreads);
     switch (w.quant) {
-    case JK_TQ2_0: hipLaunchKernelGGL((gemm_repacked_kernel<JK_TQ2_0, 8>), grid, block, 0, s, w, a, y, 0, w.rows); break;
-    case JK_I2_S: hipLaunchKernelGGL((gemm_repacked_kernel<JK_I2_S, 4>), grid, block, 0, s, w, a, y, 0, w.rows); break;
-    case JK_Q8_0: hipLaunchKernelGGL((gemm_repacked_kernel<JK_Q8_0, 1>), grid, block, 0, s, w, a, y, 0, w.rows); break;
+    case JK_TQ2_0: return launch_gemm<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows);
+    case JK_I2_S: return launch_gemm<JK_I2_S, 4>(s, w, a, y, 0, w.rows);
+    case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, 0, w.rows);
     default: return fail(JK_CAPABILITY_MISMATCH, "bitlinear: unsupported quant %d", w.quant);
     }
-    return check_launch("gemm_repacked_kernel (bitlinear)");
 }
 
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    const size_t ntn = (size_t)(r1 - r0 + kTN - 1) / kTN, ntm = (a.m + kTM - 1) / kTM;
-    const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(kThreads);
     switch (w.quant) {
-    case JK_Q8_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q8_0>, grid, block, 0, s, w, a, y, r0, r1); break;
-    case JK_Q4_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q4_0>, grid, block, 0, s, w, a, y, r0, r1); break;
-    case JK_Q4_K: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q4_K>, grid, block, 0, s, w, a, y, r0, r1); break;
-    case JK_Q6_K: hipLaunchKernelGGL(gemm_repacked_kernel<JK_Q6_K>, grid, block, 0, s, w, a, y, r0, r1); break;
-    case JK_TQ2_0: hipLaunchKernelGGL(gemm_repacked_kernel<JK_TQ2_0>, grid, block, 0, s, w, a, y, r0, r1); break;
-    case JK_I2_S: hipLaunchKernelGGL(gemm_repacked_kernel<JK_I2_S>, grid, block, 0, s, w, a, y, r0, r1); break;
+    case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, r0, r1);
+    case JK_Q4_0: return launch_gemm<JK_Q4_0, 1>(s, w, a, y, r0, r1);
+    case JK_Q4_K: return launch_gemm<JK_Q4_K, 1>(s, w, a, y, r0, r1);
+    case JK_Q6_K: return launch_gemm<JK_Q6_K, 1>(s, w, a, y, r0, r1);
+    case JK_TQ2_0: return launch_gemm<JK_TQ2_0, 1>(s, w, a, y, r0, r1);
+    case JK_I2_S: return launch_gemm<JK_I2_S, 1>(s, w, a, y, r0, r1);
     default: return fail(JK_CAPABILITY_MISMATCH, "gemm: unsupported quant %d", w.quant);
     }
-    return check_launch("gemm_repacked_kernel");
 }
 
 }  // namespace jk

@@ -391,6 +391,24 @@ def test_gemm_repacked(gpu, quant, m, rows, cols):
     assert same_bits(got_slice, ref[:, 3:rows - 5])
 
 
+@pytest.mark.parametrize("quant", [Q8_0, Q4_0, Q4_K, Q6_K, TQ2_0, I2_S])
+@pytest.mark.parametrize("m", [500, 250, 60])
+def test_gemm_tile_shapes(gpu, quant, m):
+    """8200 rows: 500 tokens launch 128x64 tiles, 250 tokens 64x64, 60 tokens 32x32 (the
+    launcher takes the largest tile that gives 256 CUs two workgroups each); the last row
+    tile and token tile are partial. Oracle on row windows."""
+    torch = gpu
+    rows, cols = 8200, 512
+    raw = synth.random_weights(quant, rows, cols, seed=m + 3 * quant, specials=True)
+    x = np.random.default_rng(m).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    got = gpu_gemm(torch, w, x, m)
+    act = O.ActQ8(x, m, cols)
+    for r0 in (0, 4091, rows - 45):
+        ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, act, r0, r0 + 45)
+        assert same_bits(got[:, r0:r0 + 45], ref), (r0, mismatch(got[:, r0:r0 + 45], ref))
+
+
 @pytest.mark.parametrize("m", [64, 512])
 def test_gemm_q8_0_prefill_shape_rows_sample(gpu, m):
     """C4 prefill shape 14336 x 4096, M tokens: full GPU GEMM, oracle on row windows."""
@@ -424,6 +442,28 @@ def test_bitlinear(gpu, quant, m, rows, cols):
     torch.cuda.synchronize()
     got = host(dy, np.float32, m * rows).reshape(m, rows)
     for i in range(m):
+        ref = O.bitlinear_i8(quant, [rows, cols], raw, a[i], float(sc[i]), rows)
+        assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
+
+
+@pytest.mark.parametrize("quant", [TQ2_0, I2_S, Q8_0])
+@pytest.mark.parametrize("m", [500, 250, 60])
+def test_bitlinear_tile_shapes(gpu, quant, m):
+    """BitLinear token batches on each GEMM tile shape (as test_gemm_tile_shapes), with the
+    block accumulation crossing chunk boundaries; oracle on every 23rd token and the last."""
+    torch = gpu
+    rows, cols = 8200, 512
+    raw = synth.gguf_weights(quant, rows, cols, seed=m + quant) if quant != Q8_0 else \
+        synth.random_weights(quant, rows, cols, seed=m, specials=True)
+    rng = np.random.default_rng(m + 1)
+    a = rng.integers(-128, 128, (m, cols)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    dy = empty(torch, 4 * m * rows)
+    jk.dev_bitlinear_i8(w, dev(torch, a), dev(torch, sc), m, cols, dy, m * rows)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, m * rows).reshape(m, rows)
+    for i in list(range(0, m, 23)) + [m - 1]:
         ref = O.bitlinear_i8(quant, [rows, cols], raw, a[i], float(sc[i]), rows)
         assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
 
