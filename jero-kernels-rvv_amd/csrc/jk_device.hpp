@@ -27,12 +27,15 @@ __device__ __forceinline__ float row_ror1(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false));
 }
 
-// Ordered f32 accumulation across the 16 lanes of a DPP row: for s in 0..g, the lane at
-// row position s computes acc = acc(position s-1) + v, so after g steps position g-1
-// holds (((acc_in + v0) + v1) + ...) + v(g-1) with acc_in taken from position 15.
-// Every lane of the wave must execute this (g is wave-uniform).
-__device__ __forceinline__ float chain_add(float acc, float v, int g) {
-    for (int s = 0; s < g; ++s) acc = row_ror1(acc) + v;
+// Ordered f32 accumulation across the 16 lanes of a DPP row: in step s the lane at row
+// position s computes acc = acc(position s-1) + v, so after the 16 straight-line steps
+// position 15 holds (((acc_in + v0) + v1) + ...) + v15 with acc_in taken from position 15.
+// A row of g < 16 values passes -0.0 in positions g..15: x + (-0.0) == x for every x
+// (+0 and -0 included), so position 15 then holds exactly the sum of the g values.
+// Every lane of the wave must execute this.
+__device__ __forceinline__ float chain_add(float acc, float v) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) acc = row_ror1(acc) + v;
     return acc;
 }
 

@@ -160,12 +160,11 @@ __global__ __launch_bounds__(64 * kVdWaves) void vec_dot_f32_kernel(WeightDev w,
     for (int it = 0; it < iters; ++it) {
         const int b = it * LPR + p;
         if (it > 0) vd_load<Q>(blk, w, r, min(b, nb - 1));
-        const float v = b < nb ? vd_block<Q>(blk, xs + (size_t)XS * min(b, nb - 1), w.tensor_scale) : 0.0f;
-        const int g = min(LPR, nb - it * LPR);
-        if constexpr (LPR == 16) acc = chain_add(acc, v, g);
-        else acc = fold_wave(acc, v, g, red);
+        const float v = b < nb ? vd_block<Q>(blk, xs + (size_t)XS * min(b, nb - 1), w.tensor_scale) : -0.0f;
+        if constexpr (LPR == 16) acc = chain_add(acc, v);
+        else acc = fold_wave(acc, v, min(LPR, nb - it * LPR), red);
     }
-    const int writer = LPR == 16 ? nb - LPR * (iters - 1) - 1 : 0;
+    const int writer = LPR == 16 ? 15 : 0;
     if (row < w.rows && p == writer) y[row] = acc;
 }
 
@@ -259,13 +258,11 @@ __global__ __launch_bounds__(256) void bitlinear_kernel(WeightDev w, const int8_
     float acc = 0.0f;
     const int nb = w.nb, iters = (nb + 15) >> 4;
     for (int it = 0; it < iters; ++it) {
-        const int g = min(16, nb - 16 * it);
-        float v = 0.0f;
-        if (p < g) v = bl_block_value(w, r, 16 * it + p, a, as);
-        acc = chain_add(acc, v, g);
+        float v = -0.0f;
+        if (p < nb - 16 * it) v = bl_block_value(w, r, 16 * it + p, a, as);
+        acc = chain_add(acc, v);
     }
-    const int g_last = nb - 16 * (iters - 1);
-    if (active && p == g_last - 1) y[(size_t)m * (size_t)w.rows + row] = acc;
+    if (active && p == 15) y[(size_t)m * (size_t)w.rows + row] = acc;
 }
 
 jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales, int m,

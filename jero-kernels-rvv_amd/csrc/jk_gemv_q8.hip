@@ -488,7 +488,7 @@ struct Walker {
 #pragma unroll
         for (int k = 0; k < T::U; ++k) {
             const int b = (it0 + k) * LPR + p;
-            v[k] = 0.0f;
+            v[k] = -0.0f;  // past the row end: the identity of the ordered fold
             if (b < nb) {
                 if constexpr (T::K) v[k] = block_value<Q>(wr[k], XkLds{s_x + b * T::XB});
                 else v[k] = block_value<Q>(wr[k], X0Lds{s_x + b * T::XB});
@@ -497,9 +497,8 @@ struct Walker {
 #pragma unroll
         for (int k = 0; k < T::U; ++k) {
             if (it0 + k < nit) {
-                const int g = min(LPR, nb - (it0 + k) * LPR);
-                if constexpr (LPR == 16) acc = chain_add(acc, v[k], g);
-                else acc = fold_wave(acc, v[k], g, red);
+                if constexpr (LPR == 16) acc = chain_add(acc, v[k]);
+                else acc = fold_wave(acc, v[k], min(LPR, nb - (it0 + k) * LPR), red);
             }
         }
         if (it0 + T::U >= nit) slot[((u - k0) / stride) * 64 + (threadIdx.x & 63)] = acc;
@@ -507,7 +506,7 @@ struct Walker {
     }
 
     // Lane that holds a row's result after the fold.
-    __device__ __forceinline__ int writer() const { return LPR == 16 ? nb - LPR * (nit - 1) - 1 : 0; }
+    __device__ __forceinline__ int writer() const { return LPR == 16 ? 15 : 0; }
 };
 
 // Register budget: 4 waves per SIMD (<= 128 VGPRs) for Q4_K / Q4_0 / Q8_0 / TQ2_0, 2 for
@@ -656,7 +655,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
 #pragma unroll
         for (int k = 0; k < UF; ++k) {
             const int b = k * LPR + p;
-            v[k] = 0.0f;
+            v[k] = -0.0f;  // past the row end: the identity of the ordered fold
             if (b < nb) {
                 if constexpr (T::K) v[k] = block_value<Q>(Wq[k], XkLds{s_x + b * T::XB});
                 else v[k] = block_value<Q>(Wq[k], X0Lds{s_x + b * T::XB});
@@ -665,9 +664,8 @@ gemv_q8_fast_kernel(GemvGroup grp) {
 #pragma unroll
         for (int k = 0; k < UF; ++k) {
             if (k < nit) {
-                const int g = min(LPR, nb - k * LPR);
-                if constexpr (LPR == 16) acc = chain_add(acc, v[k], g);
-                else acc = fold_wave(acc, v[k], g, red);
+                if constexpr (LPR == 16) acc = chain_add(acc, v[k]);
+                else acc = fold_wave(acc, v[k], min(LPR, nb - k * LPR), red);
             }
         }
         out[q] = acc;
@@ -675,7 +673,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     }
 
     // 4. stores
-    const int writer = LPR == 16 ? nb - LPR * (nit - 1) - 1 : 0;
+    const int writer = LPR == 16 ? 15 : 0;
 #pragma unroll
     for (int q = 0; q < QPW; ++q) {
         const int row = r0 + (base + NW * q) * RPU + sub;
@@ -697,19 +695,17 @@ __global__ __launch_bounds__(256) void gemv_q8_global_kernel(WeightDev w, const 
     const int nb = w.nb;
     const int iters = (nb + 15) >> 4;
     for (int it = 0; it < iters; ++it) {
-        const int g = min(16, nb - 16 * it);
         const int b = 16 * it + p;
-        float v = 0.0f;
-        if (p < g) {
+        float v = -0.0f;  // past the row end: the identity of the ordered fold
+        if (b < nb) {
             WReg<Q> wr;
             wload<Q>(wr, w, r, b);
             if constexpr (QTraits<Q>::K) v = block_value<Q>(wr, XkGlb{static_cast<const jk_block_q8k *>(x) + b});
             else v = block_value<Q>(wr, X0Glb{static_cast<const jk_block_q8_0 *>(x) + b});
         }
-        acc = chain_add(acc, v, g);
+        acc = chain_add(acc, v);
     }
-    const int g_last = nb - 16 * (iters - 1);
-    if (active && p == g_last - 1) y[row - r0] = acc;
+    if (active && p == 15) y[row - r0] = acc;
 }
 
 // ------------------------------------------------------------------ launchers
