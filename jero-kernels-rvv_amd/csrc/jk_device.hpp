@@ -152,14 +152,21 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
-// Ordered fold of one value per lane over a whole wave: lane 0 adds the g values of lanes
-// 0..g-1 in lane order to acc (acc lives in lane 0). red: 64 floats of LDS for this wave.
-__device__ __forceinline__ float fold_wave(float acc, float v, int g, float *red) {
+// Ordered fold of one value per lane over a whole wave: lane 0 adds the values of lanes
+// 0..63 in lane order to acc (acc lives in lane 0); lanes past the row end pass -0.0, the
+// exact identity of f32 addition. red: 64 floats of 16-byte aligned LDS for this wave; the
+// 16 reads are issued before the first add.
+__device__ __forceinline__ float fold_wave(float acc, float v, float *red) {
     const int l = threadIdx.x & 63;
     red[l] = v;
     wave_lds_sync();
-    if (l == 0)
-        for (int i = 0; i < g; ++i) acc += red[i];
+    if (l == 0) {
+        float4 r[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r[i] = reinterpret_cast<const float4 *>(red)[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = (((acc + r[i].x) + r[i].y) + r[i].z) + r[i].w;
+    }
     wave_lds_sync();
     return acc;
 }

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(64 * kVdWaves) void vec_dot_f32_kernel(WeightDev w,
                                                                      float *__restrict__ y) {
     constexpr int RPW = 64 / LPR, E = VdFmt<Q>::E;
     extern __shared__ __align__(16) float s_xf[];
-    __shared__ float s_red[LPR == 64 ? kVdWaves : 1][64];
+    __shared__ __align__(16) float s_red[LPR == 64 ? kVdWaves : 1][64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int sub = lane / LPR, p = lane % LPR;
     const int row = ((int)blockIdx.x * kVdWaves + wave) * RPW + sub;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(64 * kVdWaves) void vec_dot_f32_kernel(WeightDev w,
         if (it > 0) vd_load<Q>(blk, w, r, min(b, nb - 1));
         const float v = b < nb ? vd_block<Q>(blk, xs + (size_t)XS * min(b, nb - 1), w.tensor_scale) : -0.0f;
         if constexpr (LPR == 16) acc = chain_add(acc, v);
-        else acc = fold_wave(acc, v, min(LPR, nb - it * LPR), red);
+        else acc = fold_wave(acc, v, red);
     }
     const int writer = LPR == 16 ? 15 : 0;
     if (row < w.rows && p == writer) y[row] = acc;

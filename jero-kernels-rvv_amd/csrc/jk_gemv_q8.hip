@@ -498,7 +498,7 @@ struct Walker {
         for (int k = 0; k < T::U; ++k) {
             if (it0 + k < nit) {
                 if constexpr (LPR == 16) acc = chain_add(acc, v[k]);
-                else acc = fold_wave(acc, v[k], min(LPR, nb - (it0 + k) * LPR), red);
+                else acc = fold_wave(acc, v[k], red);
             }
         }
         if (it0 + T::U >= nit) slot[((u - k0) / stride) * 64 + (threadIdx.x & 63)] = acc;
@@ -521,7 +521,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kWavesP
 gemv_q8_group_kernel(GemvGroup grp) {
     using T = QTraits<Q>;
     extern __shared__ __align__(16) uint8_t s_x[];
-    __shared__ float s_red[LPR == 64 ? NW : 1][64];
+    __shared__ __align__(16) float s_red[LPR == 64 ? NW : 1][64];
 
     const GemvJob &job = grp.job[job_of_block(grp)];
     const WeightDev &w = job.w;
@@ -608,7 +608,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     using T = QTraits<Q>;
     constexpr int RPU = 64 / LPR, UF = kFastU<Q>;
     extern __shared__ __align__(16) uint8_t s_x[];
-    __shared__ float s_red[LPR == 64 ? NW : 1][64];
+    __shared__ __align__(16) float s_red[LPR == 64 ? NW : 1][64];
 
     const GemvJob &job = grp.job[job_of_block(grp)];
     const WeightDev &w = job.w;
@@ -665,7 +665,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
         for (int k = 0; k < UF; ++k) {
             if (k < nit) {
                 if constexpr (LPR == 16) acc = chain_add(acc, v[k]);
-                else acc = fold_wave(acc, v[k], min(LPR, nb - k * LPR), red);
+                else acc = fold_wave(acc, v[k], red);
             }
         }
         out[q] = acc;
