@@ -265,8 +265,110 @@ __global__ __launch_bounds__(256) void bitlinear_kernel(WeightDev w, const int8_
     if (active && p == 15) y[(size_t)m * (size_t)w.rows + row] = acc;
 }
 
+// The ternary formats for a few tokens: a workgroup of RW rows (16 lanes each, lane p takes
+// blocks p, p + 16, ... as above) issues all its weight loads first, then stages its token's
+// activation row in LDS -- each block padded by 16 bytes, so the 16 lanes of a row, which
+// read 16 different blocks at the same offset, hit distinct banks -- and the activation sum
+// of every block once, then evaluates. Same arithmetic and block order as bitlinear_kernel.
+constexpr int kBlMaxBlocks = 64;  // blocks per row (4 per lane) handled here
+template <int Q> constexpr int kBlBE = Q == JK_TQ2_0 ? 256 : 128;  // elements per block
+template <int Q> constexpr int kBlC = Q == JK_TQ2_0 ? 4 : 2;       // 16-byte chunks per block
+
+template <int Q, int UF, int RW>
+__global__ __launch_bounds__(16 * RW) void bitlinear_ternary_kernel(WeightDev w, const int8_t *__restrict__ act,
+                                                                   const float *__restrict__ act_scales,
+                                                                   float *__restrict__ y) {
+    constexpr int BE = kBlBE<Q>, C = kBlC<Q>, BS = BE + 16;  // LDS stride of a block
+    extern __shared__ __align__(16) uint8_t s_a[];           // nb blocks of BS bytes, then nb sums
+    const int tid = threadIdx.x, p = tid & 15;
+    const int row = (int)blockIdx.x * RW + (tid >> 4), m = (int)blockIdx.y;
+    const int nb = w.nb, r = min(row, w.rows - 1);
+    int *s_sum = reinterpret_cast<int *>(s_a + nb * BS);
+
+    // 1. weight loads (blocks past the row end re-read the last one and are never used)
+    uint4 q[UF][C];
+    uint32_t dq[UF];
+#pragma unroll
+    for (int k = 0; k < UF; ++k) {
+        const int b = min(16 * k + p, nb - 1);
+#pragma unroll
+        for (int c = 0; c < C; ++c) q[k][c] = ld_chunk(w, c, r, b);
+        if constexpr (Q == JK_TQ2_0) dq[k] = w.dplane[(size_t)r * (size_t)nb + (size_t)b];
+    }
+    // 2. the token's activation row, then the sum of every block
+    const uint4 *a4 = reinterpret_cast<const uint4 *>(act + (size_t)m * (size_t)w.cols);
+    for (int i = tid; i < w.cols / 16; i += 16 * RW)
+        *reinterpret_cast<uint4 *>(s_a + 16 * i + 16 * (16 * i / BE)) = a4[i];
+    lds_barrier();
+    for (int b = tid; b < nb; b += 16 * RW) {
+        const int *ab = reinterpret_cast<const int *>(s_a + b * BS);
+        int sx = 0;
+#pragma unroll
+        for (int i = 0; i < BE / 4; ++i) sx = dot4(ab[i], 0x01010101, sx);
+        s_sum[b] = sx;
+    }
+    lds_barrier();
+    // 3. block values (unpack_bitlinear_block_i8 values times the activation), block order
+    const float as = act_scales[m];
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < UF; ++k) {
+        if (16 * k >= nb) break;  // wave-uniform
+        const int b = 16 * k + p;
+        float v = -0.0f;  // past the row end: the identity of the ordered fold
+        if (b < nb) {
+            const int *av = reinterpret_cast<const int *>(s_a + b * BS);
+            int sw = 0;
+            if constexpr (Q == JK_TQ2_0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t wv = comp(q[k][i >> 2], i & 3);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) sw = dot4((int)((wv >> (2 * j)) & 0x03030303u), av[4 * i + j], sw);
+                }
+                v = (float)(sw - s_sum[b]) * (f16_finite(dq[k]) * as);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t wv = comp(q[k][c], i);
+#pragma unroll
+                        for (int grp = 0; grp < 4; ++grp)
+                            sw = dot4((int)((wv >> (6 - 2 * grp)) & 0x03030303u), av[8 * grp + 4 * c + i], sw);
+                    }
+                v = (float)(sw - s_sum[b]) * (w.tensor_scale * as);
+            }
+        }
+        acc = chain_add(acc, v);
+    }
+    if (row < w.rows && p == 15) y[(size_t)m * (size_t)w.rows + row] = acc;
+}
+
+template <int Q, int RW>
+static jk_status launch_bl_ternary(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales,
+                                   int m, float *y) {
+    const dim3 grid((unsigned)((w.rows + RW - 1) / RW), (unsigned)m), block(16 * RW);
+    const size_t lds = (size_t)w.nb * (kBlBE<Q> + 16) + (size_t)w.nb * 4;
+    if (w.nb <= 16) hipLaunchKernelGGL((bitlinear_ternary_kernel<Q, 1, RW>), grid, block, lds, s, w, act, act_scales, y);
+    else if (w.nb <= 32) hipLaunchKernelGGL((bitlinear_ternary_kernel<Q, 2, RW>), grid, block, lds, s, w, act, act_scales, y);
+    else hipLaunchKernelGGL((bitlinear_ternary_kernel<Q, 4, RW>), grid, block, lds, s, w, act, act_scales, y);
+    return check_launch("bitlinear_ternary_kernel");
+}
+
 jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales, int m,
                            float *y) {
+    // 16-byte activation rows (cols is a multiple of the block size) and up to 64 blocks a row
+    const bool ternary = w.quant == JK_TQ2_0 || w.quant == JK_I2_S;
+    if (ternary && w.nb <= kBlMaxBlocks && (reinterpret_cast<uintptr_t>(act) & 15u) == 0) {
+        // 8 rows a workgroup; 4 when that is needed to give every CU two workgroups
+        const bool narrow = (long)(w.rows + 7) / 8 * m < 512;
+        if (w.quant == JK_TQ2_0)
+            return narrow ? launch_bl_ternary<JK_TQ2_0, 4>(s, w, act, act_scales, m, y)
+                          : launch_bl_ternary<JK_TQ2_0, 8>(s, w, act, act_scales, m, y);
+        return narrow ? launch_bl_ternary<JK_I2_S, 4>(s, w, act, act_scales, m, y)
+                      : launch_bl_ternary<JK_I2_S, 8>(s, w, act, act_scales, m, y);
+    }
     hipLaunchKernelGGL(bitlinear_kernel, dim3((unsigned)((w.rows + 15) / 16), (unsigned)m), dim3(256), 0, s, w, act,
                        act_scales, y);
     return check_launch("bitlinear_kernel");

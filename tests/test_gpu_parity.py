@@ -446,6 +446,30 @@ def test_bitlinear(gpu, quant, m, rows, cols):
         assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
 
 
+@pytest.mark.parametrize("quant", [TQ2_0, I2_S])
+@pytest.mark.parametrize("m,rows,cols,offset", [(1, 9, 256 * 65, 0),   # more than 64 blocks a row
+                                                (2, 13, 2560, 1),     # activation not 16-byte aligned
+                                                (5, 11, 1024, 0)])
+def test_bitlinear_few_tokens_paths(gpu, quant, m, rows, cols, offset):
+    """The few-token BitLinear launches: the LDS-staged ternary kernel and the general kernel
+    it leaves rows of more than 64 blocks and unaligned activation rows to."""
+    torch = gpu
+    raw = synth.gguf_weights(quant, rows, cols, seed=rows + quant)
+    rng = np.random.default_rng(cols + offset)
+    a = rng.integers(-128, 128, (m, cols)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    da = torch.zeros(m * cols + 16, dtype=torch.uint8, device="cuda")
+    da[offset:offset + m * cols] = dev(torch, a)
+    dy = empty(torch, 4 * m * rows)
+    jk.dev_bitlinear_i8(w, da[offset:], dev(torch, sc), m, cols, dy, m * rows)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, m * rows).reshape(m, rows)
+    for i in range(m):
+        ref = O.bitlinear_i8(quant, [rows, cols], raw, a[i], float(sc[i]), rows)
+        assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
+
+
 @pytest.mark.parametrize("quant", [TQ2_0, I2_S, Q8_0])
 @pytest.mark.parametrize("m", [500, 250, 60])
 def test_bitlinear_tile_shapes(gpu, quant, m):
