@@ -91,23 +91,31 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
     } else if constexpr (Q == JK_Q6_K) {
         // dequantize_q6_k_block (quant.rs:594-648) visited in element order: (d * sc) * q
         // (its d == 0 -> +0.0 case needs no select, as for Q4_0 above)
+        // Four elements at a time: bytes of 4 (q - 32) (the 6-bit field with its top bit
+        // flipped, moved to the top of the byte, read back as a signed byte), times dsc / 4.
+        // dsc / 4 is exact (|d * sc| is 0 or at least 2^-24) and so is 4 (q - 32), so the
+        // product is dsc * (q - 32) rounded once, as in the reference.
         const float d = f16_finite(o.d);
-        float dsc[16];
+        float dsc4[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) dsc[j] = d * (float)(int8_t)vd_byte<Q>(o, 12, j);
+        for (int j = 0; j < 16; ++j) dsc4[j] = (d * (float)(int8_t)vd_byte<Q>(o, 12, j)) * 0.25f;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int quarter = 0; quarter < 4; ++quarter) {
 #pragma unroll
-                for (int l = 0; l < 32; ++l) {
+                for (int l = 0; l < 32; l += 4) {
                     const int lbyte = 64 * h + l + ((quarter & 1) ? 32 : 0), qbyte = 32 * h + l;
-                    // each field straight from its source dword (no shared byte temporaries)
-                    const uint32_t lo = (comp(o.c[lbyte >> 4], (lbyte & 15) >> 2) >> (8 * (lbyte & 3) + (quarter < 2 ? 0 : 4))) & 15u;
-                    const uint32_t hi2 = (comp(o.c[8 + (qbyte >> 4)], (qbyte & 15) >> 2) >> (8 * (qbyte & 3) + 2 * quarter)) & 3u;
-                    const int q = (int)(lo | (hi2 << 4)) - 32;
-                    const float wv = dsc[8 * h + (l >> 4) + 2 * quarter] * (float)q;
-                    sum += wv * xb[128 * h + 32 * quarter + l];
+                    const uint32_t L = comp(o.c[lbyte >> 4], (lbyte & 15) >> 2);
+                    const uint32_t H = comp(o.c[8 + (qbyte >> 4)], (qbyte & 15) >> 2);
+                    const uint32_t v6 = ((L >> (quarter < 2 ? 0 : 4)) & 0x0F0F0F0Fu) | (((H >> (2 * quarter)) & 0x03030303u) << 4);
+                    const uint32_t w4 = (v6 ^ 0x20202020u) << 2;
+                    const float s4 = dsc4[8 * h + (l >> 4) + 2 * quarter];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float wv = s4 * (float)(int8_t)(w4 >> (8 * i));
+                        sum += wv * xb[128 * h + 32 * quarter + l + i];
+                    }
                 }
                 // the chain is serial: an empty asm with a memory clobber keeps the next 32
                 // activation reads from being hoisted ahead of this group (bounded live range)
