@@ -154,18 +154,28 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Ordered fold of one value per lane over a whole wave: lane 0 adds the values of lanes
 // 0..63 in lane order to acc (acc lives in lane 0); lanes past the row end pass -0.0, the
-// exact identity of f32 addition. red: 64 floats of 16-byte aligned LDS for this wave; the
-// 16 reads are issued before the first add.
+// exact identity of f32 addition. red: 64 floats of 16-byte aligned LDS for this wave, read
+// 16 at a time with the next 16 requested before the current 16 are added.
 __device__ __forceinline__ float fold_wave(float acc, float v, float *red) {
     const int l = threadIdx.x & 63;
     red[l] = v;
     wave_lds_sync();
     if (l == 0) {
-        float4 r[16];
+        const float4 *r4 = reinterpret_cast<const float4 *>(red);
+        float4 cur[4], nxt[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) r[i] = reinterpret_cast<const float4 *>(red)[i];
+        for (int i = 0; i < 4; ++i) cur[i] = r4[i];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc = (((acc + r[i].x) + r[i].y) + r[i].z) + r[i].w;
+        for (int c = 0; c < 4; ++c) {
+            if (c < 3)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) nxt[i] = r4[4 * (c + 1) + i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = (((acc + cur[i].x) + cur[i].y) + cur[i].z) + cur[i].w;
+            if (c < 3)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+        }
     }
     wave_lds_sync();
     return acc;

@@ -136,7 +136,7 @@ constexpr int kVdWaves = 8;
 constexpr int kVdLdsMax = 60 * 1024;  // staged activation bytes
 
 template <int Q, int LPR, bool XL>
-__global__ __launch_bounds__(64 * kVdWaves) void vec_dot_f32_kernel(WeightDev w, const float *__restrict__ x,
+__global__ __launch_bounds__(64 * kVdWaves) __attribute__((amdgpu_waves_per_eu(4))) void vec_dot_f32_kernel(WeightDev w, const float *__restrict__ x,
                                                                      float *__restrict__ y) {
     constexpr int RPW = 64 / LPR, E = VdFmt<Q>::E;
     extern __shared__ __align__(16) float s_xf[];
