@@ -44,10 +44,11 @@ template <int TN, int TM> struct Tile {
     static constexpr int RW = TN < 64 ? TN : 64;  // weight rows per wave
     static constexpr int NT = RW / 32;            // 32-row MFMA blocks per wave
     static constexpr int WR = TN / RW;            // waves along the rows
+    static constexpr int WM = TM < 32 ? 1 : TM / 32;  // waves along the tokens
     static constexpr int XL = 8 * TM / THREADS;   // activation loads per thread and chunk
     static constexpr int XS = 4 * TM / THREADS;   // activation scales per thread and chunk
     static constexpr int WPE = TN == 128 ? 3 : 2;  // waves per SIMD the register budget allows
-    static_assert(WR * (TM / 32) == WAVES && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
+    static_assert(WR * WM == WAVES && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
 };
 
 template <int TN, int TM> struct GemmChunk {
@@ -400,13 +401,107 @@ static long cu_count() {
     return n;
 }
 
-// Tile shape of a launch: the largest tile that still gives every CU two workgroups.
-static int gemm_tile(long rows, long m) {
+// Small launches: one wave computes 32 weight rows x 16 tokens as two 16 x 16 tiles
+// (v_mfma_i32_16x16x32_i8 per 32-element group; lane l supplies row / token l % 16 and K
+// bytes 8 (l / 16) .. + 7, and holds token l % 16, rows 4 (l / 16) + r of each tile). The
+// scale products are VALU multiplies (8 a group), the reference's single rounded products.
+// Each wave's serial chain per group is about half that of a 32 x 32 tile, and the launch
+// has twice the waves. (Q6_K's 16-element groups stay on the 32 x 32 tiles: measured slower here.)
+template <int Q, int GB>
+__global__ __launch_bounds__(64) void gemm16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+    using F = GemmFmt<Q>;
+    constexpr int TN = 32, TM = 16;
+    static_assert(F::GK == 32, "32-element scale groups");
+    __shared__ __align__(16) GemmChunk<TN, TM> cs;
+    const int lane = threadIdx.x;
+    const int ntn = (r1 - r0 + TN - 1) / TN, ntm = ((int)a.m + TM - 1) / TM;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;  // as gemm_repacked_kernel
+    if (tn >= ntn) return;
+    const int n0 = r0 + tn * TN, m0 = tm * TM;
+    const int M = (int)a.m;
+    const int steps = w.cols / 32;
+    const int nchunks = (steps + kSteps - 1) / kSteps;
+    const int jl = lane & 15, kq = lane >> 4;
+
+    float acc[2][4];
+    v4i cacc[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        cacc[nt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[nt][r] = 0.0f;
+    }
+    auto step = [&](int kc, int st) {
+        const int off = 32 * st + 8 * kq;
+        const long bq = *reinterpret_cast<const long *>(cs.b + jl * kRowB + off);
+        v4i c[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const long aq = *reinterpret_cast<const long *>(cs.a + (16 * nt + jl) * kRowB + off);
+            if constexpr (GB == 1) c[nt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, bq, v4i{0, 0, 0, 0}, 0, 0, 0);
+            else c[nt] = cacc[nt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq, bq, cacc[nt], 0, 0, 0);
+        }
+        if constexpr (GB > 1) {
+            if ((kSteps * kc + st) % GB != GB - 1) return;  // block not complete: no epilogue yet
+            cacc[0] = cacc[1] = v4i{0, 0, 0, 0};
+        }
+        const float xs = cs.xs[st][jl];
+        const float xsum = F::MINS ? cs.xm[st][jl] : 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const float4 ws4 = *reinterpret_cast<const float4 *>(&cs.ws[st][16 * nt + 4 * kq]);
+            float4 wm4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (F::MINS) wm4 = *reinterpret_cast<const float4 *>(&cs.wm[st][16 * nt + 4 * kq]);
+            const float wsr[4] = {ws4.x, ws4.y, ws4.z, ws4.w};
+            [[maybe_unused]] const float wmr[4] = {wm4.x, wm4.y, wm4.z, wm4.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float t = (float)c[nt][r] * (xs * wsr[r]);
+                if constexpr (F::MINS) acc[nt][r] += t - xsum * wmr[r];
+                else acc[nt][r] += t;
+            }
+        }
+    };
+
+    Stage<TN, TM> rg;
+    chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
+    chunk_store<Q>(w, rg, cs, 0);
+    __syncthreads();
+    for (int kc = 0; kc < nchunks; ++kc) {
+        const bool more = kc + 1 < nchunks;
+        if (more) chunk_load<Q>(rg, w, a, n0, r1, m0, M, kc + 1);
+        const int nst = min(kSteps, steps - kSteps * kc);
+        for (int st = 0; st < nst; ++st) step(kc, st);
+        if (more) {
+            __syncthreads();
+            chunk_store<Q>(w, rg, cs, kc + 1);
+            __syncthreads();
+        }
+    }
+
+    const int m = m0 + jl;
+    if (m < M) {
+        const size_t ld = (size_t)(r1 - r0);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = n0 + 16 * nt + 4 * kq + r;
+                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = acc[nt][r];
+            }
+    }
+}
+
+// Tile shape of a launch: the largest tile that still gives every CU two workgroups, and the
+// 32 x 16 single-wave tiles (not for Q6_K) where 32 x 32 tiles would give fewer than four.
+static int gemm_tile(int quant, long rows, long m) {
     const long ncu = cu_count();
     auto tiles = [&](long tn, long tm) { return (rows + tn - 1) / tn * ((m + tm - 1) / tm); };
     if (tiles(128, 64) >= 2 * ncu) return 0;
     if (tiles(64, 64) >= 2 * ncu) return 1;
-    return 2;
+    if (tiles(32, 32) >= 4 * ncu || quant == JK_Q6_K) return 2;
+    return 3;
 }
 
 template <int Q, int GB, int TN, int TM>
@@ -418,10 +513,19 @@ static void launch_tile(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, f
 
 template <int Q, int GB>
 static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    switch (gemm_tile(r1 - r0, (long)a.m)) {
+    switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
     case 0: launch_tile<Q, GB, 128, 64>(s, w, a, y, r0, r1); break;
     case 1: launch_tile<Q, GB, 64, 64>(s, w, a, y, r0, r1); break;
-    default: launch_tile<Q, GB, 32, 32>(s, w, a, y, r0, r1); break;
+    case 2: launch_tile<Q, GB, 32, 32>(s, w, a, y, r0, r1); break;
+    default:
+        if constexpr (GemmFmt<Q>::GK == 32) {
+            const size_t ntn = (size_t)(r1 - r0 + 31) / 32, ntm = (a.m + 15) / 16;
+            hipLaunchKernelGGL((gemm16_kernel<Q, GB>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64), 0, s, w,
+                               a, y, r0, r1);
+        } else {
+            launch_tile<Q, GB, 32, 32>(s, w, a, y, r0, r1);  // not chosen for 16-element groups
+        }
+        break;
     }
     return check_launch("gemm_repacked_kernel");
 }
