@@ -493,14 +493,15 @@ __global__ __launch_bounds__(64) void gemm16_kernel(WeightDev w, jk_act_q8 a, fl
     }
 }
 
-// Tile shape of a launch: the largest tile that still gives every CU two workgroups, and the
-// 32 x 16 single-wave tiles (not for Q6_K) where 32 x 32 tiles would give fewer than four.
+// Tile shape of a launch: the largest tile that still gives every CU two workgroups, down to the
+// 32 x 16 single-wave tiles (not for Q6_K). (Four 32 x 32 tiles per CU beat the 32 x 16 tiles
+// with the weights cold in HBM: those re-read every weight tile twice as often.)
 static int gemm_tile(int quant, long rows, long m) {
     const long ncu = cu_count();
     auto tiles = [&](long tn, long tm) { return (rows + tn - 1) / tn * ((m + tm - 1) / tm); };
     if (tiles(128, 64) >= 2 * ncu) return 0;
     if (tiles(64, 64) >= 2 * ncu) return 1;
-    if (tiles(32, 32) >= 4 * ncu || quant == JK_Q6_K) return 2;
+    if (tiles(32, 32) >= 2 * ncu || quant == JK_Q6_K) return 2;
     return 3;
 }
 
