@@ -1,7 +1,7 @@
 /*
  * jk_oracle.c -- CPU restatement of the jero-kernels-rvv portable scalar fallback
- * for the quantized-matmul path. TEST INFRASTRUCTURE ONLY: the parity checker and
- * the timed CPU baseline; never part of the product library.
+ * for the quantized-matmul path. TEST INFRASTRUCTURE ONLY: the oracle of the parity
+ * tests and the timed CPU baseline; never part of the product library.
  *
  * Citations are file:line in the reference crate (src/...). Build with
  * -ffp-contract=off so that every `a * b + c` of the reference rounds twice.

@@ -2,8 +2,8 @@
  * jk_oracle.h -- CPU restatement of the jero-kernels-rvv portable scalar fallback
  * for the quantized-matmul path (Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S).
  *
- * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
- * product library (libjk.so) and the timed CPU baseline of bench.py. It is
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle the HIP product library
+ * (libjk.so) is compared with, and the timed CPU baseline of bench.py. It is
  * never linked into, loaded by, or called from the product path.
  *
  * Every function follows one reference function; the citation (file:line,

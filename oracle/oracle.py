@@ -1,7 +1,7 @@
 """ctypes binding of liboracle.so -- the CPU restatement of the reference's scalar path.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as the checker
-and by bench.py's cpu_baseline leg. The product path never imports this module.
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() (which compares
+the GPU result with it) and by bench.py's cpu_baseline leg. The product path never imports this module.
 Status codes follow the product library: 0 ok, 1 TensorBoundsError, 2 CapabilityMismatch.
 """
 from __future__ import annotations
