@@ -356,6 +356,28 @@ def main() -> int:
             hbm_line(name, b, us, f"{rows}x{cols}, Q8_0 activation blocks")
             for w in ws:
                 w.free()
+        # Q5_0 / Q5_K / TQ1_0 quant_q8 GEMV with caller blocks (GGUF bytes; TQ1_0 streams its
+        # 66-byte device blocks, 22% more than the 54 GGUF bytes counted here)
+        for name, quant, rows, cols in (("gemv_q5_0_q8_0 4096x4096", jk.Q5_0, 4096, 4096),
+                                        ("gemv_q5_k_q8_k 14336x4096", jk.Q5_K, 14336, 4096),
+                                        ("gemv_q5_k_q8_k 4096x14336", jk.Q5_K, 4096, 14336),
+                                        ("gemv_tq1_0_q8_k 6912x2560", jk.TQ1_0, 6912, 2560)):
+            ws = copies(quant, rows, cols, 800 + quant)
+            small = quant in jk.Q8_0_ACT
+            be = 32 if small else 256
+            bsz = (jk.BLOCK_Q8_0 if small else jk.BLOCK_Q8K).itemsize
+            xq = torch.empty(cols // be * bsz, dtype=torch.uint8, device=dev)
+            xin = torch.randn(cols, generator=gen).to(dev)
+            if small:
+                jk.dev_quantize_row_q8_0(xin, cols, xq, cols // 32)
+            else:
+                jk.dev_quantize_row_q8_k(xin, cols, xq, cols // 256)
+            y = torch.empty(rows, dtype=torch.float32, device=dev)
+            us = graph_us(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // be, y, rows, st), len(ws))
+            b = (gemv_bytes_q80 if small else gemv_bytes)(quant, rows, cols, jk)
+            hbm_line(name, b, us, f"{rows}x{cols}, {'Q8_0' if small else 'Q8_K'} activation blocks")
+            for w in ws:
+                w.free()
         # A8: f32-activation vec_dot (dequantize x f32 dot) at the Q4_K attn shape and Q6_K down
         for name, quant, rows, cols, xa in (("vec_dot_q4_k_m f32", jk.Q4_K, 4096, 4096, "x"),
                                             ("vec_dot_q6_k f32", jk.Q6_K, 4096, 14336, "h")):
@@ -367,7 +389,7 @@ def main() -> int:
             for w in ws:
                 w.free()
         # C5: ternary GEMV (Q8_K caller blocks) and BitLinear at batch 1 and 128
-        for quant, qname in ((jk.TQ2_0, "tq2_0"), (jk.I2_S, "i2_s")):
+        for quant, qname in ((jk.TQ2_0, "tq2_0"), (jk.I2_S, "i2_s"), (jk.TQ1_0, "tq1_0")):
             for rows, cols in ((6912, 2560), (2560, 6912)):
                 ws = copies(quant, rows, cols, 700 + rows)
                 wbytes = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant]

@@ -47,9 +47,12 @@ typedef enum jk_status {
 /* GGML type ids of the jero_core::QuantType variants on this path. */
 typedef enum jk_quant {
     JK_Q4_0 = 2,
+    JK_Q5_0 = 6,
     JK_Q8_0 = 8,
     JK_Q4_K = 12, /* QuantType::Q4_K_M */
+    JK_Q5_K = 13,
     JK_Q6_K = 14,
+    JK_TQ1_0 = 34,
     JK_TQ2_0 = 35,
     JK_I2_S = 36
 } jk_quant;
@@ -94,7 +97,7 @@ typedef struct jk_weight jk_weight;
 typedef struct jk_weight_info {
     int32_t quant;
     size_t rows, cols;
-    size_t device_bytes; /* bytes of the device layout */
+    size_t device_bytes; /* bytes of the device layout (GGUF bytes; 66 per 54-byte TQ1_0 block) */
     size_t gguf_bytes;   /* bytes of the GGUF payload it was built from */
 } jk_weight_info;
 
@@ -115,9 +118,11 @@ jk_status jk_copy_to_host(jk_stream s, void *dst, const void *src, size_t bytes)
 /* ---------------------------------------------------------------- weights */
 /* RepackedWeight::from_tensor (repack.rs:2288-2300) / RepackedWeight::repack when
  * rows == cols == 0 (repack.rs:2255-2285): copies the GGUF payload to the device and
- * rewrites it there into the plane layout (same byte count as GGUF). Validation follows
- * validate_matrix_view (repack.rs:1208-1281). The handle is immutable and may be used
- * from any thread and stream once the upload stream has completed. */
+ * rewrites it there into the plane layout (same byte count as GGUF, except TQ1_0, whose
+ * trits are stored 2 bits each). Formats: Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0,
+ * I2_S; others are a CapabilityMismatch. Validation follows validate_matrix_view
+ * (repack.rs:1208-1281). The handle is immutable and may be used from any thread and
+ * stream once the upload stream has completed. */
 jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, size_t cols,
                            jk_weight **out);
 jk_status jk_weight_free(jk_weight *w);
@@ -150,9 +155,10 @@ jk_status jk_quantize_absmax_i8(jk_stream s, const float *x, size_t m, size_t k,
                                 float *scales);
 
 /* ---------------------------------------------- quant_q8 integer GEMV (M=1) */
-/* gemv_q4_0_q8_0 (quant_q8.rs:1586-1605), gemv_q8_0_q8_0 (1670-1689),
- * gemv_q4_k_q8_k (3101-3123), gemv_q6_k_q8_k (3189-3211), gemv_tq2_0_q8_k (3250-3273):
- * y[rows] from the weight handle and nx pre-quantized activation blocks. */
+/* gemv_q4_0_q8_0 (quant_q8.rs:1586-1605), gemv_q5_0_q8_0 (1628-1650), gemv_q8_0_q8_0
+ * (1670-1689), gemv_q4_k_q8_k (3101-3123), gemv_q5_k_q8_k (3160-3182), gemv_q6_k_q8_k
+ * (3189-3211), gemv_tq1_0_q8_k (3219-3242), gemv_tq2_0_q8_k (3250-3273): y[rows] from the
+ * weight handle and nx pre-quantized activation blocks. */
 jk_status jk_gemv_q4_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx,
                             float *y, size_t y_len);
 jk_status jk_gemv_q8_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx,
@@ -163,16 +169,22 @@ jk_status jk_gemv_q6_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k 
                             float *y, size_t y_len);
 jk_status jk_gemv_tq2_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx,
                              float *y, size_t y_len);
-/* Row-sliced form of the five above (format taken from the handle): writes
+jk_status jk_gemv_q5_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx,
+                            float *y, size_t y_len);
+jk_status jk_gemv_q5_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx,
+                            float *y, size_t y_len);
+jk_status jk_gemv_tq1_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx,
+                             float *y, size_t y_len);
+/* Row-sliced form of the eight above (format taken from the handle): writes
  * y[row - row_begin] for rows [row_begin, row_end), identical to the full call. */
 jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t nx, float *y,
                           size_t row_begin, size_t row_end);
 
 /* Grouped quant_q8 GEMV: one launch evaluates several independent products of one
  * weight format (e.g. a layer's Q/K/V projections, or gate and up). Each job is a
- * gemv_* call of the five above over rows [row_begin, row_end) of its weight, writing
+ * gemv_* call of the eight above over rows [row_begin, row_end) of its weight, writing
  * y[row - row_begin]; its activation is either caller blocks (x_q8: BlockQ8_0 for
- * Q4_0/Q8_0, BlockQ8K for Q4_K/Q6_K/TQ2_0) or f32 values (x_f32) that the launch
+ * Q4_0/Q5_0/Q8_0, BlockQ8K for the 256-element formats) or f32 values (x_f32) that the launch
  * quantizes with quantize_row_q8_0 / quantize_row_q8_k (quant_q8.rs:395, 576) -- results
  * are identical either way. Jobs of different formats are split into separate launches.
  * No single reference function corresponds: this is the reference's per-matrix sequence
@@ -190,9 +202,10 @@ jk_status jk_gemv_q8_batch(jk_stream s, const jk_gemv_job *jobs, size_t njobs);
 jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len);
 
 /* ------------------------------------------ f32-activation matvec (vec_dot) */
-/* vec_dot_q4_0 (quant.rs:1458), vec_dot_q8_0 (1069), vec_dot_q6_k (1089),
- * VectorKernel::vec_dot_q4_k_m (lib.rs:157, scalar impl 1268-1303), vec_dot_i2_s
- * (quant.rs:2199-2240): dequantize each block and dot it with f32 x. */
+/* vec_dot_q4_0 (quant.rs:1458), vec_dot_q5_0 (2036), vec_dot_q8_0 (1069), vec_dot_q5_k
+ * (1238), vec_dot_q6_k (1089), VectorKernel::vec_dot_q4_k_m (lib.rs:157, scalar impl
+ * 1268-1303), vec_dot_i2_s (quant.rs:2199-2240): dequantize each block and dot it with
+ * f32 x. TQ1_0 / TQ2_0 have none (CapabilityMismatch). */
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y,
                          size_t y_len);
 
@@ -208,7 +221,7 @@ jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
 
 /* -------------------------------------------------------------- BitLinear */
 /* bitlinear_i8_rvv (ime.rs:882-938) applied to m tokens: y[m][rows] from act[m][k]
- * and one f32 scale per token (TQ2_0, I2_S and Q8_0 weights). */
+ * and one f32 scale per token (TQ1_0, TQ2_0, I2_S and Q8_0 weights). */
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act,
                           const float *act_scales, size_t m, size_t k, float *y, size_t y_len);
 
@@ -223,12 +236,20 @@ jk_status jk_host_vec_dot_q8_0_q8_0(const void *w, size_t w_len, const jk_block_
 jk_status jk_host_vec_dot_q4_k_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
 jk_status jk_host_vec_dot_q6_k_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
 jk_status jk_host_vec_dot_tq2_0_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
+/* vec_dot_q5_0_q8_0_blocks (quant_q8.rs:1478), vec_dot_q5_k_q8_k (3041), vec_dot_tq1_0_q8_k (3071). */
+jk_status jk_host_vec_dot_q5_0_q8_0(const void *w, size_t w_len, const jk_block_q8_0 *x, size_t nx, float *out);
+jk_status jk_host_vec_dot_q5_k_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
+jk_status jk_host_vec_dot_tq1_0_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out);
 /* gemv_q4_0_q8_0 (quant_q8.rs:1586) ... gemv_tq2_0_q8_k (3250) with a TensorView. */
 jk_status jk_host_gemv_q4_0_q8_0(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx);
 jk_status jk_host_gemv_q8_0_q8_0(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx);
 jk_status jk_host_gemv_q4_k_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
 jk_status jk_host_gemv_q6_k_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
 jk_status jk_host_gemv_tq2_0_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
+/* gemv_q5_0_q8_0 (quant_q8.rs:1628), gemv_q5_k_q8_k (3160), gemv_tq1_0_q8_k (3219). */
+jk_status jk_host_gemv_q5_0_q8_0(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx);
+jk_status jk_host_gemv_q5_k_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
+jk_status jk_host_gemv_tq1_0_q8_k(float *out, size_t out_len, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx);
 /* vec_dot_q4_0 (quant.rs:1458), vec_dot_q8_0 (1069), vec_dot_q6_k (1089),
  * VectorKernel::vec_dot_q4_k_m (lib.rs:157), vec_dot_i2_s (quant.rs:2199). */
 jk_status jk_host_vec_dot_q4_0(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
@@ -236,6 +257,9 @@ jk_status jk_host_vec_dot_q8_0(float *out, size_t out_len, const jk_tensor_view 
 jk_status jk_host_vec_dot_q6_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 jk_status jk_host_vec_dot_q4_k_m(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 jk_status jk_host_vec_dot_i2_s(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+/* vec_dot_q5_0 (quant.rs:2036), vec_dot_q5_k (1238). */
+jk_status jk_host_vec_dot_q5_0(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q5_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 /* dequantize_tensor_row / dequantize_token_row (quant.rs:2492, 2580). */
 jk_status jk_host_dequantize_tensor_row(const jk_tensor_view *w, size_t row, float *out, size_t out_len);
 /* gemm_repacked_f32_rows (repack.rs:4143-4165): quantizes input [m, cols] with

@@ -70,6 +70,10 @@ __device__ __forceinline__ int bytes_sub(uint32_t a, uint32_t k) {
     return (int)(((a | 0x80808080u) - k) ^ 0x80808080u);
 }
 
+// Bits 0..3 of n moved to bit 4 of bytes 0..3 (the four shifted copies of n occupy
+// disjoint bit ranges, so the multiply has no carries): the fifth bit of four 5-bit quants.
+__device__ __forceinline__ uint32_t bit4_of_bytes(uint32_t n) { return ((n * 0x00204081u) & 0x01010101u) << 4; }
+
 // Rust `v.round().clamp(lo, hi) as i8`: round half away from zero, NaN -> 0.
 __device__ __forceinline__ int rust_round_clamp_i8(float v, float lo, float hi) {
     float r = roundf(v);

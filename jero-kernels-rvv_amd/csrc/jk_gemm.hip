@@ -34,7 +34,7 @@ constexpr int kRowB = 144;    // padded LDS bytes per 128-byte row
 
 template <int Q> struct GemmFmt {
     static constexpr int GK = Q == JK_Q6_K ? 16 : 32;  // elements per scale group
-    static constexpr bool MINS = Q == JK_Q4_K;
+    static constexpr bool MINS = Q == JK_Q4_K || Q == JK_Q5_K;
     static constexpr int NG = 128 / GK;                 // scale groups per chunk
 };
 
@@ -55,9 +55,9 @@ template <int TN, int TM> struct GemmChunk {
     uint8_t a[TN * kRowB];  // weights, i8, [row][k]
     uint8_t b[TM * kRowB];  // activations, i8, [token][k]
     float ws[8][TN];        // weight scale per scale group of the chunk
-    float wm[4][TN];        // weight min per 32-group (Q4_K)
+    float wm[4][TN];        // weight min per 32-group (Q4_K, Q5_K)
     float xs[4][TM];        // activation scale per 32-block
-    float xm[4][TM];        // activation sum per 32-block (Q4_K)
+    float xm[4][TM];        // activation sum per 32-block (Q4_K, Q5_K)
 };
 
 // One 16-byte global load without the streaming hint: a weight tile is read once per
@@ -73,17 +73,19 @@ __device__ __forceinline__ const uint8_t *plane_ptr(const WeightDev &w, int c, i
 // is in flight while the previous chunk is evaluated; nothing between the loads depends on
 // a loaded value. Every thread stages part of both tiles, so the four waves (one per SIMD)
 // carry the same load and unpack work.
-//  Q8_0 / Q4_0: a chunk is 4 blocks, 64 contiguous bytes per (plane, row); 4 consecutive
-//   lanes read one such segment (piece t % 4 = block 4kc + t % 4), load i covers rows
-//   t / 4 + TN/2 (i % 2) of plane i / 2. Scales: row t / 2, blocks 4kc + 2 (t % 2) ...
+//  Q8_0 / Q4_0 / Q5_0: a chunk is 4 blocks, 64 contiguous bytes per (plane, row); 4
+//   consecutive lanes read one such segment (piece t % 4 = block 4kc + t % 4), load i covers
+//   rows t / 4 + TN/2 (i % 2) of plane i / 2 (Q5_0: with the word of the same block).
+//   Scales: row t / 2, blocks 4kc + 2 (t % 2) ...
 //  K-quants, TQ2_0 (256-element blocks): chunk kc is half h = kc % 2 of block kc / 2;
 //   I2_S (128-element blocks): chunk kc is block kc. Thread t takes row t / 2 and part
 //   j = t % 2 of the chunk's planes.
 //  Activations: load i covers token t / 8 + (threads / 8) i, piece t % 8 of its 128-byte
 //   row; scale j (and sum) of entry e = XS t + j: token e / 4, block 4kc + e % 4.
 template <int TN, int TM> struct Stage {
-    uint4 w[4];                         // weight plane bytes
-    uint32_t wd[2];                     // weight f16 scales (Q8_0 / Q4_0: two blocks; Q6_K, TQ2_0: d)
+    uint4 w[5];                         // weight plane bytes
+    uint32_t wd[2];                     // weight f16 scales (Q8_0 / Q4_0 / Q5_0: two blocks; Q6_K, TQ2_0: d)
+    uint32_t wh[2];                     // Q5_0: high-bit words of the blocks of w[0], w[1]
     uint4 x[Tile<TN, TM>::XL];          // activation bytes
     uint32_t xd[2][Tile<TN, TM>::XS];   // activation scale, sum (Q4_K)
 };
@@ -93,12 +95,13 @@ template <int TN, int TM> struct Stage {
 template <int Q, int TN, int TM>
 __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage<TN, TM> &r) {
     const int nb = w.nb, t = threadIdx.x;
-    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
+    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0 || Q == JK_Q5_0) {
         const int b = min(4 * kc + (t & 3), nb - 1);
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
             const int n = min(n0 + (t >> 2) + TN / 2 * (i & 1), r1 - 1);
             r.w[i] = ldg16(plane_ptr(w, i >> 1, n, b));
+            if constexpr (Q == JK_Q5_0) r.wh[i] = w.hplane[(size_t)n * (size_t)nb + (size_t)b];
         }
         const size_t srow = (size_t)min(n0 + (t >> 1), r1 - 1) * (size_t)nb;
 #pragma unroll
@@ -114,6 +117,12 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
             r.w[0] = ldg16(plane_ptr(w, 0, n, b));  // d, dmin, 12 packed 6-bit scales / mins
             r.w[1] = ldg16(plane_ptr(w, 1 + 2 * (2 * h + j), n, b));
             r.w[2] = ldg16(plane_ptr(w, 2 + 2 * (2 * h + j), n, b));
+        } else if constexpr (Q == JK_Q5_K) {
+            r.w[0] = ldg16(plane_ptr(w, 0, n, b));  // d, dmin, 12 packed 6-bit scales / mins
+            r.w[1] = ldg16(plane_ptr(w, 3 + 2 * (2 * h + j), n, b));
+            r.w[2] = ldg16(plane_ptr(w, 4 + 2 * (2 * h + j), n, b));
+            r.w[3] = ldg16(plane_ptr(w, 1, n, b));  // qh[0..16)
+            r.w[4] = ldg16(plane_ptr(w, 2, n, b));  // qh[16..32)
         } else if constexpr (Q == JK_Q6_K) {
             r.w[0] = ldg16(plane_ptr(w, 4 * h + j, n, b));      // ql, quarters 0 and 2
             r.w[1] = ldg16(plane_ptr(w, 4 * h + j + 2, n, b));  // ql, quarters 1 and 3
@@ -185,13 +194,26 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
             if constexpr (GemmFmt<Q>::MINS) c.xm[e & 3][e >> 2] = __uint_as_float(r.xd[1][j]);
         }
     }
-    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
+    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0 || Q == JK_Q5_0) {
         const int piece = t & 3;
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
             uint8_t *dst = c.a + ((t >> 2) + TN / 2 * (i & 1)) * kRowB + 32 * piece;
             if constexpr (Q == JK_Q8_0) {
                 *reinterpret_cast<uint4 *>(dst + 16 * (i >> 1)) = r.w[i];
+            } else if constexpr (Q == JK_Q5_0) {
+                // unpack_q5_0_block_i8 (quant.rs:139-157): (nibble | 16 * bit) - 16, bit j of
+                // the word for element j
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t v = comp(r.w[i], k), qh = r.wh[i];
+                    lo[k] = (uint32_t)bytes_sub((v & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (4 * k)) & 15u), 0x10101010u);
+                    hi[k] = (uint32_t)bytes_sub(((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (16 + 4 * k)) & 15u),
+                                                0x10101010u);
+                }
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             } else {
                 *reinterpret_cast<uint4 *>(dst) = nib4(r.w[i], 0, 0x08080808u);
                 *reinterpret_cast<uint4 *>(dst + 16) = nib4(r.w[i], 4, 0x08080808u);
@@ -222,6 +244,32 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
             *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh) = nib4(r.w[1], 4 * hh, 0u);
             *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh + 16) = nib4(r.w[2], 4 * hh, 0u);
         }
+    } else if constexpr (Q == JK_Q5_K) {
+        // The Q4_K arm with the Q5_K bits (repack.rs:1959-2002): quarter c' = 2h + j takes qs
+        // planes 3 + 2c', 4 + 2c'; element l (l < 32) of its low half adds 16 * bit 2c' of
+        // qh[l], element 32 + l of its high half bit 2c' + 1
+        const uint4 hd = r.w[0];
+        const float d = f16_finite(hd.x & 0xFFFFu), dmin = f16_finite(hd.x >> 16);
+        const uint32_t sc = h == 0 ? (hd.y & 0x3F3F3F3Fu) : ((hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u));
+        const uint32_t mv = h == 0 ? (hd.z & 0x3F3F3F3Fu) : (((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int g = 2 * j + e;
+            c.ws[g][row] = d * (float)((sc >> (8 * g)) & 255u);
+            c.wm[g][row] = dmin * (float)((mv >> (8 * g)) & 255u);
+        }
+        const int qsh = 2 * (2 * h + j);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint4 qv = r.w[1 + p], hv = r.w[3 + p];
+                uint32_t o[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    o[k] = ((comp(qv, k) >> (4 * hh)) & 0x0F0F0F0Fu) | (((comp(hv, k) >> (qsh + hh)) & 0x01010101u) << 4);
+                *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh + 16 * p) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
     } else if constexpr (Q == JK_Q6_K) {
         // dequantize_q6_k_block's element order (quant.rs:594-648): 16-group g = j + 2 qq of
         // half h (quarter qq) takes ql bytes 16j + 32(qq % 2) of the half, qh bytes 16j, the
@@ -555,7 +603,9 @@ jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q
     switch (w.quant) {
     case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, r0, r1);
     case JK_Q4_0: return launch_gemm<JK_Q4_0, 1>(s, w, a, y, r0, r1);
+    case JK_Q5_0: return launch_gemm<JK_Q5_0, 1>(s, w, a, y, r0, r1);
     case JK_Q4_K: return launch_gemm<JK_Q4_K, 1>(s, w, a, y, r0, r1);
+    case JK_Q5_K: return launch_gemm<JK_Q5_K, 1>(s, w, a, y, r0, r1);
     case JK_Q6_K: return launch_gemm<JK_Q6_K, 1>(s, w, a, y, r0, r1);
     case JK_TQ2_0: return launch_gemm<JK_TQ2_0, 1>(s, w, a, y, r0, r1);
     case JK_I2_S: return launch_gemm<JK_I2_S, 1>(s, w, a, y, r0, r1);

@@ -16,24 +16,27 @@ namespace jk {
 
 // ----------------------------------------------------------- f32-activation matvec
 // vec_dot_{q4_0,q8_0,q6_k}_scalar (quant.rs:1401-1436, 899-934, 1012-1047),
-// vec_dot_q4_k_m_scalar (lib.rs:1268-1303), vec_dot_i2_s (quant.rs:2199-2240): for each
-// block, dot_product_f32_scalar(dequantized block, x block) (lib.rs:770-778) -- one product
-// and one add per element in element order from +0.0 -- and row_sum (from +0.0) adds the
-// block dots in block order.
+// vec_dot_q4_k_m_scalar (lib.rs:1268-1303), vec_dot_q5_k_scalar (quant.rs:1181-1219),
+// vec_dot_q5_0 -> vec_dot_generic_block (quant.rs:2036-2054, 1995-2029), vec_dot_i2_s
+// (quant.rs:2199-2240): for each block, dot_product_f32_scalar(dequantized block, x block)
+// (lib.rs:770-778) -- one product and one add per element in element order from +0.0 --
+// and row_sum (from +0.0) adds the block dots in block order.
 //
 // Mapping: lane p of a row's LPR lanes takes blocks p, p + LPR, ...; a block's element
 // chain runs in the lane, fully unrolled, on the block's bytes held in registers (16-byte
 // plane loads) and the activation staged once per workgroup in LDS (or read through the
 // caches when it does not fit); the block values are folded across lanes in block order.
 template <int Q> struct VdFmt {
-    static constexpr int E = Q == JK_Q4_0 || Q == JK_Q8_0 ? 32 : Q == JK_I2_S ? 128 : 256;  // elements
-    static constexpr int C = Q == JK_Q4_0 ? 1 : Q == JK_Q8_0 || Q == JK_I2_S ? 2 : Q == JK_Q4_K ? 9 : 13;
-    static constexpr bool D = Q == JK_Q4_0 || Q == JK_Q8_0 || Q == JK_Q6_K;  // f16 scale in the d-plane
+    static constexpr int E = fmt_of(Q).be;         // elements
+    static constexpr int C = fmt_of(Q).chunks;     // 16-byte chunks
+    static constexpr bool D = fmt_of(Q).d_off >= 0;  // f16 scale in the d-plane
+    static constexpr bool H = fmt_of(Q).h_off >= 0;  // field in the word plane
 };
 
 template <int Q> struct VdBlock {
     uint4 c[VdFmt<Q>::C];
     uint32_t d;
+    uint32_t h;
 };
 
 template <int Q>
@@ -41,6 +44,7 @@ __device__ __forceinline__ void vd_load(VdBlock<Q> &o, const WeightDev &w, int r
 #pragma unroll
     for (int c = 0; c < VdFmt<Q>::C; ++c) o.c[c] = ld_chunk(w, c, r, b);
     if constexpr (VdFmt<Q>::D) o.d = w.dplane[(size_t)r * (size_t)w.nb + (size_t)b];
+    if constexpr (VdFmt<Q>::H) o.h = w.hplane[(size_t)r * (size_t)w.nb + (size_t)b];
 }
 
 // Byte k (0..15 within chunk c) of the block's chunks.
@@ -52,16 +56,19 @@ __device__ __forceinline__ uint32_t vd_byte(const VdBlock<Q> &o, int c, int k) {
 template <int Q>
 __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__restrict__ xb, float i2s_scale) {
     float sum = 0.0f;
-    if constexpr (Q == JK_Q4_0 || Q == JK_Q8_0) {
-        // dequantize_q4_0_block / dequantize_q8_0_block (quant.rs:550-588). The reference
-        // writes +0.0 for d == 0 where d * q gives +-0: no sum observes the difference, since
-        // a sum that starts at +0.0 never becomes -0 under round-to-nearest addition (the
-        // products are finite, so NaN cases are unchanged as well).
+    if constexpr (Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_Q8_0) {
+        // dequantize_q4_0_block / dequantize_q8_0_block (quant.rs:550-588), dequantize_q5_0_block
+        // (160-164, scale_i8_into_f32 94-102). The reference writes +0.0 for d == 0 where d * q
+        // gives +-0: no sum observes the difference, since a sum that starts at +0.0 never
+        // becomes -0 under round-to-nearest addition (the products are finite, so NaN cases
+        // are unchanged as well).
         const float d = f16_finite(o.d);
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             int qv;
             if constexpr (Q == JK_Q4_0) qv = (int)((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) - 8;
+            else if constexpr (Q == JK_Q5_0)
+                qv = (int)(((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) | (((o.h >> i) & 1u) << 4)) - 16;
             else qv = (int)(int8_t)vd_byte<Q>(o, i >> 4, i & 15);
             const float wv = d * (float)qv;
             sum += wv * xb[i];
@@ -83,6 +90,31 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
 #pragma unroll
                 for (int l = 0; l < 32; ++l) {
                     const uint32_t q = (vd_byte<Q>(o, 1 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u;
+                    const float wv = d1 * (float)q - m1;
+                    sum += wv * xb[64 * c + 32 * hi + l];
+                }
+            }
+        }
+    } else if constexpr (Q == JK_Q5_K) {
+        // dequantize_q5_k_block (quant.rs:651-706): y = d1 * q - m1 with q = nibble + 16 * bit.
+        // Its d == 0 && dmin == 0 -> +0.0 case gives +-0 products here, which no sum from
+        // +0.0 observes (as for Q4_0 above).
+        const uint4 h = o.c[0];
+        const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
+        const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t scv = c < 2 ? sc_lo : sc_hi, mv = c < 2 ? m_lo : m_hi;
+            const int j = (2 * c) & 3;
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+                const float d1 = d * (float)byte_of(scv, j + hi), m1 = dmin * (float)byte_of(mv, j + hi);
+#pragma unroll
+                for (int l = 0; l < 32; ++l) {
+                    const uint32_t q = ((vd_byte<Q>(o, 3 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u) |
+                                       (((vd_byte<Q>(o, 1 + (l >> 4), l & 15) >> (2 * c + hi)) & 1u) << 4);
                     const float wv = d1 * (float)q - m1;
                     sum += wv * xb[64 * c + 32 * hi + l];
                 }
@@ -196,8 +228,10 @@ static jk_status launch_vd(hipStream_t s, const WeightDev &w, const float *x, fl
 jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y) {
     switch (w.quant) {
     case JK_Q4_0: return launch_vd<JK_Q4_0>(s, w, x, y);
+    case JK_Q5_0: return launch_vd<JK_Q5_0>(s, w, x, y);
     case JK_Q8_0: return launch_vd<JK_Q8_0>(s, w, x, y);
     case JK_Q4_K: return launch_vd<JK_Q4_K>(s, w, x, y);
+    case JK_Q5_K: return launch_vd<JK_Q5_K>(s, w, x, y);
     case JK_Q6_K: return launch_vd<JK_Q6_K>(s, w, x, y);
     case JK_I2_S: return launch_vd<JK_I2_S>(s, w, x, y);
     default: return fail(JK_CAPABILITY_MISMATCH, "vec_dot_f32: unsupported quant %d", w.quant);

@@ -1,4 +1,5 @@
-// jk_gemv_q8.hip -- batch-1 quant_q8 GEMV (Q4_0/Q8_0 x Q8_0, Q4_K/Q6_K/TQ2_0 x Q8_K).
+// jk_gemv_q8.hip -- batch-1 quant_q8 GEMV (Q4_0/Q5_0/Q8_0 x Q8_0, Q4_K/Q5_K/Q6_K/TQ2_0 x Q8_K;
+// TQ1_0 weights are held in the TQ2_0 layout).
 //
 // One launch serves a group of up to kMaxGemvJobs independent matrix-vector products of
 // one weight format (e.g. the Q, K and V projections of a layer, or gate and up). Each
@@ -73,11 +74,12 @@ struct X0Glb {
 };
 
 template <int Q> struct QTraits {
-    static constexpr bool K = Q == JK_Q4_K || Q == JK_Q6_K || Q == JK_TQ2_0;  // Q8_K activations
-    static constexpr int XB = K ? kXkBytes : kX0Bytes;                        // LDS bytes per block
-    static constexpr int XE = K ? 256 : 32;                                   // elements per block
-    static constexpr int C = fmt_of(Q).chunks;                                // 16-byte weight chunks
-    static constexpr bool D = fmt_of(Q).d_off >= 0;                           // scale in the d-plane
+    static constexpr bool K = fmt_of(Q).be == 256;      // Q8_K activations
+    static constexpr int XB = K ? kXkBytes : kX0Bytes;  // LDS bytes per block
+    static constexpr int XE = K ? 256 : 32;             // elements per block
+    static constexpr int C = fmt_of(Q).chunks;          // 16-byte weight chunks
+    static constexpr bool D = fmt_of(Q).d_off >= 0;     // scale in the d-plane
+    static constexpr bool H = fmt_of(Q).h_off >= 0;     // field in the word plane
     // blocks per lane per batch: about 64-144 weight bytes per lane per batch (two
     // batches are in flight per wave)
     static constexpr int U = C >= 4 ? 1 : C == 2 ? 2 : 4;
@@ -86,6 +88,7 @@ template <int Q> struct QTraits {
 template <int Q> struct WReg {
     uint4 c[QTraits<Q>::C];
     uint32_t d;
+    uint32_t h;
 };
 
 // Loads block b of row r with 128-bit non-temporal loads. xo (0 or 16) is XORed into
@@ -106,6 +109,8 @@ __device__ __forceinline__ void wload(WReg<Q> &o, const WeightDev &w, int r, int
     }
     if constexpr (QTraits<Q>::D)
         o.d = *reinterpret_cast<const uint16_t *>(reinterpret_cast<const uint8_t *>(w.dplane) + ((blk << 1) ^ (xo >> 3)));
+    if constexpr (QTraits<Q>::H)
+        o.h = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(w.hplane) + ((blk << 2) ^ (xo >> 2)));
 }
 
 // ------------------------------------------------------------------ block values
@@ -124,6 +129,27 @@ __device__ __forceinline__ float val_q4_0(const WReg<JK_Q4_0> &wr, const X &x) {
         s = dot4((int)((comp(q, i) >> 4) & 0x0F0F0F0Fu), x.q(4 + i), s);
     }
     s -= 8 * x.sum();
+    return (float)s * (dw * xd);
+}
+
+// dot_q5_0_q8_0_block_scalar (quant_q8.rs:688-703): q = (nibble | 16 * bit) - 16, so
+// sum(q * x) = sum((nibble | 16 * bit) * x) - 16 * sum(x), exactly. Bit j of the word holds
+// the fifth bit of element j (j < 16: low nibble of byte j; j >= 16: high nibble of byte j - 16).
+template <class X>
+__device__ __forceinline__ float val_q5_0(const WReg<JK_Q5_0> &wr, const X &x) {
+    const float dw = f16_finite(wr.d);
+    const float xd = x.d();
+    if (dw == 0.0f || xd == 0.0f) return 0.0f;
+    const uint4 q = wr.c[0];
+    const uint32_t qh = wr.h;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t wd = comp(q, i);
+        s = dot4((int)((wd & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (4 * i)) & 15u)), x.q(i), s);
+        s = dot4((int)(((wd >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (16 + 4 * i)) & 15u)), x.q(4 + i), s);
+    }
+    s -= 16 * x.sum();
     return (float)s * (dw * xd);
 }
 
@@ -173,6 +199,42 @@ __device__ __forceinline__ float val_q4_k(const WReg<JK_Q4_K> &wr, const X &x) {
     return (d * xd) * (float)sumi - (dmin * xd) * (float)sum_mins;
 }
 
+// dot_q5_k_q8_k_block_scalar (quant_q8.rs:1866-1899): the Q4_K evaluation with each quant's
+// fifth bit, bit 2c (low nibbles) or 2c + 1 (high nibbles) of qh[l] for chunk c, at bit 4.
+// Chunks: 0 the header, 1-2 qh[0..32), 3 + 2c and 4 + 2c the 32 qs bytes of chunk c.
+template <class X>
+__device__ __forceinline__ float val_q5_k(const WReg<JK_Q5_K> &wr, const X &x) {
+    const uint4 h = wr.c[0];
+    const float xd = x.d();
+    const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
+    if ((d == 0.0f && dmin == 0.0f) || xd == 0.0f) return 0.0f;
+    const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    int sumi = 0, sum_mins = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint4 qa = wr.c[3 + 2 * c], qb = wr.c[4 + 2 * c];
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t wd = comp(i < 4 ? qa : qb, i & 3);
+            const uint32_t hd = comp(wr.c[1 + (i >> 2)], i & 3);
+            lo = dot4((int)((wd & 0x0F0F0F0Fu) | (((hd >> (2 * c)) & 0x01010101u) << 4)), x.q(16 * c + i), lo);
+            hi = dot4((int)(((wd >> 4) & 0x0F0F0F0Fu) | (((hd >> (2 * c + 1)) & 0x01010101u) << 4)),
+                      x.q(16 * c + 8 + i), hi);
+        }
+        const uint32_t scv = c < 2 ? sc_lo : sc_hi, mv = c < 2 ? m_lo : m_hi;
+        const int j = (2 * c) & 3;
+        sumi += byte_of(scv, j) * lo + byte_of(scv, j + 1) * hi;
+        const int bl = x.bsum(4 * c) + x.bsum(4 * c + 1);
+        const int bh = x.bsum(4 * c + 2) + x.bsum(4 * c + 3);
+        sum_mins += byte_of(mv, j) * bl + byte_of(mv, j + 1) * bh;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return (d * xd) * (float)sumi - (dmin * xd) * (float)sum_mins;
+}
+
 // dot_q6_k_q8_k_block_scalar (quant_q8.rs:1903-1942): per 16-element group j,
 // sum((q - 32) * x) = sum(q * x) - 32 * sum(x), with sum(x) from the recomputed sums.
 template <class X>
@@ -211,7 +273,9 @@ __device__ __forceinline__ float val_q6_k(const WReg<JK_Q6_K> &wr, const X &x) {
 }
 
 // dot_tq2_0_q8_k_block_scalar (quant_q8.rs:1992-2003): sum((t - 1) * x) = sum(t * x) - sum(x).
-// The device dword holds element 4j+i of activation dword j in bits 2j of byte i.
+// The device dword holds element 4j+i of activation dword j in bits 2j of byte i. TQ1_0
+// weights (dot_tq1_0_q8_k_block, quant_q8.rs:1977-1988: the same arithmetic on the trits of
+// unpack_tq1_0_lut) are stored in this layout and take this path.
 template <class X>
 __device__ __forceinline__ float val_tq2_0(const WReg<JK_TQ2_0> &wr, const X &x) {
     const float dw = f16_finite(wr.d);
@@ -232,8 +296,10 @@ __device__ __forceinline__ float val_tq2_0(const WReg<JK_TQ2_0> &wr, const X &x)
 template <int Q, class X>
 __device__ __forceinline__ float block_value(const WReg<Q> &wr, const X &x) {
     if constexpr (Q == JK_Q4_0) return val_q4_0(wr, x);
+    else if constexpr (Q == JK_Q5_0) return val_q5_0(wr, x);
     else if constexpr (Q == JK_Q8_0) return val_q8_0(wr, x);
     else if constexpr (Q == JK_Q4_K) return val_q4_k(wr, x);
+    else if constexpr (Q == JK_Q5_K) return val_q5_k(wr, x);
     else if constexpr (Q == JK_Q6_K) return val_q6_k(wr, x);
     else return val_tq2_0(wr, x);
 }
@@ -600,7 +666,7 @@ gemv_q8_group_kernel(GemvGroup grp) {
 // g * upg + w + NW * q (q < QPW); a wave issues all its weight loads up front, evaluates
 // them and keeps the results in registers until one store pass at the end. Without a loop
 // the compiler keeps every load where it is written and every wait exact.
-template <int Q> constexpr int kFastU = Q == JK_Q4_0 || Q == JK_Q8_0 ? 8 : Q == JK_TQ2_0 ? 2 : 1;
+template <int Q> constexpr int kFastU = Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_Q8_0 ? 8 : Q == JK_TQ2_0 ? 2 : 1;
 
 template <int Q, int LPR, bool F32, int NW, int QPW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<Q>))) void
@@ -848,8 +914,10 @@ jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n) {
     if (n <= 0) return JK_OK;
     switch (jobs[0].w.quant) {
     case JK_Q4_0: return launch_group_q<JK_Q4_0>(s, jobs, n);
+    case JK_Q5_0: return launch_group_q<JK_Q5_0>(s, jobs, n);
     case JK_Q8_0: return launch_group_q<JK_Q8_0>(s, jobs, n);
     case JK_Q4_K: return launch_group_q<JK_Q4_K>(s, jobs, n);
+    case JK_Q5_K: return launch_group_q<JK_Q5_K>(s, jobs, n);
     case JK_Q6_K: return launch_group_q<JK_Q6_K>(s, jobs, n);
     case JK_TQ2_0: return launch_group_q<JK_TQ2_0>(s, jobs, n);
     default: return fail(JK_CAPABILITY_MISMATCH, "gemv: unsupported quant %d", jobs[0].w.quant);

@@ -138,6 +138,15 @@ jk_status jk_host_vec_dot_q6_k_q8_k(const void *w, size_t w_len, const jk_block_
 jk_status jk_host_vec_dot_tq2_0_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out) {
     return host_vec_dot_row(JK_TQ2_0, w, w_len, x, nx, out, sizeof(jk_block_q8k));
 }
+jk_status jk_host_vec_dot_q5_0_q8_0(const void *w, size_t w_len, const jk_block_q8_0 *x, size_t nx, float *out) {
+    return host_vec_dot_row(JK_Q5_0, w, w_len, x, nx, out, sizeof(jk_block_q8_0));
+}
+jk_status jk_host_vec_dot_q5_k_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out) {
+    return host_vec_dot_row(JK_Q5_K, w, w_len, x, nx, out, sizeof(jk_block_q8k));
+}
+jk_status jk_host_vec_dot_tq1_0_q8_k(const void *w, size_t w_len, const jk_block_q8k *x, size_t nx, float *out) {
+    return host_vec_dot_row(JK_TQ1_0, w, w_len, x, nx, out, sizeof(jk_block_q8k));
+}
 
 jk_status jk_host_gemv_q4_0_q8_0(float *out, size_t n, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx) {
     return host_gemv(JK_Q4_0, out, n, w, x, nx, sizeof(jk_block_q8_0));
@@ -154,6 +163,15 @@ jk_status jk_host_gemv_q6_k_q8_k(float *out, size_t n, const jk_tensor_view *w, 
 jk_status jk_host_gemv_tq2_0_q8_k(float *out, size_t n, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx) {
     return host_gemv(JK_TQ2_0, out, n, w, x, nx, sizeof(jk_block_q8k));
 }
+jk_status jk_host_gemv_q5_0_q8_0(float *out, size_t n, const jk_tensor_view *w, const jk_block_q8_0 *x, size_t nx) {
+    return host_gemv(JK_Q5_0, out, n, w, x, nx, sizeof(jk_block_q8_0));
+}
+jk_status jk_host_gemv_q5_k_q8_k(float *out, size_t n, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx) {
+    return host_gemv(JK_Q5_K, out, n, w, x, nx, sizeof(jk_block_q8k));
+}
+jk_status jk_host_gemv_tq1_0_q8_k(float *out, size_t n, const jk_tensor_view *w, const jk_block_q8k *x, size_t nx) {
+    return host_gemv(JK_TQ1_0, out, n, w, x, nx, sizeof(jk_block_q8k));
+}
 
 jk_status jk_host_vec_dot_q4_0(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
     return host_vec_dot_f32(JK_Q4_0, out, n, w, in, in_len);
@@ -169,6 +187,12 @@ jk_status jk_host_vec_dot_q4_k_m(float *out, size_t n, const jk_tensor_view *w, 
 }
 jk_status jk_host_vec_dot_i2_s(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
     return host_vec_dot_f32(JK_I2_S, out, n, w, in, in_len);
+}
+jk_status jk_host_vec_dot_q5_0(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_Q5_0, out, n, w, in, in_len);
+}
+jk_status jk_host_vec_dot_q5_k(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_Q5_K, out, n, w, in, in_len);
 }
 
 // dequantize_tensor_row (quant.rs:2492-2568) with validate_token_row_geometry (1749-1808).
@@ -238,7 +262,7 @@ jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view 
                                float act_scale) {
     if (!w || (!w->bytes && w->byte_len) || (w->ndim && !w->shape)) return fail(JK_TENSOR_BOUNDS, "null tensor view");
     const int q = w->quant;
-    if (q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
+    if (q != JK_TQ1_0 && q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
         return fail(JK_TENSOR_BOUNDS, "BitLinear: unsupported quant type %d", q);
     if (w->ndim == 0) return fail(JK_TENSOR_BOUNDS, "BitLinear: empty tensor shape");
     const Fmt f = fmt_of(q);

@@ -4,22 +4,33 @@
 // 16-byte chunks; chunk c of block b of row r lives in plane c at
 //     planes + ((c * rows + r) * nb + b) * 16
 // and the block's f16 scale, when it is not inside a chunk, lives in the scale
-// plane at dplane[r * nb + b]. Lanes that walk consecutive blocks of one row
-// therefore read consecutive 16-byte chunks (one coalesced 128-bit load per
-// lane per plane), and the layout holds exactly the GGUF bytes:
+// plane at dplane[r * nb + b]; a 4-byte field that is neither (Q5_0's high bits)
+// lives in the word plane at hplane[r * nb + b]. Lanes that walk consecutive
+// blocks of one row therefore read consecutive 16-byte chunks (one coalesced
+// 128-bit load per lane per plane), and the layout holds exactly the GGUF bytes:
 //
-//   format  block  bytes  chunks (16 B)                         scale plane
-//   Q4_0     32     18    qs[0..16)                             d
-//   Q8_0     32     34    qs[0..16), qs[16..32)                 d
-//   Q4_K    256    144    [d dmin scales12], qs[16c..16c+16)    -
-//   Q6_K    256    210    ql x8, qh x4, scales x1               d
-//   TQ2_0   256     66    qs x4 (2-bit fields transposed 4x4    d
+//   format  block  bytes  chunks (16 B)                         scale  word
+//   Q4_0     32     18    qs[0..16)                             d      -
+//   Q5_0     32     22    qs[0..16)                             d      qh
+//   Q8_0     32     34    qs[0..16), qs[16..32)                 d      -
+//   Q4_K    256    144    [d dmin scales12], qs[16c..16c+16)    -      -
+//   Q5_K    256    176    [d dmin scales12], qh x2, qs x8       -      -
+//   Q6_K    256    210    ql x8, qh x4, scales x1               d      -
+//   TQ2_0   256     66    qs x4 (2-bit fields transposed 4x4    d      -
 //                         inside every dword, see below)
 //   I2_S    128     32    bytes[0..16), bytes[16..32)           - (tensor scale)
 //
 // TQ2_0 transposition: GGUF byte i of a dword holds elements 4i+j in bits 2j.
 // The device dword holds element 4j+i in bits 2j of byte i, so that
 // (w >> 2j) & 0x03030303 is the four elements of activation dword j.
+//
+// TQ1_0 (54 bytes: d, then base-3 digits, five per byte) is the one format that is
+// re-encoded at upload: its trits are decoded once and stored in the TQ2_0 device
+// layout (66 bytes per block), which every kernel then reads as TQ2_0. The two
+// formats have the same arithmetic on every entry point (the TQ1_0 and TQ2_0 arms
+// of the reference differ only in how the trits are unpacked); decoding five base-3
+// digits per byte in the kernels would cost about twice the VALU budget that
+// streaming the 54-byte blocks at full HBM bandwidth leaves.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -37,17 +48,26 @@ struct Fmt {
     int chunks;  // 16-byte chunks per block in the planes
     int d_off;   // byte offset of the f16 scale inside the GGUF block, -1 if none
     int q_off;   // byte offset of chunk 0 inside the GGUF block
+    int h_off;   // byte offset of the word-plane field inside the GGUF block, -1 if none
 };
 
+// Device layout of each GGUF format (TQ1_0: the GGUF block geometry; its device
+// layout is TQ2_0's, see dev_quant).
 __host__ __device__ constexpr Fmt fmt_of(int q) {
-    return q == JK_Q4_0   ? Fmt{JK_Q4_0, 32, 18, 1, 0, 2}
-           : q == JK_Q8_0 ? Fmt{JK_Q8_0, 32, 34, 2, 0, 2}
-           : q == JK_Q4_K ? Fmt{JK_Q4_K, 256, 144, 9, -1, 0}
-           : q == JK_Q6_K ? Fmt{JK_Q6_K, 256, 210, 13, 208, 0}
-           : q == JK_TQ2_0 ? Fmt{JK_TQ2_0, 256, 66, 4, 0, 2}
-           : q == JK_I2_S  ? Fmt{JK_I2_S, 128, 32, 2, -1, 0}
-                           : Fmt{0, 0, 0, 0, -1, 0};
+    return q == JK_Q4_0   ? Fmt{JK_Q4_0, 32, 18, 1, 0, 2, -1}
+           : q == JK_Q5_0 ? Fmt{JK_Q5_0, 32, 22, 1, 0, 6, 2}
+           : q == JK_Q8_0 ? Fmt{JK_Q8_0, 32, 34, 2, 0, 2, -1}
+           : q == JK_Q4_K ? Fmt{JK_Q4_K, 256, 144, 9, -1, 0, -1}
+           : q == JK_Q5_K ? Fmt{JK_Q5_K, 256, 176, 11, -1, 0, -1}
+           : q == JK_Q6_K ? Fmt{JK_Q6_K, 256, 210, 13, 208, 0, -1}
+           : q == JK_TQ1_0 ? Fmt{JK_TQ1_0, 256, 54, 0, 0, 2, -1}
+           : q == JK_TQ2_0 ? Fmt{JK_TQ2_0, 256, 66, 4, 0, 2, -1}
+           : q == JK_I2_S  ? Fmt{JK_I2_S, 128, 32, 2, -1, 0, -1}
+                           : Fmt{0, 0, 0, 0, -1, 0, -1};
 }
+
+// Format of the device layout a GGUF format is stored in.
+__host__ __device__ constexpr int dev_quant(int q) { return q == JK_TQ1_0 ? JK_TQ2_0 : q; }
 
 inline bool fmt_known(int q) { return fmt_of(q).be != 0; }
 inline size_t trailer_bytes(int q) { return q == JK_I2_S ? 32 : 0; }
@@ -56,6 +76,7 @@ inline size_t trailer_bytes(int q) { return q == JK_I2_S ? 32 : 0; }
 struct WeightDev {
     const uint8_t *planes;
     const uint16_t *dplane;
+    const uint32_t *hplane;
     float tensor_scale;
     int quant;
     int rows;
@@ -88,7 +109,8 @@ struct GemvGroup {
 }  // namespace jk
 
 struct jk_weight {
-    jk::WeightDev dev;
+    jk::WeightDev dev;  // dev.quant: the device layout (dev_quant of quant)
+    int quant;          // GGUF format of the uploaded tensor
     int device;
     size_t device_bytes;
     size_t gguf_bytes;
@@ -122,7 +144,8 @@ jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, si
 jk_status check_launch(const char *what);
 
 // Kernel launchers (device tier internals). All arguments are validated by callers.
-jk_status launch_repack(hipStream_t s, const WeightDev &w, const uint8_t *gguf);
+// gguf_quant: the GGUF format of the staged payload (w.quant is its device layout).
+jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf);
 jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1, float *out);
 jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk_block_q8_0 *out);
 jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk_block_q8k *out);

@@ -14,35 +14,62 @@ __device__ __forceinline__ uint32_t tq2_transpose(uint32_t v) {
     return o;
 }
 
-// One thread per (row, block): cut the GGUF block into its 16-byte chunks and scale.
-// The stores are the only writes of the planes; the weight handle is read-only after.
-__global__ __launch_bounds__(256) void repack_kernel(WeightDev w, const uint8_t *__restrict__ g) {
+__device__ __forceinline__ uint32_t le32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// Dword k (0..63) of the TQ2_0 payload that holds the trits of a TQ1_0 block: byte i of
+// the payload holds elements 4i..4i+3 as t + 1 in bits 2j. The TQ1_0 trits are the
+// base-3 digits of its bytes 2..52 (element 5i + j = digit j of byte 2 + i, least
+// significant first) and the lowest digit of byte 53 (element 255), as in
+// unpack_tq1_0_block_i8 (ime.rs:595-632).
+__device__ uint32_t tq1_as_tq2_dword(const uint8_t *src, int k) {
+    uint32_t out = 0;
+    for (int e4 = 0; e4 < 16; ++e4) {
+        const int e = 16 * k + e4;  // element; bits 2 * e4 of the dword
+        unsigned v;
+        if (e < 255) {
+            v = src[2 + e / 5];
+            for (int j = e % 5; j > 0; --j) v /= 3u;
+        } else {
+            v = src[53];
+        }
+        out |= (v % 3u) << (2 * e4);
+    }
+    return out;
+}
+
+// One thread per (row, block): cut the GGUF block into its 16-byte chunks, scale and
+// word (TQ1_0: re-encoded as the TQ2_0 payload first). The stores are the only writes of
+// the planes; the weight handle is read-only after.
+__global__ __launch_bounds__(256) void repack_kernel(WeightDev w, int gq, const uint8_t *__restrict__ g) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t total = (size_t)w.rows * (size_t)w.nb;
     if (idx >= total) return;
-    const Fmt f = fmt_of(w.quant);
-    const uint8_t *src = g + idx * (size_t)f.bb;
+    const Fmt f = fmt_of(w.quant);    // device layout
+    const Fmt fg = fmt_of(gq);        // GGUF block
+    const uint8_t *src = g + idx * (size_t)fg.bb;
     const int r = (int)(idx / (size_t)w.nb), b = (int)(idx % (size_t)w.nb);
     for (int c = 0; c < f.chunks; ++c) {
         uint32_t d4[4];
         for (int k = 0; k < 4; ++k) {
-            const uint8_t *p = src + f.q_off + 16 * c + 4 * k;
-            d4[k] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+            d4[k] = gq == JK_TQ1_0 ? tq1_as_tq2_dword(src, 4 * c + k) : le32(src + f.q_off + 16 * c + 4 * k);
             if (f.quant == JK_TQ2_0) d4[k] = tq2_transpose(d4[k]);
         }
         uint4 *dst = const_cast<uint4 *>(chunk_ptr(w, c, r, b));
         *dst = make_uint4(d4[0], d4[1], d4[2], d4[3]);
     }
-    if (f.d_off >= 0) {
+    if (f.d_off >= 0) {  // TQ1_0 and TQ2_0 both hold d at byte 0
         uint16_t h = (uint16_t)(src[f.d_off] | (src[f.d_off + 1] << 8));
         const_cast<uint16_t *>(w.dplane)[idx] = h;
     }
+    if (f.h_off >= 0) const_cast<uint32_t *>(w.hplane)[idx] = le32(src + f.h_off);
 }
 
-jk_status launch_repack(hipStream_t s, const WeightDev &w, const uint8_t *gguf) {
+jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf) {
     const size_t total = (size_t)w.rows * (size_t)w.nb;
     const unsigned grid = (unsigned)((total + 255) / 256);
-    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, w, gguf);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, w, gguf_quant, gguf);
     return check_launch("repack_kernel");
 }
 
@@ -52,9 +79,10 @@ __device__ __forceinline__ uint8_t chunk_byte(const uint4 &v, int i) {
 }
 
 // Dequantizes block b of row r into out[0..be) with the GGUF block dequantizers' arithmetic:
-// dequantize_q4_0_block (quant.rs:550-568), dequantize_q8_0_block (571-588),
-// dequantize_q4_k_m_block (lib.rs:720-766), dequantize_q6_k_block (quant.rs:594-648),
-// the TQ2_0 arm (quant.rs:2369-2378) and dequantize_i2_s_block (quant.rs:380-387).
+// dequantize_q4_0_block (quant.rs:550-568), dequantize_q5_0_block (160-164),
+// dequantize_q8_0_block (571-588), dequantize_q4_k_m_block (lib.rs:720-766),
+// dequantize_q5_k_block (quant.rs:651-706), dequantize_q6_k_block (594-648), the TQ1_0
+// and TQ2_0 arms (2359-2378; one device layout) and dequantize_i2_s_block (380-387).
 __device__ void dequant_block(const WeightDev &w, int r, int b, float *out) {
     switch (w.quant) {
     case JK_Q4_0: {
@@ -64,6 +92,19 @@ __device__ void dequant_block(const WeightDev &w, int r, int b, float *out) {
             const uint8_t x = chunk_byte(q, i);
             out[i] = d == 0.0f ? 0.0f : d * (float)((int)(x & 15) - 8);
             out[i + 16] = d == 0.0f ? 0.0f : d * (float)((int)(x >> 4) - 8);
+        }
+        break;
+    }
+    case JK_Q5_0: {  // dequantize_q5_0_block (quant.rs:160-164) via unpack_q5_0_block_i8 (139-157)
+        const float d = ld_dscale(w, r, b);
+        const uint4 q = ld_chunk(w, 0, r, b);
+        const uint32_t qh = w.hplane[(size_t)r * (size_t)w.nb + (size_t)b];
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t x = chunk_byte(q, i);
+            const int q0 = (int)((x & 15) | (((qh >> i) & 1u) << 4)) - 16;
+            const int q1 = (int)((x >> 4) | (((qh >> (i + 16)) & 1u) << 4)) - 16;
+            out[i] = d == 0.0f ? 0.0f : d * (float)q0;
+            out[i + 16] = d == 0.0f ? 0.0f : d * (float)q1;
         }
         break;
     }
@@ -95,6 +136,36 @@ __device__ void dequant_block(const WeightDev &w, int r, int b, float *out) {
                     const int l = 16 * half + i;
                     out[64 * c + l] = d1 * (float)(x & 15) - m1;
                     out[64 * c + 32 + l] = d2 * (float)(x >> 4) - m2;
+                }
+            }
+        }
+        break;
+    }
+    case JK_Q5_K: {  // dequantize_q5_k_block (quant.rs:651-706)
+        const uint4 h = ld_chunk(w, 0, r, b);
+        const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
+        if (d == 0.0f && dmin == 0.0f) {
+            for (int i = 0; i < 256; ++i) out[i] = 0.0f;
+            break;
+        }
+        uint8_t s[12], sc[8], m[8];
+        for (int i = 0; i < 12; ++i) s[i] = chunk_byte(h, 4 + i);
+        for (int j = 0; j < 4; ++j) { sc[j] = s[j] & 63; m[j] = s[j + 4] & 63; }
+        for (int j = 4; j < 8; ++j) {
+            sc[j] = (uint8_t)((s[j + 4] & 15) | ((s[j - 4] >> 6) << 4));
+            m[j] = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+        }
+        const uint4 qh[2] = {ld_chunk(w, 1, r, b), ld_chunk(w, 2, r, b)};
+        for (int c = 0; c < 4; ++c) {
+            const float d1 = d * (float)sc[2 * c], m1 = dmin * (float)m[2 * c];
+            const float d2 = d * (float)sc[2 * c + 1], m2 = dmin * (float)m[2 * c + 1];
+            for (int half = 0; half < 2; ++half) {
+                const uint4 q = ld_chunk(w, 3 + 2 * c + half, r, b);
+                for (int i = 0; i < 16; ++i) {
+                    const uint8_t x = chunk_byte(q, i), hb = chunk_byte(qh[half], i);
+                    const int l = 16 * half + i;
+                    out[64 * c + l] = d1 * (float)((x & 15) + ((hb >> (2 * c)) & 1) * 16) - m1;
+                    out[64 * c + 32 + l] = d2 * (float)((x >> 4) + ((hb >> (2 * c + 1)) & 1) * 16) - m2;
                 }
             }
         }

@@ -41,9 +41,12 @@ jk_status check_launch(const char *what) {
 static const char *quant_name(int q) {
     switch (q) {
     case JK_Q4_0: return "Q4_0";
+    case JK_Q5_0: return "Q5_0";
     case JK_Q8_0: return "Q8_0";
     case JK_Q4_K: return "Q4_K_M";
+    case JK_Q5_K: return "Q5_K";
     case JK_Q6_K: return "Q6_K";
+    case JK_TQ1_0: return "TQ1_0";
     case JK_TQ2_0: return "TQ2_0";
     case JK_I2_S: return "I2_S";
     default: return "unsupported";
@@ -212,17 +215,20 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
     if (rows >= kMaxRows || cols / (size_t)fmt_of(w->quant).be >= kMaxRows ||
         rows * (cols / (size_t)fmt_of(w->quant).be) >= ((size_t)1 << 28))
         return fail(JK_TENSOR_BOUNDS, "%s: matrix [%zu, %zu] exceeds the device index range", tname(w), rows, cols);
-    const Fmt f = fmt_of(w->quant);
+    const Fmt f = fmt_of(w->quant);             // GGUF block geometry
+    const Fmt fd = fmt_of(dev_quant(w->quant));  // device layout
     const size_t nb = cols / f.be;
     const size_t payload = rows * nb * f.bb;
-    const size_t plane_bytes = rows * nb * (size_t)f.chunks * 16;
-    const size_t dbytes = f.d_off >= 0 ? rows * nb * 2 : 0;
+    const size_t plane_bytes = rows * nb * (size_t)fd.chunks * 16;
+    const size_t dbytes = fd.d_off >= 0 ? rows * nb * 2 : 0;
+    const size_t dpad = (dbytes + 255) / 256 * 256;  // keeps the word plane 256-byte aligned
+    const size_t hbytes = fd.h_off >= 0 ? rows * nb * 4 : 0;
     jk_weight *h = new jk_weight();
     memset(h, 0, sizeof *h);
     JK_HIP(hipGetDevice(&h->device));
     hipStream_t st = (hipStream_t)s;
     uint8_t *staging = nullptr;
-    hipError_t e = hipMalloc(&h->alloc, plane_bytes + dbytes + 256);
+    hipError_t e = hipMalloc(&h->alloc, plane_bytes + dpad + hbytes + 256);
     if (e == hipSuccess) e = hipMalloc(&staging, payload);
     if (e == hipSuccess) e = hipMemcpyAsync(staging, w->bytes, payload, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) {
@@ -233,16 +239,18 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
     }
     h->dev.planes = (const uint8_t *)h->alloc;
     h->dev.dplane = dbytes ? (const uint16_t *)((uint8_t *)h->alloc + plane_bytes) : nullptr;
-    h->dev.quant = w->quant;
+    h->dev.hplane = hbytes ? (const uint32_t *)((uint8_t *)h->alloc + plane_bytes + dpad) : nullptr;
+    h->dev.quant = dev_quant(w->quant);
+    h->quant = w->quant;
     h->dev.rows = (int)rows;
     h->dev.cols = (int)cols;
     h->dev.nb = (int)nb;
     h->dev.tensor_scale = w->quant == JK_I2_S
                               ? read_trailer_scale((const uint8_t *)w->bytes + payload, w->byte_len - payload)
                               : 0.0f;
-    h->device_bytes = plane_bytes + dbytes;
+    h->device_bytes = plane_bytes + dbytes + hbytes;
     h->gguf_bytes = payload + trailer_bytes(w->quant);
-    jk_status rs = launch_repack(st, h->dev, staging);
+    jk_status rs = launch_repack(st, h->dev, w->quant, staging);
     // The staging buffer may only be released once the repack kernel has consumed it.
     hipError_t se = hipStreamSynchronize(st);
     (void)hipFree(staging);
@@ -265,7 +273,7 @@ jk_status jk_weight_free(jk_weight *w) {
 
 jk_status jk_weight_get_info(const jk_weight *w, jk_weight_info *out) {
     if (!w || !out) return fail(JK_TENSOR_BOUNDS, "null weight handle");
-    out->quant = w->dev.quant;
+    out->quant = w->quant;
     out->rows = (size_t)w->dev.rows;
     out->cols = (size_t)w->dev.cols;
     out->device_bytes = w->device_bytes;
@@ -366,10 +374,10 @@ jk_status jk_quantize_absmax_i8(jk_stream s, const float *x, size_t m, size_t k,
 static jk_status gemv_check(const jk_weight *w, int quant, const void *x, size_t nx, const float *y,
                             size_t r0, size_t r1, const char *name) {
     if (!w) return fail(JK_TENSOR_BOUNDS, "%s: null weight handle", name);
-    if (quant && w->dev.quant != quant)
+    if (quant && w->quant != quant)
         return fail(JK_TENSOR_BOUNDS, "%s: expected %s quant type, got %s", name, quant_name(quant),
-                    quant_name(w->dev.quant));
-    if (w->dev.quant == JK_I2_S)
+                    quant_name(w->quant));
+    if (w->quant == JK_I2_S)
         return fail(JK_CAPABILITY_MISMATCH, "%s: I2_S has no quant_q8 GEMV", name);
     // check_q8_block_len (quant_q8.rs:1562-1578)
     if (nx != (size_t)w->dev.nb)
@@ -403,6 +411,15 @@ jk_status jk_gemv_q6_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k 
 jk_status jk_gemv_tq2_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx, float *y, size_t n) {
     return gemv_full(s, w, JK_TQ2_0, x, nx, y, n, "gemv_tq2_0_q8_k");
 }
+jk_status jk_gemv_q5_0_q8_0(jk_stream s, const jk_weight *w, const jk_block_q8_0 *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_Q5_0, x, nx, y, n, "gemv_q5_0_q8_0");
+}
+jk_status jk_gemv_q5_k_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_Q5_K, x, nx, y, n, "gemv_q5_k_q8_k");
+}
+jk_status jk_gemv_tq1_0_q8_k(jk_stream s, const jk_weight *w, const jk_block_q8k *x, size_t nx, float *y, size_t n) {
+    return gemv_full(s, w, JK_TQ1_0, x, nx, y, n, "gemv_tq1_0_q8_k");
+}
 
 jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t nx, float *y, size_t r0, size_t r1) {
     JK_TRY(gemv_check(w, 0, x, nx, y, r0, r1, "gemv_q8_rows"));
@@ -415,8 +432,8 @@ jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t
 static jk_status gemv_job_check(const jk_gemv_job *j, size_t i, GemvJob *out) {
     const jk_weight *w = j->w;
     if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: null weight handle", i);
-    const int q = w->dev.quant;
-    if (q != JK_Q4_0 && q != JK_Q8_0 && q != JK_Q4_K && q != JK_Q6_K && q != JK_TQ2_0)
+    const int q = w->quant;
+    if (q == JK_I2_S)
         return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_batch: job %zu: %s has no quant_q8 GEMV", i, quant_name(q));
     if ((j->x_q8 == nullptr) == (j->x_f32 == nullptr))
         return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: exactly one of x_q8 and x_f32 must be set", i);
@@ -475,8 +492,9 @@ jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t
 // -------------------------------------------------------------- vec_dot (f32)
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
     if (!w) return fail(JK_TENSOR_BOUNDS, "vec_dot: null weight handle");
-    int q = w->dev.quant;
-    if (q == JK_TQ2_0) return fail(JK_CAPABILITY_MISMATCH, "vec_dot: TQ2_0 has no f32-activation matvec");
+    int q = w->quant;
+    if (q == JK_TQ2_0 || q == JK_TQ1_0)
+        return fail(JK_CAPABILITY_MISMATCH, "vec_dot: %s has no f32-activation matvec", quant_name(q));
     if (n != (size_t)w->dev.cols || y_len != (size_t)w->dev.rows)
         return fail(JK_TENSOR_BOUNDS, "vec_dot: matrix [%d, %d] does not match output len %zu and input len %zu",
                     w->dev.rows, w->dev.cols, y_len, n);
@@ -514,9 +532,9 @@ jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
                           size_t k, float *y, size_t y_len) {
     if (!w) return fail(JK_TENSOR_BOUNDS, "bitlinear: null weight handle");
-    int q = w->dev.quant;
+    int q = w->quant;
     // validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
-    if (q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
+    if (q != JK_TQ1_0 && q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
         return fail(JK_TENSOR_BOUNDS, "bitlinear: unsupported quant type %s", quant_name(q));
     if (m == 0 || k != (size_t)w->dev.cols || y_len != m * (size_t)w->dev.rows)
         return fail(JK_TENSOR_BOUNDS, "bitlinear: weights [%d, %d] do not match m=%zu k=%zu out=%zu", w->dev.rows,

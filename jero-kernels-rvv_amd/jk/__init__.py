@@ -24,10 +24,13 @@ LIB_PATH = os.path.join(PACKAGE_DIR, "libjk.so")
 HEADER_PATH = os.path.join(os.path.dirname(PACKAGE_DIR), "include", "jk.h")
 
 # ---------------------------------------------------------------- formats
-Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = 2, 8, 12, 14, 35, 36
-QUANT_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K_M", Q6_K: "Q6_K", TQ2_0: "TQ2_0", I2_S: "I2_S"}
-BLOCK_ELEMENTS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256, TQ2_0: 256, I2_S: 128}
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210, TQ2_0: 66, I2_S: 32}
+Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S = 2, 6, 8, 12, 13, 14, 34, 35, 36
+QUANT_NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K_M", Q5_K: "Q5_K", Q6_K: "Q6_K",
+               TQ1_0: "TQ1_0", TQ2_0: "TQ2_0", I2_S: "I2_S"}
+BLOCK_ELEMENTS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, TQ1_0: 256, TQ2_0: 256, I2_S: 128}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, TQ1_0: 54, TQ2_0: 66, I2_S: 32}
+# Formats whose quant_q8 GEMV takes BlockQ8_0 activations (the others take BlockQ8K).
+Q8_0_ACT = (Q4_0, Q5_0, Q8_0)
 TRAILER_BYTES = {I2_S: 32}
 
 # BlockQ8_0 (quant_q8.rs:37-44) and BlockQ8K (62-72), #[repr(C)] byte layouts.
@@ -190,6 +193,21 @@ def vec_dot_tq2_0_q8_k(w_blocks, x_blocks) -> float:
     return _vec_dot_row("jk_host_vec_dot_tq2_0_q8_k", w_blocks, x_blocks)
 
 
+def vec_dot_q5_0_q8_0_blocks(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:1478"""
+    return _vec_dot_row("jk_host_vec_dot_q5_0_q8_0", w_blocks, x_blocks)
+
+
+def vec_dot_q5_k_q8_k(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:3041"""
+    return _vec_dot_row("jk_host_vec_dot_q5_k_q8_k", w_blocks, x_blocks)
+
+
+def vec_dot_tq1_0_q8_k(w_blocks, x_blocks) -> float:
+    """quant_q8.rs:3071"""
+    return _vec_dot_row("jk_host_vec_dot_tq1_0_q8_k", w_blocks, x_blocks)
+
+
 def _gemv(fn: str, out: np.ndarray, weights: TensorView, x_blocks) -> None:
     x = np.ascontiguousarray(x_blocks)
     v = weights.c()
@@ -221,6 +239,21 @@ def gemv_tq2_0_q8_k(out, weights, x_blocks):
     _gemv("jk_host_gemv_tq2_0_q8_k", out, weights, x_blocks)
 
 
+def gemv_q5_0_q8_0(out, weights, x_blocks):
+    """quant_q8.rs:1628"""
+    _gemv("jk_host_gemv_q5_0_q8_0", out, weights, x_blocks)
+
+
+def gemv_q5_k_q8_k(out, weights, x_blocks):
+    """quant_q8.rs:3160"""
+    _gemv("jk_host_gemv_q5_k_q8_k", out, weights, x_blocks)
+
+
+def gemv_tq1_0_q8_k(out, weights, x_blocks):
+    """quant_q8.rs:3219"""
+    _gemv("jk_host_gemv_tq1_0_q8_k", out, weights, x_blocks)
+
+
 def _vec_dot_f32(fn: str, out: np.ndarray, weights: TensorView, inp) -> None:
     x = _f32(inp).reshape(-1)
     v = weights.c()
@@ -250,6 +283,16 @@ def vec_dot_q4_k_m(out, weights, inp):
 def vec_dot_i2_s(out, weights, inp):
     """quant.rs:2199"""
     _vec_dot_f32("jk_host_vec_dot_i2_s", out, weights, inp)
+
+
+def vec_dot_q5_0(out, weights, inp):
+    """quant.rs:2036"""
+    _vec_dot_f32("jk_host_vec_dot_q5_0", out, weights, inp)
+
+
+def vec_dot_q5_k(out, weights, inp):
+    """quant.rs:1238"""
+    _vec_dot_f32("jk_host_vec_dot_q5_k", out, weights, inp)
 
 
 def dequantize_tensor_row(weights: TensorView, row: int, out: np.ndarray) -> None:
@@ -337,7 +380,8 @@ def dev_quantize_absmax_i8(x, m, k, q, scales, stream=None):
 
 
 _GEMV_FN = {Q4_0: "jk_gemv_q4_0_q8_0", Q8_0: "jk_gemv_q8_0_q8_0", Q4_K: "jk_gemv_q4_k_q8_k",
-            Q6_K: "jk_gemv_q6_k_q8_k", TQ2_0: "jk_gemv_tq2_0_q8_k"}
+            Q6_K: "jk_gemv_q6_k_q8_k", TQ2_0: "jk_gemv_tq2_0_q8_k", Q5_0: "jk_gemv_q5_0_q8_0",
+            Q5_K: "jk_gemv_q5_k_q8_k", TQ1_0: "jk_gemv_tq1_0_q8_k"}
 
 
 def dev_gemv_q8(w: Weight, x, nx, y, y_len, stream=None, fn: str | None = None):

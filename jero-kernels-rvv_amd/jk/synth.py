@@ -2,9 +2,13 @@
 
 Distributions (one GGUF block per row-block, little-endian):
   Q4_0   d = f16(|N(0,1)| * 0.02 / 8), 16 bytes of uniform nibbles
+  Q5_0   d = f16(|N(0,1)| * 0.02 / 16), 4 random high-bit bytes, 16 bytes of uniform nibbles
   Q8_0   d = f16(|N(0,1)| * 0.02 / 127), 32 quants uniform in [-127, 127]
   Q4_K   d, dmin = f16(|N(0,1)| * 0.01), 12 random scale bytes, 128 random quant bytes
+  Q5_K   d, dmin = f16(|N(0,1)| * 0.005), 12 random scale bytes, 160 random qh / quant bytes
   Q6_K   128 B ql + 64 B qh random, 16 i8 scales uniform in [-32, 31], d = f16(|N(0,1)| * 0.001)
+  TQ1_0  trits uniform in {-1, 0, +1}, five base-3 digits per byte (element 5i+j = digit j of
+         byte 2+i, element 255 = byte 53), d = f16(1.0)
   TQ2_0  trits uniform in {-1, 0, +1} packed 2 bits each (element 4i+j = bits 2j of qs[i]), d = f16(1.0)
   I2_S   trits uniform in {-1, 0, +1} (byte g: elements g, 32+g, 64+g, 96+g in bits 7:6..1:0),
          32-byte trailer holding the f32 tensor scale 1.0
@@ -14,7 +18,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import BLOCK_BYTES, BLOCK_ELEMENTS, I2_S, Q4_0, Q4_K, Q6_K, Q8_0, TQ2_0
+from . import BLOCK_BYTES, BLOCK_ELEMENTS, I2_S, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, TQ1_0, TQ2_0
 
 
 def _f16_bits(v: np.ndarray) -> np.ndarray:
@@ -38,6 +42,9 @@ def gguf_weights(quant: int, rows: int, cols: int, seed: int) -> np.ndarray:
     if quant == Q4_0:
         _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.02 / 8))
         blocks[:, 2:] = rng.integers(0, 256, size=(nb, 16), dtype=np.uint8)
+    elif quant == Q5_0:
+        _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.02 / 16))
+        blocks[:, 2:] = rng.integers(0, 256, size=(nb, 20), dtype=np.uint8)
     elif quant == Q8_0:
         _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.02 / 127))
         blocks[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
@@ -45,6 +52,10 @@ def gguf_weights(quant: int, rows: int, cols: int, seed: int) -> np.ndarray:
         _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.01))
         _put_u16(blocks, 2, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.01))
         blocks[:, 4:] = rng.integers(0, 256, size=(nb, 140), dtype=np.uint8)
+    elif quant == Q5_K:
+        _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.005))
+        _put_u16(blocks, 2, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.005))
+        blocks[:, 4:] = rng.integers(0, 256, size=(nb, 172), dtype=np.uint8)
     elif quant == Q6_K:
         blocks[:, :192] = rng.integers(0, 256, size=(nb, 192), dtype=np.uint8)
         blocks[:, 192:208] = rng.integers(-32, 32, size=(nb, 16), dtype=np.int8).view(np.uint8)
@@ -52,6 +63,12 @@ def gguf_weights(quant: int, rows: int, cols: int, seed: int) -> np.ndarray:
     elif quant == TQ2_0:
         t = rng.integers(0, 3, size=(nb, 64, 4), dtype=np.uint8)  # 2-bit value = trit + 1
         blocks[:, 2:] = t[..., 0] | (t[..., 1] << 2) | (t[..., 2] << 4) | (t[..., 3] << 6)
+        _put_u16(blocks, 0, np.full(nb, 0x3C00, dtype=np.uint16))
+    elif quant == TQ1_0:
+        t = rng.integers(0, 3, size=(nb, 256), dtype=np.int64)  # digit = trit + 1
+        digits = t[:, :255].reshape(nb, 51, 5)
+        blocks[:, 2:53] = (digits * np.array([1, 3, 9, 27, 81])).sum(axis=2).astype(np.uint8)
+        blocks[:, 53] = t[:, 255].astype(np.uint8)
         _put_u16(blocks, 0, np.full(nb, 0x3C00, dtype=np.uint16))
     elif quant == I2_S:
         t = rng.integers(0, 3, size=(nb, 4, 32), dtype=np.uint8)  # [group][g] -> element 32*group + g
@@ -74,7 +91,8 @@ def random_weights(quant: int, rows: int, cols: int, seed: int, specials: bool =
     nb = rows * (cols // be)
     blocks = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
     # keep normal scales modest so sums stay finite; specials override some of them
-    scale_offs = {Q4_0: [0], Q8_0: [0], Q4_K: [0, 2], Q6_K: [208], TQ2_0: [0]}.get(quant, [])
+    scale_offs = {Q4_0: [0], Q5_0: [0], Q8_0: [0], Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], TQ1_0: [0],
+                  TQ2_0: [0]}.get(quant, [])
     for off in scale_offs:
         mag = rng.uniform(1e-4, 0.05, size=nb) * rng.choice([-1.0, 1.0], size=nb)
         _put_u16(blocks, off, _f16_bits(mag))

@@ -17,8 +17,8 @@
 /* ------------------------------------------------------------------------- */
 size_t or_block_elements(int q) {
     switch (q) {
-    case OR_Q4_0: case OR_Q8_0: return 32;
-    case OR_Q4_K: case OR_Q6_K: case OR_TQ2_0: return 256;
+    case OR_Q4_0: case OR_Q8_0: case OR_Q5_0: return 32;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_TQ1_0: case OR_TQ2_0: return 256;
     case OR_I2_S: return 128;
     default: return 0;
     }
@@ -27,8 +27,11 @@ size_t or_block_elements(int q) {
 size_t or_block_bytes(int q) {
     switch (q) {
     case OR_Q4_0: return 18;
+    case OR_Q5_0: return 22;
     case OR_Q8_0: return 34;
     case OR_Q4_K: return 144;
+    case OR_Q5_K: return 176;
+    case OR_TQ1_0: return 54;
     case OR_Q6_K: return 210;
     case OR_TQ2_0: return 66;
     case OR_I2_S: return 32;
@@ -155,6 +158,68 @@ void or_dequantize_q6_k_block(const uint8_t *blk, float *out) {
     }
 }
 
+/* quant.rs:139-157: q = (nibble | 16 * bit) - 16 with the 32 high bits in a little-endian
+ * u32 at bytes 2..6 (bit j for element j, bit j + 16 for element j + 16). */
+float or_unpack_q5_0_block_i8(const uint8_t *blk, int8_t *out) {
+    float d = or_f16_to_f32_finite(rd16(blk));
+    uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+    for (int j = 0; j < 16; j++) {
+        uint8_t b = blk[6 + j];
+        int h0 = (int)((qh >> j) & 1u) << 4, h1 = (int)((qh >> (j + 16)) & 1u) << 4;
+        out[j] = (int8_t)(((b & 0x0F) | h0) - 16);
+        out[j + 16] = (int8_t)((((b >> 4) & 0x0F) | h1) - 16);
+    }
+    return d;
+}
+
+static void scale_i8_into_f32(float scale, const int8_t *q, float *out, int n);
+
+/* quant.rs:160-164 */
+void or_dequantize_q5_0_block(const uint8_t *blk, float *out) {
+    int8_t q[32];
+    float d = or_unpack_q5_0_block_i8(blk, q);
+    scale_i8_into_f32(d, q, out, 32);
+}
+
+/* quant.rs:651-706: both scales zero -> all +0.0; else d1 * q - m1 per element (q up to 31) */
+void or_dequantize_q5_k_block(const uint8_t *blk, float *out) {
+    float d = or_f16_to_f32_finite(rd16(blk));
+    float dmin = or_f16_to_f32_finite(rd16(blk + 2));
+    if (d == 0.0f && dmin == 0.0f) { for (int i = 0; i < 256; i++) out[i] = 0.0f; return; }
+    uint8_t sc[8], m[8];
+    unpack_k4_scales_mins(blk + 4, sc, m);
+    const uint8_t *qh = blk + 16, *qs = blk + 48;
+    for (int c = 0; c < 4; c++) {
+        float d1 = d * (float)sc[2 * c], m1 = dmin * (float)m[2 * c];
+        float d2 = d * (float)sc[2 * c + 1], m2 = dmin * (float)m[2 * c + 1];
+        uint8_t u1 = (uint8_t)(1u << (2 * c)), u2 = (uint8_t)(2u << (2 * c));
+        for (int l = 0; l < 32; l++) {
+            uint8_t q1 = (uint8_t)((qs[32 * c + l] & 0x0F) + ((qh[l] & u1) ? 16 : 0));
+            out[64 * c + l] = d1 * (float)q1 - m1;
+        }
+        for (int l = 0; l < 32; l++) {
+            uint8_t q2 = (uint8_t)((qs[32 * c + l] >> 4) + ((qh[l] & u2) ? 16 : 0));
+            out[64 * c + 32 + l] = d2 * (float)q2 - m2;
+        }
+    }
+}
+
+/* ime.rs:595-632 (the crate's TQ1_0 layout): d at bytes 0..2, then bytes 2..53 each carry
+ * five base-3 digits, least significant first (element 5i + j = digit j of byte 2 + i),
+ * and byte 53 carries element 255 as its lowest digit; trit t maps to t - 1. */
+float or_unpack_tq1_0_block_i8(const uint8_t *blk, int8_t *out) {
+    float s = or_f16_to_f32_finite(rd16(blk));
+    for (int i = 0; i < 51; i++) {
+        unsigned b = blk[2 + i];
+        for (int j = 0; j < 5; j++) {
+            out[5 * i + j] = (int8_t)((int)(b % 3u) - 1);
+            b /= 3u;
+        }
+    }
+    out[255] = (int8_t)((int)(blk[53] % 3u) - 1);
+    return s;
+}
+
 /* ime.rs:636-658: crate layout, d first, element 4i+j = bits 2j of qs[i] */
 float or_unpack_tq2_0_block_i8(const uint8_t *blk, int8_t *out) {
     float s = or_f16_to_f32_finite(rd16(blk));
@@ -207,6 +272,14 @@ static void dequant_block_any(int q, const uint8_t *blk, float i2s_scale, float 
     case OR_Q8_0: or_dequantize_q8_0_block(blk, out); break;
     case OR_Q4_K: or_dequantize_q4_k_block(blk, out); break;
     case OR_Q6_K: or_dequantize_q6_k_block(blk, out); break;
+    case OR_Q5_0: or_dequantize_q5_0_block(blk, out); break; /* quant.rs:2306-2310 */
+    case OR_Q5_K: or_dequantize_q5_k_block(blk, out); break; /* quant.rs:2335-2339 */
+    case OR_TQ1_0: { /* quant.rs:2359-2368 */
+        int8_t t[256];
+        float d = or_unpack_tq1_0_block_i8(blk, t);
+        scale_i8_into_f32(d, t, out, 256);
+        break;
+    }
     case OR_TQ2_0: { /* quant.rs:2369-2378 */
         int8_t t[256];
         float d = or_unpack_tq2_0_block_i8(blk, t);
@@ -553,11 +626,62 @@ static float dot_tq2_0_q8_k_block(const uint8_t *w, const or_block_q8k *x) {
 
 typedef float (*blockdot_fn)(const uint8_t *, const void *);
 
+/* quant_q8.rs:688-703 */
+static float dot_q5_0_q8_0_block(const uint8_t *w, const or_block_q8_0 *x) {
+    float dw = or_f16_to_f32_finite(rd16(w));
+    if (dw == 0.0f || x->d == 0.0f) return 0.0f;
+    int8_t q[32];
+    or_unpack_q5_0_block_i8(w, q);
+    int32_t sumi = 0;
+    for (int j = 0; j < 16; j++) sumi += q[j] * x->qs[j] + q[j + 16] * x->qs[j + 16];
+    return (float)sumi * (dw * x->d);
+}
+
+/* quant_q8.rs:1866-1899: the Q4_K recipe with a fifth bit (+16) from qh */
+static float dot_q5_k_q8_k_block(const uint8_t *w, const or_block_q8k *x) {
+    float d = or_f16_to_f32_finite(rd16(w)), dmin = or_f16_to_f32_finite(rd16(w + 2));
+    if ((d == 0.0f && dmin == 0.0f) || x->d == 0.0f) return 0.0f;
+    uint8_t sc[8], m[8];
+    unpack_k4_scales_mins(w + 4, sc, m);
+    const uint8_t *qh = w + 16, *qs = w + 48;
+    int32_t sumi = 0, sum_mins = 0;
+    for (int c = 0; c < 4; c++) {
+        uint8_t u1 = (uint8_t)(1u << (2 * c)), u2 = (uint8_t)(2u << (2 * c));
+        int32_t lo = 0, hi = 0;
+        for (int l = 0; l < 32; l++) {
+            uint8_t b = qs[32 * c + l];
+            int32_t h1 = (qh[l] & u1) ? 16 : 0, h2 = (qh[l] & u2) ? 16 : 0;
+            lo += ((int32_t)(b & 0x0F) | h1) * x->qs[64 * c + l];
+            hi += ((int32_t)(b >> 4) | h2) * x->qs[64 * c + 32 + l];
+        }
+        sumi += (int32_t)sc[2 * c] * lo + (int32_t)sc[2 * c + 1] * hi;
+        int32_t bl = (int32_t)x->bsums[4 * c] + x->bsums[4 * c + 1];
+        int32_t bh = (int32_t)x->bsums[4 * c + 2] + x->bsums[4 * c + 3];
+        sum_mins += (int32_t)m[2 * c] * bl + (int32_t)m[2 * c + 1] * bh;
+    }
+    return (d * x->d) * (float)sumi - (dmin * x->d) * (float)sum_mins;
+}
+
+/* quant_q8.rs:1977-1988 with unpack_tq1_0_lut (1966-1975), whose table holds the same
+ * base-3 digits as unpack_tq1_0_block_i8 */
+static float dot_tq1_0_q8_k_block(const uint8_t *w, const or_block_q8k *x) {
+    if (x->d == 0.0f) return 0.0f;
+    int8_t t[256];
+    float dw = or_unpack_tq1_0_block_i8(w, t);
+    if (dw == 0.0f) return 0.0f;
+    int32_t dot = 0;
+    for (int i = 0; i < 256; i++) dot += t[i] * x->qs[i];
+    return (float)dot * (dw * x->d);
+}
+
 static float bd_q4_0(const uint8_t *w, const void *x) { return dot_q4_0_q8_0_block(w, x); }
 static float bd_q8_0(const uint8_t *w, const void *x) { return dot_q8_0_q8_0_block(w, x); }
 static float bd_q4_k(const uint8_t *w, const void *x) { return dot_q4_k_q8_k_block(w, x); }
 static float bd_q6_k(const uint8_t *w, const void *x) { return dot_q6_k_q8_k_block(w, x); }
 static float bd_tq2_0(const uint8_t *w, const void *x) { return dot_tq2_0_q8_k_block(w, x); }
+static float bd_q5_0(const uint8_t *w, const void *x) { return dot_q5_0_q8_0_block(w, x); }
+static float bd_q5_k(const uint8_t *w, const void *x) { return dot_q5_k_q8_k_block(w, x); }
+static float bd_tq1_0(const uint8_t *w, const void *x) { return dot_tq1_0_q8_k_block(w, x); }
 
 static blockdot_fn blockdot_for(int q, size_t *xsz) {
     switch (q) {
@@ -566,11 +690,15 @@ static blockdot_fn blockdot_for(int q, size_t *xsz) {
     case OR_Q4_K: *xsz = sizeof(or_block_q8k); return bd_q4_k;
     case OR_Q6_K: *xsz = sizeof(or_block_q8k); return bd_q6_k;
     case OR_TQ2_0: *xsz = sizeof(or_block_q8k); return bd_tq2_0;
+    case OR_Q5_0: *xsz = sizeof(or_block_q8_0); return bd_q5_0;
+    case OR_Q5_K: *xsz = sizeof(or_block_q8k); return bd_q5_k;
+    case OR_TQ1_0: *xsz = sizeof(or_block_q8k); return bd_tq1_0;
     default: return 0;
     }
 }
 
-/* Row drivers dot_*_row (quant_q8.rs:1217-1238, 2815-2830, 2902-2915, 2987-2993):
+/* Row drivers dot_*_row (quant_q8.rs:1217-1238, 1290-1311, 2815-2830, 2860-2873, 2902-2915,
+ * 2944-2950, 2987-2993):
  * `.map(block_dot).sum()` -> fold from -0.0 in block order. */
 static float row_sum_neg0(blockdot_fn f, const uint8_t *w, size_t bb, const uint8_t *x, size_t xsz,
                           size_t nb) {
@@ -608,6 +736,18 @@ int or_vec_dot_q6_k_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, 
 /* quant_q8.rs:3086 */
 int or_vec_dot_tq2_0_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx, float *out) {
     return vec_dot_rowblocks(OR_TQ2_0, w, w_len, x, nx, out);
+}
+/* vec_dot_q5_0_q8_0_blocks (quant_q8.rs:1478) */
+int or_vec_dot_q5_0_q8_0(const uint8_t *w, size_t w_len, const or_block_q8_0 *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_Q5_0, w, w_len, x, nx, out);
+}
+/* quant_q8.rs:3041 */
+int or_vec_dot_q5_k_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_Q5_K, w, w_len, x, nx, out);
+}
+/* quant_q8.rs:3071 */
+int or_vec_dot_tq1_0_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx, float *out) {
+    return vec_dot_rowblocks(OR_TQ1_0, w, w_len, x, nx, out);
 }
 
 /* run_4row_chunked_gemv (quant_q8.rs:1510-1560) with accumulate = false:
@@ -663,6 +803,18 @@ int or_gemv_q6_k_q8_k(float *out, size_t out_len, const or_tensor_view *w, const
 int or_gemv_tq2_0_q8_k(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8k *x, size_t nx) {
     return gemv_entry(OR_TQ2_0, out, out_len, w, x, nx);
 }
+/* quant_q8.rs:1628-1650 */
+int or_gemv_q5_0_q8_0(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8_0 *x, size_t nx) {
+    return gemv_entry(OR_Q5_0, out, out_len, w, x, nx);
+}
+/* quant_q8.rs:3160-3182 */
+int or_gemv_q5_k_q8_k(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8k *x, size_t nx) {
+    return gemv_entry(OR_Q5_K, out, out_len, w, x, nx);
+}
+/* quant_q8.rs:3219-3242 */
+int or_gemv_tq1_0_q8_k(float *out, size_t out_len, const or_tensor_view *w, const or_block_q8k *x, size_t nx) {
+    return gemv_entry(OR_TQ1_0, out, out_len, w, x, nx);
+}
 
 /* ------------------------------------------------------------------------- */
 /* f32-activation matvec: dequantize block, dot_product_f32_scalar, row sum   */
@@ -712,6 +864,14 @@ int or_vec_dot_q4_k_m(float *out, size_t out_len, const or_tensor_view *w, const
 int or_vec_dot_i2_s(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
     return vec_dot_f32_entry(OR_I2_S, out, out_len, w, in, in_len);
 }
+/* vec_dot_q5_0 (quant.rs:2036-2054) -> vec_dot_generic_block (1995-2029) */
+int or_vec_dot_q5_0(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q5_0, out, out_len, w, in, in_len);
+}
+/* vec_dot_q5_k (quant.rs:1238-1251) -> vec_dot_q5_k_scalar (1181-1219) */
+int or_vec_dot_q5_k(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q5_K, out, out_len, w, in, in_len);
+}
 
 /* ------------------------------------------------------------------------- */
 /* Repacked block-scaled i8 weights and GEMM                                  */
@@ -745,7 +905,7 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
     if (st) return st;
     int cps = w->quant == OR_Q6_K ? 1 : 2;
     size_t k_padded = (cols + 31) / 32 * 32, sg = k_padded / 16 / cps;
-    int has_mins = w->quant == OR_Q4_K;
+    int has_mins = w->quant == OR_Q4_K || w->quant == OR_Q5_K;
     if (sg_out) *sg_out = sg;
     if (has_mins_out) *has_mins_out = has_mins;
     if (cps_out) *cps_out = cps;
@@ -797,6 +957,37 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
                         qr[256 * b + 64 * c + 32 + l] = (int8_t)(blk[16 + 32 * c + l] >> 4);
                     }
                 }
+                break;
+            }
+            case OR_Q5_0: { /* repack.rs:1830-1843 */
+                int8_t t[32];
+                float d = or_unpack_q5_0_block_i8(blk, t);
+                sr[b] = d;
+                if (d != 0.0f) memcpy(qr + 32 * b, t, 32);
+                break;
+            }
+            case OR_Q5_K: { /* repack.rs:1959-2002 */
+                float d = or_f16_to_f32_finite(rd16(blk)), dmin = or_f16_to_f32_finite(rd16(blk + 2));
+                uint8_t sc[8], m[8];
+                unpack_k4_scales_mins(blk + 4, sc, m);
+                const uint8_t *qh = blk + 16, *qs = blk + 48;
+                for (int c = 0; c < 4; c++) {
+                    size_t g0 = 8 * b + 2 * c;
+                    sr[g0] = d * (float)sc[2 * c];
+                    mr[g0] = dmin * (float)m[2 * c];
+                    sr[g0 + 1] = d * (float)sc[2 * c + 1];
+                    mr[g0 + 1] = dmin * (float)m[2 * c + 1];
+                    uint8_t u1 = (uint8_t)(1u << (2 * c)), u2 = (uint8_t)(2u << (2 * c));
+                    for (int l = 0; l < 32; l++) {
+                        qr[256 * b + 64 * c + l] = (int8_t)((qs[32 * c + l] & 0x0F) + ((qh[l] & u1) ? 16 : 0));
+                        qr[256 * b + 64 * c + 32 + l] = (int8_t)((qs[32 * c + l] >> 4) + ((qh[l] & u2) ? 16 : 0));
+                    }
+                }
+                break;
+            }
+            case OR_TQ1_0: { /* repack.rs:2046-2060: trits always written */
+                float d = or_unpack_tq1_0_block_i8(blk, qr + 256 * b);
+                for (int s = 0; s < 8; s++) sr[8 * b + s] = d;
                 break;
             }
             case OR_Q6_K: { /* repack.rs:2003-2046 */
@@ -884,11 +1075,11 @@ int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t
 /* BitLinear: bitlinear_i8_rvv (ime.rs:882-938)                               */
 /* ------------------------------------------------------------------------- */
 
-/* validate_bitlinear_dimensions (ime.rs:660-763); TQ1_0 is outside this path. */
+/* validate_bitlinear_dimensions (ime.rs:660-763) */
 int or_bitlinear_i8(float *out, size_t out_len, const or_tensor_view *w, const int8_t *act,
                     size_t act_len, float act_scale) {
     int q = w->quant;
-    if (q != OR_TQ2_0 && q != OR_Q8_0 && q != OR_I2_S) return OR_TENSOR_BOUNDS;
+    if (q != OR_TQ1_0 && q != OR_TQ2_0 && q != OR_Q8_0 && q != OR_I2_S) return OR_TENSOR_BOUNDS;
     if (w->ndim == 0) return OR_TENSOR_BOUNDS;
     size_t be = or_block_elements(q), bb = or_block_bytes(q);
     if (w->ndim == 2) {
@@ -911,7 +1102,8 @@ int or_bitlinear_i8(float *out, size_t out_len, const or_tensor_view *w, const i
         for (size_t b = 0; b < nb; b++) {
             const uint8_t *blk = w->bytes + (r * nb + b) * bb;
             float bs; /* unpack_bitlinear_block_i8, ime.rs:792-871 */
-            if (q == OR_TQ2_0) bs = or_unpack_tq2_0_block_i8(blk, wb);
+            if (q == OR_TQ1_0) bs = or_unpack_tq1_0_block_i8(blk, wb);
+            else if (q == OR_TQ2_0) bs = or_unpack_tq2_0_block_i8(blk, wb);
             else if (q == OR_Q8_0) {
                 bs = or_f16_to_f32_finite(rd16(blk));
                 for (int i = 0; i < 32; i++) wb[i] = (int8_t)blk[2 + i];

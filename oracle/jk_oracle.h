@@ -1,6 +1,7 @@
 /*
  * jk_oracle.h -- CPU restatement of the jero-kernels-rvv portable scalar fallback
- * for the quantized-matmul path (Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S).
+ * for the quantized-matmul path (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0,
+ * I2_S).
  *
  * TEST INFRASTRUCTURE ONLY. This library is the oracle the HIP product library
  * (libjk.so) is compared with, and the timed CPU baseline of bench.py. It is
@@ -30,9 +31,12 @@ enum { OR_OK = 0, OR_TENSOR_BOUNDS = 1, OR_CAPABILITY_MISMATCH = 2 };
 /* GGML type ids (the reference's QuantType variants on this path). */
 enum {
     OR_Q4_0 = 2,
+    OR_Q5_0 = 6,
     OR_Q8_0 = 8,
     OR_Q4_K = 12, /* QuantType::Q4_K_M */
+    OR_Q5_K = 13,
     OR_Q6_K = 14,
+    OR_TQ1_0 = 34,
     OR_TQ2_0 = 35,
     OR_I2_S = 36
 };
@@ -83,6 +87,10 @@ void or_dequantize_q4_0_block(const uint8_t *blk, float *out);
 void or_dequantize_q8_0_block(const uint8_t *blk, float *out);
 void or_dequantize_q4_k_block(const uint8_t *blk, float *out);
 void or_dequantize_q6_k_block(const uint8_t *blk, float *out);
+float or_unpack_q5_0_block_i8(const uint8_t *blk, int8_t *out);
+void or_dequantize_q5_0_block(const uint8_t *blk, float *out);
+void or_dequantize_q5_k_block(const uint8_t *blk, float *out);
+float or_unpack_tq1_0_block_i8(const uint8_t *blk, int8_t *out);
 float or_unpack_tq2_0_block_i8(const uint8_t *blk, int8_t *out);
 void or_unpack_i2_s_block_i8(const uint8_t *blk, int8_t *out);
 void or_dequantize_i2_s_block(const uint8_t *blk, float scale, float *out);
@@ -112,6 +120,12 @@ int or_vec_dot_q6_k_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, 
                          float *out);
 int or_vec_dot_tq2_0_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx,
                           float *out);
+int or_vec_dot_q5_0_q8_0(const uint8_t *w, size_t w_len, const or_block_q8_0 *x, size_t nx,
+                         float *out);
+int or_vec_dot_q5_k_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx,
+                         float *out);
+int or_vec_dot_tq1_0_q8_k(const uint8_t *w, size_t w_len, const or_block_q8k *x, size_t nx,
+                          float *out);
 int or_gemv_q4_0_q8_0(float *out, size_t out_len, const or_tensor_view *w,
                       const or_block_q8_0 *x, size_t nx);
 int or_gemv_q8_0_q8_0(float *out, size_t out_len, const or_tensor_view *w,
@@ -121,6 +135,12 @@ int or_gemv_q4_k_q8_k(float *out, size_t out_len, const or_tensor_view *w,
 int or_gemv_q6_k_q8_k(float *out, size_t out_len, const or_tensor_view *w,
                       const or_block_q8k *x, size_t nx);
 int or_gemv_tq2_0_q8_k(float *out, size_t out_len, const or_tensor_view *w,
+                       const or_block_q8k *x, size_t nx);
+int or_gemv_q5_0_q8_0(float *out, size_t out_len, const or_tensor_view *w,
+                      const or_block_q8_0 *x, size_t nx);
+int or_gemv_q5_k_q8_k(float *out, size_t out_len, const or_tensor_view *w,
+                      const or_block_q8k *x, size_t nx);
+int or_gemv_tq1_0_q8_k(float *out, size_t out_len, const or_tensor_view *w,
                        const or_block_q8k *x, size_t nx);
 /* Same computation restricted to output rows [r0, r1) (row-partitioned CPU baseline). */
 int or_gemv_rows(int quant, float *out, const uint8_t *w, size_t rows, size_t cols,
@@ -136,6 +156,10 @@ int or_vec_dot_q6_k(float *out, size_t out_len, const or_tensor_view *w, const f
 int or_vec_dot_q4_k_m(float *out, size_t out_len, const or_tensor_view *w, const float *in,
                       size_t in_len);
 int or_vec_dot_i2_s(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                    size_t in_len);
+int or_vec_dot_q5_0(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                    size_t in_len);
+int or_vec_dot_q5_k(float *out, size_t out_len, const or_tensor_view *w, const float *in,
                     size_t in_len);
 
 /* ---- repacked (block-scaled i8) GEMM ---- */

@@ -54,6 +54,8 @@ def lib() -> C.CDLL:
         h.or_f16_to_f32_finite.restype = C.c_float
         h.or_f16_to_f32_finite.argtypes = [C.c_uint16]
         h.or_unpack_tq2_0_block_i8.restype = C.c_float
+        h.or_unpack_tq1_0_block_i8.restype = C.c_float
+        h.or_unpack_q5_0_block_i8.restype = C.c_float
         h.or_read_i2_s_trailer_scale.restype = C.c_float
         h.or_act_q8_bytes.restype = _sz
         h.or_act_q8_bytes.argtypes = [_sz, _sz]
@@ -117,6 +119,20 @@ def unpack_tq2_0_block_i8(block: np.ndarray):
     b = np.ascontiguousarray(block, dtype=np.uint8)
     out = np.zeros(256, dtype=np.int8)
     s = lib().or_unpack_tq2_0_block_i8(_p(b), _p(out))
+    return s, out
+
+
+def unpack_tq1_0_block_i8(block: np.ndarray):
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(256, dtype=np.int8)
+    s = lib().or_unpack_tq1_0_block_i8(_p(b), _p(out))
+    return s, out
+
+
+def unpack_q5_0_block_i8(block: np.ndarray):
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.zeros(32, dtype=np.int8)
+    s = lib().or_unpack_q5_0_block_i8(_p(b), _p(out))
     return s, out
 
 
@@ -195,9 +211,12 @@ def quantize_absmax_i8(x: np.ndarray):
 
 # ----------------------------------------------------------------- quant_q8 path
 _VEC_DOT_Q8 = {2: "or_vec_dot_q4_0_q8_0", 8: "or_vec_dot_q8_0_q8_0", 12: "or_vec_dot_q4_k_q8_k",
-               14: "or_vec_dot_q6_k_q8_k", 35: "or_vec_dot_tq2_0_q8_k"}
+               14: "or_vec_dot_q6_k_q8_k", 35: "or_vec_dot_tq2_0_q8_k", 6: "or_vec_dot_q5_0_q8_0",
+               13: "or_vec_dot_q5_k_q8_k", 34: "or_vec_dot_tq1_0_q8_k"}
 _GEMV_Q8 = {2: "or_gemv_q4_0_q8_0", 8: "or_gemv_q8_0_q8_0", 12: "or_gemv_q4_k_q8_k", 14: "or_gemv_q6_k_q8_k",
-            35: "or_gemv_tq2_0_q8_k"}
+            35: "or_gemv_tq2_0_q8_k", 6: "or_gemv_q5_0_q8_0", 13: "or_gemv_q5_k_q8_k", 34: "or_gemv_tq1_0_q8_k"}
+# Formats whose GEMV takes BlockQ8_0 activations (the others take BlockQ8K).
+Q8_0_ACT = (2, 6, 8)
 
 
 def vec_dot_q8(quant: int, w_row: np.ndarray, x_blocks: np.ndarray) -> float:
@@ -226,7 +245,7 @@ def gemv_rows(quant: int, data: np.ndarray, rows: int, cols: int, x_blocks: np.n
 
 
 _VEC_DOT_F32 = {2: "or_vec_dot_q4_0", 8: "or_vec_dot_q8_0", 14: "or_vec_dot_q6_k", 12: "or_vec_dot_q4_k_m",
-                36: "or_vec_dot_i2_s"}
+                36: "or_vec_dot_i2_s", 6: "or_vec_dot_q5_0", 13: "or_vec_dot_q5_k"}
 
 
 def vec_dot_f32(quant: int, shape, data: np.ndarray, x: np.ndarray, out_len: int) -> np.ndarray:

@@ -9,8 +9,9 @@ tests (tests/test_oracle_kat.py) and by closed-form / float64 properties
 check the HIP library against fixed data, and a later change of the oracle shows up as a
 fixture mismatch.
 
-Run from the repository root:  python tests/golden/make_golden.py
-Each case is one .npz (no pickled objects) holding its inputs and expected outputs.
+Run from the repository root:  python tests/golden/make_golden.py [--all]
+(without --all only the missing fixtures are written). Each case is one .npz (no pickled
+objects) holding its inputs and expected outputs.
 """
 from __future__ import annotations
 
@@ -28,7 +29,7 @@ sys.path.insert(0, os.path.join(REPO, "jero-kernels-rvv_amd"))
 import oracle as O  # noqa: E402
 import refgen as R  # noqa: E402
 
-Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = 2, 8, 12, 14, 35, 36
+Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S = 2, 6, 8, 12, 13, 14, 34, 35, 36
 
 # quant -> (LCG weight filler of the reference's tests, weight seed, activation seed)
 CASES = {
@@ -37,9 +38,14 @@ CASES = {
     Q4_K: (R.fill_q4_k, 0x53, 0x63),
     Q6_K: (R.fill_q6_k, 0x54, 0x64),
     TQ2_0: (R.fill_tq2_0, 0x55, 0x65),
+    Q5_0: (R.fill_q5_0, 0x57, 0x67),
+    Q5_K: (R.fill_q5_k, 0x58, 0x68),
+    TQ1_0: (R.fill_tq1_0, 0x59, 0x69),
 }
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", TQ2_0: "tq2_0", I2_S: "i2_s"}
-F32_PATH = {Q4_0, Q8_0, Q4_K, Q6_K, I2_S}  # formats with an f32-activation vec_dot entry
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", TQ2_0: "tq2_0", I2_S: "i2_s", Q5_0: "q5_0",
+         Q5_K: "q5_k", TQ1_0: "tq1_0"}
+F32_PATH = {Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, I2_S}  # formats with an f32-activation vec_dot entry
+Q8_0_ACT = (Q4_0, Q5_0, Q8_0)  # formats whose GEMV takes BlockQ8_0 activations
 ROWS, COLS, TOKENS = 8, 512, 3
 
 
@@ -64,7 +70,7 @@ def case(quant: int, wseed: int, xseed: int) -> dict:
            "xseed": np.int64(xseed), "w": w, "x": x, "X": X}
     out["deq"] = np.stack([O.dequantize_tensor_row(quant, shape, w, r, COLS) for r in range(ROWS)])
     if quant != I2_S:
-        xq = O.quantize_row_q8_0(x) if quant in (Q4_0, Q8_0) else O.quantize_row_q8_k(x)
+        xq = O.quantize_row_q8_0(x) if quant in Q8_0_ACT else O.quantize_row_q8_k(x)
         out["xq"] = xq.view(np.uint8).reshape(-1)
         out["y_gemv"] = O.gemv_q8(quant, shape, w, xq, ROWS)
         act = O.ActQ8(X, TOKENS, COLS)
@@ -72,7 +78,7 @@ def case(quant: int, wseed: int, xseed: int) -> dict:
         out["y_gemm_rows"] = O.gemm_repacked(quant, shape, w, ROWS, COLS, act, 2, 7)
     if quant in F32_PATH:
         out["y_vec_f32"] = O.vec_dot_f32(quant, shape, w, x, ROWS)
-    if quant in (TQ2_0, I2_S):
+    if quant in (TQ1_0, TQ2_0, I2_S):
         a, s = O.quantize_absmax_i8(x)
         out["act_i8"], out["act_scale"] = a, np.float32(s)
         out["y_bitlinear"] = O.bitlinear_i8(quant, shape, w, a, s, ROWS)
@@ -98,11 +104,17 @@ def quantizer_case() -> dict:
 
 def main() -> None:
     O.build()
-    for quant, (_, wseed, xseed) in CASES.items():
-        np.savez(os.path.join(HERE, f"{NAMES[quant]}.npz"), **case(quant, wseed, xseed))
-    np.savez(os.path.join(HERE, "i2_s.npz"), **case(I2_S, 0x56, 0x66))
-    np.savez(os.path.join(HERE, "quantizers.npz"), **quantizer_case())
-    print("wrote", sorted(f for f in os.listdir(HERE) if f.endswith(".npz")))
+    everything = "--all" in sys.argv[1:]
+    todo = {f"{NAMES[q]}.npz": (lambda q=q, ws=ws, xs=xs: case(q, ws, xs)) for q, (_, ws, xs) in CASES.items()}
+    todo["i2_s.npz"] = lambda: case(I2_S, 0x56, 0x66)
+    todo["quantizers.npz"] = quantizer_case
+    written = []
+    for name, make in todo.items():
+        path = os.path.join(HERE, name)
+        if everything or not os.path.exists(path):
+            np.savez(path, **make())
+            written.append(name)
+    print("wrote", sorted(written))
 
 
 if __name__ == "__main__":

@@ -113,6 +113,52 @@ def fill_tq2_0(rows: int, cols: int, seed: int) -> np.ndarray:
     return raw
 
 
+def fill_q5_0(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:97-115"""
+    nb = cols // 32
+    raw = np.zeros(rows * nb * 22, np.uint8)
+    g = Lcg(seed)
+    scales = [0x2C00, 0x3000, 0x3200, 0x3400]
+    for r in range(rows):
+        for b in range(nb):
+            off = (r * nb + b) * 22
+            raw[off:off + 2] = _u16(scales[(r + b) % 4])
+            qh = g.hi32()
+            raw[off + 2:off + 6] = [(qh >> (8 * i)) & 0xFF for i in range(4)]
+            for j in range(16):
+                raw[off + 6 + j] = g.hi32() & 0xFF
+    return raw
+
+
+def fill_q5_k(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:156-174"""
+    nb = cols // 256
+    raw = np.zeros(rows * nb * 176, np.uint8)
+    g = Lcg(seed)
+    for blk in range(rows * nb):
+        off = blk * 176
+        raw[off:off + 2] = _u16(0x3000)
+        raw[off + 2:off + 4] = _u16(0x2800)
+        for idx in range(4, 16):
+            raw[off + idx] = g.hi32() % 31 + 1
+        for idx in range(16, 176):
+            raw[off + idx] = g.hi32() & 0xFF
+    return raw
+
+
+def fill_tq1_0(rows: int, cols: int, seed: int) -> np.ndarray:
+    """tests/wave4_quant_gemv_and_argmax.rs:196-209"""
+    nb = cols // 256
+    raw = np.zeros(rows * nb * 54, np.uint8)
+    g = Lcg(seed)
+    for blk in range(rows * nb):
+        off = blk * 54
+        raw[off:off + 2] = _u16(0x3400)
+        for idx in range(2, 54):
+            raw[off + idx] = g.hi32() % 243
+    return raw
+
+
 def cosine(a, b) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

@@ -19,8 +19,10 @@ import oracle as O
 import refgen as R
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = 2, 8, 12, 14, 35, 36
-FILL = {Q4_0: R.fill_q4_0, Q8_0: R.fill_q8_0, Q4_K: R.fill_q4_k, Q6_K: R.fill_q6_k, TQ2_0: R.fill_tq2_0}
+Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S = 2, 6, 8, 12, 13, 14, 34, 35, 36
+FILL = {Q4_0: R.fill_q4_0, Q8_0: R.fill_q8_0, Q4_K: R.fill_q4_k, Q6_K: R.fill_q6_k, TQ2_0: R.fill_tq2_0,
+        Q5_0: R.fill_q5_0, Q5_K: R.fill_q5_k, TQ1_0: R.fill_tq1_0}
+Q8_0_ACT = (Q4_0, Q5_0, Q8_0)
 CASES = sorted(p for p in glob.glob(os.path.join(HERE, "*.npz")) if not p.endswith("quantizers.npz"))
 
 
@@ -38,7 +40,7 @@ def dequant_q8_blocks(quant, xq_bytes, n):
     """f64 values of the quantized activation blocks (Q8_0: f32 d + 32 i8; Q8_K: f32 d,
     256 i8, 16 i16 bsums)."""
     raw = np.asarray(xq_bytes, np.uint8)
-    if quant in (Q4_0, Q8_0):
+    if quant in Q8_0_ACT:
         blk = raw.reshape(-1, 36)
         d = blk[:, :4].copy().view(np.float32)[:, 0].astype(np.float64)
         q = blk[:, 4:].view(np.int8).astype(np.float64)
@@ -51,7 +53,8 @@ def dequant_q8_blocks(quant, xq_bytes, n):
 
 def test_fixtures_present():
     names = {os.path.basename(p) for p in glob.glob(os.path.join(HERE, "*.npz"))}
-    assert {"q4_0.npz", "q8_0.npz", "q4_k.npz", "q6_k.npz", "tq2_0.npz", "i2_s.npz", "quantizers.npz"} <= names
+    assert {"q4_0.npz", "q5_0.npz", "q8_0.npz", "q4_k.npz", "q5_k.npz", "q6_k.npz", "tq1_0.npz", "tq2_0.npz",
+            "i2_s.npz", "quantizers.npz"} <= names
 
 
 @pytest.mark.parametrize("path", CASES, ids=os.path.basename)
@@ -73,7 +76,7 @@ def test_oracle_reproduces_fixture(path):
     deq = np.stack([O.dequantize_tensor_row(quant, shape, w, r, cols) for r in range(rows)])
     assert bits_equal(deq, f["deq"])
     if "xq" in f:
-        xq = O.quantize_row_q8_0(f["x"]) if quant in (Q4_0, Q8_0) else O.quantize_row_q8_k(f["x"])
+        xq = O.quantize_row_q8_0(f["x"]) if quant in Q8_0_ACT else O.quantize_row_q8_k(f["x"])
         assert np.array_equal(xq.view(np.uint8).reshape(-1), f["xq"])
         assert bits_equal(O.gemv_q8(quant, shape, w, xq, rows), f["y_gemv"])
         act = O.ActQ8(f["X"], f["X"].shape[0], cols)

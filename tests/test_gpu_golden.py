@@ -16,11 +16,12 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = jk.Q4_0, jk.Q8_0, jk.Q4_K, jk.Q6_K, jk.TQ2_0, jk.I2_S
+Q5_0, Q5_K, TQ1_0 = jk.Q5_0, jk.Q5_K, jk.TQ1_0
 CASES = sorted(p for p in glob.glob(os.path.join(HERE, "*.npz")) if not p.endswith("quantizers.npz"))
 GEMV = {Q4_0: jk.gemv_q4_0_q8_0, Q8_0: jk.gemv_q8_0_q8_0, Q4_K: jk.gemv_q4_k_q8_k, Q6_K: jk.gemv_q6_k_q8_k,
-        TQ2_0: jk.gemv_tq2_0_q8_k}
+        TQ2_0: jk.gemv_tq2_0_q8_k, Q5_0: jk.gemv_q5_0_q8_0, Q5_K: jk.gemv_q5_k_q8_k, TQ1_0: jk.gemv_tq1_0_q8_k}
 VEC_F32 = {Q4_0: jk.vec_dot_q4_0, Q8_0: jk.vec_dot_q8_0, Q6_K: jk.vec_dot_q6_k, Q4_K: jk.vec_dot_q4_k_m,
-           I2_S: jk.vec_dot_i2_s}
+           I2_S: jk.vec_dot_i2_s, Q5_0: jk.vec_dot_q5_0, Q5_K: jk.vec_dot_q5_k}
 
 
 def load(path):
@@ -43,7 +44,7 @@ def test_golden_case(gpu, path):
         jk.dequantize_tensor_row(view, r, out)
         assert bits_equal(out, f["deq"][r]), (path, "dequant row", r)
     if "xq" in f:
-        xq = jk.quantize_row_q8_0(f["x"]) if quant in (Q4_0, Q8_0) else jk.quantize_row_q8_k(f["x"])
+        xq = jk.quantize_row_q8_0(f["x"]) if quant in jk.Q8_0_ACT else jk.quantize_row_q8_k(f["x"])
         assert np.array_equal(xq.view(np.uint8).reshape(-1), f["xq"]), (path, "activation blocks")
         y = np.zeros(rows, np.float32)
         GEMV[quant](y, view, xq)

@@ -15,7 +15,9 @@ from jk import synth
 pytestmark = pytest.mark.gpu
 
 Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = jk.Q4_0, jk.Q8_0, jk.Q4_K, jk.Q6_K, jk.TQ2_0, jk.I2_S
-GEMV_FORMATS = [Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0]
+Q5_0, Q5_K, TQ1_0 = jk.Q5_0, jk.Q5_K, jk.TQ1_0
+GEMV_FORMATS = [Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0]
+ALL_FORMATS = GEMV_FORMATS + [I2_S]
 
 
 def same_bits(a, b) -> bool:
@@ -51,7 +53,7 @@ def host(t, dtype, count=None):
 
 
 def x_blocks(quant, x):
-    return O.quantize_row_q8_0(x) if quant in (Q4_0, Q8_0) else O.quantize_row_q8_k(x)
+    return O.quantize_row_q8_0(x) if quant in jk.Q8_0_ACT else O.quantize_row_q8_k(x)
 
 
 def gpu_gemv(torch, w, xq, r0=0, r1=None):
@@ -154,13 +156,16 @@ def test_absmax_quantizers(gpu, k):
 
 
 # ------------------------------------------------------------------ weights
-@pytest.mark.parametrize("quant", [Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S])
+@pytest.mark.parametrize("quant", ALL_FORMATS)
 def test_upload_and_dequantize_rows(gpu, quant):
     torch = gpu
     rows, cols = 19, 2048
     raw = synth.random_weights(quant, rows, cols, seed=quant, specials=True)
     w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
-    assert w.device_bytes == rows * cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[quant]
+    dev_quant = TQ2_0 if quant == TQ1_0 else quant  # TQ1_0 trits are held 2 bits each
+    assert w.quant == quant
+    assert w.gguf_bytes == rows * cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[quant] + jk.TRAILER_BYTES.get(quant, 0)
+    assert w.device_bytes == rows * cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[dev_quant]
     dy = empty(torch, 4 * rows * cols)
     jk.dev_dequantize_rows(w, 0, rows, dy, rows * cols)
     torch.cuda.synchronize()
@@ -207,6 +212,10 @@ CONFIG_MATRICES = [
 ] + [(f"C3 {n}", q, r, c) for n, q, r, c in synth.LLAMA3_8B_LAYER] + [
     ("C5 TQ2_0 6912x2560", TQ2_0, 6912, 2560),
     ("C5 TQ2_0 2560x6912", TQ2_0, 2560, 6912),
+    ("Q5_0 4096x4096", Q5_0, 4096, 4096),
+    ("Q5_K 14336x4096", Q5_K, 14336, 4096),
+    ("Q5_K 4096x14336", Q5_K, 4096, 14336),
+    ("TQ1_0 6912x2560", TQ1_0, 6912, 2560),
 ]
 
 
@@ -276,7 +285,7 @@ def test_gemv_q8_caller_q8k_with_inconsistent_bsums(gpu):
     rows, cols = 7, 1024
     x = O.quantize_row_q8_k(synth.activations(cols, 9))
     x["bsums"] = np.random.default_rng(1).integers(-3000, 3000, x["bsums"].shape, dtype=np.int16)
-    for quant in (Q4_K, Q6_K, TQ2_0):
+    for quant in (Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0):
         raw = synth.gguf_weights(quant, rows, cols, seed=quant)
         ref = O.gemv_q8(quant, [rows, cols], raw, x, rows)
         w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
@@ -298,7 +307,7 @@ def test_gemv_q8_batch_mixed_jobs(gpu):
         raw = synth.gguf_weights(quant, rows, cols, seed=50 + i)
         w = jk.Weight(jk.TensorView(f"w{i}", quant, [rows, cols], raw), rows, cols)
         xq = x_blocks(quant, xs[cols])
-        key = (quant in (Q4_0, Q8_0), cols)
+        key = (quant in jk.Q8_0_ACT, cols)
         if key not in dq:
             dq[key] = dev(torch, xq)
         full = O.gemv_q8(quant, [rows, cols], raw, xq, rows)
@@ -340,7 +349,7 @@ def test_gemv_q8_batch_validation(gpu):
 
 
 # ------------------------------------------------------------------ f32 vec_dot
-@pytest.mark.parametrize("quant", [Q4_0, Q8_0, Q4_K, Q6_K, I2_S])
+@pytest.mark.parametrize("quant", [Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, I2_S])
 @pytest.mark.parametrize("rows,cols", [(1, 256), (5, 4352), (33, 4096)])
 def test_vec_dot_f32(gpu, quant, rows, cols):
     torch = gpu
@@ -377,7 +386,7 @@ def gpu_gemm(torch, w, x, m, r0=0, r1=None):
     return host(dy, np.float32, m * (r1 - r0)).reshape(m, r1 - r0)
 
 
-@pytest.mark.parametrize("quant", [Q8_0, Q4_0, Q4_K, Q6_K, TQ2_0, I2_S])
+@pytest.mark.parametrize("quant", ALL_FORMATS)
 @pytest.mark.parametrize("m,rows,cols", [(1, 37, 512), (5, 64, 256), (70, 100, 1024), (64, 128, 4096)])
 def test_gemm_repacked(gpu, quant, m, rows, cols):
     torch = gpu
@@ -391,7 +400,7 @@ def test_gemm_repacked(gpu, quant, m, rows, cols):
     assert same_bits(got_slice, ref[:, 3:rows - 5])
 
 
-@pytest.mark.parametrize("quant", [Q8_0, Q4_0, Q4_K, Q6_K, TQ2_0, I2_S])
+@pytest.mark.parametrize("quant", ALL_FORMATS)
 @pytest.mark.parametrize("m", [500, 250, 128, 30])
 def test_gemm_tile_shapes(gpu, quant, m):
     """8200 rows: 500 tokens launch 128x64 tiles, 250 tokens 64x64, 128 tokens 32x32, 30
@@ -426,7 +435,7 @@ def test_gemm_q8_0_prefill_shape_rows_sample(gpu, m):
 
 
 # ------------------------------------------------------------------ BitLinear
-@pytest.mark.parametrize("quant", [TQ2_0, I2_S, Q8_0])
+@pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S, Q8_0])
 @pytest.mark.parametrize("m,rows,cols", [(1, 7, 256), (3, 64, 2560), (2, 2560, 6912),
                                          # token batches take the int8-MFMA path
                                          (16, 300, 2560), (37, 129, 768), (128, 2560, 6912), (128, 6912, 2560)])
@@ -447,7 +456,7 @@ def test_bitlinear(gpu, quant, m, rows, cols):
         assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
 
 
-@pytest.mark.parametrize("quant", [TQ2_0, I2_S])
+@pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S])
 @pytest.mark.parametrize("m,rows,cols,offset", [(1, 9, 256 * 65, 0),   # more than 64 blocks a row
                                                 (2, 13, 2560, 1),     # activation not 16-byte aligned
                                                 (5, 11, 1024, 0)])
@@ -471,7 +480,7 @@ def test_bitlinear_few_tokens_paths(gpu, quant, m, rows, cols, offset):
         assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
 
 
-@pytest.mark.parametrize("quant", [TQ2_0, I2_S, Q8_0])
+@pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S, Q8_0])
 @pytest.mark.parametrize("m", [500, 250, 128, 30])
 def test_bitlinear_tile_shapes(gpu, quant, m):
     """BitLinear token batches on each GEMM tile shape (as test_gemm_tile_shapes), with the
@@ -524,3 +533,78 @@ def test_host_tier_matches_oracle(gpu):
     jk.host_gemm_repacked_f32(g, w, xs, 3, 5, 35)
     ref = O.gemm_repacked(Q8_0, [40, 1024], w8, 40, 1024, O.ActQ8(xs, 3, 1024), 5, 35)
     assert same_bits(g.reshape(3, 30), ref)
+
+
+def test_tq1_0_and_tq2_0_jobs_share_a_batch(gpu):
+    """TQ1_0 handles use the TQ2_0 device layout: a batch mixing the two formats runs as one
+    launch and each job still matches its own format's oracle GEMV."""
+    torch = gpu
+    cols = 2560
+    x = synth.activations(cols, 77)
+    dxf = torch.from_numpy(x).cuda()
+    jobs, expect, outs = [], [], []
+    for i, (quant, rows) in enumerate(((TQ1_0, 300), (TQ2_0, 200), (TQ1_0, 77))):
+        raw = synth.gguf_weights(quant, rows, cols, seed=90 + i)
+        w = jk.Weight(jk.TensorView(f"t{i}", quant, [rows, cols], raw), rows, cols)
+        y = empty(torch, 4 * rows)
+        jobs.append((w, None, dxf, y, 0, rows))
+        expect.append(O.gemv_q8(quant, [rows, cols], raw, O.quantize_row_q8_k(x), rows))
+        outs.append((y, rows))
+    jk.dev_gemv_q8_batch(jobs)
+    torch.cuda.synchronize()
+    for (y, n), ref in zip(outs, expect):
+        got = host(y, np.float32, n)
+        assert same_bits(got, ref), mismatch(got, ref)
+
+
+def test_host_tier_new_formats(gpu):
+    """Host-tier mirrors of the Q5_0 / Q5_K / TQ1_0 entries against the oracle."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(2048).astype(np.float32)
+    x8, xk = O.quantize_row_q8_0(x), O.quantize_row_q8_k(x)
+    for quant, gemv, xq in ((Q5_0, jk.gemv_q5_0_q8_0, x8), (Q5_K, jk.gemv_q5_k_q8_k, xk),
+                            (TQ1_0, jk.gemv_tq1_0_q8_k, xk)):
+        raw = synth.random_weights(quant, 6, 2048, seed=quant, specials=True)
+        out = np.zeros(6, np.float32)
+        gemv(out, jk.TensorView("w", quant, [2048, 6], raw), xq)
+        assert same_bits(out, O.gemv_q8(quant, [2048, 6], raw, xq, 6)), quant
+    raw = synth.random_weights(Q5_0, 3, 2048, seed=1, specials=True)
+    v = jk.vec_dot_q5_0_q8_0_blocks(raw[:64 * 22], x8)
+    assert same_bits(np.float32([v]), np.float32([O.vec_dot_q8(Q5_0, raw[:64 * 22], x8)]))
+    raw = synth.random_weights(Q5_K, 3, 2048, seed=2, specials=True)
+    v = jk.vec_dot_q5_k_q8_k(raw[:8 * 176], xk)
+    assert same_bits(np.float32([v]), np.float32([O.vec_dot_q8(Q5_K, raw[:8 * 176], xk)]))
+    raw = synth.gguf_weights(TQ1_0, 3, 2048, seed=3)
+    v = jk.vec_dot_tq1_0_q8_k(raw[:8 * 54], xk)
+    assert same_bits(np.float32([v]), np.float32([O.vec_dot_q8(TQ1_0, raw[:8 * 54], xk)]))
+    for quant, fn in ((Q5_0, jk.vec_dot_q5_0), (Q5_K, jk.vec_dot_q5_k)):
+        raw = synth.random_weights(quant, 5, 2048, seed=quant + 1, specials=True)
+        f = np.zeros(5, np.float32)
+        fn(f, jk.TensorView("w", quant, [2048, 5], raw), x)
+        assert same_bits(f, O.vec_dot_f32(quant, [2048, 5], raw, x, 5)), quant
+        row = np.zeros(2048, np.float32)
+        jk.dequantize_tensor_row(jk.TensorView("w", quant, [2048, 5], raw), 3, row)
+        assert same_bits(row, O.dequantize_tensor_row(quant, [2048, 5], raw, 3, 2048)), quant
+    tq = synth.gguf_weights(TQ1_0, 5, 512, seed=1)
+    a = rng.integers(-128, 128, 512).astype(np.int8)
+    bl = np.zeros(5, np.float32)
+    jk.bitlinear_i8(bl, jk.TensorView("w", TQ1_0, [5, 512], tq), a, 0.02)
+    assert same_bits(bl, O.bitlinear_i8(TQ1_0, [5, 512], tq, a, 0.02, 5))
+
+
+def test_new_format_validation(gpu):
+    torch = gpu
+    raw = synth.gguf_weights(TQ1_0, 4, 256, seed=1)
+    w = jk.Weight(jk.TensorView("w", TQ1_0, [4, 256], raw), 4, 256)
+    x = torch.zeros(256, dtype=torch.float32, device="cuda")
+    y = torch.zeros(4, dtype=torch.float32, device="cuda")
+    xq = dev(torch, O.quantize_row_q8_k(np.ones(256, np.float32)))
+    with pytest.raises(jk.TensorBoundsError):  # a TQ1_0 handle is not a TQ2_0 weight
+        jk.dev_gemv_q8(w, xq, 1, y, 4, fn="jk_gemv_tq2_0_q8_k")
+    jk.dev_gemv_q8(w, xq, 1, y, 4)
+    with pytest.raises(jk.CapabilityMismatch):  # no f32-activation matvec for TQ1_0
+        jk.dev_vec_dot_f32(w, x, 256, y, 4)
+    w5 = jk.Weight(jk.TensorView("w5", Q5_K, [4, 256], synth.gguf_weights(Q5_K, 4, 256, seed=2)), 4, 256)
+    with pytest.raises(jk.TensorBoundsError):  # Q5_K is not a BitLinear format
+        jk.dev_bitlinear_i8(w5, torch.zeros(256, dtype=torch.int8, device="cuda"), y[:1], 1, 256, y, 4)
+    torch.cuda.synchronize()
