@@ -47,11 +47,16 @@ typedef enum jk_status {
 /* GGML type ids of the jero_core::QuantType variants on this path. */
 typedef enum jk_quant {
     JK_Q4_0 = 2,
+    JK_Q4_1 = 3,
     JK_Q5_0 = 6,
+    JK_Q5_1 = 7,
     JK_Q8_0 = 8,
+    JK_Q2_K = 10,
+    JK_Q3_K = 11,
     JK_Q4_K = 12, /* QuantType::Q4_K_M */
     JK_Q5_K = 13,
     JK_Q6_K = 14,
+    JK_IQ4_NL = 20,
     JK_TQ1_0 = 34,
     JK_TQ2_0 = 35,
     JK_I2_S = 36
@@ -119,8 +124,10 @@ jk_status jk_copy_to_host(jk_stream s, void *dst, const void *src, size_t bytes)
 /* RepackedWeight::from_tensor (repack.rs:2288-2300) / RepackedWeight::repack when
  * rows == cols == 0 (repack.rs:2255-2285): copies the GGUF payload to the device and
  * rewrites it there into the plane layout (same byte count as GGUF, except TQ1_0, whose
- * trits are stored 2 bits each). Formats: Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0,
- * I2_S; others are a CapabilityMismatch. Validation follows validate_matrix_view
+ * trits are stored 2 bits each, and Q3_K, padded from 110 to 112 bytes). Formats: Q4_0, Q4_1,
+ * Q5_0, Q5_1, Q8_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S (the formats of
+ * BlockScaledTileLayout::for_tensor, repack.rs:1308-1333, and so of PackedNibbleMatrix,
+ * repack.rs:4788); others are a CapabilityMismatch. Validation follows validate_matrix_view
  * (repack.rs:1208-1281). The handle is immutable and may be used from any thread and
  * stream once the upload stream has completed. */
 jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, size_t cols,
@@ -202,15 +209,19 @@ jk_status jk_gemv_q8_batch(jk_stream s, const jk_gemv_job *jobs, size_t njobs);
 jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len);
 
 /* ------------------------------------------ f32-activation matvec (vec_dot) */
-/* vec_dot_q4_0 (quant.rs:1458), vec_dot_q5_0 (2036), vec_dot_q8_0 (1069), vec_dot_q5_k
- * (1238), vec_dot_q6_k (1089), VectorKernel::vec_dot_q4_k_m (lib.rs:157, scalar impl
- * 1268-1303), vec_dot_i2_s (quant.rs:2199-2240): dequantize each block and dot it with
- * f32 x. TQ1_0 / TQ2_0 have none (CapabilityMismatch). */
+/* vec_dot_q4_0 (quant.rs:1458), vec_dot_q4_1 (2062), vec_dot_q5_0 (2036), vec_dot_q5_1
+ * (2081), vec_dot_q8_0 (1069), vec_dot_iq4_nl (2138), vec_dot_q2_k (2100), vec_dot_q3_k
+ * (2119), VectorKernel::vec_dot_q4_k_m (lib.rs:157, scalar impl 1268-1303), vec_dot_q5_k
+ * (quant.rs:1238), vec_dot_q6_k (1089), vec_dot_i2_s (2199-2240): dequantize each block
+ * and dot it with f32 x. TQ1_0 / TQ2_0 have none (CapabilityMismatch). */
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y,
                          size_t y_len);
 
 /* ----------------------------------------------------- repacked GEMV / GEMM */
-/* gemm_repacked_rows (repack.rs:4087-4094) / RepackedWeight::gemm_rows (2661-2668):
+/* Every format of jk_weight_upload. PackedNibbleMatrix::gemm / gemm_rows / gemv
+ * (repack.rs:4945-4985) compute the same products for its formats (Q4_0, Q4_1, IQ4_NL,
+ * Q4_K) and map to these calls on a handle from jk_weight_upload.
+ * gemm_repacked_rows (repack.rs:4087-4094) / RepackedWeight::gemm_rows (2661-2668):
  * y[m][row - row_begin] for rows [row_begin, row_end), y_len = m * (row_end - row_begin).
  * gemv_repacked_rows (repack.rs:4014-4061) is the m == 1 case. */
 jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
@@ -257,9 +268,15 @@ jk_status jk_host_vec_dot_q8_0(float *out, size_t out_len, const jk_tensor_view 
 jk_status jk_host_vec_dot_q6_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 jk_status jk_host_vec_dot_q4_k_m(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 jk_status jk_host_vec_dot_i2_s(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
-/* vec_dot_q5_0 (quant.rs:2036), vec_dot_q5_k (1238). */
+/* vec_dot_q5_0 (quant.rs:2036), vec_dot_q5_k (1238), vec_dot_q4_1 (2062), vec_dot_q5_1 (2081),
+ * vec_dot_q2_k (2100), vec_dot_q3_k (2119), vec_dot_iq4_nl (2138). */
 jk_status jk_host_vec_dot_q5_0(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 jk_status jk_host_vec_dot_q5_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q4_1(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q5_1(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q2_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_q3_k(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
+jk_status jk_host_vec_dot_iq4_nl(float *out, size_t out_len, const jk_tensor_view *w, const float *in, size_t in_len);
 /* dequantize_tensor_row / dequantize_token_row (quant.rs:2492, 2580). */
 jk_status jk_host_dequantize_tensor_row(const jk_tensor_view *w, size_t row, float *out, size_t out_len);
 /* gemm_repacked_f32_rows (repack.rs:4143-4165): quantizes input [m, cols] with

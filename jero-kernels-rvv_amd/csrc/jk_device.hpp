@@ -74,6 +74,23 @@ __device__ __forceinline__ int bytes_sub(uint32_t a, uint32_t k) {
 // disjoint bit ranges, so the multiply has no carries): the fifth bit of four 5-bit quants.
 __device__ __forceinline__ uint32_t bit4_of_bytes(uint32_t n) { return ((n * 0x00204081u) & 0x01010101u) << 4; }
 
+// KVALUES_IQ4NL (quant.rs:76-78) of four 4-bit indices, one per byte: two byte permutes over
+// the 16-byte table (v_perm_b32 picks bytes 0..3 from its second source and 4..7 from its
+// first, by the low 3 bits of each selector byte), then a per-byte select on index bit 3.
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t idx) {
+    const uint32_t t0 = 0xBFAD9881u, t1 = 0xF6EADDCFu;  // -127 -104 -83 -65 | -49 -35 -22 -10
+    const uint32_t t2 = 0x26190D01u, t3 = 0x71594535u;  //    1   13  25  38 |  53  69  89 113
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel), hi = __builtin_amdgcn_perm(t3, t2, sel);
+    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+
+// Word i of block b of row r in the word plane (fields of h_len bytes).
+__device__ __forceinline__ uint32_t ld_word(const WeightDev &w, int r, int b, int h_len, int i) {
+    return w.hplane[((size_t)r * (size_t)w.nb + (size_t)b) * (size_t)(h_len / 4) + (size_t)i];
+}
+
 // Rust `v.round().clamp(lo, hi) as i8`: round half away from zero, NaN -> 0.
 __device__ __forceinline__ int rust_round_clamp_i8(float v, float lo, float hi) {
     float r = roundf(v);

@@ -33,9 +33,13 @@ constexpr int kSteps = 4;     // 32-element steps per chunk
 constexpr int kRowB = 144;    // padded LDS bytes per 128-byte row
 
 template <int Q> struct GemmFmt {
-    static constexpr int GK = Q == JK_Q6_K ? 16 : 32;  // elements per scale group
-    static constexpr bool MINS = Q == JK_Q4_K || Q == JK_Q5_K;
+    static constexpr int GK = Q == JK_Q6_K || Q == JK_Q3_K || Q == JK_Q2_K ? 16 : 32;  // elements per scale group
+    static constexpr bool MINS = Q == JK_Q4_K || Q == JK_Q5_K || Q == JK_Q4_1 || Q == JK_Q5_1 || Q == JK_Q2_K;
     static constexpr int NG = 128 / GK;                 // scale groups per chunk
+    static constexpr int NM = MINS ? NG : 1;            // min / activation-sum rows staged per chunk
+    // 32-element blocks, 4 per chunk, staged like Q4_0
+    static constexpr bool B32 = Q == JK_Q8_0 || Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_Q4_1 || Q == JK_Q5_1 ||
+                                Q == JK_IQ4_NL;
 };
 
 template <int TN, int TM> struct Tile {
@@ -47,17 +51,19 @@ template <int TN, int TM> struct Tile {
     static constexpr int WM = TM < 32 ? 1 : TM / 32;  // waves along the tokens
     static constexpr int XL = 8 * TM / THREADS;   // activation loads per thread and chunk
     static constexpr int XS = 4 * TM / THREADS;   // activation scales per thread and chunk
+    static constexpr int XS16 = 8 * TM / THREADS; // activation 16-sums per thread and chunk (Q2_K)
     static constexpr int WPE = TN == 128 ? 3 : 2;  // waves per SIMD the register budget allows
     static_assert(WR * WM == WAVES && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
 };
 
-template <int TN, int TM> struct GemmChunk {
+template <int Q, int TN, int TM> struct GemmChunk {
+    static constexpr int NM = GemmFmt<Q>::NM;
     uint8_t a[TN * kRowB];  // weights, i8, [row][k]
     uint8_t b[TM * kRowB];  // activations, i8, [token][k]
     float ws[8][TN];        // weight scale per scale group of the chunk
-    float wm[4][TN];        // weight min per 32-group (Q4_K, Q5_K)
+    float wm[NM][TN];       // weight min per scale group (formats with mins)
     float xs[4][TM];        // activation scale per 32-block
-    float xm[4][TM];        // activation sum per 32-block (Q4_K, Q5_K)
+    float xm[NM][TM];       // activation sum per scale group: per 32-block, or per 16 (Q2_K)
 };
 
 // One 16-byte global load without the streaming hint: a weight tile is read once per
@@ -84,10 +90,11 @@ __device__ __forceinline__ const uint8_t *plane_ptr(const WeightDev &w, int c, i
 //   row; scale j (and sum) of entry e = XS t + j: token e / 4, block 4kc + e % 4.
 template <int TN, int TM> struct Stage {
     uint4 w[5];                         // weight plane bytes
-    uint32_t wd[2];                     // weight f16 scales (Q8_0 / Q4_0 / Q5_0: two blocks; Q6_K, TQ2_0: d)
-    uint32_t wh[2];                     // Q5_0: high-bit words of the blocks of w[0], w[1]
+    uint32_t wd[2];                     // weight scales: f16 d (or the d | m word) of two blocks; K-formats: d
+    uint32_t wh[2];                     // Q5_0 / Q5_1: high-bit words of the blocks of w[0], w[1]
     uint4 x[Tile<TN, TM>::XL];          // activation bytes
-    uint32_t xd[2][Tile<TN, TM>::XS];   // activation scale, sum (Q4_K)
+    uint32_t xd[2][Tile<TN, TM>::XS];   // activation scale, sum per 32-block
+    uint32_t x16[Tile<TN, TM>::XS16];   // activation sums per 16 (Q2_K)
 };
 
 // Blocks past the row end (a partial last chunk) are read clamped and never used; rows
@@ -95,17 +102,23 @@ template <int TN, int TM> struct Stage {
 template <int Q, int TN, int TM>
 __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage<TN, TM> &r) {
     const int nb = w.nb, t = threadIdx.x;
-    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0 || Q == JK_Q5_0) {
+    if constexpr (GemmFmt<Q>::B32) {
+        constexpr int HW = fmt_of(Q).h_len / 4;  // words per block in the word plane
         const int b = min(4 * kc + (t & 3), nb - 1);
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
             const int n = min(n0 + (t >> 2) + TN / 2 * (i & 1), r1 - 1);
             r.w[i] = ldg16(plane_ptr(w, i >> 1, n, b));
             if constexpr (Q == JK_Q5_0) r.wh[i] = w.hplane[(size_t)n * (size_t)nb + (size_t)b];
+            if constexpr (Q == JK_Q5_1) r.wh[i] = w.hplane[((size_t)n * (size_t)nb + (size_t)b) * 2 + 1];
         }
         const size_t srow = (size_t)min(n0 + (t >> 1), r1 - 1) * (size_t)nb;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) r.wd[j] = w.dplane[srow + (size_t)min(4 * kc + 2 * (t & 1) + j, nb - 1)];
+        for (int j = 0; j < 2; ++j) {
+            const size_t blk = srow + (size_t)min(4 * kc + 2 * (t & 1) + j, nb - 1);
+            if constexpr (Q == JK_Q4_1 || Q == JK_Q5_1) r.wd[j] = w.hplane[blk * HW];  // d | m << 16
+            else r.wd[j] = w.dplane[blk];
+        }
     } else {
         const int n = min(n0 + (t >> 1), r1 - 1), j = t & 1;
         if constexpr (Q == JK_I2_S) {
@@ -123,6 +136,17 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
             r.w[2] = ldg16(plane_ptr(w, 4 + 2 * (2 * h + j), n, b));
             r.w[3] = ldg16(plane_ptr(w, 1, n, b));  // qh[0..16)
             r.w[4] = ldg16(plane_ptr(w, 2, n, b));  // qh[16..32)
+        } else if constexpr (Q == JK_Q2_K) {
+            r.w[0] = ldg16(plane_ptr(w, 0, n, b));          // 16 scale / min bytes
+            r.w[1] = ldg16(plane_ptr(w, 1 + 2 * h, n, b));  // qs of the half, bytes 0..15
+            r.w[2] = ldg16(plane_ptr(w, 2 + 2 * h, n, b));  // qs of the half, bytes 16..31
+            r.wd[0] = w.hplane[(size_t)n * (size_t)nb + (size_t)b];  // d | dmin << 16
+        } else if constexpr (Q == JK_Q3_K) {
+            r.w[0] = ldg16(plane_ptr(w, 0, n, b));          // hmask bytes 0..15
+            r.w[1] = ldg16(plane_ptr(w, 1, n, b));          // hmask bytes 16..31
+            r.w[2] = ldg16(plane_ptr(w, 2 + 2 * h, n, b));  // qs of the half, bytes 0..15
+            r.w[3] = ldg16(plane_ptr(w, 3 + 2 * h, n, b));  // qs of the half, bytes 16..31
+            r.w[4] = ldg16(plane_ptr(w, 6, n, b));          // 12 packed scales, d
         } else if constexpr (Q == JK_Q6_K) {
             r.w[0] = ldg16(plane_ptr(w, 4 * h + j, n, b));      // ql, quarters 0 and 2
             r.w[1] = ldg16(plane_ptr(w, 4 * h + j + 2, n, b));  // ql, quarters 1 and 3
@@ -153,7 +177,16 @@ __device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, 
         const size_t sidx =
             (size_t)min(m0 + (e >> 2), M - 1) * a.k_blocks32 + (size_t)min(4 * kc + (e & 3), (int)a.k_blocks32 - 1);
         r.xd[0][j] = __float_as_uint(a.scales[sidx]);
-        r.xd[1][j] = GemmFmt<Q>::MINS ? __float_as_uint(a.sums[sidx]) : 0u;
+        r.xd[1][j] = GemmFmt<Q>::MINS && GemmFmt<Q>::GK == 32 ? __float_as_uint(a.sums[sidx]) : 0u;
+    }
+    if constexpr (GemmFmt<Q>::MINS && GemmFmt<Q>::GK == 16) {  // x_sums_16 (repack.rs:3061-3066)
+#pragma unroll
+        for (int j = 0; j < T::XS16; ++j) {
+            const int e = T::XS16 * t + j;
+            const size_t sidx = (size_t)min(m0 + (e >> 3), M - 1) * a.k_chunks +
+                                (size_t)min(8 * kc + (e & 7), (int)a.k_chunks - 1);
+            r.x16[j] = __float_as_uint(a.sums16[sidx]);
+        }
     }
 }
 
@@ -180,8 +213,10 @@ __device__ __forceinline__ uint4 crumb4(uint4 v, int sh) {
 // (repack.rs:1724-2103) and write them, with the scale (and min) of each scale group, to
 // the chunk's LDS tiles.
 template <int Q, int TN, int TM>
-__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, TM> &r, GemmChunk<TN, TM> &c, int kc) {
+__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, TM> &r, GemmChunk<Q, TN, TM> &c,
+                                            int kc) {
     using T = Tile<TN, TM>;
+    using F = GemmFmt<Q>;
     const int t = threadIdx.x;
     {  // activations
 #pragma unroll
@@ -191,16 +226,44 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
         for (int j = 0; j < T::XS; ++j) {
             const int e = T::XS * t + j;
             c.xs[e & 3][e >> 2] = __uint_as_float(r.xd[0][j]);
-            if constexpr (GemmFmt<Q>::MINS) c.xm[e & 3][e >> 2] = __uint_as_float(r.xd[1][j]);
+            if constexpr (F::MINS && F::GK == 32) c.xm[e & 3][e >> 2] = __uint_as_float(r.xd[1][j]);
         }
+        if constexpr (F::MINS && F::GK == 16)
+#pragma unroll
+            for (int j = 0; j < T::XS16; ++j) {
+                const int e = T::XS16 * t + j;
+                c.xm[e & 7][e >> 3] = __uint_as_float(r.x16[j]);
+            }
     }
-    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0 || Q == JK_Q5_0) {
+    if constexpr (F::B32) {
         const int piece = t & 3;
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
             uint8_t *dst = c.a + ((t >> 2) + TN / 2 * (i & 1)) * kRowB + 32 * piece;
             if constexpr (Q == JK_Q8_0) {
                 *reinterpret_cast<uint4 *>(dst + 16 * (i >> 1)) = r.w[i];
+            } else if constexpr (Q == JK_Q4_1) {  // unpack_q4_1_block_i8 (quant.rs:117-129): the nibbles
+                *reinterpret_cast<uint4 *>(dst) = nib4(r.w[i], 0, 0u);
+                *reinterpret_cast<uint4 *>(dst + 16) = nib4(r.w[i], 4, 0u);
+            } else if constexpr (Q == JK_Q5_1) {  // unpack_q5_1_block_i8 (quant.rs:168-187): nibble | 16 * bit
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t v = comp(r.w[i], k), qh = r.wh[i];
+                    lo[k] = (v & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (4 * k)) & 15u);
+                    hi[k] = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (16 + 4 * k)) & 15u);
+                }
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            } else if constexpr (Q == JK_IQ4_NL) {  // unpack_iq4_nl_block_i8 (quant.rs:333-345)
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    lo[k] = iq4nl_lookup(comp(r.w[i], k) & 0x0F0F0F0Fu);
+                    hi[k] = iq4nl_lookup((comp(r.w[i], k) >> 4) & 0x0F0F0F0Fu);
+                }
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             } else if constexpr (Q == JK_Q5_0) {
                 // unpack_q5_0_block_i8 (quant.rs:139-157): (nibble | 16 * bit) - 16, bit j of
                 // the word for element j
@@ -220,7 +283,13 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
             }
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) c.ws[2 * (t & 1) + j][t >> 1] = f16_finite(r.wd[j]);
+        for (int j = 0; j < 2; ++j) {
+            c.ws[2 * (t & 1) + j][t >> 1] = f16_finite(r.wd[j] & 0xFFFFu);
+            if constexpr (Q == JK_Q4_1 || Q == JK_Q5_1) {  // repack.rs:1814-1860: min stored as -m
+                const float m = f16_finite(r.wd[j] >> 16);
+                c.wm[2 * (t & 1) + j][t >> 1] = m == 0.0f ? 0.0f : -m;
+            }
+        }
         return;
     }
     const int row = t >> 1, j = t & 1, h = kc & 1;
@@ -270,6 +339,53 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                     o[k] = ((comp(qv, k) >> (4 * hh)) & 0x0F0F0F0Fu) | (((comp(hv, k) >> (qsh + hh)) & 0x01010101u) << 4);
                 *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh + 16 * p) = make_uint4(o[0], o[1], o[2], o[3]);
             }
+    } else if constexpr (Q == JK_Q2_K) {
+        // unpack_q2_k_block_i8 (quant.rs:197-235), repack.rs:1876-1895: 16-group g = 2 jq + part of
+        // the half (jq = 2j .. 2j + 1 here) is the 2-bit field 2 jq of qs bytes 16 part .. of the half;
+        // scale d * (sc & 15), min dmin * (sc >> 4) with sc = scales[8h + g]
+        const float d = f16_finite(r.wd[0] & 0xFFFFu), dmin = f16_finite(r.wd[0] >> 16);
+#pragma unroll
+        for (int jo = 0; jo < 2; ++jo) {
+            const int jq = 2 * j + jo;
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                const int g = 2 * jq + part;
+                const uint32_t sc = (comp(r.w[0], (8 * h + g) >> 2) >> (8 * ((8 * h + g) & 3))) & 255u;
+                c.ws[g][row] = d * (float)(sc & 15u);
+                c.wm[g][row] = dmin * (float)(sc >> 4);
+                const uint4 qv = r.w[1 + part];
+                *reinterpret_cast<uint4 *>(dst + 32 * jq + 16 * part) =
+                    make_uint4((qv.x >> (2 * jq)) & 0x03030303u, (qv.y >> (2 * jq)) & 0x03030303u,
+                               (qv.z >> (2 * jq)) & 0x03030303u, (qv.w >> (2 * jq)) & 0x03030303u);
+            }
+        }
+    } else if constexpr (Q == JK_Q3_K) {
+        // unpack_q3_k_block_i8 (quant.rs:254-317), repack.rs:1896-1911: 16-group g = 2 jq + part of
+        // the half takes the 2-bit field 2 jq of qs bytes 16 part .. of the half, minus 4 where bit
+        // 4h + jq of hmask byte 16 part + l is clear; scale d * (6-bit scale 8h + g - 32)
+        const uint4 tail = r.w[4];
+        const float d = f16_finite(tail.w & 0xFFFFu);
+#pragma unroll
+        for (int jo = 0; jo < 2; ++jo) {
+            const int jq = 2 * j + jo;
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                const int g = 2 * jq + part, is = 8 * h + g;
+                const uint32_t lb = (comp(tail, (is & 7) >> 2) >> (8 * (is & 3))) & 255u;
+                const uint32_t lo = is < 8 ? (lb & 15u) : (lb >> 4);
+                const uint32_t hi = (((tail.z >> (8 * (is & 3))) & 255u) >> (2 * (is >> 2))) & 3u;
+                c.ws[g][row] = d * (float)((int)(lo | (hi << 4)) - 32);
+                const uint4 qv = r.w[2 + part], hv = r.w[part];
+                uint32_t o[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t v = (comp(qv, k) >> (2 * jq)) & 0x03030303u;
+                    const uint32_t hb = (comp(hv, k) >> (4 * h + jq)) & 0x01010101u;
+                    o[k] = (uint32_t)bytes_sub(v | (hb << 2), 0x04040404u);
+                }
+                *reinterpret_cast<uint4 *>(dst + 32 * jq + 16 * part) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
     } else if constexpr (Q == JK_Q6_K) {
         // dequantize_q6_k_block's element order (quant.rs:594-648): 16-group g = j + 2 qq of
         // half h (quarter qq) takes ql bytes 16j + 32(qq % 2) of the half, qh bytes 16j, the
@@ -324,7 +440,7 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
     using T = Tile<TN, TM>;
     constexpr int NT = T::NT, RW = T::RW;
     static_assert(GB == 1 || F::GK == 32, "block accumulation needs 32-element steps");
-    __shared__ __align__(16) GemmChunk<TN, TM> cs;
+    __shared__ __align__(16) GemmChunk<Q, TN, TM> cs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave % T::WR, wmi = wave / T::WR;  // wave tile: rows RW * wn .., tokens 32 * wmi ..
     // Workgroup i runs on XCD i % 8. Tile order: the token tiles of one weight row tile go
@@ -355,7 +471,7 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
     // chunk kc from LDS
     auto step = [&](int kc, int st) {
         const float xs = cs.xs[st][tok];
-        const float xsum = F::MINS ? cs.xm[st][tok] : 0.0f;
+        const float xsum32 = F::MINS && F::GK == 32 ? cs.xm[st][tok] : 0.0f;
 #pragma unroll
         for (int gg = 0; gg < 32 / F::GK; ++gg) {
             v16i c[NT];
@@ -393,7 +509,12 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
             const int g = (32 / F::GK) * st + gg;
             const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][srow], xs, v32f{0}, 0, 0, 0);
             v32f pm;
-            if constexpr (F::MINS) pm = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.wm[st][srow], xsum, v32f{0}, 0, 0, 0);
+            // mins: per 32-group with the 32-block activation sum, or per 16-group (Q2_K) with
+            // the 16-element sum (accumulate_scaled_tile_scalar, repack.rs:3061-3077)
+            if constexpr (F::MINS && F::GK == 32)
+                pm = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.wm[st][srow], xsum32, v32f{0}, 0, 0, 0);
+            if constexpr (F::MINS && F::GK == 16)
+                pm = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.wm[g][srow], cs.xm[g][tok], v32f{0}, 0, 0, 0);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -460,7 +581,7 @@ __global__ __launch_bounds__(64) void gemm16_kernel(WeightDev w, jk_act_q8 a, fl
     using F = GemmFmt<Q>;
     constexpr int TN = 32, TM = 16;
     static_assert(F::GK == 32, "32-element scale groups");
-    __shared__ __align__(16) GemmChunk<TN, TM> cs;
+    __shared__ __align__(16) GemmChunk<Q, TN, TM> cs;
     const int lane = threadIdx.x;
     const int ntn = (r1 - r0 + TN - 1) / TN, ntm = ((int)a.m + TM - 1) / TM;
     const int wg = (int)blockIdx.x, local = wg >> 3;
@@ -547,9 +668,10 @@ __global__ __launch_bounds__(64) void gemm16_kernel(WeightDev w, jk_act_q8 a, fl
 static int gemm_tile(int quant, long rows, long m) {
     const long ncu = cu_count();
     auto tiles = [&](long tn, long tm) { return (rows + tn - 1) / tn * ((m + tm - 1) / tm); };
-    if (tiles(128, 64) >= 2 * ncu) return 0;
+    // (Q2_K's 16-element mins do not fit the 128 x 64 tile's register budget without spills)
+    if (tiles(128, 64) >= 2 * ncu && quant != JK_Q2_K) return 0;
     if (tiles(64, 64) >= 2 * ncu) return 1;
-    if (tiles(32, 32) >= 2 * ncu || quant == JK_Q6_K) return 2;
+    if (tiles(32, 32) >= 2 * ncu || quant == JK_Q6_K || quant == JK_Q3_K || quant == JK_Q2_K) return 2;
     return 3;
 }
 
@@ -606,6 +728,11 @@ jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q
     case JK_Q5_0: return launch_gemm<JK_Q5_0, 1>(s, w, a, y, r0, r1);
     case JK_Q4_K: return launch_gemm<JK_Q4_K, 1>(s, w, a, y, r0, r1);
     case JK_Q5_K: return launch_gemm<JK_Q5_K, 1>(s, w, a, y, r0, r1);
+    case JK_Q4_1: return launch_gemm<JK_Q4_1, 1>(s, w, a, y, r0, r1);
+    case JK_Q5_1: return launch_gemm<JK_Q5_1, 1>(s, w, a, y, r0, r1);
+    case JK_IQ4_NL: return launch_gemm<JK_IQ4_NL, 1>(s, w, a, y, r0, r1);
+    case JK_Q2_K: return launch_gemm<JK_Q2_K, 1>(s, w, a, y, r0, r1);
+    case JK_Q3_K: return launch_gemm<JK_Q3_K, 1>(s, w, a, y, r0, r1);
     case JK_Q6_K: return launch_gemm<JK_Q6_K, 1>(s, w, a, y, r0, r1);
     case JK_TQ2_0: return launch_gemm<JK_TQ2_0, 1>(s, w, a, y, r0, r1);
     case JK_I2_S: return launch_gemm<JK_I2_S, 1>(s, w, a, y, r0, r1);

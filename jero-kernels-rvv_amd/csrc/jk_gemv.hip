@@ -36,7 +36,7 @@ template <int Q> struct VdFmt {
 template <int Q> struct VdBlock {
     uint4 c[VdFmt<Q>::C];
     uint32_t d;
-    uint32_t h;
+    uint32_t h[2];
 };
 
 template <int Q>
@@ -44,7 +44,9 @@ __device__ __forceinline__ void vd_load(VdBlock<Q> &o, const WeightDev &w, int r
 #pragma unroll
     for (int c = 0; c < VdFmt<Q>::C; ++c) o.c[c] = ld_chunk(w, c, r, b);
     if constexpr (VdFmt<Q>::D) o.d = w.dplane[(size_t)r * (size_t)w.nb + (size_t)b];
-    if constexpr (VdFmt<Q>::H) o.h = w.hplane[(size_t)r * (size_t)w.nb + (size_t)b];
+    if constexpr (VdFmt<Q>::H)
+#pragma unroll
+        for (int i = 0; i < fmt_of(Q).h_len / 4; ++i) o.h[i] = ld_word(w, r, b, fmt_of(Q).h_len, i);
 }
 
 // Byte k (0..15 within chunk c) of the block's chunks.
@@ -68,7 +70,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
             int qv;
             if constexpr (Q == JK_Q4_0) qv = (int)((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) - 8;
             else if constexpr (Q == JK_Q5_0)
-                qv = (int)(((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) | (((o.h >> i) & 1u) << 4)) - 16;
+                qv = (int)(((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) | (((o.h[0] >> i) & 1u) << 4)) - 16;
             else qv = (int)(int8_t)vd_byte<Q>(o, i >> 4, i & 15);
             const float wv = d * (float)qv;
             sum += wv * xb[i];
@@ -92,6 +94,73 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                     const uint32_t q = (vd_byte<Q>(o, 1 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u;
                     const float wv = d1 * (float)q - m1;
                     sum += wv * xb[64 * c + 32 * hi + l];
+                }
+            }
+        }
+    } else if constexpr (Q == JK_Q4_1 || Q == JK_Q5_1) {
+        // dequantize_q4_1_block / dequantize_q5_1_block (quant.rs:132-136, 190-195) via
+        // affine_i8_into_f32 (104-113): d * q + m, or +0.0 when d and m are both zero
+        const float d = f16_finite(o.h[0] & 0xFFFFu), m = f16_finite(o.h[0] >> 16);
+        const bool z = d == 0.0f && m == 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            uint32_t q = (vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u;
+            if constexpr (Q == JK_Q5_1) q |= ((o.h[1] >> i) & 1u) << 4;
+            const float wv = z ? 0.0f : d * (float)q + m;
+            sum += wv * xb[i];
+        }
+    } else if constexpr (Q == JK_IQ4_NL) {
+        // dequantize_iq4_nl_block (quant.rs:348-356): d * KVALUES_IQ4NL[nibble] (+0.0 for d == 0,
+        // which no sum from +0.0 observes, as above)
+        const float d = f16_finite(o.d);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = iq4nl_lookup(comp(o.c[0], k) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += (d * (float)(int8_t)(lo >> (8 * i))) * xb[4 * k + i];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t hi = iq4nl_lookup((comp(o.c[0], k) >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += (d * (float)(int8_t)(hi >> (8 * i))) * xb[16 + 4 * k + i];
+        }
+    } else if constexpr (Q == JK_Q2_K) {
+        // dequantize_q2_k_block (quant.rs:238-252): element 128 half + 32 j + 16 part + l is the
+        // 2-bit field 2j of qs byte 32 half + 16 part + l, times d * (sc & 15), minus dmin * (sc >> 4)
+        const float d = f16_finite(o.h[0] & 0xFFFFu), dmin = f16_finite(o.h[0] >> 16);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const uint32_t sc = vd_byte<Q>(o, 0, g);
+            const float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+            const int half = g >> 3, j = (g >> 1) & 3, part = g & 1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t v = (comp(o.c[1 + 2 * half + part], k) >> (2 * j)) & 0x03030303u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sum += (dl * (float)((v >> (8 * i)) & 3u) - ml) * xb[16 * g + 4 * k + i];
+            }
+        }
+    } else if constexpr (Q == JK_Q3_K) {
+        // dequantize_q3_k_block (quant.rs:320-331): element 128 half + 32 j + 16 part + l is the
+        // 2-bit field 2j of qs byte 32 half + 16 part + l, minus 4 when bit 4 half + j of hmask
+        // byte 16 part + l is clear, times d * (scale - 32)
+        const uint4 tail = o.c[6];
+        const float d = f16_finite(tail.w & 0xFFFFu);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const uint32_t lo = g < 8 ? (vd_byte<Q>(o, 6, g) & 15u) : (vd_byte<Q>(o, 6, g - 8) >> 4);
+            const uint32_t hi = (vd_byte<Q>(o, 6, 8 + (g & 3)) >> (2 * (g >> 2))) & 3u;
+            const float dl = d * (float)((int)(lo | (hi << 4)) - 32);
+            const int half = g >> 3, j = (g >> 1) & 3, part = g & 1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t v = (comp(o.c[2 + 2 * half + part], k) >> (2 * j)) & 0x03030303u;
+                const uint32_t h = (comp(o.c[part], k) >> (4 * half + j)) & 0x01010101u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qv = (int)((v >> (8 * i)) & 3u) - ((h >> (8 * i)) & 1u ? 0 : 4);
+                    sum += (dl * (float)qv) * xb[16 * g + 4 * k + i];
                 }
             }
         }
@@ -232,6 +301,11 @@ jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, 
     case JK_Q8_0: return launch_vd<JK_Q8_0>(s, w, x, y);
     case JK_Q4_K: return launch_vd<JK_Q4_K>(s, w, x, y);
     case JK_Q5_K: return launch_vd<JK_Q5_K>(s, w, x, y);
+    case JK_Q4_1: return launch_vd<JK_Q4_1>(s, w, x, y);
+    case JK_Q5_1: return launch_vd<JK_Q5_1>(s, w, x, y);
+    case JK_IQ4_NL: return launch_vd<JK_IQ4_NL>(s, w, x, y);
+    case JK_Q2_K: return launch_vd<JK_Q2_K>(s, w, x, y);
+    case JK_Q3_K: return launch_vd<JK_Q3_K>(s, w, x, y);
     case JK_Q6_K: return launch_vd<JK_Q6_K>(s, w, x, y);
     case JK_I2_S: return launch_vd<JK_I2_S>(s, w, x, y);
     default: return fail(JK_CAPABILITY_MISMATCH, "vec_dot_f32: unsupported quant %d", w.quant);

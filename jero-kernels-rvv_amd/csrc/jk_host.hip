@@ -194,6 +194,21 @@ jk_status jk_host_vec_dot_q5_0(float *out, size_t n, const jk_tensor_view *w, co
 jk_status jk_host_vec_dot_q5_k(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
     return host_vec_dot_f32(JK_Q5_K, out, n, w, in, in_len);
 }
+jk_status jk_host_vec_dot_q4_1(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_Q4_1, out, n, w, in, in_len);
+}
+jk_status jk_host_vec_dot_q5_1(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_Q5_1, out, n, w, in, in_len);
+}
+jk_status jk_host_vec_dot_q2_k(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_Q2_K, out, n, w, in, in_len);
+}
+jk_status jk_host_vec_dot_q3_k(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_Q3_K, out, n, w, in, in_len);
+}
+jk_status jk_host_vec_dot_iq4_nl(float *out, size_t n, const jk_tensor_view *w, const float *in, size_t in_len) {
+    return host_vec_dot_f32(JK_IQ4_NL, out, n, w, in, in_len);
+}
 
 // dequantize_tensor_row (quant.rs:2492-2568) with validate_token_row_geometry (1749-1808).
 jk_status jk_host_dequantize_tensor_row(const jk_tensor_view *w, size_t row, float *out, size_t out_len) {
@@ -262,8 +277,7 @@ jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view 
                                float act_scale) {
     if (!w || (!w->bytes && w->byte_len) || (w->ndim && !w->shape)) return fail(JK_TENSOR_BOUNDS, "null tensor view");
     const int q = w->quant;
-    if (q != JK_TQ1_0 && q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
-        return fail(JK_TENSOR_BOUNDS, "BitLinear: unsupported quant type %d", q);
+    if (!has_bitlinear(q)) return fail(JK_TENSOR_BOUNDS, "BitLinear: unsupported quant type %d", q);
     if (w->ndim == 0) return fail(JK_TENSOR_BOUNDS, "BitLinear: empty tensor shape");
     const Fmt f = fmt_of(q);
     if (w->ndim == 2) {

@@ -4,15 +4,21 @@
 // 16-byte chunks; chunk c of block b of row r lives in plane c at
 //     planes + ((c * rows + r) * nb + b) * 16
 // and the block's f16 scale, when it is not inside a chunk, lives in the scale
-// plane at dplane[r * nb + b]; a 4-byte field that is neither (Q5_0's high bits)
-// lives in the word plane at hplane[r * nb + b]. Lanes that walk consecutive
-// blocks of one row therefore read consecutive 16-byte chunks (one coalesced
-// 128-bit load per lane per plane), and the layout holds exactly the GGUF bytes:
+// plane at dplane[r * nb + b]; a 4- or 8-byte field that is neither (high bits,
+// d / m pairs) lives in the word plane, hplane[(r * nb + b) * h_len / 4 ..]. Lanes
+// that walk consecutive blocks of one row therefore read consecutive 16-byte
+// chunks (one coalesced 128-bit load per lane per plane), and the layout holds
+// exactly the GGUF bytes (Q3_K: 2 bytes of padding in its last chunk):
 //
 //   format  block  bytes  chunks (16 B)                         scale  word
 //   Q4_0     32     18    qs[0..16)                             d      -
+//   Q4_1     32     20    qs[0..16)                             -      d m
 //   Q5_0     32     22    qs[0..16)                             d      qh
+//   Q5_1     32     24    qs[0..16)                             -      d m qh
 //   Q8_0     32     34    qs[0..16), qs[16..32)                 d      -
+//   IQ4_NL   32     18    qs[0..16)                             d      -
+//   Q2_K    256     84    scales16, qs x4                       -      d dmin
+//   Q3_K    256    110    hmask x2, qs x4, [scales12 d 0 0]     -      -
 //   Q4_K    256    144    [d dmin scales12], qs[16c..16c+16)    -      -
 //   Q5_K    256    176    [d dmin scales12], qh x2, qs x8       -      -
 //   Q6_K    256    210    ql x8, qh x4, scales x1               d      -
@@ -49,27 +55,40 @@ struct Fmt {
     int d_off;   // byte offset of the f16 scale inside the GGUF block, -1 if none
     int q_off;   // byte offset of chunk 0 inside the GGUF block
     int h_off;   // byte offset of the word-plane field inside the GGUF block, -1 if none
+    int h_len;   // bytes of the word-plane field (4 or 8)
 };
 
 // Device layout of each GGUF format (TQ1_0: the GGUF block geometry; its device
 // layout is TQ2_0's, see dev_quant).
 __host__ __device__ constexpr Fmt fmt_of(int q) {
-    return q == JK_Q4_0   ? Fmt{JK_Q4_0, 32, 18, 1, 0, 2, -1}
-           : q == JK_Q5_0 ? Fmt{JK_Q5_0, 32, 22, 1, 0, 6, 2}
-           : q == JK_Q8_0 ? Fmt{JK_Q8_0, 32, 34, 2, 0, 2, -1}
-           : q == JK_Q4_K ? Fmt{JK_Q4_K, 256, 144, 9, -1, 0, -1}
-           : q == JK_Q5_K ? Fmt{JK_Q5_K, 256, 176, 11, -1, 0, -1}
-           : q == JK_Q6_K ? Fmt{JK_Q6_K, 256, 210, 13, 208, 0, -1}
-           : q == JK_TQ1_0 ? Fmt{JK_TQ1_0, 256, 54, 0, 0, 2, -1}
-           : q == JK_TQ2_0 ? Fmt{JK_TQ2_0, 256, 66, 4, 0, 2, -1}
-           : q == JK_I2_S  ? Fmt{JK_I2_S, 128, 32, 2, -1, 0, -1}
-                           : Fmt{0, 0, 0, 0, -1, 0, -1};
+    return q == JK_Q4_0    ? Fmt{JK_Q4_0, 32, 18, 1, 0, 2, -1, 0}
+           : q == JK_Q4_1   ? Fmt{JK_Q4_1, 32, 20, 1, -1, 4, 0, 4}
+           : q == JK_Q5_0   ? Fmt{JK_Q5_0, 32, 22, 1, 0, 6, 2, 4}
+           : q == JK_Q5_1   ? Fmt{JK_Q5_1, 32, 24, 1, -1, 8, 0, 8}
+           : q == JK_Q8_0   ? Fmt{JK_Q8_0, 32, 34, 2, 0, 2, -1, 0}
+           : q == JK_IQ4_NL ? Fmt{JK_IQ4_NL, 32, 18, 1, 0, 2, -1, 0}
+           : q == JK_Q2_K   ? Fmt{JK_Q2_K, 256, 84, 5, -1, 0, 80, 4}
+           : q == JK_Q3_K   ? Fmt{JK_Q3_K, 256, 110, 7, -1, 0, -1, 0}
+           : q == JK_Q4_K   ? Fmt{JK_Q4_K, 256, 144, 9, -1, 0, -1, 0}
+           : q == JK_Q5_K   ? Fmt{JK_Q5_K, 256, 176, 11, -1, 0, -1, 0}
+           : q == JK_Q6_K   ? Fmt{JK_Q6_K, 256, 210, 13, 208, 0, -1, 0}
+           : q == JK_TQ1_0  ? Fmt{JK_TQ1_0, 256, 54, 0, 0, 2, -1, 0}
+           : q == JK_TQ2_0  ? Fmt{JK_TQ2_0, 256, 66, 4, 0, 2, -1, 0}
+           : q == JK_I2_S   ? Fmt{JK_I2_S, 128, 32, 2, -1, 0, -1, 0}
+                            : Fmt{0, 0, 0, 0, -1, 0, -1, 0};
 }
 
 // Format of the device layout a GGUF format is stored in.
 __host__ __device__ constexpr int dev_quant(int q) { return q == JK_TQ1_0 ? JK_TQ2_0 : q; }
 
 inline bool fmt_known(int q) { return fmt_of(q).be != 0; }
+// Formats with a quant_q8 GEMV / a BitLinear product / an f32-activation vec_dot in the reference.
+inline bool has_q8_gemv(int q) {
+    return q == JK_Q4_0 || q == JK_Q5_0 || q == JK_Q8_0 || q == JK_Q4_K || q == JK_Q5_K || q == JK_Q6_K ||
+           q == JK_TQ1_0 || q == JK_TQ2_0;
+}
+inline bool has_bitlinear(int q) { return q == JK_TQ1_0 || q == JK_TQ2_0 || q == JK_I2_S || q == JK_Q8_0; }
+inline bool has_vec_dot_f32(int q) { return fmt_known(q) && q != JK_TQ1_0 && q != JK_TQ2_0; }
 inline size_t trailer_bytes(int q) { return q == JK_I2_S ? 32 : 0; }
 
 // Plain-old-data view of a weight handle that kernels take by value.

@@ -53,7 +53,13 @@ __global__ __launch_bounds__(256) void repack_kernel(WeightDev w, int gq, const 
     for (int c = 0; c < f.chunks; ++c) {
         uint32_t d4[4];
         for (int k = 0; k < 4; ++k) {
-            d4[k] = gq == JK_TQ1_0 ? tq1_as_tq2_dword(src, 4 * c + k) : le32(src + f.q_off + 16 * c + 4 * k);
+            const int off = f.q_off + 16 * c + 4 * k;
+            if (gq == JK_TQ1_0) d4[k] = tq1_as_tq2_dword(src, 4 * c + k);
+            else if (off + 4 <= fg.bb) d4[k] = le32(src + off);
+            else {  // the last chunk of a Q3_K block: bytes past the block are zero padding
+                d4[k] = 0;
+                for (int i = 0; off + i < fg.bb; ++i) d4[k] |= (uint32_t)src[off + i] << (8 * i);
+            }
             if (f.quant == JK_TQ2_0) d4[k] = tq2_transpose(d4[k]);
         }
         uint4 *dst = const_cast<uint4 *>(chunk_ptr(w, c, r, b));
@@ -63,7 +69,8 @@ __global__ __launch_bounds__(256) void repack_kernel(WeightDev w, int gq, const 
         uint16_t h = (uint16_t)(src[f.d_off] | (src[f.d_off + 1] << 8));
         const_cast<uint16_t *>(w.dplane)[idx] = h;
     }
-    if (f.h_off >= 0) const_cast<uint32_t *>(w.hplane)[idx] = le32(src + f.h_off);
+    for (int i = 0; f.h_off >= 0 && i < f.h_len / 4; ++i)
+        const_cast<uint32_t *>(w.hplane)[idx * (size_t)(f.h_len / 4) + i] = le32(src + f.h_off + 4 * i);
 }
 
 jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf) {
@@ -79,7 +86,8 @@ __device__ __forceinline__ uint8_t chunk_byte(const uint4 &v, int i) {
 }
 
 // Dequantizes block b of row r into out[0..be) with the GGUF block dequantizers' arithmetic:
-// dequantize_q4_0_block (quant.rs:550-568), dequantize_q5_0_block (160-164),
+// dequantize_q4_0_block (quant.rs:550-568), dequantize_q5_0_block (160-164), the Q4_1, Q5_1,
+// IQ4_NL, Q2_K and Q3_K block dequantizers (132-356),
 // dequantize_q8_0_block (571-588), dequantize_q4_k_m_block (lib.rs:720-766),
 // dequantize_q5_k_block (quant.rs:651-706), dequantize_q6_k_block (594-648), the TQ1_0
 // and TQ2_0 arms (2359-2378; one device layout) and dequantize_i2_s_block (380-387).
@@ -105,6 +113,65 @@ __device__ void dequant_block(const WeightDev &w, int r, int b, float *out) {
             const int q1 = (int)((x >> 4) | (((qh >> (i + 16)) & 1u) << 4)) - 16;
             out[i] = d == 0.0f ? 0.0f : d * (float)q0;
             out[i + 16] = d == 0.0f ? 0.0f : d * (float)q1;
+        }
+        break;
+    }
+    case JK_Q4_1:
+    case JK_Q5_1: {  // dequantize_q4_1_block / dequantize_q5_1_block (quant.rs:132-136, 190-195):
+                     // affine_i8_into_f32 (104-113), both zero -> +0.0, else d * q + m
+        const int hl = w.quant == JK_Q4_1 ? 4 : 8;
+        const uint32_t dm = ld_word(w, r, b, hl, 0), qh = hl == 8 ? ld_word(w, r, b, hl, 1) : 0u;
+        const float d = f16_finite(dm & 0xFFFFu), m = f16_finite(dm >> 16);
+        const uint4 q = ld_chunk(w, 0, r, b);
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t x = chunk_byte(q, i);
+            const int q0 = (int)((x & 15) | (((qh >> i) & 1u) << 4));
+            const int q1 = (int)((x >> 4) | (((qh >> (i + 16)) & 1u) << 4));
+            const bool z = d == 0.0f && m == 0.0f;
+            out[i] = z ? 0.0f : d * (float)q0 + m;
+            out[i + 16] = z ? 0.0f : d * (float)q1 + m;
+        }
+        break;
+    }
+    case JK_IQ4_NL: {  // dequantize_iq4_nl_block (quant.rs:348-356)
+        const float d = ld_dscale(w, r, b);
+        const uint4 q = ld_chunk(w, 0, r, b);
+        for (int i = 0; i < 16; ++i) {
+            const uint8_t x = chunk_byte(q, i);
+            const int v0 = (int)(int8_t)(iq4nl_lookup(x & 15u) & 255u), v1 = (int)(int8_t)(iq4nl_lookup(x >> 4) & 255u);
+            out[i] = d == 0.0f ? 0.0f : d * (float)v0;
+            out[i + 16] = d == 0.0f ? 0.0f : d * (float)v1;
+        }
+        break;
+    }
+    case JK_Q2_K: {  // dequantize_q2_k_block (quant.rs:238-252) with unpack_q2_k_block_i8 (197-235)
+        const uint32_t dd = ld_word(w, r, b, 4, 0);
+        const float d = f16_finite(dd & 0xFFFFu), dmin = f16_finite(dd >> 16);
+        const uint4 scv = ld_chunk(w, 0, r, b);
+        for (int e = 0; e < 256; ++e) {
+            const int half = e >> 7, j = (e >> 5) & 3, part = (e >> 4) & 1, l = e & 15;
+            const int is = e >> 4;
+            const uint8_t sc = chunk_byte(scv, is);
+            const float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
+            const int qb = 32 * half + 16 * part + l;  // byte of qs (chunks 1..4)
+            const int qv = (chunk_byte(ld_chunk(w, 1 + (qb >> 4), r, b), qb & 15) >> (2 * j)) & 3;
+            out[e] = dl * (float)qv - ml;
+        }
+        break;
+    }
+    case JK_Q3_K: {  // dequantize_q3_k_block (quant.rs:320-331) with unpack_q3_k_block_i8 (254-317)
+        const uint4 tail = ld_chunk(w, 6, r, b);  // 12 scale bytes, d, padding
+        const float d = f16_finite(tail.w & 0xFFFFu);
+        for (int e = 0; e < 256; ++e) {
+            const int half = e >> 7, j = (e >> 5) & 3, part = (e >> 4) & 1, l = e & 15;
+            const int is = e >> 4;
+            const int lo = is < 8 ? (chunk_byte(tail, is) & 15) : (chunk_byte(tail, is - 8) >> 4);
+            const int hi = (chunk_byte(tail, 8 + (is & 3)) >> (2 * (is >> 2))) & 3;
+            const float dl = d * (float)((lo | (hi << 4)) - 32);
+            const int qb = 32 * half + 16 * part + l, hb = 16 * part + l;
+            const int v = (chunk_byte(ld_chunk(w, 2 + (qb >> 4), r, b), qb & 15) >> (2 * j)) & 3;
+            const int h = (chunk_byte(ld_chunk(w, hb >> 4, r, b), hb & 15) >> (4 * half + j)) & 1;
+            out[e] = dl * (float)(v - (h ? 0 : 4));
         }
         break;
     }

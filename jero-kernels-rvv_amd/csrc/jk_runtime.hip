@@ -41,7 +41,12 @@ jk_status check_launch(const char *what) {
 static const char *quant_name(int q) {
     switch (q) {
     case JK_Q4_0: return "Q4_0";
+    case JK_Q4_1: return "Q4_1";
     case JK_Q5_0: return "Q5_0";
+    case JK_Q5_1: return "Q5_1";
+    case JK_IQ4_NL: return "IQ4_NL";
+    case JK_Q2_K: return "Q2_K";
+    case JK_Q3_K: return "Q3_K";
     case JK_Q8_0: return "Q8_0";
     case JK_Q4_K: return "Q4_K_M";
     case JK_Q5_K: return "Q5_K";
@@ -222,7 +227,7 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
     const size_t plane_bytes = rows * nb * (size_t)fd.chunks * 16;
     const size_t dbytes = fd.d_off >= 0 ? rows * nb * 2 : 0;
     const size_t dpad = (dbytes + 255) / 256 * 256;  // keeps the word plane 256-byte aligned
-    const size_t hbytes = fd.h_off >= 0 ? rows * nb * 4 : 0;
+    const size_t hbytes = fd.h_off >= 0 ? rows * nb * (size_t)fd.h_len : 0;
     jk_weight *h = new jk_weight();
     memset(h, 0, sizeof *h);
     JK_HIP(hipGetDevice(&h->device));
@@ -377,8 +382,8 @@ static jk_status gemv_check(const jk_weight *w, int quant, const void *x, size_t
     if (quant && w->quant != quant)
         return fail(JK_TENSOR_BOUNDS, "%s: expected %s quant type, got %s", name, quant_name(quant),
                     quant_name(w->quant));
-    if (w->quant == JK_I2_S)
-        return fail(JK_CAPABILITY_MISMATCH, "%s: I2_S has no quant_q8 GEMV", name);
+    if (!has_q8_gemv(w->quant))
+        return fail(JK_CAPABILITY_MISMATCH, "%s: %s has no quant_q8 GEMV", name, quant_name(w->quant));
     // check_q8_block_len (quant_q8.rs:1562-1578)
     if (nx != (size_t)w->dev.nb)
         return fail(JK_TENSOR_BOUNDS, "%s: x_blocks len %zu != expected %d", name, nx, w->dev.nb);
@@ -433,7 +438,7 @@ static jk_status gemv_job_check(const jk_gemv_job *j, size_t i, GemvJob *out) {
     const jk_weight *w = j->w;
     if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: null weight handle", i);
     const int q = w->quant;
-    if (q == JK_I2_S)
+    if (!has_q8_gemv(q))
         return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_batch: job %zu: %s has no quant_q8 GEMV", i, quant_name(q));
     if ((j->x_q8 == nullptr) == (j->x_f32 == nullptr))
         return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: exactly one of x_q8 and x_f32 must be set", i);
@@ -493,7 +498,7 @@ jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
     if (!w) return fail(JK_TENSOR_BOUNDS, "vec_dot: null weight handle");
     int q = w->quant;
-    if (q == JK_TQ2_0 || q == JK_TQ1_0)
+    if (!has_vec_dot_f32(q))
         return fail(JK_CAPABILITY_MISMATCH, "vec_dot: %s has no f32-activation matvec", quant_name(q));
     if (n != (size_t)w->dev.cols || y_len != (size_t)w->dev.rows)
         return fail(JK_TENSOR_BOUNDS, "vec_dot: matrix [%d, %d] does not match output len %zu and input len %zu",
@@ -534,7 +539,7 @@ jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, co
     if (!w) return fail(JK_TENSOR_BOUNDS, "bitlinear: null weight handle");
     int q = w->quant;
     // validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
-    if (q != JK_TQ1_0 && q != JK_TQ2_0 && q != JK_I2_S && q != JK_Q8_0)
+    if (!has_bitlinear(q))
         return fail(JK_TENSOR_BOUNDS, "bitlinear: unsupported quant type %s", quant_name(q));
     if (m == 0 || k != (size_t)w->dev.cols || y_len != m * (size_t)w->dev.rows)
         return fail(JK_TENSOR_BOUNDS, "bitlinear: weights [%d, %d] do not match m=%zu k=%zu out=%zu", w->dev.rows,

@@ -25,10 +25,18 @@ HEADER_PATH = os.path.join(os.path.dirname(PACKAGE_DIR), "include", "jk.h")
 
 # ---------------------------------------------------------------- formats
 Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S = 2, 6, 8, 12, 13, 14, 34, 35, 36
+Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL = 3, 7, 10, 11, 20
 QUANT_NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K_M", Q5_K: "Q5_K", Q6_K: "Q6_K",
-               TQ1_0: "TQ1_0", TQ2_0: "TQ2_0", I2_S: "I2_S"}
-BLOCK_ELEMENTS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, TQ1_0: 256, TQ2_0: 256, I2_S: 128}
-BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, TQ1_0: 54, TQ2_0: 66, I2_S: 32}
+               TQ1_0: "TQ1_0", TQ2_0: "TQ2_0", I2_S: "I2_S", Q4_1: "Q4_1", Q5_1: "Q5_1", Q2_K: "Q2_K",
+               Q3_K: "Q3_K", IQ4_NL: "IQ4_NL"}
+BLOCK_ELEMENTS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, TQ1_0: 256, TQ2_0: 256, I2_S: 128,
+                  Q4_1: 32, Q5_1: 32, IQ4_NL: 32, Q2_K: 256, Q3_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, TQ1_0: 54, TQ2_0: 66, I2_S: 32,
+               Q4_1: 20, Q5_1: 24, IQ4_NL: 18, Q2_K: 84, Q3_K: 110}
+# Formats with a quant_q8 GEMV, with an f32-activation vec_dot, with a BitLinear product.
+GEMV_FORMATS = (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0)
+VEC_DOT_F32_FORMATS = (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, I2_S)
+BITLINEAR_FORMATS = (TQ1_0, TQ2_0, I2_S, Q8_0)
 # Formats whose quant_q8 GEMV takes BlockQ8_0 activations (the others take BlockQ8K).
 Q8_0_ACT = (Q4_0, Q5_0, Q8_0)
 TRAILER_BYTES = {I2_S: 32}
@@ -293,6 +301,31 @@ def vec_dot_q5_0(out, weights, inp):
 def vec_dot_q5_k(out, weights, inp):
     """quant.rs:1238"""
     _vec_dot_f32("jk_host_vec_dot_q5_k", out, weights, inp)
+
+
+def vec_dot_q4_1(out, weights, inp):
+    """quant.rs:2062"""
+    _vec_dot_f32("jk_host_vec_dot_q4_1", out, weights, inp)
+
+
+def vec_dot_q5_1(out, weights, inp):
+    """quant.rs:2081"""
+    _vec_dot_f32("jk_host_vec_dot_q5_1", out, weights, inp)
+
+
+def vec_dot_q2_k(out, weights, inp):
+    """quant.rs:2100"""
+    _vec_dot_f32("jk_host_vec_dot_q2_k", out, weights, inp)
+
+
+def vec_dot_q3_k(out, weights, inp):
+    """quant.rs:2119"""
+    _vec_dot_f32("jk_host_vec_dot_q3_k", out, weights, inp)
+
+
+def vec_dot_iq4_nl(out, weights, inp):
+    """quant.rs:2138"""
+    _vec_dot_f32("jk_host_vec_dot_iq4_nl", out, weights, inp)
 
 
 def dequantize_tensor_row(weights: TensorView, row: int, out: np.ndarray) -> None:

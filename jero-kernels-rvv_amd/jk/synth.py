@@ -10,6 +10,10 @@ Distributions (one GGUF block per row-block, little-endian):
   TQ1_0  trits uniform in {-1, 0, +1}, five base-3 digits per byte (element 5i+j = digit j of
          byte 2+i, element 255 = byte 53), d = f16(1.0)
   TQ2_0  trits uniform in {-1, 0, +1} packed 2 bits each (element 4i+j = bits 2j of qs[i]), d = f16(1.0)
+  Q4_1, Q5_1  d = f16(|N(0,1)| * 0.02 / 16), m = f16(N(0,1) * 0.01), random quant (and high-bit) bytes
+  IQ4_NL d = f16(|N(0,1)| * 0.02 / 127), 16 bytes of uniform nibble indices
+  Q2_K   16 random scale / min bytes, 64 random quant bytes, d, dmin = f16(|N(0,1)| * 0.01)
+  Q3_K   96 random hmask / quant bytes, 12 random packed scale bytes, d = f16(|N(0,1)| * 0.002)
   I2_S   trits uniform in {-1, 0, +1} (byte g: elements g, 32+g, 64+g, 96+g in bits 7:6..1:0),
          32-byte trailer holding the f32 tensor scale 1.0
 Activations are f32 ~ N(0, 1).
@@ -18,7 +22,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import BLOCK_BYTES, BLOCK_ELEMENTS, I2_S, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, TQ1_0, TQ2_0
+from . import (BLOCK_BYTES, BLOCK_ELEMENTS, I2_S, IQ4_NL, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0,
+               TQ1_0, TQ2_0)
 
 
 def _f16_bits(v: np.ndarray) -> np.ndarray:
@@ -64,6 +69,20 @@ def gguf_weights(quant: int, rows: int, cols: int, seed: int) -> np.ndarray:
         t = rng.integers(0, 3, size=(nb, 64, 4), dtype=np.uint8)  # 2-bit value = trit + 1
         blocks[:, 2:] = t[..., 0] | (t[..., 1] << 2) | (t[..., 2] << 4) | (t[..., 3] << 6)
         _put_u16(blocks, 0, np.full(nb, 0x3C00, dtype=np.uint16))
+    elif quant in (Q4_1, Q5_1):
+        _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.02 / 16))
+        _put_u16(blocks, 2, _f16_bits(rng.standard_normal(nb) * 0.01))
+        blocks[:, 4:] = rng.integers(0, 256, size=(nb, bb - 4), dtype=np.uint8)
+    elif quant == IQ4_NL:
+        _put_u16(blocks, 0, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.02 / 127))
+        blocks[:, 2:] = rng.integers(0, 256, size=(nb, 16), dtype=np.uint8)
+    elif quant == Q2_K:
+        blocks[:, :80] = rng.integers(0, 256, size=(nb, 80), dtype=np.uint8)
+        _put_u16(blocks, 80, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.01))
+        _put_u16(blocks, 82, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.01))
+    elif quant == Q3_K:
+        blocks[:, :108] = rng.integers(0, 256, size=(nb, 108), dtype=np.uint8)
+        _put_u16(blocks, 108, _f16_bits(np.abs(rng.standard_normal(nb)) * 0.002))
     elif quant == TQ1_0:
         t = rng.integers(0, 3, size=(nb, 256), dtype=np.int64)  # digit = trit + 1
         digits = t[:, :255].reshape(nb, 51, 5)
@@ -92,7 +111,7 @@ def random_weights(quant: int, rows: int, cols: int, seed: int, specials: bool =
     blocks = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
     # keep normal scales modest so sums stay finite; specials override some of them
     scale_offs = {Q4_0: [0], Q5_0: [0], Q8_0: [0], Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], TQ1_0: [0],
-                  TQ2_0: [0]}.get(quant, [])
+                  TQ2_0: [0], Q4_1: [0, 2], Q5_1: [0, 2], IQ4_NL: [0], Q2_K: [80, 82], Q3_K: [108]}.get(quant, [])
     for off in scale_offs:
         mag = rng.uniform(1e-4, 0.05, size=nb) * rng.choice([-1.0, 1.0], size=nb)
         _put_u16(blocks, off, _f16_bits(mag))

@@ -17,8 +17,8 @@
 /* ------------------------------------------------------------------------- */
 size_t or_block_elements(int q) {
     switch (q) {
-    case OR_Q4_0: case OR_Q8_0: case OR_Q5_0: return 32;
-    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_TQ1_0: case OR_TQ2_0: return 256;
+    case OR_Q4_0: case OR_Q8_0: case OR_Q5_0: case OR_Q4_1: case OR_Q5_1: case OR_IQ4_NL: return 32;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_TQ1_0: case OR_TQ2_0: case OR_Q2_K: case OR_Q3_K: return 256;
     case OR_I2_S: return 128;
     default: return 0;
     }
@@ -27,7 +27,12 @@ size_t or_block_elements(int q) {
 size_t or_block_bytes(int q) {
     switch (q) {
     case OR_Q4_0: return 18;
+    case OR_Q4_1: return 20;
     case OR_Q5_0: return 22;
+    case OR_Q5_1: return 24;
+    case OR_IQ4_NL: return 18;
+    case OR_Q2_K: return 84;
+    case OR_Q3_K: return 110;
     case OR_Q8_0: return 34;
     case OR_Q4_K: return 144;
     case OR_Q5_K: return 176;
@@ -220,6 +225,128 @@ float or_unpack_tq1_0_block_i8(const uint8_t *blk, int8_t *out) {
     return s;
 }
 
+/* quant.rs:117-129: quants are the nibbles (0..15), (d, m) returned */
+static void unpack_q4_1_block_i8(const uint8_t *blk, int8_t *out, float *d, float *m) {
+    *d = or_f16_to_f32_finite(rd16(blk));
+    *m = or_f16_to_f32_finite(rd16(blk + 2));
+    for (int i = 0; i < 16; i++) {
+        out[i] = (int8_t)(blk[4 + i] & 0x0F);
+        out[i + 16] = (int8_t)((blk[4 + i] >> 4) & 0x0F);
+    }
+}
+
+/* quant.rs:168-187: quants 0..31 with the fifth bit from the u32 at bytes 4..8 */
+static void unpack_q5_1_block_i8(const uint8_t *blk, int8_t *out, float *d, float *m) {
+    *d = or_f16_to_f32_finite(rd16(blk));
+    *m = or_f16_to_f32_finite(rd16(blk + 2));
+    uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) | ((uint32_t)blk[7] << 24);
+    for (int j = 0; j < 16; j++) {
+        uint8_t b = blk[8 + j];
+        out[j] = (int8_t)((b & 0x0F) | (((qh >> j) & 1u) << 4));
+        out[j + 16] = (int8_t)(((b >> 4) & 0x0F) | (((qh >> (j + 16)) & 1u) << 4));
+    }
+}
+
+/* affine_i8_into_f32 (quant.rs:104-113): both zero -> +0.0, else d * q + m */
+static void affine_i8_into_f32(float d, float m, const int8_t *q, float *out, int n) {
+    if (d == 0.0f && m == 0.0f) { for (int i = 0; i < n; i++) out[i] = 0.0f; return; }
+    for (int i = 0; i < n; i++) out[i] = d * (float)q[i] + m;
+}
+
+/* quant.rs:132-136 */
+void or_dequantize_q4_1_block(const uint8_t *blk, float *out) {
+    int8_t q[32];
+    float d, m;
+    unpack_q4_1_block_i8(blk, q, &d, &m);
+    affine_i8_into_f32(d, m, q, out, 32);
+}
+
+/* quant.rs:190-195 */
+void or_dequantize_q5_1_block(const uint8_t *blk, float *out) {
+    int8_t q[32];
+    float d, m;
+    unpack_q5_1_block_i8(blk, q, &d, &m);
+    affine_i8_into_f32(d, m, q, out, 32);
+}
+
+/* quant.rs:197-235: scales[16] at 0, qs[64] at 16, d at 80, dmin at 82. Sub-block is
+ * (16 elements) has scale d * (sc & 15) and min dmin * (sc >> 4); its quants are the 2-bit
+ * field 2j of qs[32 half + 16 (is % 2) + l] for is = 8 half + 2j + (is % 2). */
+void or_unpack_q2_k_block_i8(const uint8_t *blk, int8_t *q, float *scales, float *mins) {
+    const uint8_t *sc = blk, *qs = blk + 16;
+    float d = or_f16_to_f32_finite(rd16(blk + 80)), dmin = or_f16_to_f32_finite(rd16(blk + 82));
+    int is = 0;
+    for (int half = 0; half < 2; half++)
+        for (int j = 0; j < 4; j++)
+            for (int part = 0; part < 2; part++, is++) {
+                scales[is] = d * (float)(sc[is] & 0x0F);
+                mins[is] = dmin * (float)(sc[is] >> 4);
+                for (int l = 0; l < 16; l++)
+                    q[128 * half + 32 * j + 16 * part + l] = (int8_t)((qs[32 * half + 16 * part + l] >> (2 * j)) & 3);
+            }
+}
+
+/* quant.rs:238-252: dl * q - ml per 16-element sub-block */
+void or_dequantize_q2_k_block(const uint8_t *blk, float *out) {
+    int8_t q[256];
+    float sc[16], mn[16];
+    or_unpack_q2_k_block_i8(blk, q, sc, mn);
+    for (int sb = 0; sb < 16; sb++)
+        for (int l = 0; l < 16; l++) out[16 * sb + l] = sc[sb] * (float)q[16 * sb + l] - mn[sb];
+}
+
+/* quant.rs:254-317: hmask[32] at 0, qs[64] at 32, 12 packed 6-bit scales at 96, d at 108.
+ * The 16 scales (6 bits, biased by 32) are the low nibbles of bytes 0..8 (scales 0..7) or
+ * the high nibbles (8..15), with bits 4..5 from byte 8 + (is % 4) at shift 2 (is / 4). Quant
+ * of element 128 half + 32 j + 16 part + l: 2-bit field 2j of qs[32 half + 16 part + l], minus
+ * 4 when bit (4 half + j) of hmask[16 part + l] is clear. */
+void or_unpack_q3_k_block_i8(const uint8_t *blk, int8_t *q, float *scales) {
+    const uint8_t *hm = blk, *qs = blk + 32, *raw = blk + 96;
+    float d = or_f16_to_f32_finite(rd16(blk + 108));
+    for (int is = 0; is < 16; is++) {
+        int lo = is < 8 ? (raw[is] & 0x0F) : (raw[is - 8] >> 4);
+        int hi = (raw[8 + (is & 3)] >> (2 * (is >> 2))) & 3;
+        scales[is] = d * (float)((int8_t)(lo | (hi << 4)) - 32);
+    }
+    for (int half = 0; half < 2; half++)
+        for (int j = 0; j < 4; j++)
+            for (int part = 0; part < 2; part++)
+                for (int l = 0; l < 16; l++) {
+                    int v = (qs[32 * half + 16 * part + l] >> (2 * j)) & 3;
+                    int hb = (hm[16 * part + l] >> (4 * half + j)) & 1;
+                    q[128 * half + 32 * j + 16 * part + l] = (int8_t)(v - (hb ? 0 : 4));
+                }
+}
+
+/* quant.rs:320-331: dl * q */
+void or_dequantize_q3_k_block(const uint8_t *blk, float *out) {
+    int8_t q[256];
+    float sc[16];
+    or_unpack_q3_k_block_i8(blk, q, sc);
+    for (int sb = 0; sb < 16; sb++)
+        for (int l = 0; l < 16; l++) out[16 * sb + l] = sc[sb] * (float)q[16 * sb + l];
+}
+
+/* KVALUES_IQ4NL (quant.rs:76-78) */
+static const int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* quant.rs:333-345 */
+float or_unpack_iq4_nl_block_i8(const uint8_t *blk, int8_t *out) {
+    float d = or_f16_to_f32_finite(rd16(blk));
+    for (int j = 0; j < 16; j++) {
+        out[j] = kvalues_iq4nl[blk[2 + j] & 0x0F];
+        out[j + 16] = kvalues_iq4nl[blk[2 + j] >> 4];
+    }
+    return d;
+}
+
+/* quant.rs:348-356 */
+void or_dequantize_iq4_nl_block(const uint8_t *blk, float *out) {
+    int8_t q[32];
+    float d = or_unpack_iq4_nl_block_i8(blk, q);
+    scale_i8_into_f32(d, q, out, 32);
+}
+
 /* ime.rs:636-658: crate layout, d first, element 4i+j = bits 2j of qs[i] */
 float or_unpack_tq2_0_block_i8(const uint8_t *blk, int8_t *out) {
     float s = or_f16_to_f32_finite(rd16(blk));
@@ -273,6 +400,11 @@ static void dequant_block_any(int q, const uint8_t *blk, float i2s_scale, float 
     case OR_Q4_K: or_dequantize_q4_k_block(blk, out); break;
     case OR_Q6_K: or_dequantize_q6_k_block(blk, out); break;
     case OR_Q5_0: or_dequantize_q5_0_block(blk, out); break; /* quant.rs:2306-2310 */
+    case OR_Q4_1: or_dequantize_q4_1_block(blk, out); break; /* quant.rs:2301-2305 */
+    case OR_Q5_1: or_dequantize_q5_1_block(blk, out); break; /* quant.rs:2311-2315 */
+    case OR_Q2_K: or_dequantize_q2_k_block(blk, out); break; /* quant.rs:2321-2325 */
+    case OR_Q3_K: or_dequantize_q3_k_block(blk, out); break; /* quant.rs:2326-2330 */
+    case OR_IQ4_NL: or_dequantize_iq4_nl_block(blk, out); break; /* quant.rs:2345-2358 */
     case OR_Q5_K: or_dequantize_q5_k_block(blk, out); break; /* quant.rs:2335-2339 */
     case OR_TQ1_0: { /* quant.rs:2359-2368 */
         int8_t t[256];
@@ -868,6 +1000,23 @@ int or_vec_dot_i2_s(float *out, size_t out_len, const or_tensor_view *w, const f
 int or_vec_dot_q5_0(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
     return vec_dot_f32_entry(OR_Q5_0, out, out_len, w, in, in_len);
 }
+/* vec_dot_q4_1 (quant.rs:2062), vec_dot_q5_1 (2081), vec_dot_q2_k (2100), vec_dot_q3_k (2119),
+ * vec_dot_iq4_nl (2138): vec_dot_generic_block (1995-2029) over the block dequantizer */
+int or_vec_dot_q4_1(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q4_1, out, out_len, w, in, in_len);
+}
+int or_vec_dot_q5_1(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q5_1, out, out_len, w, in, in_len);
+}
+int or_vec_dot_q2_k(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q2_K, out, out_len, w, in, in_len);
+}
+int or_vec_dot_q3_k(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_Q3_K, out, out_len, w, in, in_len);
+}
+int or_vec_dot_iq4_nl(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
+    return vec_dot_f32_entry(OR_IQ4_NL, out, out_len, w, in, in_len);
+}
 /* vec_dot_q5_k (quant.rs:1238-1251) -> vec_dot_q5_k_scalar (1181-1219) */
 int or_vec_dot_q5_k(float *out, size_t out_len, const or_tensor_view *w, const float *in, size_t in_len) {
     return vec_dot_f32_entry(OR_Q5_K, out, out_len, w, in, in_len);
@@ -903,9 +1052,10 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
     if (!known_quant(w->quant)) return OR_CAPABILITY_MISMATCH;
     int st = validate_matrix_view(w, rows, cols);
     if (st) return st;
-    int cps = w->quant == OR_Q6_K ? 1 : 2;
+    int cps = (w->quant == OR_Q6_K || w->quant == OR_Q3_K || w->quant == OR_Q2_K) ? 1 : 2;
     size_t k_padded = (cols + 31) / 32 * 32, sg = k_padded / 16 / cps;
-    int has_mins = w->quant == OR_Q4_K || w->quant == OR_Q5_K;
+    int has_mins = w->quant == OR_Q4_K || w->quant == OR_Q5_K || w->quant == OR_Q4_1 || w->quant == OR_Q5_1 ||
+                   w->quant == OR_Q2_K;
     if (sg_out) *sg_out = sg;
     if (has_mins_out) *has_mins_out = has_mins;
     if (cps_out) *cps_out = cps;
@@ -957,6 +1107,33 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
                         qr[256 * b + 64 * c + 32 + l] = (int8_t)(blk[16 + 32 * c + l] >> 4);
                     }
                 }
+                break;
+            }
+            case OR_Q4_1: case OR_Q5_1: { /* repack.rs:1814-1829, 1845-1860: quants always written */
+                float d, m;
+                if (w->quant == OR_Q4_1) unpack_q4_1_block_i8(blk, qr + 32 * b, &d, &m);
+                else unpack_q5_1_block_i8(blk, qr + 32 * b, &d, &m);
+                sr[b] = d;
+                mr[b] = m == 0.0f ? 0.0f : -m;
+                break;
+            }
+            case OR_IQ4_NL: { /* repack.rs:1861-1875 */
+                int8_t t[32];
+                float d = or_unpack_iq4_nl_block_i8(blk, t);
+                sr[b] = d;
+                if (d != 0.0f) memcpy(qr + 32 * b, t, 32);
+                break;
+            }
+            case OR_Q2_K: { /* repack.rs:1876-1895 */
+                float sc[16], mn[16];
+                or_unpack_q2_k_block_i8(blk, qr + 256 * b, sc, mn);
+                for (int s = 0; s < 16; s++) { sr[16 * b + s] = sc[s]; mr[16 * b + s] = mn[s]; }
+                break;
+            }
+            case OR_Q3_K: { /* repack.rs:1896-1911 */
+                float sc[16];
+                or_unpack_q3_k_block_i8(blk, qr + 256 * b, sc);
+                for (int s = 0; s < 16; s++) sr[16 * b + s] = sc[s];
                 break;
             }
             case OR_Q5_0: { /* repack.rs:1830-1843 */

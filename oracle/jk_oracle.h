@@ -1,7 +1,7 @@
 /*
  * jk_oracle.h -- CPU restatement of the jero-kernels-rvv portable scalar fallback
- * for the quantized-matmul path (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0,
- * I2_S).
+ * for the quantized-matmul path (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL, Q2_K, Q3_K, Q4_K,
+ * Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S).
  *
  * TEST INFRASTRUCTURE ONLY. This library is the oracle the HIP product library
  * (libjk.so) is compared with, and the timed CPU baseline of bench.py. It is
@@ -31,11 +31,16 @@ enum { OR_OK = 0, OR_TENSOR_BOUNDS = 1, OR_CAPABILITY_MISMATCH = 2 };
 /* GGML type ids (the reference's QuantType variants on this path). */
 enum {
     OR_Q4_0 = 2,
+    OR_Q4_1 = 3,
     OR_Q5_0 = 6,
+    OR_Q5_1 = 7,
     OR_Q8_0 = 8,
+    OR_Q2_K = 10,
+    OR_Q3_K = 11,
     OR_Q4_K = 12, /* QuantType::Q4_K_M */
     OR_Q5_K = 13,
     OR_Q6_K = 14,
+    OR_IQ4_NL = 20,
     OR_TQ1_0 = 34,
     OR_TQ2_0 = 35,
     OR_I2_S = 36
@@ -91,6 +96,14 @@ float or_unpack_q5_0_block_i8(const uint8_t *blk, int8_t *out);
 void or_dequantize_q5_0_block(const uint8_t *blk, float *out);
 void or_dequantize_q5_k_block(const uint8_t *blk, float *out);
 float or_unpack_tq1_0_block_i8(const uint8_t *blk, int8_t *out);
+void or_dequantize_q4_1_block(const uint8_t *blk, float *out);
+void or_dequantize_q5_1_block(const uint8_t *blk, float *out);
+void or_unpack_q2_k_block_i8(const uint8_t *blk, int8_t *q, float *scales, float *mins);
+void or_dequantize_q2_k_block(const uint8_t *blk, float *out);
+void or_unpack_q3_k_block_i8(const uint8_t *blk, int8_t *q, float *scales);
+void or_dequantize_q3_k_block(const uint8_t *blk, float *out);
+float or_unpack_iq4_nl_block_i8(const uint8_t *blk, int8_t *out);
+void or_dequantize_iq4_nl_block(const uint8_t *blk, float *out);
 float or_unpack_tq2_0_block_i8(const uint8_t *blk, int8_t *out);
 void or_unpack_i2_s_block_i8(const uint8_t *blk, int8_t *out);
 void or_dequantize_i2_s_block(const uint8_t *blk, float scale, float *out);
@@ -161,6 +174,16 @@ int or_vec_dot_q5_0(float *out, size_t out_len, const or_tensor_view *w, const f
                     size_t in_len);
 int or_vec_dot_q5_k(float *out, size_t out_len, const or_tensor_view *w, const float *in,
                     size_t in_len);
+int or_vec_dot_q4_1(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                    size_t in_len);
+int or_vec_dot_q5_1(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                    size_t in_len);
+int or_vec_dot_q2_k(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                    size_t in_len);
+int or_vec_dot_q3_k(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                    size_t in_len);
+int or_vec_dot_iq4_nl(float *out, size_t out_len, const or_tensor_view *w, const float *in,
+                      size_t in_len);
 
 /* ---- repacked (block-scaled i8) GEMM ---- */
 int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t *q,

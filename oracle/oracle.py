@@ -56,6 +56,7 @@ def lib() -> C.CDLL:
         h.or_unpack_tq2_0_block_i8.restype = C.c_float
         h.or_unpack_tq1_0_block_i8.restype = C.c_float
         h.or_unpack_q5_0_block_i8.restype = C.c_float
+        h.or_unpack_iq4_nl_block_i8.restype = C.c_float
         h.or_read_i2_s_trailer_scale.restype = C.c_float
         h.or_act_q8_bytes.restype = _sz
         h.or_act_q8_bytes.argtypes = [_sz, _sz]
@@ -245,7 +246,8 @@ def gemv_rows(quant: int, data: np.ndarray, rows: int, cols: int, x_blocks: np.n
 
 
 _VEC_DOT_F32 = {2: "or_vec_dot_q4_0", 8: "or_vec_dot_q8_0", 14: "or_vec_dot_q6_k", 12: "or_vec_dot_q4_k_m",
-                36: "or_vec_dot_i2_s", 6: "or_vec_dot_q5_0", 13: "or_vec_dot_q5_k"}
+                36: "or_vec_dot_i2_s", 6: "or_vec_dot_q5_0", 13: "or_vec_dot_q5_k", 3: "or_vec_dot_q4_1",
+                7: "or_vec_dot_q5_1", 10: "or_vec_dot_q2_k", 11: "or_vec_dot_q3_k", 20: "or_vec_dot_iq4_nl"}
 
 
 def vec_dot_f32(quant: int, shape, data: np.ndarray, x: np.ndarray, out_len: int) -> np.ndarray:

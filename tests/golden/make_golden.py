@@ -30,6 +30,7 @@ import oracle as O  # noqa: E402
 import refgen as R  # noqa: E402
 
 Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S = 2, 6, 8, 12, 13, 14, 34, 35, 36
+Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL = 3, 7, 10, 11, 20
 
 # quant -> (LCG weight filler of the reference's tests, weight seed, activation seed)
 CASES = {
@@ -41,10 +42,17 @@ CASES = {
     Q5_0: (R.fill_q5_0, 0x57, 0x67),
     Q5_K: (R.fill_q5_k, 0x58, 0x68),
     TQ1_0: (R.fill_tq1_0, 0x59, 0x69),
+    # formats without a quant_q8 GEMV: the construction of tests/test_repack_gemv_gemm.rs:86-270
+    Q4_1: (lambda r, c, s: R.build_synthetic(Q4_1, r, c, s), 0x5A, 0x6A),
+    Q5_1: (lambda r, c, s: R.build_synthetic(Q5_1, r, c, s), 0x5B, 0x6B),
+    Q2_K: (lambda r, c, s: R.build_synthetic(Q2_K, r, c, s), 0x5C, 0x6C),
+    Q3_K: (lambda r, c, s: R.build_synthetic(Q3_K, r, c, s), 0x5D, 0x6D),
+    IQ4_NL: (lambda r, c, s: R.build_synthetic(IQ4_NL, r, c, s), 0x5E, 0x6E),
 }
 NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", TQ2_0: "tq2_0", I2_S: "i2_s", Q5_0: "q5_0",
-         Q5_K: "q5_k", TQ1_0: "tq1_0"}
-F32_PATH = {Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, I2_S}  # formats with an f32-activation vec_dot entry
+         Q5_K: "q5_k", TQ1_0: "tq1_0", Q4_1: "q4_1", Q5_1: "q5_1", Q2_K: "q2_k", Q3_K: "q3_k", IQ4_NL: "iq4_nl"}
+F32_PATH = {Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, I2_S, Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL}  # f32-activation vec_dot
+GEMV_PATH = {Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0}  # quant_q8 GEMV
 Q8_0_ACT = (Q4_0, Q5_0, Q8_0)  # formats whose GEMV takes BlockQ8_0 activations
 ROWS, COLS, TOKENS = 8, 512, 3
 
@@ -69,10 +77,11 @@ def case(quant: int, wseed: int, xseed: int) -> dict:
     out = {"quant": np.int32(quant), "rows": np.int32(ROWS), "cols": np.int32(COLS), "wseed": np.int64(wseed),
            "xseed": np.int64(xseed), "w": w, "x": x, "X": X}
     out["deq"] = np.stack([O.dequantize_tensor_row(quant, shape, w, r, COLS) for r in range(ROWS)])
-    if quant != I2_S:
+    if quant in GEMV_PATH:
         xq = O.quantize_row_q8_0(x) if quant in Q8_0_ACT else O.quantize_row_q8_k(x)
         out["xq"] = xq.view(np.uint8).reshape(-1)
         out["y_gemv"] = O.gemv_q8(quant, shape, w, xq, ROWS)
+    if quant != I2_S:
         act = O.ActQ8(X, TOKENS, COLS)
         out["y_gemm"] = O.gemm_repacked(quant, shape, w, ROWS, COLS, act, 0, ROWS)
         out["y_gemm_rows"] = O.gemm_repacked(quant, shape, w, ROWS, COLS, act, 2, 7)

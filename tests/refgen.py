@@ -159,6 +159,59 @@ def fill_tq1_0(rows: int, cols: int, seed: int) -> np.ndarray:
     return raw
 
 
+# Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL block geometry
+_SYN_BE = {3: 32, 7: 32, 20: 32, 10: 256, 11: 256}
+_SYN_BB = {3: 20, 7: 24, 20: 18, 10: 84, 11: 110}
+
+
+def _f16(v: float) -> int:
+    return int(np.float16(v).view(np.uint16))
+
+
+def _u16b(v: int):
+    return [v & 0xFF, v >> 8]
+
+
+def build_synthetic(quant: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """build_synthetic_quant_tensor (tests/test_repack_gemv_gemm.rs:86-270) for these formats;
+    f16 bits from its f32_to_f16_bits (31-45), exact for the values used."""
+    nb = cols // _SYN_BE[quant]
+    raw = np.zeros(rows * nb * _SYN_BB[quant], np.uint8)
+    for r in range(rows):
+        for b in range(nb):
+            off = (r * nb + b) * _SYN_BB[quant]
+            blk = raw[off:off + _SYN_BB[quant]]
+            if quant == 3:
+                blk[0:2] = _u16b(_f16(0.0625 * (1.0 + ((r + b) % 4) * 0.5)))
+                blk[2:4] = _u16b(_f16(-0.25 + ((r * 3 + b) % 5) * 0.125))
+                for i in range(16):
+                    blk[4 + i] = ((r * 7 + b * 3 + i + seed) & 15) | (((r * 11 + b * 5 + i * 3 + seed) & 15) << 4)
+            elif quant == 7:
+                blk[0:2] = _u16b(_f16(0.0625 * (1.0 + ((r + b) % 3) * 0.25)))
+                blk[2:4] = _u16b(_f16(-0.25 + ((r * 2 + b * 3) % 7) * 0.0625))
+                qh = ((r * 0x517CC1B7) ^ (b * 0x27220A95) ^ seed) & 0xFFFFFFFF
+                blk[4:8] = [(qh >> (8 * i)) & 0xFF for i in range(4)]
+                for i in range(16):
+                    blk[8 + i] = ((r * 9 + b * 7 + i + seed) & 15) | (((r * 3 + b * 11 + i * 7 + seed) & 15) << 4)
+            elif quant == 10:
+                for s in range(16):
+                    blk[s] = (((r * 5 + b * 3 + s + 1) % 15 + 1) & 15) | ((((r * 3 + b * 7 + s + 2) % 13) & 15) << 4)
+                for i in range(64):
+                    blk[16 + i] = (r * 17 + b * 11 + i * 5 + seed) & 0xFF
+                blk[80:82], blk[82:84] = _u16b(_f16(0.0625)), _u16b(_f16(0.03125))
+            elif quant == 11:
+                for i in range(96):
+                    blk[i] = (r * 13 + b * 7 + i * 9 + seed) & 0xFF
+                for s in range(12):
+                    blk[96 + s] = (r * 19 + b * 23 + s * 11 + seed + 7) & 0xFF
+                blk[108:110] = _u16b(_f16(0.0625))
+            else:  # IQ4_NL
+                blk[0:2] = _u16b(_f16(0.03125 * (1.0 + ((r + b) % 4) * 0.25)))
+                for i in range(16):
+                    blk[2 + i] = ((r * 5 + b * 3 + i + seed) & 15) | (((r * 7 + b * 9 + i * 3 + seed) & 15) << 4)
+    return raw
+
+
 def cosine(a, b) -> float:
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

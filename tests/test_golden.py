@@ -20,8 +20,10 @@ import refgen as R
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0, I2_S = 2, 6, 8, 12, 13, 14, 34, 35, 36
+Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL = 3, 7, 10, 11, 20
 FILL = {Q4_0: R.fill_q4_0, Q8_0: R.fill_q8_0, Q4_K: R.fill_q4_k, Q6_K: R.fill_q6_k, TQ2_0: R.fill_tq2_0,
         Q5_0: R.fill_q5_0, Q5_K: R.fill_q5_k, TQ1_0: R.fill_tq1_0}
+FILL.update({q: (lambda r, c, s, q=q: R.build_synthetic(q, r, c, s)) for q in (Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL)})
 Q8_0_ACT = (Q4_0, Q5_0, Q8_0)
 CASES = sorted(p for p in glob.glob(os.path.join(HERE, "*.npz")) if not p.endswith("quantizers.npz"))
 
@@ -54,7 +56,7 @@ def dequant_q8_blocks(quant, xq_bytes, n):
 def test_fixtures_present():
     names = {os.path.basename(p) for p in glob.glob(os.path.join(HERE, "*.npz"))}
     assert {"q4_0.npz", "q5_0.npz", "q8_0.npz", "q4_k.npz", "q5_k.npz", "q6_k.npz", "tq1_0.npz", "tq2_0.npz",
-            "i2_s.npz", "quantizers.npz"} <= names
+            "i2_s.npz", "q4_1.npz", "q5_1.npz", "q2_k.npz", "q3_k.npz", "iq4_nl.npz", "quantizers.npz"} <= names
 
 
 @pytest.mark.parametrize("path", CASES, ids=os.path.basename)
@@ -79,6 +81,7 @@ def test_oracle_reproduces_fixture(path):
         xq = O.quantize_row_q8_0(f["x"]) if quant in Q8_0_ACT else O.quantize_row_q8_k(f["x"])
         assert np.array_equal(xq.view(np.uint8).reshape(-1), f["xq"])
         assert bits_equal(O.gemv_q8(quant, shape, w, xq, rows), f["y_gemv"])
+    if "y_gemm" in f:
         act = O.ActQ8(f["X"], f["X"].shape[0], cols)
         assert bits_equal(O.gemm_repacked(quant, shape, w, rows, cols, act, 0, rows), f["y_gemm"])
         assert bits_equal(O.gemm_repacked(quant, shape, w, rows, cols, act, 2, 7), f["y_gemm_rows"])
@@ -99,6 +102,7 @@ def test_fixture_outputs_match_float64_products(path):
         ref = deq @ dequant_q8_blocks(quant, f["xq"], cols)
         got = f["y_gemv"].astype(np.float64)
         assert np.linalg.norm(got - ref) <= 1e-5 * np.linalg.norm(ref)
+    if "y_gemm" in f:
         # per-32 activation quantization of X against the unquantized product
         ref_m = f["X"].astype(np.float64) @ deq.T
         got_m = f["y_gemm"].astype(np.float64)

@@ -21,7 +21,8 @@ CASES = sorted(p for p in glob.glob(os.path.join(HERE, "*.npz")) if not p.endswi
 GEMV = {Q4_0: jk.gemv_q4_0_q8_0, Q8_0: jk.gemv_q8_0_q8_0, Q4_K: jk.gemv_q4_k_q8_k, Q6_K: jk.gemv_q6_k_q8_k,
         TQ2_0: jk.gemv_tq2_0_q8_k, Q5_0: jk.gemv_q5_0_q8_0, Q5_K: jk.gemv_q5_k_q8_k, TQ1_0: jk.gemv_tq1_0_q8_k}
 VEC_F32 = {Q4_0: jk.vec_dot_q4_0, Q8_0: jk.vec_dot_q8_0, Q6_K: jk.vec_dot_q6_k, Q4_K: jk.vec_dot_q4_k_m,
-           I2_S: jk.vec_dot_i2_s, Q5_0: jk.vec_dot_q5_0, Q5_K: jk.vec_dot_q5_k}
+           I2_S: jk.vec_dot_i2_s, Q5_0: jk.vec_dot_q5_0, Q5_K: jk.vec_dot_q5_k, jk.Q4_1: jk.vec_dot_q4_1,
+           jk.Q5_1: jk.vec_dot_q5_1, jk.Q2_K: jk.vec_dot_q2_k, jk.Q3_K: jk.vec_dot_q3_k, jk.IQ4_NL: jk.vec_dot_iq4_nl}
 
 
 def load(path):
@@ -49,6 +50,7 @@ def test_golden_case(gpu, path):
         y = np.zeros(rows, np.float32)
         GEMV[quant](y, view, xq)
         assert bits_equal(y, f["y_gemv"]), (path, "gemv", y, f["y_gemv"])
+    if "y_gemm" in f:
         w = jk.Weight(view, rows, cols)
         m = f["X"].shape[0]
         yg = np.zeros(m * rows, np.float32)

@@ -16,8 +16,11 @@ pytestmark = pytest.mark.gpu
 
 Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, I2_S = jk.Q4_0, jk.Q8_0, jk.Q4_K, jk.Q6_K, jk.TQ2_0, jk.I2_S
 Q5_0, Q5_K, TQ1_0 = jk.Q5_0, jk.Q5_K, jk.TQ1_0
+Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL = jk.Q4_1, jk.Q5_1, jk.Q2_K, jk.Q3_K, jk.IQ4_NL
 GEMV_FORMATS = [Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, TQ1_0, TQ2_0]
-ALL_FORMATS = GEMV_FORMATS + [I2_S]
+ALL_FORMATS = GEMV_FORMATS + [I2_S, Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL]
+# device bytes per block where they differ from the GGUF bytes
+DEVICE_BLOCK_BYTES = {TQ1_0: 66, Q3_K: 112}
 
 
 def same_bits(a, b) -> bool:
@@ -162,10 +165,10 @@ def test_upload_and_dequantize_rows(gpu, quant):
     rows, cols = 19, 2048
     raw = synth.random_weights(quant, rows, cols, seed=quant, specials=True)
     w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
-    dev_quant = TQ2_0 if quant == TQ1_0 else quant  # TQ1_0 trits are held 2 bits each
+    nblk = rows * cols // jk.BLOCK_ELEMENTS[quant]
     assert w.quant == quant
-    assert w.gguf_bytes == rows * cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[quant] + jk.TRAILER_BYTES.get(quant, 0)
-    assert w.device_bytes == rows * cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[dev_quant]
+    assert w.gguf_bytes == nblk * jk.BLOCK_BYTES[quant] + jk.TRAILER_BYTES.get(quant, 0)
+    assert w.device_bytes == nblk * DEVICE_BLOCK_BYTES.get(quant, jk.BLOCK_BYTES[quant])
     dy = empty(torch, 4 * rows * cols)
     jk.dev_dequantize_rows(w, 0, rows, dy, rows * cols)
     torch.cuda.synchronize()
@@ -349,7 +352,7 @@ def test_gemv_q8_batch_validation(gpu):
 
 
 # ------------------------------------------------------------------ f32 vec_dot
-@pytest.mark.parametrize("quant", [Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, I2_S])
+@pytest.mark.parametrize("quant", list(jk.VEC_DOT_F32_FORMATS))
 @pytest.mark.parametrize("rows,cols", [(1, 256), (5, 4352), (33, 4096)])
 def test_vec_dot_f32(gpu, quant, rows, cols):
     torch = gpu
@@ -608,3 +611,33 @@ def test_new_format_validation(gpu):
     with pytest.raises(jk.TensorBoundsError):  # Q5_K is not a BitLinear format
         jk.dev_bitlinear_i8(w5, torch.zeros(256, dtype=torch.int8, device="cuda"), y[:1], 1, 256, y, 4)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("quant", [Q4_1, Q5_1, Q2_K, Q3_K, IQ4_NL, I2_S])
+def test_formats_without_q8_gemv(gpu, quant):
+    """Formats the reference offers no quant_q8 GEMV (nor BitLinear, except I2_S) for are refused
+    with the reference's error kinds, before any device work."""
+    torch = gpu
+    rows, cols = 4, 256
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], synth.gguf_weights(quant, rows, cols, seed=1)), rows, cols)
+    x = torch.zeros(cols, dtype=torch.float32, device="cuda")
+    y = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    with pytest.raises(jk.CapabilityMismatch):
+        jk.dev_gemv_q8_f32(w, x, cols, y, rows)
+    with pytest.raises(jk.CapabilityMismatch):
+        jk.dev_gemv_q8_rows(w, x, 1, y, 0, rows)
+    if quant != I2_S:
+        with pytest.raises(jk.TensorBoundsError):
+            jk.dev_bitlinear_i8(w, torch.zeros(cols, dtype=torch.int8, device="cuda"), y[:1], 1, cols, y, rows)
+    torch.cuda.synchronize()
+
+
+def test_host_tier_vec_dot_more_formats(gpu):
+    """Host-tier f32 matvec mirrors of the Q4_1 / Q5_1 / Q2_K / Q3_K / IQ4_NL entries."""
+    x = np.random.default_rng(8).standard_normal(1024).astype(np.float32)
+    for quant, fn in ((Q4_1, jk.vec_dot_q4_1), (Q5_1, jk.vec_dot_q5_1), (Q2_K, jk.vec_dot_q2_k),
+                      (Q3_K, jk.vec_dot_q3_k), (IQ4_NL, jk.vec_dot_iq4_nl)):
+        raw = synth.random_weights(quant, 7, 1024, seed=quant, specials=True)
+        f = np.zeros(7, np.float32)
+        fn(f, jk.TensorView("w", quant, [1024, 7], raw), x)
+        assert same_bits(f, O.vec_dot_f32(quant, [1024, 7], raw, x, 7)), quant
