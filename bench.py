@@ -422,6 +422,39 @@ def main() -> int:
                         log(f"  {name:28s} {us:8.2f} us  {tops:7.2f} TOPS")
                 for w in ws:
                     w.free()
+        # Repacked GEMM of every other weight format at the prefill shape (14336x4096, 512
+        # tokens; the activation quantized once beforehand), kernel-only, graph-timed over 4
+        # weight copies: compute-bound at this token count, so the copies need not exceed the cache
+        M, N, K = 512, 14336, 4096
+        xin = torch.randn(M, K, generator=gen).to(dev)
+        need = jk.act_q8_bytes(M, K)
+        store = torch.empty(need, dtype=torch.uint8, device=dev)
+        act = jk.act_q8_bind(store, need, M, K)
+        jk.dev_quantize_act_q8(xin, M, K, act)
+        y = torch.empty(M * N, dtype=torch.float32, device=dev)
+        for quant in (jk.Q4_0, jk.Q4_1, jk.Q5_0, jk.Q5_1, jk.IQ4_NL, jk.Q4_K, jk.Q5_K, jk.Q6_K, jk.Q2_K, jk.Q3_K,
+                      jk.TQ1_0):
+            data = synth.gguf_weights(quant, N, K, seed=900 + quant)
+            ws = [jk.Weight(jk.TensorView(f"g{i}", quant, (N, K), data), N, K) for i in range(4)]
+            us = graph_us(lambda i, st: jk.dev_gemm_repacked(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
+            tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            name = f"gemm_repacked {jk.QUANT_NAMES[quant]} M=512"
+            secondary[name] = {"us": round(us, 3), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                               "bound": "mfma", "workload": f"{N}x{K} weights x {M} tokens, kernel only"}
+            log(f"  {name:28s} {us:8.2f} us  {tops:7.2f} TOPS")
+            for w in ws:
+                w.free()
+        del xin, store, y
+        # f32-activation vec_dot of the other K-quants at the 4096x4096 attention shape
+        for quant in (jk.Q5_K, jk.Q2_K, jk.Q3_K):
+            rows, cols = 4096, 4096
+            ws = copies(quant, rows, cols, 950 + quant)
+            y = torch.empty(rows, dtype=torch.float32, device=dev)
+            us = graph_us(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts["x"], cols, y, rows, st), len(ws))
+            b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + 4 * cols + 4 * rows
+            hbm_line(f"vec_dot_{jk.QUANT_NAMES[quant].lower()} f32", b, us, f"{rows}x{cols}, f32 activation")
+            for w in ws:
+                w.free()
         # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
         yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
         us = graph_us(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
