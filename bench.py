@@ -5,8 +5,9 @@ of algorithmic bytes (GGUF weight bytes + Q8_K activation blocks + f32 outputs).
 is one token's decode pass over ``--layers`` layers of distinct weights (32 = the whole
 Llama-3-8B stack, 4.4 GB, far larger than the 256 MB Infinity Cache). Per layer the seven
 GEMVs (Q/K/V/O 4096-wide and gate/up 14336x4096 in Q4_K, down 4096x14336 in Q6_K) run in
-dependency order as four grouped launches -- {Q,K,V}, {O}, {gate,up}, {down} -- each
-quantizing its f32 activation to Q8_K on the device (bit-exact quantize_row_q8_k). The
+dependency order as grouped launches -- {Q,K,V}, {O}, {gate,up}, {down} -- each quantizing
+its f32 activation to Q8_K on the device (bit-exact quantize_row_q8_k); the down projection's
+input is SiLU(gate) * up of the layer's own gate / up outputs, fused into its quantizer. The
 step is captured once in a HIP graph and replayed.
 
 Also reported on the same JSON line:
@@ -88,6 +89,10 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch the step eagerly instead of a HIP graph")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the per-kernel lines of the other workloads (C1, C2, C5, vec_dot f32, quantizers)")
+    ap.add_argument("--ffn", choices=("swiglu", "synthetic"), default="synthetic",
+                    help="ffn_down input of the timed step: a fixed synthetic activation quantized to Q8_K, or "
+                         "SwiGLU of the layer's gate / up outputs fused into its Q8_K quantizer (a Llama "
+                         "feed-forward block; also reported as a secondary line)")
     ap.add_argument("--down", choices=("fused", "split"), default="split",
                     help="ffn_down activation: quantized inside the GEMV launch, or by its own launch")
     args = ap.parse_args()
@@ -151,30 +156,35 @@ def main() -> int:
         layer_jobs.append(per)
     lib = jk.lib()
 
-    def launch_stage(stage, arr, n, stream):
+    def launch_stage(stage, arr, n, stream, ffn):
         if stage == "ffn_down" and args.down == "split":
-            jk.dev_quantize_row_q8_k(acts["h"], 14336, h_q8, 56, stream)
+            if ffn == "swiglu":  # h = SiLU(gate) * up of this layer, quantized without writing h
+                jk.dev_quantize_row_q8_k_gated(jk.ACT_SWIGLU, outs["ffn_gate"], outs["ffn_up"], 14336, h_q8, 56, stream)
+            else:
+                jk.dev_quantize_row_q8_k(acts["h"], 14336, h_q8, 56, stream)
         st = lib.jk_gemv_q8_batch(jk._vp(stream), arr, jk._sz(n))
         if st != 0:
             raise jk.K3Error(lib.jk_last_error().decode())
 
-    def run_layers(stream):
+    def run_layers(stream, ffn=args.ffn):
         for per in layer_jobs:
             for stage, arr, n in per:
-                launch_stage(stage, arr, n, stream)
+                launch_stage(stage, arr, n, stream, ffn)
 
-    graph = None
-    if not args.no_graph:
+    def capture(ffn):
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            run_layers(side.cuda_stream)  # warm-up outside capture
+            run_layers(side.cuda_stream, ffn)  # warm-up outside capture
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run_layers(torch.cuda.current_stream().cuda_stream)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run_layers(torch.cuda.current_stream().cuda_stream, ffn)
         torch.cuda.synchronize()
+        return g
+
+    graph = None if args.no_graph else capture(args.ffn)
 
     def step():
         if graph is not None:
@@ -212,13 +222,13 @@ def main() -> int:
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for per in layer_jobs:
-                launch_stage(stage, per[si][1], per[si][2], side.cuda_stream)
+                launch_stage(stage, per[si][1], per[si][2], side.cuda_stream, args.ffn)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
             cs = torch.cuda.current_stream().cuda_stream
             for per in layer_jobs:
-                launch_stage(stage, per[si][1], per[si][2], cs)
+                launch_stage(stage, per[si][1], per[si][2], cs, args.ffn)
         g.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -307,6 +317,27 @@ def main() -> int:
     # a HIP graph and timed with HIP events on the capturing stream (per-launch time includes
     # the graph's inter-launch gap). Bytes are algorithmic (weight bytes + activation + output).
     secondary = {}
+    if not args.no_secondary and graph is not None:
+        # The same step with ffn_down's input computed as in a Llama feed-forward block:
+        # SwiGLU(gate, up) of the layer's own outputs, fused into the Q8_K quantizer.
+        other = "swiglu" if args.ffn == "synthetic" else "synthetic"
+        g2 = capture(other)
+        for _ in range(args.warmup):
+            g2.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g2.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms2 = e0.elapsed_time(e1) / args.steps
+        del g2
+        secondary[f"decode step, ffn_down input {other}"] = {
+            "ms_per_step": round(ms2, 5), "gbs": round(step_bytes / (ms2 * 1e-3) / 1e9, 1),
+            "workload": f"the headline step ({args.layers} layers) with ffn_down's Q8_K input "
+                        + ("SwiGLU(gate, up) fused into its quantizer" if other == "swiglu" else "synthetic")}
+        log(f"  decode step, ffn_down input {other}: {ms2:.4f} ms/step")
     if not args.no_secondary:
         def graph_us(launch, n, reps=5):
             side = torch.cuda.Stream()
@@ -455,6 +486,28 @@ def main() -> int:
             hbm_line(f"vec_dot_{jk.QUANT_NAMES[quant].lower()} f32", b, us, f"{rows}x{cols}, f32 activation")
             for w in ws:
                 w.free()
+        # Greedy lm_head: Q6_K 128256 x 4096 GEMV with argmax_f32 fused into the launch, against
+        # the GEMV followed by a separate argmax launch (the logits written and read back)
+        rows, cols = 128256, 4096
+        ws_lm = copies(jk.Q6_K, rows, cols, 990)
+        xq = torch.empty(cols // 256 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
+        jk.dev_quantize_row_q8_k(acts["x"], cols, xq, cols // 256)
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        amw = torch.empty(jk.argmax_workspace_bytes(rows), dtype=torch.uint8, device=dev)
+        idx = torch.empty(1, dtype=torch.int32, device=dev)
+        b = gemv_bytes(jk.Q6_K, rows, cols, jk)
+        us = graph_us(lambda i, st: jk.dev_gemv_q8_argmax(ws_lm[i % len(ws_lm)], xq, None, cols // 256, None, idx, amw, st),
+                      len(ws_lm))
+        hbm_line("lm_head Q6_K gemv+argmax", b - 4 * rows, us, f"{rows}x{cols}, fused argmax, no logits written")
+
+        def two(i, st):
+            jk.dev_gemv_q8(ws_lm[i % len(ws_lm)], xq, cols // 256, y, rows, st)
+            jk.dev_argmax_f32(y, rows, idx, amw, st)
+
+        us = graph_us(two, len(ws_lm))
+        hbm_line("lm_head Q6_K gemv, argmax", b + 4 * rows, us, f"{rows}x{cols}, logits written and re-read")
+        for w in ws_lm:
+            w.free()
         # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
         yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
         us = graph_us(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
@@ -531,6 +584,8 @@ def main() -> int:
                    "layers": args.layers, "hidden": 4096, "ffn": 14336, "kv_rows": 1024,
                    "bytes_per_step": step_bytes, "launch": "eager" if graph is None else "hip_graph",
                    "launches_per_layer": 4 + (args.down == "split"), "down_activation": args.down,
+                   "ffn_down_input": "SwiGLU(gate, up) fused into its Q8_K quantizer" if args.ffn == "swiglu"
+                   else "synthetic",
                    "parallelism": "single_gpu"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "decode_tok_s_equiv": round(1e3 / ms_per_step * args.layers / 32, 1),

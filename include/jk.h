@@ -230,6 +230,43 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
 jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
                            size_t y_len, size_t row_begin, size_t row_end);
 
+/* --------------------------------- the step after the products (epilogues) */
+/* Gated activations of a feed-forward block: out = act(gate) * up elementwise. */
+typedef enum jk_act {
+    JK_ACT_SWIGLU = 1, /* swiglu_f32 (swiglu.rs:62-121): gate / (1 + exp(-gate)) * up, 0 below -20, gate above 20 */
+    JK_ACT_RELU2 = 2   /* relu_squared_gate_f32 (lib.rs:1111-1147): max(gate, 0)^2 * up */
+} jk_act;
+/* swiglu_f32 (swiglu.rs:62), relu_squared_gate_f32 (lib.rs:1111) over n device values. SwiGLU
+ * uses the device's single-precision exp: results agree with the reference within the
+ * reference's own tolerance for its vector path (max(1e-6, 1e-5 |y|)); ReLU^2 is bit-exact. */
+jk_status jk_swiglu_f32(jk_stream s, const float *gate, const float *up, size_t n, float *out);
+jk_status jk_relu_squared_gate_f32(jk_stream s, const float *gate, const float *up, size_t n, float *out);
+/* The activation fused into the next product's activation quantizer: quantize_row_q8_k
+ * (quant_q8.rs:576) / QuantizedActQ8::quantize_into (repack.rs:542) of act(gate, up), without
+ * writing the intermediate. Identical to jk_swiglu_f32 / jk_relu_squared_gate_f32 followed by
+ * jk_quantize_row_q8_k / jk_quantize_act_q8 (no reference counterpart for the fusion itself). */
+jk_status jk_quantize_row_q8_k_gated(jk_stream s, int act, const float *gate, const float *up, size_t n,
+                                     jk_block_q8k *out, size_t out_blocks);
+jk_status jk_quantize_act_q8_gated(jk_stream s, int act, const float *gate, const float *up, size_t m, size_t k,
+                                   const jk_act_q8 *act_q8);
+/* argmax_f32 (lib.rs:662, scalar recipe 555-568): *index = the lowest index of the largest
+ * non-NaN value, -1 when x is empty or all NaN (Option::None). The device workspace holds one
+ * 8-byte partial result per workgroup: at least jk_argmax_workspace_bytes(n) bytes, 8-byte
+ * aligned, needing no initialization (each call overwrites what it reads). Calls that share a
+ * workspace must not overlap (same stream, or synchronized). */
+size_t jk_argmax_workspace_bytes(size_t n);
+jk_status jk_argmax_f32(jk_stream s, const float *x, size_t n, int32_t *index, void *workspace,
+                        size_t workspace_bytes);
+/* A quant_q8 GEMV (as jk_gemv_q8_f32 with x_f32, or the format's jk_gemv_* with caller blocks
+ * x_q8 of x_len blocks) with argmax_f32 of its output fused into the GEMV's store phase: each
+ * workgroup reduces the rows it wrote and one small launch after it reduces the workgroups, so
+ * *index = argmax of y, computed from the same bits; y may be NULL when only the index is wanted
+ * (a greedy lm_head step). Exactly one of x_q8 / x_f32 is set; x_len counts its blocks or
+ * values. The workspace is as for jk_argmax_f32 with n = the weight's rows. No single reference
+ * function corresponds: gemv_* followed by argmax_f32. */
+jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
+                            float *y, int32_t *index, void *workspace, size_t workspace_bytes);
+
 /* -------------------------------------------------------------- BitLinear */
 /* bitlinear_i8_rvv (ime.rs:882-938) applied to m tokens: y[m][rows] from act[m][k]
  * and one f32 scale per token (TQ1_0, TQ2_0, I2_S and Q8_0 weights). */
@@ -283,6 +320,13 @@ jk_status jk_host_dequantize_tensor_row(const jk_tensor_view *w, size_t row, flo
  * QuantizedActQ8 semantics, then the repacked GEMM; out[m][row_end - row_begin]. */
 jk_status jk_host_gemm_repacked_f32(float *out, size_t out_len, const jk_weight *w, const float *input,
                                    size_t m, size_t row_begin, size_t row_end);
+/* swiglu_f32 (swiglu.rs:62), relu_squared_gate_f32 (lib.rs:1111), argmax_f32 (lib.rs:662;
+ * *index = -1 for None) on host slices. */
+jk_status jk_host_swiglu_f32(float *out, size_t out_len, const float *gate, size_t gate_len, const float *up,
+                             size_t up_len);
+jk_status jk_host_relu_squared_gate_f32(float *out, size_t out_len, const float *gate, size_t gate_len,
+                                        const float *up, size_t up_len);
+jk_status jk_host_argmax_f32(const float *x, size_t n, int64_t *index);
 /* bitlinear_i8_rvv (ime.rs:882-938). */
 jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view *w, const int8_t *act,
                                size_t act_len, float act_scale);

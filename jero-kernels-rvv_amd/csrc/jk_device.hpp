@@ -202,4 +202,61 @@ __device__ __forceinline__ float fold_wave(float acc, float v, float *red) {
     return acc;
 }
 
+// ------------------------------------------------------------ gated activations
+// swiglu_f32_scalar (swiglu.rs:98-121) and relu_squared_gate_scalar (lib.rs:1140-1147) of one
+// element; ACT 0 passes g through. expf is the library's single-precision exponential.
+constexpr int kActNone = 0, kActSwiglu = 1, kActRelu2 = 2;
+template <int ACT>
+__device__ __forceinline__ float gated(float g, float u) {
+    if constexpr (ACT == kActSwiglu) {
+        const float silu = g < -20.0f ? 0.0f : (g > 20.0f ? g : g / (1.0f + expf(-g)));
+        return silu * u;
+    } else if constexpr (ACT == kActRelu2) {
+        const float relu = g > 0.0f ? g : 0.0f;
+        return relu * relu * u;
+    } else {
+        return g;
+    }
+}
+
+// ------------------------------------------------------------ argmax keys
+// argmax_f32_scalar (lib.rs:555-568) as a maximum over 64-bit keys: the high word orders the
+// values (sign-magnitude bits mapped to an unsigned order, -0.0 folded onto +0.0 because the
+// two compare equal), the low word is ~index so that among equal values the lowest index has
+// the largest key. NaN maps to 0, below every value's key (-inf's key is 0x007FFFFF << 32).
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    if (__builtin_isnan(v)) return 0ull;
+    const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+__device__ __forceinline__ int argmax_index(unsigned long long key) {
+    return key == 0ull ? -1 : (int)(0xFFFFFFFFu - (uint32_t)key);
+}
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long t = __shfl_xor(k, o, 64);
+        k = t > k ? t : k;
+    }
+    return k;
+}
+
+// Workgroup maximum of every thread's key, stored by thread 0 to *slot (plain store: the slots
+// of a launch are reduced by the next kernel on the stream, after this launch has completed --
+// no device-scope atomics or fences, which on this part would serialize across the XCDs' L2s).
+// Every thread of the workgroup must call it. s_keys: one LDS slot per wave; nw waves.
+__device__ __forceinline__ void argmax_store_wg(unsigned long long key, unsigned long long *slot,
+                                                unsigned long long *s_keys, int nw) {
+    key = wave_max_key(key);
+    const int t = threadIdx.x;
+    if ((t & 63) == 0) s_keys[t >> 6] = key;
+    __syncthreads();
+    if (t == 0) {
+        unsigned long long k = 0ull;
+        for (int i = 0; i < nw; ++i) k = s_keys[i] > k ? s_keys[i] : k;
+        *slot = k;
+    }
+}
+
 }  // namespace jk

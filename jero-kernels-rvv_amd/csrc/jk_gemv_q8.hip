@@ -651,12 +651,24 @@ gemv_q8_group_kernel(GemvGroup grp) {
         wk.load(B, w, bd ? ua : ub, bd ? ia : ib, bd);
     }
 
-    // 5. results out of the LDS slots
+    // 5. results out of the LDS slots (and, for an argmax job, the key of each result row)
     wave_lds_sync();
     const int wr_lane = wk.writer();
+    unsigned long long key = 0ull;
     for (int u = u0, k = 0; u < wk.units; u += wk.stride, ++k) {
         const int row = wk.row_of(u);
-        if (row < wk.r1 && wk.p == wr_lane) job.y[row - wk.r0] = slot[k * 64 + lane];
+        if (row < wk.r1 && wk.p == wr_lane) {
+            const float v = slot[k * 64 + lane];
+            if (job.y) job.y[row - wk.r0] = v;
+            if (job.am_slots) {
+                const unsigned long long kk = argmax_key(v, (uint32_t)(row - wk.r0));
+                key = kk > key ? kk : key;
+            }
+        }
+    }
+    if (job.am_slots) {
+        __shared__ unsigned long long s_keys[NW];
+        argmax_store_wg(key, job.am_slots + ((int)blockIdx.x - job.wg0), s_keys, NW);
     }
 }
 
@@ -738,12 +750,23 @@ gemv_q8_fast_kernel(GemvGroup grp) {
         if (q + 2 < QPW) load_unit(q + 2, W[q & 1]);
     }
 
-    // 4. stores
+    // 4. stores (and, for an argmax job, the key of each result row)
     const int writer = LPR == 16 ? 15 : 0;
+    unsigned long long key = 0ull;
 #pragma unroll
     for (int q = 0; q < QPW; ++q) {
         const int row = r0 + (base + NW * q) * RPU + sub;
-        if (base + NW * q < units && row < r1 && p == writer) job.y[row - r0] = out[q];
+        if (base + NW * q < units && row < r1 && p == writer) {
+            if (job.y) job.y[row - r0] = out[q];
+            if (job.am_slots) {
+                const unsigned long long kk = argmax_key(out[q], (uint32_t)(row - r0));
+                key = kk > key ? kk : key;
+            }
+        }
+    }
+    if (job.am_slots) {
+        __shared__ unsigned long long s_keys[NW];
+        argmax_store_wg(key, job.am_slots + ((int)blockIdx.x - job.wg0), s_keys, NW);
     }
 }
 
@@ -751,7 +774,8 @@ gemv_q8_fast_kernel(GemvGroup grp) {
 // Activations read from global memory (matrices whose activation exceeds the LDS budget).
 template <int Q>
 __global__ __launch_bounds__(256) void gemv_q8_global_kernel(WeightDev w, const void *__restrict__ x,
-                                                             float *__restrict__ y, int r0, int r1) {
+                                                             float *__restrict__ y, int r0, int r1,
+                                                             unsigned long long *am_slots) {
     const int p = threadIdx.x & 15;
     const int row = r0 + (int)((blockIdx.x * 256u + threadIdx.x) >> 4);
     const bool active = row < r1;
@@ -771,7 +795,12 @@ __global__ __launch_bounds__(256) void gemv_q8_global_kernel(WeightDev w, const 
         }
         acc = chain_add(acc, v);
     }
-    if (active && p == 15) y[row - r0] = acc;
+    if (active && p == 15 && y) y[row - r0] = acc;
+    if (am_slots) {
+        __shared__ unsigned long long s_keys[4];
+        argmax_store_wg(active && p == 15 ? argmax_key(acc, (uint32_t)(row - r0)) : 0ull, am_slots + blockIdx.x, s_keys,
+                        4);
+    }
 }
 
 // ------------------------------------------------------------------ launchers
@@ -804,6 +833,13 @@ static int cu_count() {
     return n;
 }
 
+// The argmax of each argmax job of a launched group: reduce its workgroups' keys.
+static jk_status launch_group_argmax(hipStream_t s, const GemvGroup &g) {
+    for (int i = 0; i < g.njobs; ++i)
+        if (g.job[i].am_slots) JK_TRY(launch_argmax_slots(s, g.job[i].am_slots, g.job[i].nwg, g.job[i].am_index));
+    return JK_OK;
+}
+
 template <int Q, int LPR, bool F32, int NW>
 static jk_status launch_group_run(hipStream_t s, GemvGroup &g, size_t lds) {
     // (lds: the staged activation; the result slots are appended below)
@@ -827,7 +863,8 @@ static jk_status launch_group_run(hipStream_t s, GemvGroup &g, size_t lds) {
     }
     for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
     hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * NW), lds, s, g);
-    return check_launch("gemv_q8_group_kernel");
+    JK_TRY(check_launch("gemv_q8_group_kernel"));
+    return launch_group_argmax(s, g);
 }
 
 template <int Q, int LPR, bool F32, int NW, int QPW>
@@ -843,7 +880,8 @@ static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds, int up
     }
     for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
     hipLaunchKernelGGL((gemv_q8_fast_kernel<Q, LPR, F32, NW, QPW>), dim3((unsigned)wgs), dim3(64 * NW), lds, s, g);
-    return check_launch("gemv_q8_fast_kernel");
+    JK_TRY(check_launch("gemv_q8_fast_kernel"));
+    return launch_group_argmax(s, g);
 }
 
 // Fast-kernel launch. Measured on MI355X: 8-wave workgroups with one unit per wave (about
@@ -873,9 +911,11 @@ static jk_status launch_group_q(hipStream_t s, const GemvJob *jobs, int n) {
             const GemvJob &j = jobs[i];
             if (j.xf) return fail(JK_CAPABILITY_MISMATCH, "gemv: f32 activations need K <= %d",
                                   kMaxLdsX / T::XB * T::XE);
-            hipLaunchKernelGGL(gemv_q8_global_kernel<Q>, dim3((unsigned)((j.r1 - j.r0 + 15) / 16)), dim3(256), 0, s,
-                               j.w, j.xq, j.y, j.r0, j.r1);
+            const int nwg = (j.r1 - j.r0 + 15) / 16;
+            hipLaunchKernelGGL(gemv_q8_global_kernel<Q>, dim3((unsigned)nwg), dim3(256), 0, s, j.w, j.xq, j.y, j.r0,
+                               j.r1, j.am_slots);
             JK_TRY(check_launch("gemv_q8_global_kernel"));
+            if (j.am_slots) JK_TRY(launch_argmax_slots(s, j.am_slots, nwg, j.am_index));
         }
         return JK_OK;
     }

@@ -3,6 +3,7 @@
 // Each call validates exactly as the reference entry it mirrors, then stages its
 // operands on the current device, runs the device-tier kernel, copies the result back
 // and synchronizes. Engines that keep weights resident use the device tier instead.
+#include <limits.h>
 #include <string.h>
 
 #include <vector>
@@ -270,6 +271,50 @@ jk_status jk_host_gemm_repacked_f32(float *out, size_t out_len, const jk_weight 
     JK_TRY(launch_quantize_act_q8(nullptr, (const float *)dx.p, act));
     JK_TRY(launch_gemm_repacked(nullptr, w->dev, act, (float *)dy.p, (int)r0, (int)r1));
     return d2h(out, dy.p, out_len * sizeof(float));
+}
+
+// swiglu_f32 (swiglu.rs:62) / relu_squared_gate_f32 (lib.rs:1111) on host slices, with the
+// reference's length check (validate_gated_activation_args, swiglu.rs:33-52).
+static jk_status host_gated(int act, float *out, size_t out_len, const float *gate, size_t gate_len, const float *up,
+                            size_t up_len) {
+    if (gate_len == 0 || out_len != gate_len || up_len != gate_len)
+        return fail(JK_TENSOR_BOUNDS, "dimension mismatch: gate=%zu, up=%zu, out=%zu", gate_len, up_len, out_len);
+    if (!out || !gate || !up) return fail(JK_TENSOR_BOUNDS, "null pointer");
+    const size_t b = gate_len * sizeof(float);
+    DevBuf dg, du, dy;
+    JK_TRY(dg.alloc(b));
+    JK_TRY(du.alloc(b));
+    JK_TRY(dy.alloc(b));
+    JK_TRY(h2d(dg.p, gate, b));
+    JK_TRY(h2d(du.p, up, b));
+    JK_TRY(launch_gated(nullptr, act, (const float *)dg.p, (const float *)du.p, gate_len, (float *)dy.p));
+    return d2h(out, dy.p, b);
+}
+
+jk_status jk_host_swiglu_f32(float *out, size_t out_len, const float *gate, size_t gate_len, const float *up,
+                             size_t up_len) {
+    return host_gated(JK_ACT_SWIGLU, out, out_len, gate, gate_len, up, up_len);
+}
+
+jk_status jk_host_relu_squared_gate_f32(float *out, size_t out_len, const float *gate, size_t gate_len,
+                                        const float *up, size_t up_len) {
+    return host_gated(JK_ACT_RELU2, out, out_len, gate, gate_len, up, up_len);
+}
+
+// argmax_f32 (lib.rs:662): *index = -1 for None.
+jk_status jk_host_argmax_f32(const float *x, size_t n, int64_t *index) {
+    if (!index || (n && !x)) return fail(JK_TENSOR_BOUNDS, "argmax: null pointer");
+    if (n > (size_t)INT32_MAX) return fail(JK_TENSOR_BOUNDS, "argmax: %zu values exceed the int32 index range", n);
+    DevBuf dx, dws, di;
+    JK_TRY(dx.alloc(n * sizeof(float)));
+    JK_TRY(dws.alloc(argmax_ws_bytes(n)));
+    JK_TRY(di.alloc(sizeof(int32_t)));
+    JK_TRY(h2d(dx.p, x, n * sizeof(float)));
+    JK_TRY(launch_argmax(nullptr, (const float *)dx.p, n, (int32_t *)di.p, dws.p));
+    int32_t idx = -1;
+    JK_TRY(d2h(&idx, di.p, sizeof idx));
+    *index = idx;
+    return JK_OK;
 }
 
 // bitlinear_i8_rvv (ime.rs:882-938) with validate_bitlinear_dimensions (660-763).

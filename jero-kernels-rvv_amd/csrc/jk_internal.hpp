@@ -112,7 +112,9 @@ struct GemvJob {
     WeightDev w;
     const void *xq;
     const float *xf;
-    float *y;
+    float *y;                       // may be null when am_slots is set (argmax only)
+    unsigned long long *am_slots;   // argmax of the job's outputs: one key per workgroup, or null
+    int32_t *am_index;              // where the reduction of the slots writes the index
     int r0, r1, wg0, nwg;
     int upg;  // units per workgroup (fast kernel)
     int pad;
@@ -169,6 +171,16 @@ jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1,
 jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk_block_q8_0 *out);
 jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk_block_q8k *out);
 jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 &a);
+// act: 0 none, 1 SwiGLU, 2 ReLU^2 of (x, up) -- the jk_act values.
+jk_status launch_quantize_q8_k_gated(hipStream_t s, int act, const float *x, const float *up, size_t nblocks,
+                                     jk_block_q8k *out);
+jk_status launch_quantize_act_q8_gated(hipStream_t s, int act, const float *x, const float *up, const jk_act_q8 &a);
+jk_status launch_gated(hipStream_t s, int act, const float *gate, const float *up, size_t n, float *out);
+jk_status launch_argmax(hipStream_t s, const float *x, size_t n, int32_t *index, void *ws);
+// Reduces n argmax keys (one per workgroup of a finished launch) to the index.
+jk_status launch_argmax_slots(hipStream_t s, const unsigned long long *slots, int n, int32_t *index);
+// Workspace bytes for an argmax over n values (standalone) or n output rows (fused GEMV).
+size_t argmax_ws_bytes(size_t n);
 jk_status launch_absmax_i8(hipStream_t s, const float *x, const float *norm_w, size_t m, size_t k,
                            float eps, int8_t *q, float *scales);
 jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1);

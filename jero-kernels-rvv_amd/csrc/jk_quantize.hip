@@ -33,16 +33,19 @@ jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk
 }
 
 // quantize_block_q8_k_scalar (quant_q8.rs:447-475): one wave per block, 4 elements per lane,
-// bsums[j] = sum of the 16 quants of lanes 4j..4j+3.
-__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restrict__ x, size_t nblocks,
-                                                            jk_block_q8k *__restrict__ out) {
+// bsums[j] = sum of the 16 quants of lanes 4j..4j+3. With ACT != 0 the input element is the
+// gated activation gated<ACT>(x[i], up[i]) (SwiGLU or ReLU^2), computed in the load.
+template <int ACT>
+__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restrict__ x, const float *__restrict__ up,
+                                                            size_t nblocks, jk_block_q8k *__restrict__ out) {
     const size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int l = threadIdx.x & 63;
     const bool live = blk < nblocks;
     float v[4];
     float a = 0.0f;
     for (int i = 0; i < 4; ++i) {
-        v[i] = live ? x[blk * 256 + 4 * l + i] : 0.0f;
+        const size_t e = blk * 256 + 4 * l + i;
+        v[i] = live ? gated<ACT>(x[e], ACT ? up[e] : 0.0f) : 0.0f;
         a = fmaxf(a, __builtin_isfinite(v[i]) ? fabsf(v[i]) : 0.0f);
     }
     const float amax = wave_max<64>(a);
@@ -64,8 +67,15 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restr
 }
 
 jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk_block_q8k *out) {
-    const size_t threads = nblocks * 64;
-    hipLaunchKernelGGL(quantize_q8_k_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, nblocks, out);
+    return launch_quantize_q8_k_gated(s, kActNone, x, nullptr, nblocks, out);
+}
+
+jk_status launch_quantize_q8_k_gated(hipStream_t s, int act, const float *x, const float *up, size_t nblocks,
+                                     jk_block_q8k *out) {
+    const dim3 grid((unsigned)((nblocks * 64 + 255) / 256)), block(256);
+    if (act == kActSwiglu) hipLaunchKernelGGL(quantize_q8_k_kernel<kActSwiglu>, grid, block, 0, s, x, up, nblocks, out);
+    else if (act == kActRelu2) hipLaunchKernelGGL(quantize_q8_k_kernel<kActRelu2>, grid, block, 0, s, x, up, nblocks, out);
+    else hipLaunchKernelGGL(quantize_q8_k_kernel<kActNone>, grid, block, 0, s, x, up, nblocks, out);
     return check_launch("quantize_q8_k_kernel");
 }
 
@@ -92,27 +102,35 @@ __device__ __forceinline__ float lane_chain(const float (&v)[4], float init) {
 // block (zero block below 1e-30), scale = absmax / 127, q = round(x * 127 / absmax) clamped
 // to +-127, and the sequential sum from +0.0; the two x_sums_16 entries are Rust `.sum()`
 // folds from -0.0; super_scales_256 (repack.rs:612-621) is the max of the superblock's
-// block scales from 0.0. Elements past k (the zero-padded tail) take part as +0.0.
-template <bool V4>
-__global__ __launch_bounds__(256) void quantize_act_q8_kernel(const float *__restrict__ x, jk_act_q8 a) {
+// block scales from 0.0. Elements past k (the zero-padded tail) take part as +0.0. With ACT != 0
+// the element is the gated activation gated<ACT>(x, up) of the two input rows.
+template <bool V4, int ACT>
+__global__ __launch_bounds__(256) void quantize_act_q8_kernel(const float *__restrict__ x, const float *__restrict__ up,
+                                                              jk_act_q8 a) {
     const size_t wv = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     if (wv >= a.m * a.sb256) return;  // wave-uniform
     const int l = (int)(threadIdx.x & 63);
     const size_t row = wv / a.sb256, sb = wv % a.sb256;
     const size_t e0 = sb * 256 + 4 * (size_t)l;
     const float *src = x + row * a.k;
+    const float *usrc = ACT ? up + row * a.k : nullptr;
     float v[4];
     if constexpr (V4) {
         if (e0 + 3 < a.k) {
             const float4 f = *reinterpret_cast<const float4 *>(src + e0);
             v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            if constexpr (ACT != kActNone) {
+                const float4 u = *reinterpret_cast<const float4 *>(usrc + e0);
+                v[0] = gated<ACT>(v[0], u.x); v[1] = gated<ACT>(v[1], u.y);
+                v[2] = gated<ACT>(v[2], u.z); v[3] = gated<ACT>(v[3], u.w);
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = e0 + i < a.k ? src[e0 + i] : 0.0f;
+            for (int i = 0; i < 4; ++i) v[i] = e0 + i < a.k ? gated<ACT>(src[e0 + i], ACT ? usrc[e0 + i] : 0.0f) : 0.0f;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = e0 + i < a.k ? src[e0 + i] : 0.0f;
+        for (int i = 0; i < 4; ++i) v[i] = e0 + i < a.k ? gated<ACT>(src[e0 + i], ACT ? usrc[e0 + i] : 0.0f) : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = __builtin_isfinite(v[i]) ? v[i] : 0.0f;
@@ -144,11 +162,23 @@ __global__ __launch_bounds__(256) void quantize_act_q8_kernel(const float *__res
     if (l == 0) a.super256[row * a.sb256 + sb] = mx;
 }
 
-jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 &a) {
+template <int ACT>
+static void launch_act_q8(hipStream_t s, const float *x, const float *up, const jk_act_q8 &a) {
     const size_t waves = a.m * a.sb256;
     const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
-    if ((a.k & 3) == 0 && ((uintptr_t)x & 15) == 0) hipLaunchKernelGGL(quantize_act_q8_kernel<true>, grid, block, 0, s, x, a);
-    else hipLaunchKernelGGL(quantize_act_q8_kernel<false>, grid, block, 0, s, x, a);
+    const bool v4 = (a.k & 3) == 0 && ((uintptr_t)x & 15) == 0 && (!ACT || ((uintptr_t)up & 15) == 0);
+    if (v4) hipLaunchKernelGGL((quantize_act_q8_kernel<true, ACT>), grid, block, 0, s, x, up, a);
+    else hipLaunchKernelGGL((quantize_act_q8_kernel<false, ACT>), grid, block, 0, s, x, up, a);
+}
+
+jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 &a) {
+    return launch_quantize_act_q8_gated(s, kActNone, x, nullptr, a);
+}
+
+jk_status launch_quantize_act_q8_gated(hipStream_t s, int act, const float *x, const float *up, const jk_act_q8 &a) {
+    if (act == kActSwiglu) launch_act_q8<kActSwiglu>(s, x, up, a);
+    else if (act == kActRelu2) launch_act_q8<kActRelu2>(s, x, up, a);
+    else launch_act_q8<kActNone>(s, x, up, a);
     return check_launch("quantize_act_q8_kernel");
 }
 

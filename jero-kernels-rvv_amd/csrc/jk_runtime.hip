@@ -3,6 +3,7 @@
 //
 // Validation mirrors the reference validators cited at each entry and always runs
 // before any device work is enqueued (fail closed).
+#include <limits.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -492,6 +493,90 @@ jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t
     if (!x) return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: null input");
     jk_gemv_job j = {w, nullptr, x, y, 0, (size_t)w->dev.rows};
     return jk_gemv_q8_batch(s, &j, 1);
+}
+
+// --------------------------------------------------------------- epilogues
+// validate_gated_activation_args (swiglu.rs:33-52; lib.rs:1112-1125 likewise)
+static jk_status gated_check(const char *name, const float *gate, const float *up, size_t n, const void *out) {
+    if (n == 0) return fail(JK_TENSOR_BOUNDS, "%s: dimension mismatch: gate=0", name);
+    if (!gate || !up || !out) return fail(JK_TENSOR_BOUNDS, "%s: null pointer", name);
+    return JK_OK;
+}
+
+jk_status jk_swiglu_f32(jk_stream s, const float *gate, const float *up, size_t n, float *out) {
+    JK_TRY(gated_check("swiglu", gate, up, n, out));
+    return launch_gated((hipStream_t)s, JK_ACT_SWIGLU, gate, up, n, out);
+}
+
+jk_status jk_relu_squared_gate_f32(jk_stream s, const float *gate, const float *up, size_t n, float *out) {
+    JK_TRY(gated_check("relu_squared", gate, up, n, out));
+    return launch_gated((hipStream_t)s, JK_ACT_RELU2, gate, up, n, out);
+}
+
+jk_status jk_quantize_row_q8_k_gated(jk_stream s, int act, const float *gate, const float *up, size_t n,
+                                     jk_block_q8k *out, size_t out_blocks) {
+    if (act != JK_ACT_SWIGLU && act != JK_ACT_RELU2)
+        return fail(JK_CAPABILITY_MISMATCH, "quantize_row_q8_k_gated: unknown activation %d", act);
+    JK_TRY(gated_check("quantize_row_q8_k_gated", gate, up, n, out));
+    if (n % 256)
+        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: input length %zu must be a positive multiple of 256", n);
+    if (out_blocks != n / 256)
+        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: output block count %zu != expected %zu", out_blocks, n / 256);
+    return launch_quantize_q8_k_gated((hipStream_t)s, act, gate, up, n / 256, out);
+}
+
+jk_status jk_quantize_act_q8_gated(jk_stream s, int act, const float *gate, const float *up, size_t m, size_t k,
+                                   const jk_act_q8 *a) {
+    if (act != JK_ACT_SWIGLU && act != JK_ACT_RELU2)
+        return fail(JK_CAPABILITY_MISMATCH, "quantize_act_q8_gated: unknown activation %d", act);
+    if (!a || a->m != m || a->k != k || m == 0 || k == 0)
+        return fail(JK_TENSOR_BOUNDS, "quantize_act_q8_gated: activation buffer does not hold [%zu, %zu]", m, k);
+    if (!gate || !up) return fail(JK_TENSOR_BOUNDS, "quantize_act_q8_gated: null input");
+    return launch_quantize_act_q8_gated((hipStream_t)s, act, gate, up, *a);
+}
+
+size_t jk_argmax_workspace_bytes(size_t n) { return argmax_ws_bytes(n); }
+
+static jk_status argmax_ws_check(const char *what, const void *ws, size_t ws_bytes, size_t n) {
+    if (!ws) return fail(JK_TENSOR_BOUNDS, "%s: null workspace", what);
+    if ((uintptr_t)ws % 8) return fail(JK_TENSOR_BOUNDS, "%s: workspace must be 8-byte aligned", what);
+    if (ws_bytes < argmax_ws_bytes(n))
+        return fail(JK_TENSOR_BOUNDS, "%s: workspace of %zu bytes < %zu needed for %zu values", what, ws_bytes,
+                    argmax_ws_bytes(n), n);
+    return JK_OK;
+}
+
+jk_status jk_argmax_f32(jk_stream s, const float *x, size_t n, int32_t *index, void *ws, size_t ws_bytes) {
+    if (!index || (n && !x)) return fail(JK_TENSOR_BOUNDS, "argmax: null pointer");
+    if (n > (size_t)INT32_MAX) return fail(JK_TENSOR_BOUNDS, "argmax: %zu values exceed the int32 index range", n);
+    JK_TRY(argmax_ws_check("argmax", ws, ws_bytes, n));
+    return launch_argmax((hipStream_t)s, x, n, index, ws);
+}
+
+jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
+                            float *y, int32_t *index, void *ws, size_t ws_bytes) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: null weight handle");
+    if (!has_q8_gemv(w->quant))
+        return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_argmax: %s has no quant_q8 GEMV", quant_name(w->quant));
+    if ((x_q8 == nullptr) == (x_f32 == nullptr))
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: exactly one of x_q8 and x_f32 must be set");
+    if (x_q8 ? x_len != (size_t)w->dev.nb : x_len != (size_t)w->dev.cols)
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: activation length %zu does not match the weight", x_len);
+    if ((uintptr_t)x_q8 % 4 || (uintptr_t)x_f32 % 16)
+        return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: x_q8 must be 4-byte and x_f32 16-byte aligned");
+    if (!index) return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: null pointer");
+    JK_TRY(argmax_ws_check("gemv_q8_argmax", ws, ws_bytes, (size_t)w->dev.rows));
+    GemvJob j;
+    memset(&j, 0, sizeof j);
+    j.w = w->dev;
+    j.xq = x_q8;
+    j.xf = x_f32;
+    j.y = y;
+    j.am_slots = static_cast<unsigned long long *>(ws);
+    j.am_index = index;
+    j.r0 = 0;
+    j.r1 = w->dev.rows;
+    return launch_gemv_group((hipStream_t)s, &j, 1);
 }
 
 // -------------------------------------------------------------- vec_dot (f32)

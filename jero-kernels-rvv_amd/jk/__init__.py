@@ -476,3 +476,68 @@ def host_gemm_repacked_f32(out: np.ndarray, w: Weight, inp, m: int, r0: int, r1:
     x = _f32(inp).reshape(-1)
     _check(lib().jk_host_gemm_repacked_f32(_vp(out.ctypes.data), _sz(out.size), w.handle, _vp(x.ctypes.data), _sz(m),
                                            _sz(r0), _sz(r1)))
+
+
+# ---------------------------------------------------------------- epilogues
+ACT_SWIGLU, ACT_RELU2 = 1, 2
+
+
+def swiglu_f32(out: np.ndarray, gate, up) -> None:
+    """swiglu_f32 (swiglu.rs:62) on host slices."""
+    g, u = _f32(gate).reshape(-1), _f32(up).reshape(-1)
+    _check(lib().jk_host_swiglu_f32(_vp(out.ctypes.data), _sz(out.size), _vp(g.ctypes.data), _sz(g.size),
+                                    _vp(u.ctypes.data), _sz(u.size)))
+
+
+def relu_squared_gate_f32(out: np.ndarray, gate, up) -> None:
+    """relu_squared_gate_f32 (lib.rs:1111) on host slices."""
+    g, u = _f32(gate).reshape(-1), _f32(up).reshape(-1)
+    _check(lib().jk_host_relu_squared_gate_f32(_vp(out.ctypes.data), _sz(out.size), _vp(g.ctypes.data), _sz(g.size),
+                                               _vp(u.ctypes.data), _sz(u.size)))
+
+
+def argmax_f32(logits):
+    """argmax_f32 (lib.rs:662): the index, or None for empty / all-NaN input."""
+    x = _f32(logits).reshape(-1)
+    idx = C.c_int64(-1)
+    _check(lib().jk_host_argmax_f32(_vp(x.ctypes.data if x.size else 0), _sz(x.size), C.byref(idx)))
+    return None if idx.value < 0 else int(idx.value)
+
+
+def dev_swiglu_f32(gate, up, n, out, stream=None):
+    _check(lib().jk_swiglu_f32(_vp(stream or 0), _vp(_ptr(gate)), _vp(_ptr(up)), _sz(n), _vp(_ptr(out))))
+
+
+def dev_relu_squared_gate_f32(gate, up, n, out, stream=None):
+    _check(lib().jk_relu_squared_gate_f32(_vp(stream or 0), _vp(_ptr(gate)), _vp(_ptr(up)), _sz(n), _vp(_ptr(out))))
+
+
+def dev_quantize_row_q8_k_gated(act: int, gate, up, n, out, out_blocks, stream=None):
+    _check(lib().jk_quantize_row_q8_k_gated(_vp(stream or 0), C.c_int(act), _vp(_ptr(gate)), _vp(_ptr(up)), _sz(n),
+                                            _vp(_ptr(out)), _sz(out_blocks)))
+
+
+def dev_quantize_act_q8_gated(act: int, gate, up, m, k, act_q8: ActQ8C, stream=None):
+    _check(lib().jk_quantize_act_q8_gated(_vp(stream or 0), C.c_int(act), _vp(_ptr(gate)), _vp(_ptr(up)), _sz(m),
+                                          _sz(k), C.byref(act_q8)))
+
+
+def argmax_workspace_bytes(n: int) -> int:
+    """Device workspace bytes for an argmax over n values, or a fused GEMV argmax of n rows."""
+    f = lib().jk_argmax_workspace_bytes
+    f.restype = _sz
+    return int(f(_sz(n)))
+
+
+def _ws_bytes(ws, ws_bytes):
+    return ws_bytes if ws_bytes is not None else (ws.numel() * ws.element_size() if ws is not None else 0)
+
+
+def dev_argmax_f32(x, n, index, ws, stream=None, ws_bytes=None):
+    _check(lib().jk_argmax_f32(_vp(stream or 0), _vp(_ptr(x)), _sz(n), _vp(_ptr(index)), _vp(_ptr(ws)),
+                               _sz(_ws_bytes(ws, ws_bytes))))
+
+
+def dev_gemv_q8_argmax(w: Weight, x_q8, x_f32, x_len, y, index, ws, stream=None, ws_bytes=None):
+    _check(lib().jk_gemv_q8_argmax(_vp(stream or 0), w.handle, _vp(_ptr(x_q8)), _vp(_ptr(x_f32)), _sz(x_len),
+                                   _vp(_ptr(y)), _vp(_ptr(index)), _vp(_ptr(ws)), _sz(_ws_bytes(ws, ws_bytes))))

@@ -1296,3 +1296,46 @@ int or_bitlinear_i8(float *out, size_t out_len, const or_tensor_view *w, const i
     }
     return OR_OK;
 }
+
+/* ------------------------------------------------------------------------- */
+/* The step after the path: gated activations and argmax                      */
+/* ------------------------------------------------------------------------- */
+
+/* swiglu_f32_scalar (swiglu.rs:98-121): silu = 0 below -20, g above 20, else
+ * g / (1 + exp(-g)); out = silu * up. Rust's f32::exp is the platform libm expf. */
+int or_swiglu_f32(float *out, const float *gate, const float *up, size_t n) {
+    if (n == 0) return OR_TENSOR_BOUNDS;
+    for (size_t i = 0; i < n; i++) {
+        float g = gate[i], silu;
+        if (g < -20.0f) silu = 0.0f;
+        else if (g > 20.0f) silu = g;
+        else silu = g / (1.0f + expf(-g));
+        out[i] = silu * up[i];
+    }
+    return OR_OK;
+}
+
+/* relu_squared_gate_scalar (lib.rs:1140-1147): relu = g > 0 ? g : 0; out = relu * relu * up */
+int or_relu_squared_gate_f32(float *out, const float *gate, const float *up, size_t n) {
+    if (n == 0) return OR_TENSOR_BOUNDS;
+    for (size_t i = 0; i < n; i++) {
+        float g = gate[i];
+        float relu = g > 0.0f ? g : 0.0f;
+        out[i] = relu * relu * up[i];
+    }
+    return OR_OK;
+}
+
+/* argmax_f32_scalar (lib.rs:555-568): lowest index of the largest non-NaN value (values
+ * that compare equal, +0.0 and -0.0 included, keep the first); -1 for empty or all-NaN. */
+long or_argmax_f32(const float *x, size_t n) {
+    long best = -1;
+    float best_val = -INFINITY;
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i];
+        if (isnan(v)) continue;
+        if (best < 0 || v > best_val) { best_val = v; best = (long)i; }
+    }
+    return best;
+}
+

@@ -192,6 +192,11 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
 int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t rows,
                      size_t cols, const or_act_q8 *act, size_t r0, size_t r1);
 
+/* ---- gated activations, argmax ---- */
+int or_swiglu_f32(float *out, const float *gate, const float *up, size_t n);
+int or_relu_squared_gate_f32(float *out, const float *gate, const float *up, size_t n);
+long or_argmax_f32(const float *x, size_t n);
+
 /* ---- BitLinear ---- */
 int or_bitlinear_i8(float *out, size_t out_len, const or_tensor_view *w, const int8_t *act,
                     size_t act_len, float act_scale);

@@ -290,3 +290,29 @@ def bitlinear_i8(quant: int, shape, data: np.ndarray, act: np.ndarray, act_scale
     _ok(lib().or_bitlinear_i8(_p(out), _sz(out_len), C.byref(v.c), _p(a), _sz(a.size), C.c_float(act_scale)),
         "bitlinear")
     return out
+
+
+# ----------------------------------------------------------------- gated activations, argmax
+def swiglu_f32(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)
+    u = np.ascontiguousarray(up, dtype=np.float32).reshape(-1)
+    out = np.zeros(g.size, dtype=np.float32)
+    _ok(lib().or_swiglu_f32(_p(out), _p(g), _p(u), _sz(g.size)), "swiglu")
+    return out
+
+
+def relu_squared_gate_f32(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)
+    u = np.ascontiguousarray(up, dtype=np.float32).reshape(-1)
+    out = np.zeros(g.size, dtype=np.float32)
+    _ok(lib().or_relu_squared_gate_f32(_p(out), _p(g), _p(u), _sz(g.size)), "relu_squared")
+    return out
+
+
+def argmax_f32(x: np.ndarray) -> int:
+    """Index of the maximum (lowest on ties), -1 for empty or all-NaN input."""
+    a = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    f = lib().or_argmax_f32
+    f.restype = C.c_long
+    return int(f(_p(a) if a.size else None, _sz(a.size)))
+
