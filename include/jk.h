@@ -134,6 +134,46 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
                            jk_weight **out);
 jk_status jk_weight_free(jk_weight *w);
 jk_status jk_weight_get_info(const jk_weight *w, jk_weight_info *out);
+
+/* BlockScaledTileLayout (repack.rs:1286-1449): the tile-grid geometry of a weight, as
+ * RepackedWeight::block_scaled_layout (repack.rs:2372) / BlockScaledTileLayout::for_tensor
+ * (repack.rs:1308) compute it. The reference's buffer lengths are reported for callers that
+ * size work by them; device_bytes is what jk_weight_create allocates (the plane layout). */
+typedef struct jk_weight_layout {
+    int32_t quant;
+    size_t rows, cols, row_bytes, k_padded;
+    size_t n_tiles;          /* rows.div_ceil(8) */
+    size_t k_chunks;         /* k_padded / 16 */
+    size_t chunks_per_scale; /* 1 for Q6_K / Q3_K / Q2_K, else 2 */
+    size_t scale_groups;     /* k_chunks / chunks_per_scale */
+    int32_t has_mins;        /* Q4_K, Q5_K, Q4_1, Q5_1, Q2_K */
+    size_t total_tiles, total_scales, total_mins;
+    size_t device_bytes, gguf_bytes;
+    float tensor_scale; /* I2_S: the trailer's per-tensor scale (read_i2_s_trailer_scale), else 0 */
+} jk_weight_layout;
+/* Same formats and validation as jk_weight_upload with explicit rows, cols (no orientation
+ * inference, as for_tensor). */
+jk_status jk_weight_layout_for(const jk_tensor_view *w, size_t rows, size_t cols, jk_weight_layout *out);
+/* The allocation half of RepackedWeight::from_tile_buffers (repack.rs:2386-2450): a device
+ * handle for layout whose planes are zero (all-zero blocks) until tile ranges are written. */
+jk_status jk_weight_create(jk_stream s, const jk_weight_layout *layout, jk_weight **out);
+/* repack_into_tile_range (repack.rs:1579-1650): repacks the 8-row tiles [tile_begin, tile_end)
+ * of w's GGUF bytes (the whole tensor view, as in the reference; only those rows are copied)
+ * into the handle on the device. The view must be the one the layout was computed from (same
+ * format and dimensions; for I2_S the same trailer scale). Returns once the host bytes are no
+ * longer read. Calls for disjoint tile ranges may run concurrently from several host threads
+ * (each on its own stream); an empty range is a no-op. */
+jk_status jk_weight_upload_tile_range(jk_stream s, jk_weight *w, const jk_tensor_view *view, size_t tile_begin,
+                                      size_t tile_end);
+/* The same from GGUF bytes already in device memory: gguf holds exactly the rows of tiles
+ * [tile_begin, tile_end) (row_bytes each; the last tile may be partial). Allocates nothing
+ * and does not synchronize: gguf must stay valid until the stream reaches the repack. */
+jk_status jk_weight_repack_tile_range(jk_stream s, jk_weight *w, const void *gguf, size_t gguf_len,
+                                      size_t tile_begin, size_t tile_end);
+/* The validation half of from_tile_buffers: fails (TensorBounds) unless every tile has been
+ * written, then makes the handle usable by the compute entry points (which refuse an unsealed
+ * handle) and immutable (further tile writes are refused). */
+jk_status jk_weight_seal(jk_weight *w);
 /* dequantize_tensor_row (quant.rs:2492-2568) over output rows [row_begin, row_end):
  * out[(row - row_begin) * cols + col], bit-exact with the GGUF block dequantizers.
  * RepackedWeight::dequantize_row (repack.rs:2529-2598) agrees up to the sign of zero. */

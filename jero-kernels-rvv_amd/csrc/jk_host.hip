@@ -252,6 +252,7 @@ jk_status jk_host_dequantize_tensor_row(const jk_tensor_view *w, size_t row, flo
 jk_status jk_host_gemm_repacked_f32(float *out, size_t out_len, const jk_weight *w, const float *input, size_t m,
                                    size_t r0, size_t r1) {
     if (!w) return fail(JK_TENSOR_BOUNDS, "gemm_repacked_f32: null weight handle");
+    if (!w->ready) return fail(JK_TENSOR_BOUNDS, "gemm_repacked_f32: the weight has not been sealed (jk_weight_seal)");
     const size_t cols = (size_t)w->dev.cols;
     if (m == 0 || !input)
         return fail(JK_TENSOR_BOUNDS, "gemm_repacked_f32: input must hold m * cols = %zu * %zu values", m, cols);

@@ -39,6 +39,8 @@
 // streaming the 54-byte blocks at full HBM bandwidth leaves.
 #pragma once
 
+#include <mutex>
+#include <vector>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -130,12 +132,18 @@ struct GemvGroup {
 }  // namespace jk
 
 struct jk_weight {
-    jk::WeightDev dev;  // dev.quant: the device layout (dev_quant of quant)
-    int quant;          // GGUF format of the uploaded tensor
-    int device;
-    size_t device_bytes;
-    size_t gguf_bytes;
-    void *alloc;  // base of the device allocation (planes, then scale plane)
+    jk::WeightDev dev = {};  // dev.quant: the device layout (dev_quant of quant)
+    int quant = 0;           // GGUF format of the uploaded tensor
+    int device = 0;
+    size_t device_bytes = 0;
+    size_t gguf_bytes = 0;
+    size_t row_bytes = 0;     // GGUF bytes of one row
+    void *alloc = nullptr;    // base of the device allocation (planes, then scale plane)
+    // Assembly from tile ranges (jk_weight_create .. jk_weight_seal): which 8-row tiles have
+    // been written. Compute entry points accept the handle only once it is sealed.
+    std::mutex mu;
+    std::vector<uint8_t> tile_done;
+    bool ready = false;
 };
 
 namespace jk {
@@ -166,7 +174,8 @@ jk_status check_launch(const char *what);
 
 // Kernel launchers (device tier internals). All arguments are validated by callers.
 // gguf_quant: the GGUF format of the staged payload (w.quant is its device layout).
-jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf);
+// Repacks GGUF rows [r0, r1) (gguf: exactly those rows' bytes, in device memory) into w's planes.
+jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf, int r0, int r1);
 jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1, float *out);
 jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk_block_q8_0 *out);
 jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk_block_q8k *out);

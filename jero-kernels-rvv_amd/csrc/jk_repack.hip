@@ -42,14 +42,16 @@ __device__ uint32_t tq1_as_tq2_dword(const uint8_t *src, int k) {
 // One thread per (row, block): cut the GGUF block into its 16-byte chunks, scale and
 // word (TQ1_0: re-encoded as the TQ2_0 payload first). The stores are the only writes of
 // the planes; the weight handle is read-only after.
-__global__ __launch_bounds__(256) void repack_kernel(WeightDev w, int gq, const uint8_t *__restrict__ g) {
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)w.rows * (size_t)w.nb;
-    if (idx >= total) return;
+// One thread per GGUF block of rows [r0, r0 + nrows); g holds exactly those rows' GGUF bytes.
+__global__ __launch_bounds__(256) void repack_kernel(WeightDev w, int gq, const uint8_t *__restrict__ g, int r0,
+                                                     int nrows) {
+    const size_t li = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (li >= (size_t)nrows * (size_t)w.nb) return;
     const Fmt f = fmt_of(w.quant);    // device layout
     const Fmt fg = fmt_of(gq);        // GGUF block
-    const uint8_t *src = g + idx * (size_t)fg.bb;
-    const int r = (int)(idx / (size_t)w.nb), b = (int)(idx % (size_t)w.nb);
+    const uint8_t *src = g + li * (size_t)fg.bb;
+    const int r = r0 + (int)(li / (size_t)w.nb), b = (int)(li % (size_t)w.nb);
+    const size_t idx = (size_t)r * (size_t)w.nb + (size_t)b;
     for (int c = 0; c < f.chunks; ++c) {
         uint32_t d4[4];
         for (int k = 0; k < 4; ++k) {
@@ -73,10 +75,11 @@ __global__ __launch_bounds__(256) void repack_kernel(WeightDev w, int gq, const 
         const_cast<uint32_t *>(w.hplane)[idx * (size_t)(f.h_len / 4) + i] = le32(src + f.h_off + 4 * i);
 }
 
-jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf) {
-    const size_t total = (size_t)w.rows * (size_t)w.nb;
+jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf, int r0, int r1) {
+    if (r1 <= r0) return JK_OK;
+    const size_t total = (size_t)(r1 - r0) * (size_t)w.nb;
     const unsigned grid = (unsigned)((total + 255) / 256);
-    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, w, gguf_quant, gguf);
+    hipLaunchKernelGGL(repack_kernel, dim3(grid), dim3(256), 0, s, w, gguf_quant, gguf, r0, r1 - r0);
     return check_launch("repack_kernel");
 }
 

@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -198,6 +199,103 @@ jk_status jk_copy_to_host(jk_stream s, void *dst, const void *src, size_t bytes)
 }
 
 // ------------------------------------------------------------------ weights
+// Byte sizes of the device layout of a [rows, cols] weight in GGUF format quant.
+struct PlaneSizes {
+    size_t nb, payload, plane_bytes, dbytes, dpad, hbytes;
+};
+static PlaneSizes plane_sizes(int quant, size_t rows, size_t cols) {
+    const Fmt f = fmt_of(quant);             // GGUF block geometry
+    const Fmt fd = fmt_of(dev_quant(quant));  // device layout
+    PlaneSizes p;
+    p.nb = cols / f.be;
+    p.payload = rows * p.nb * f.bb;
+    p.plane_bytes = rows * p.nb * (size_t)fd.chunks * 16;
+    p.dbytes = fd.d_off >= 0 ? rows * p.nb * 2 : 0;
+    p.dpad = (p.dbytes + 255) / 256 * 256;  // keeps the word plane 256-byte aligned
+    p.hbytes = fd.h_off >= 0 ? rows * p.nb * (size_t)fd.h_len : 0;
+    return p;
+}
+
+// Checks a view and explicit dimensions as BlockScaledTileLayout::for_tensor does
+// (repack.rs:1308-1333, validate_matrix_view 1208-1281), plus the kernels' index range.
+static jk_status check_view_dims(const jk_tensor_view *w, size_t rows, size_t cols) {
+    if (!w || (!w->bytes && w->byte_len) || (w->ndim && !w->shape)) return fail(JK_TENSOR_BOUNDS, "null tensor view");
+    if (!fmt_known(w->quant))
+        return fail(JK_CAPABILITY_MISMATCH, "%s: quant type %d is not supported by libjk", tname(w), (int)w->quant);
+    JK_TRY(validate_matrix_view(w, rows, cols));
+    const size_t be = (size_t)fmt_of(w->quant).be;
+    if (rows >= kMaxRows || cols / be >= kMaxRows || rows * (cols / be) >= ((size_t)1 << 28))
+        return fail(JK_TENSOR_BOUNDS, "%s: matrix [%zu, %zu] exceeds the device index range", tname(w), rows, cols);
+    return JK_OK;
+}
+
+// A handle with its device allocation and plane pointers; the planes' contents are undefined.
+static jk_status alloc_handle(int quant, size_t rows, size_t cols, float tensor_scale, jk_weight **out) {
+    const PlaneSizes p = plane_sizes(quant, rows, cols);
+    jk_weight *h = new jk_weight();
+    hipError_t e = hipGetDevice(&h->device);
+    if (e == hipSuccess) e = hipMalloc(&h->alloc, p.plane_bytes + p.dpad + p.hbytes + 256);
+    if (e != hipSuccess) {
+        delete h;
+        return hip_fail(e, "weight allocation");
+    }
+    h->dev.planes = (const uint8_t *)h->alloc;
+    h->dev.dplane = p.dbytes ? (const uint16_t *)((uint8_t *)h->alloc + p.plane_bytes) : nullptr;
+    h->dev.hplane = p.hbytes ? (const uint32_t *)((uint8_t *)h->alloc + p.plane_bytes + p.dpad) : nullptr;
+    h->dev.quant = dev_quant(quant);
+    h->quant = quant;
+    h->dev.rows = (int)rows;
+    h->dev.cols = (int)cols;
+    h->dev.nb = (int)p.nb;
+    h->dev.tensor_scale = tensor_scale;
+    h->device_bytes = p.plane_bytes + p.dbytes + p.hbytes;
+    h->gguf_bytes = p.payload + trailer_bytes(quant);
+    h->row_bytes = p.nb * (size_t)fmt_of(quant).bb;
+    h->tile_done.assign((rows + 7) / 8, 0);
+    *out = h;
+    return JK_OK;
+}
+
+static void free_handle(jk_weight *h) {
+    if (h->alloc) (void)hipFree(h->alloc);
+    delete h;
+}
+
+// Copies rows [r0, r1) of a host GGUF payload to a transient device buffer and repacks them
+// into h; returns once the stream has consumed the host bytes and the buffer.
+static jk_status upload_rows(hipStream_t st, jk_weight *h, const uint8_t *rows_bytes, size_t r0, size_t r1,
+                             const char *what) {
+    const size_t bytes = (r1 - r0) * h->row_bytes;
+    uint8_t *staging = nullptr;
+    hipError_t e = hipMalloc(&staging, bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(staging, rows_bytes, bytes, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) {
+        if (staging) (void)hipFree(staging);
+        return hip_fail(e, what);
+    }
+    const jk_status rs = launch_repack(st, h->dev, h->quant, staging, (int)r0, (int)r1);
+    // The staging buffer may only be released once the repack kernel has consumed it.
+    const hipError_t se = hipStreamSynchronize(st);
+    (void)hipFree(staging);
+    if (rs != JK_OK) return rs;
+    if (se != hipSuccess) return hip_fail(se, what);
+    return JK_OK;
+}
+
+// Tile bookkeeping of a handle being assembled: refuses a sealed handle or a bad range.
+static jk_status tile_range_check(jk_weight *w, size_t tb, size_t te, const char *what) {
+    if (w->ready) return fail(JK_TENSOR_BOUNDS, "%s: the weight is sealed and immutable", what);
+    const size_t n_tiles = w->tile_done.size();
+    if (tb > te || te > n_tiles)
+        return fail(JK_TENSOR_BOUNDS, "%s: tile_range %zu..%zu exceeds n_tiles (%zu)", what, tb, te, n_tiles);
+    return JK_OK;
+}
+
+static void mark_tiles(jk_weight *w, size_t tb, size_t te) {
+    std::lock_guard<std::mutex> lock(w->mu);
+    for (size_t t = tb; t < te; ++t) w->tile_done[t] = 1;
+}
+
 jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, size_t cols,
                            jk_weight **out) {
     if (!out) return fail(JK_TENSOR_BOUNDS, "null weight out-pointer");
@@ -217,61 +315,138 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
         else if (d1 % be == 0 && d0 % be != 0) { rows = d0; cols = d1; }
         else { rows = d1; cols = d0; }
     }
-    JK_TRY(validate_matrix_view(w, rows, cols));
-    if (rows >= kMaxRows || cols / (size_t)fmt_of(w->quant).be >= kMaxRows ||
-        rows * (cols / (size_t)fmt_of(w->quant).be) >= ((size_t)1 << 28))
-        return fail(JK_TENSOR_BOUNDS, "%s: matrix [%zu, %zu] exceeds the device index range", tname(w), rows, cols);
-    const Fmt f = fmt_of(w->quant);             // GGUF block geometry
-    const Fmt fd = fmt_of(dev_quant(w->quant));  // device layout
-    const size_t nb = cols / f.be;
-    const size_t payload = rows * nb * f.bb;
-    const size_t plane_bytes = rows * nb * (size_t)fd.chunks * 16;
-    const size_t dbytes = fd.d_off >= 0 ? rows * nb * 2 : 0;
-    const size_t dpad = (dbytes + 255) / 256 * 256;  // keeps the word plane 256-byte aligned
-    const size_t hbytes = fd.h_off >= 0 ? rows * nb * (size_t)fd.h_len : 0;
-    jk_weight *h = new jk_weight();
-    memset(h, 0, sizeof *h);
-    JK_HIP(hipGetDevice(&h->device));
-    hipStream_t st = (hipStream_t)s;
-    uint8_t *staging = nullptr;
-    hipError_t e = hipMalloc(&h->alloc, plane_bytes + dpad + hbytes + 256);
-    if (e == hipSuccess) e = hipMalloc(&staging, payload);
-    if (e == hipSuccess) e = hipMemcpyAsync(staging, w->bytes, payload, hipMemcpyHostToDevice, st);
-    if (e != hipSuccess) {
-        if (staging) (void)hipFree(staging);
-        if (h->alloc) (void)hipFree(h->alloc);
-        delete h;
-        return hip_fail(e, "jk_weight_upload");
+    JK_TRY(check_view_dims(w, rows, cols));
+    const size_t payload = plane_sizes(w->quant, rows, cols).payload;
+    const float scale = w->quant == JK_I2_S
+                            ? read_trailer_scale((const uint8_t *)w->bytes + payload, w->byte_len - payload)
+                            : 0.0f;
+    jk_weight *h = nullptr;
+    JK_TRY(alloc_handle(w->quant, rows, cols, scale, &h));
+    const jk_status st = upload_rows((hipStream_t)s, h, (const uint8_t *)w->bytes, 0, rows, "jk_weight_upload");
+    if (st != JK_OK) {
+        free_handle(h);
+        return st;
     }
-    h->dev.planes = (const uint8_t *)h->alloc;
-    h->dev.dplane = dbytes ? (const uint16_t *)((uint8_t *)h->alloc + plane_bytes) : nullptr;
-    h->dev.hplane = hbytes ? (const uint32_t *)((uint8_t *)h->alloc + plane_bytes + dpad) : nullptr;
-    h->dev.quant = dev_quant(w->quant);
-    h->quant = w->quant;
-    h->dev.rows = (int)rows;
-    h->dev.cols = (int)cols;
-    h->dev.nb = (int)nb;
-    h->dev.tensor_scale = w->quant == JK_I2_S
-                              ? read_trailer_scale((const uint8_t *)w->bytes + payload, w->byte_len - payload)
-                              : 0.0f;
-    h->device_bytes = plane_bytes + dbytes + hbytes;
-    h->gguf_bytes = payload + trailer_bytes(w->quant);
-    jk_status rs = launch_repack(st, h->dev, w->quant, staging);
-    // The staging buffer may only be released once the repack kernel has consumed it.
-    hipError_t se = hipStreamSynchronize(st);
-    (void)hipFree(staging);
-    if (rs != JK_OK || se != hipSuccess) {
-        (void)hipFree(h->alloc);
-        delete h;
-        return rs != JK_OK ? rs : hip_fail(se, "jk_weight_upload repack");
+    mark_tiles(h, 0, h->tile_done.size());
+    h->ready = true;
+    *out = h;
+    return JK_OK;
+}
+
+jk_status jk_weight_layout_for(const jk_tensor_view *w, size_t rows, size_t cols, jk_weight_layout *out) {
+    if (!out) return fail(JK_TENSOR_BOUNDS, "null layout out-pointer");
+    JK_TRY(check_view_dims(w, rows, cols));
+    const int q = w->quant;
+    const PlaneSizes p = plane_sizes(q, rows, cols);
+    memset(out, 0, sizeof *out);
+    out->quant = q;
+    out->rows = rows;
+    out->cols = cols;
+    out->row_bytes = p.nb * (size_t)fmt_of(q).bb;
+    out->k_padded = (cols + 31) / 32 * 32;  // ACT_Q8_GROUP_ELEMENTS
+    out->n_tiles = (rows + 7) / 8;          // tile_count (ime.rs:70), TILE_N = 8
+    out->k_chunks = out->k_padded / 16;     // TILE_K = 16
+    out->chunks_per_scale = (q == JK_Q6_K || q == JK_Q3_K || q == JK_Q2_K) ? 1 : 2;
+    out->scale_groups = out->k_chunks / out->chunks_per_scale;
+    out->has_mins = q == JK_Q4_K || q == JK_Q5_K || q == JK_Q4_1 || q == JK_Q5_1 || q == JK_Q2_K;
+    out->total_tiles = out->n_tiles * out->k_chunks;
+    out->total_scales = out->n_tiles * out->scale_groups * 8;
+    out->total_mins = out->has_mins ? out->total_scales : 0;
+    out->device_bytes = p.plane_bytes + p.dbytes + p.hbytes;
+    out->gguf_bytes = p.payload + trailer_bytes(q);
+    out->tensor_scale =
+        q == JK_I2_S ? read_trailer_scale((const uint8_t *)w->bytes + p.payload, w->byte_len - p.payload) : 0.0f;
+    return JK_OK;
+}
+
+jk_status jk_weight_create(jk_stream s, const jk_weight_layout *L, jk_weight **out) {
+    if (!out) return fail(JK_TENSOR_BOUNDS, "null weight out-pointer");
+    *out = nullptr;
+    if (!L) return fail(JK_TENSOR_BOUNDS, "jk_weight_create: null layout");
+    if (!fmt_known(L->quant))
+        return fail(JK_CAPABILITY_MISMATCH, "jk_weight_create: quant type %d is not supported by libjk", (int)L->quant);
+    const size_t be = (size_t)fmt_of(L->quant).be;
+    if (L->rows == 0 || L->cols == 0 || L->cols % be || L->rows >= kMaxRows || L->cols / be >= kMaxRows ||
+        L->rows * (L->cols / be) >= ((size_t)1 << 28))
+        return fail(JK_TENSOR_BOUNDS, "jk_weight_create: invalid dimensions [%zu, %zu]", L->rows, L->cols);
+    const PlaneSizes p = plane_sizes(L->quant, L->rows, L->cols);
+    if (L->n_tiles != (L->rows + 7) / 8 || L->row_bytes != p.nb * (size_t)fmt_of(L->quant).bb ||
+        L->device_bytes != p.plane_bytes + p.dbytes + p.hbytes)
+        return fail(JK_TENSOR_BOUNDS, "jk_weight_create: the layout does not describe a [%zu, %zu] %s weight", L->rows,
+                    L->cols, quant_name(L->quant));
+    jk_weight *h = nullptr;
+    JK_TRY(alloc_handle(L->quant, L->rows, L->cols, L->quant == JK_I2_S ? L->tensor_scale : 0.0f, &h));
+    const size_t total = p.plane_bytes + p.dpad + p.hbytes + 256;
+    hipError_t e = hipMemsetAsync(h->alloc, 0, total, (hipStream_t)s);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)s);
+    if (e != hipSuccess) {
+        free_handle(h);
+        return hip_fail(e, "jk_weight_create");
     }
     *out = h;
     return JK_OK;
 }
 
+jk_status jk_weight_upload_tile_range(jk_stream s, jk_weight *w, const jk_tensor_view *v, size_t tb, size_t te) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "repack_into_tile_range: null weight handle");
+    const size_t rows = (size_t)w->dev.rows, cols = (size_t)w->dev.cols;
+    JK_TRY(check_view_dims(v, rows, cols));
+    if (v->quant != w->quant)
+        return fail(JK_TENSOR_BOUNDS, "%s: view format %s does not match the weight's %s", tname(v),
+                    quant_name(v->quant), quant_name(w->quant));
+    if (w->quant == JK_I2_S) {
+        const size_t payload = rows * w->row_bytes;
+        const float sc = read_trailer_scale((const uint8_t *)v->bytes + payload, v->byte_len - payload);
+        if (memcmp(&sc, &w->dev.tensor_scale, 4))
+            return fail(JK_TENSOR_BOUNDS, "%s: I2_S trailer scale differs from the layout's", tname(v));
+    }
+    JK_TRY(tile_range_check(w, tb, te, "repack_into_tile_range"));
+    if (tb == te) return JK_OK;
+    const size_t r0 = tb * 8, r1 = std::min(rows, te * 8);
+    JK_TRY(upload_rows((hipStream_t)s, w, (const uint8_t *)v->bytes + r0 * w->row_bytes, r0, r1,
+                       "repack_into_tile_range"));
+    mark_tiles(w, tb, te);
+    return JK_OK;
+}
+
+jk_status jk_weight_repack_tile_range(jk_stream s, jk_weight *w, const void *gguf, size_t gguf_len, size_t tb,
+                                      size_t te) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "repack_tile_range: null weight handle");
+    JK_TRY(tile_range_check(w, tb, te, "repack_tile_range"));
+    const size_t r0 = tb * 8, r1 = std::min((size_t)w->dev.rows, te * 8);
+    const size_t need = tb == te ? 0 : (r1 - r0) * w->row_bytes;
+    if (gguf_len != need)
+        return fail(JK_TENSOR_BOUNDS, "repack_tile_range: %zu bytes != %zu for tiles %zu..%zu", gguf_len, need, tb, te);
+    if (tb == te) return JK_OK;
+    if (!gguf) return fail(JK_TENSOR_BOUNDS, "repack_tile_range: null GGUF bytes");
+    JK_TRY(launch_repack((hipStream_t)s, w->dev, w->quant, (const uint8_t *)gguf, (int)r0, (int)r1));
+    mark_tiles(w, tb, te);
+    return JK_OK;
+}
+
+jk_status jk_weight_seal(jk_weight *w) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "from_tile_buffers: null weight handle");
+    std::lock_guard<std::mutex> lock(w->mu);
+    size_t missing = 0, first = 0;
+    for (size_t t = 0; t < w->tile_done.size(); ++t)
+        if (!w->tile_done[t] && missing++ == 0) first = t;
+    if (missing)
+        return fail(JK_TENSOR_BOUNDS, "from_tile_buffers: %zu of %zu tiles never written (first: tile %zu)", missing,
+                    w->tile_done.size(), first);
+    w->ready = true;
+    return JK_OK;
+}
+
+// Compute entry points accept only a complete (sealed) handle.
+static jk_status weight_usable(const jk_weight *w, const char *what) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "%s: null weight handle", what);
+    if (!w->ready) return fail(JK_TENSOR_BOUNDS, "%s: the weight has not been sealed (jk_weight_seal)", what);
+    return JK_OK;
+}
+
 jk_status jk_weight_free(jk_weight *w) {
     if (!w) return JK_OK;
-    hipError_t e = hipFree(w->alloc);
+    hipError_t e = w->alloc ? hipFree(w->alloc) : hipSuccess;
     delete w;
     if (e != hipSuccess) return hip_fail(e, "jk_weight_free");
     return JK_OK;
@@ -289,7 +464,7 @@ jk_status jk_weight_get_info(const jk_weight *w, jk_weight_info *out) {
 
 jk_status jk_weight_dequantize_rows(jk_stream s, const jk_weight *w, size_t r0, size_t r1, float *out,
                                     size_t out_len) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "null weight handle");
+    JK_TRY(weight_usable(w, "dequantize_rows"));
     if (r0 >= r1 || r1 > (size_t)w->dev.rows)
         return fail(JK_TENSOR_BOUNDS, "row range %zu..%zu out of bounds for %d rows", r0, r1, w->dev.rows);
     if (out_len != (r1 - r0) * (size_t)w->dev.cols)
@@ -379,7 +554,7 @@ jk_status jk_quantize_absmax_i8(jk_stream s, const float *x, size_t m, size_t k,
 // --------------------------------------------------------------- quant_q8 GEMV
 static jk_status gemv_check(const jk_weight *w, int quant, const void *x, size_t nx, const float *y,
                             size_t r0, size_t r1, const char *name) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "%s: null weight handle", name);
+    JK_TRY(weight_usable(w, name));
     if (quant && w->quant != quant)
         return fail(JK_TENSOR_BOUNDS, "%s: expected %s quant type, got %s", name, quant_name(quant),
                     quant_name(w->quant));
@@ -438,6 +613,7 @@ jk_status jk_gemv_q8_rows(jk_stream s, const jk_weight *w, const void *x, size_t
 static jk_status gemv_job_check(const jk_gemv_job *j, size_t i, GemvJob *out) {
     const jk_weight *w = j->w;
     if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: null weight handle", i);
+    JK_TRY(weight_usable(w, "gemv_q8_batch"));
     const int q = w->quant;
     if (!has_q8_gemv(q))
         return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_batch: job %zu: %s has no quant_q8 GEMV", i, quant_name(q));
@@ -485,7 +661,7 @@ jk_status jk_gemv_q8_batch(jk_stream s, const jk_gemv_job *jobs, size_t njobs) {
 }
 
 jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: null weight handle");
+    JK_TRY(weight_usable(w, "gemv_q8_f32"));
     if (n != (size_t)w->dev.cols)
         return fail(JK_TENSOR_BOUNDS, "gemv_q8_f32: input len %zu != cols %d", n, w->dev.cols);
     if (y_len != (size_t)w->dev.rows)
@@ -555,7 +731,7 @@ jk_status jk_argmax_f32(jk_stream s, const float *x, size_t n, int32_t *index, v
 
 jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
                             float *y, int32_t *index, void *ws, size_t ws_bytes) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: null weight handle");
+    JK_TRY(weight_usable(w, "gemv_q8_argmax"));
     if (!has_q8_gemv(w->quant))
         return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_argmax: %s has no quant_q8 GEMV", quant_name(w->quant));
     if ((x_q8 == nullptr) == (x_f32 == nullptr))
@@ -581,7 +757,7 @@ jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, c
 
 // -------------------------------------------------------------- vec_dot (f32)
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "vec_dot: null weight handle");
+    JK_TRY(weight_usable(w, "vec_dot"));
     int q = w->quant;
     if (!has_vec_dot_f32(q))
         return fail(JK_CAPABILITY_MISMATCH, "vec_dot: %s has no f32-activation matvec", quant_name(q));
@@ -597,6 +773,7 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
                            size_t r0, size_t r1) {
     // execute_gemm_repacked_rows (repack.rs:2725-2778)
     if (!w || !act) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null argument");
+    JK_TRY(weight_usable(w, "gemm_repacked"));
     if (act->k != (size_t)w->dev.cols)
         return fail(JK_TENSOR_BOUNDS, "gemm_repacked: activation k %zu != weight cols %d", act->k, w->dev.cols);
     if (r0 > r1 || r1 > (size_t)w->dev.rows)
@@ -621,7 +798,7 @@ jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
 // ---------------------------------------------------------------- BitLinear
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
                           size_t k, float *y, size_t y_len) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "bitlinear: null weight handle");
+    JK_TRY(weight_usable(w, "bitlinear"));
     int q = w->quant;
     // validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
     if (!has_bitlinear(q))

@@ -90,6 +90,18 @@ class WeightInfoC(C.Structure):
     _fields_ = [("quant", C.c_int32), ("rows", _sz), ("cols", _sz), ("device_bytes", _sz), ("gguf_bytes", _sz)]
 
 
+class WeightLayoutC(C.Structure):
+    """BlockScaledTileLayout (repack.rs:1286-1449) plus the device layout's byte counts."""
+    _fields_ = [("quant", C.c_int32), ("rows", _sz), ("cols", _sz), ("row_bytes", _sz), ("k_padded", _sz),
+                ("n_tiles", _sz), ("k_chunks", _sz), ("chunks_per_scale", _sz), ("scale_groups", _sz),
+                ("has_mins", C.c_int32), ("total_tiles", _sz), ("total_scales", _sz), ("total_mins", _sz),
+                ("device_bytes", _sz), ("gguf_bytes", _sz), ("tensor_scale", C.c_float)]
+
+    def scales_for_tiles(self, count: int) -> int:
+        """BlockScaledTileLayout::scales_for_tiles (repack.rs:1446)."""
+        return count * self.scale_groups * 8
+
+
 _lib_handle = None
 
 
@@ -351,6 +363,14 @@ def sync(stream=None) -> None:
     _check(lib().jk_stream_sync(_vp(stream or 0)))
 
 
+def block_scaled_layout(view: TensorView, rows: int, cols: int) -> WeightLayoutC:
+    """RepackedWeight::block_scaled_layout (repack.rs:2372)."""
+    out = WeightLayoutC()
+    v = view.c()
+    _check(lib().jk_weight_layout_for(C.byref(v), _sz(rows), _sz(cols), C.byref(out)))
+    return out
+
+
 class Weight:
     """Device-resident weight (RepackedWeight::from_tensor, repack.rs:2288)."""
 
@@ -359,10 +379,40 @@ class Weight:
         v = view.c()
         _check(lib().jk_weight_upload(_vp(stream or 0), C.byref(v), _sz(rows), _sz(cols), C.byref(h)))
         self._h = h
+        self._info()
+
+    def _info(self):
         info = WeightInfoC()
-        _check(lib().jk_weight_get_info(h, C.byref(info)))
+        _check(lib().jk_weight_get_info(self._h, C.byref(info)))
         self.quant, self.rows, self.cols = info.quant, info.rows, info.cols
         self.device_bytes, self.gguf_bytes = info.device_bytes, info.gguf_bytes
+
+    @classmethod
+    def create(cls, layout: WeightLayoutC, stream=None) -> "Weight":
+        """An empty handle for layout, to be filled by tile ranges and sealed (the buffers of
+        RepackedWeight::from_tile_buffers, repack.rs:2386, on the device)."""
+        self = cls.__new__(cls)
+        h = _vp()
+        _check(lib().jk_weight_create(_vp(stream or 0), C.byref(layout), C.byref(h)))
+        self._h = h
+        self._info()
+        return self
+
+    def repack_into_tile_range(self, view: TensorView, tile_begin: int, tile_end: int, stream=None) -> None:
+        """repack_into_tile_range (repack.rs:1579) into this handle."""
+        v = view.c()
+        _check(lib().jk_weight_upload_tile_range(_vp(stream or 0), self._h, C.byref(v), _sz(tile_begin),
+                                                 _sz(tile_end)))
+
+    def repack_tile_range(self, gguf_dev, gguf_len: int, tile_begin: int, tile_end: int, stream=None) -> None:
+        """The same from GGUF bytes already in device memory (no allocation, asynchronous)."""
+        _check(lib().jk_weight_repack_tile_range(_vp(stream or 0), self._h, _vp(_ptr(gguf_dev)), _sz(gguf_len),
+                                                 _sz(tile_begin), _sz(tile_end)))
+
+    def seal(self) -> "Weight":
+        """RepackedWeight::from_tile_buffers (repack.rs:2386): every tile written, then usable."""
+        _check(lib().jk_weight_seal(self._h))
+        return self
 
     @property
     def handle(self):

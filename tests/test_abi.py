@@ -105,3 +105,47 @@ def test_weight_upload_validation_fails_closed():
         jk.Weight(jk.TensorView("w", jk.Q8_0, [4, 64], np.zeros(100, np.uint8)), rows=4, cols=64)
     with pytest.raises(jk.TensorBoundsError):  # 3D tensor
         jk.Weight(jk.TensorView("w", jk.Q8_0, [2, 2, 32], np.zeros(136, np.uint8)))
+
+
+LAYOUT_FORMATS = [jk.Q4_0, jk.Q4_1, jk.Q5_0, jk.Q5_1, jk.Q8_0, jk.IQ4_NL, jk.Q2_K, jk.Q3_K, jk.Q4_K, jk.Q5_K,
+                  jk.Q6_K, jk.TQ1_0, jk.TQ2_0, jk.I2_S]
+
+
+@pytest.mark.parametrize("quant", LAYOUT_FORMATS)
+@pytest.mark.parametrize("rows,cols", [(67, 512), (19, 256), (8, 768), (1, 256)])
+def test_weight_layout_for(quant, rows, cols):
+    """BlockScaledTileLayout::from_validated_dims (repack.rs:1339-1372) and its totals
+    (1424-1449): tiles of 8 rows, 16-element K chunks over K padded to 32, one chunk per scale
+    for the 16-element-scale formats, mins for the asymmetric ones; device bytes are the GGUF
+    bytes except TQ1_0 (66 per 54-byte block) and Q3_K (112 per 110)."""
+    nb = cols // jk.BLOCK_ELEMENTS[quant]
+    raw = np.zeros(rows * nb * jk.BLOCK_BYTES[quant] + jk.TRAILER_BYTES.get(quant, 0), np.uint8)
+    if quant == jk.I2_S:
+        raw[-32:-28] = np.frombuffer(np.float32(0.75).tobytes(), np.uint8)
+    L = jk.block_scaled_layout(jk.TensorView("w", quant, [cols, rows], raw), rows, cols)
+    cps = 1 if quant in (jk.Q6_K, jk.Q3_K, jk.Q2_K) else 2
+    k_padded = -(-cols // 32) * 32
+    assert (L.quant, L.rows, L.cols, L.row_bytes) == (quant, rows, cols, nb * jk.BLOCK_BYTES[quant])
+    assert (L.k_padded, L.n_tiles, L.k_chunks, L.chunks_per_scale) == (k_padded, -(-rows // 8), k_padded // 16, cps)
+    assert L.scale_groups == k_padded // 16 // cps
+    assert bool(L.has_mins) == (quant in (jk.Q4_K, jk.Q5_K, jk.Q4_1, jk.Q5_1, jk.Q2_K))
+    assert L.total_tiles == L.n_tiles * L.k_chunks and L.total_scales == L.n_tiles * L.scale_groups * 8
+    assert L.total_mins == (L.total_scales if L.has_mins else 0)
+    assert L.scales_for_tiles(3) == 3 * L.scale_groups * 8
+    dev_block = {jk.TQ1_0: 66, jk.Q3_K: 112}.get(quant, jk.BLOCK_BYTES[quant])
+    assert L.device_bytes == rows * nb * dev_block and L.gguf_bytes == raw.size
+    assert L.tensor_scale == (0.75 if quant == jk.I2_S else 0.0)
+
+
+def test_weight_layout_validation_fails_closed():
+    raw = np.zeros(67 * 2 * 144, np.uint8)
+    with pytest.raises(jk.CapabilityMismatch):  # dense / unsupported (repack.rs:1325-1335)
+        jk.block_scaled_layout(jk.TensorView("w", 1, [512, 67], raw), 67, 512)
+    with pytest.raises(jk.TensorBoundsError):  # cols not a multiple of the block
+        jk.block_scaled_layout(jk.TensorView("w", jk.Q4_K, [500, 67], raw), 67, 500)
+    with pytest.raises(jk.TensorBoundsError):  # shape does not match
+        jk.block_scaled_layout(jk.TensorView("w", jk.Q4_K, [512, 66], raw), 67, 512)
+    with pytest.raises(jk.TensorBoundsError):  # short buffer
+        jk.block_scaled_layout(jk.TensorView("w", jk.Q4_K, [512, 67], raw[:-1]), 67, 512)
+    with pytest.raises(jk.TensorBoundsError):  # no inference from rows = cols = 0 (for_tensor)
+        jk.block_scaled_layout(jk.TensorView("w", jk.Q4_K, [512, 67], raw), 0, 0)
