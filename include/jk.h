@@ -174,6 +174,39 @@ jk_status jk_weight_repack_tile_range(jk_stream s, jk_weight *w, const void *ggu
  * written, then makes the handle usable by the compute entry points (which refuse an unsealed
  * handle) and immutable (further tile writes are refused). */
 jk_status jk_weight_seal(jk_weight *w);
+
+/* ------------------------------------------------------------------ GGUF */
+/* GGUF v2 / v3 files, memory-mapped and bounds-checked. The reference reads its weights as
+ * jero_core::TensorView byte slices of such a file (dims [ne0, ne1] = [cols, rows]); no
+ * reference function corresponds to the reader itself. ggml type ids are the jk_quant values. */
+typedef struct jk_gguf jk_gguf;
+typedef struct jk_gguf_file_info {
+    uint32_t version;
+    size_t n_tensors, n_kv;
+    size_t alignment;   /* general.alignment, default 32 */
+    size_t data_offset; /* file offset of the tensor data section */
+    size_t file_bytes;
+} jk_gguf_file_info;
+typedef struct jk_gguf_tensor {
+    const char *name; /* valid until jk_gguf_close */
+    uint32_t ggml_type;
+    uint32_t n_dims;
+    uint64_t ne[4];      /* ne[0] is the contiguous (column) dimension */
+    size_t offset;       /* file offset of the data */
+    size_t nbytes;       /* 0 when the type's size is not known to this library */
+    const void *data;    /* the mapped bytes (NULL when nbytes is 0); valid until jk_gguf_close */
+} jk_gguf_tensor;
+jk_status jk_gguf_open(const char *path, jk_gguf **out);
+jk_status jk_gguf_close(jk_gguf *g);
+jk_status jk_gguf_get_file_info(const jk_gguf *g, jk_gguf_file_info *out);
+jk_status jk_gguf_tensor_info(const jk_gguf *g, size_t index, jk_gguf_tensor *out);
+jk_status jk_gguf_find(const jk_gguf *g, const char *name, size_t *index);
+/* RepackedWeight::from_tensor of a 2D tensor of the file, assembled as from_tile_buffers from
+ * tile ranges (repack.rs:1579, 2386): rows are streamed in chunks of about chunk_bytes (0: 64
+ * MiB) through two pinned host buffers, copied out of the mapping by several host threads while
+ * the previous chunk is transferred and repacked on stream s. The result is the handle
+ * jk_weight_upload makes of the same bytes; returns once it is complete and sealed. */
+jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t index, size_t chunk_bytes, jk_weight **out);
 /* dequantize_tensor_row (quant.rs:2492-2568) over output rows [row_begin, row_end):
  * out[(row - row_begin) * cols + col], bit-exact with the GGUF block dequantizers.
  * RepackedWeight::dequantize_row (repack.rs:2529-2598) agrees up to the sign of zero. */

@@ -409,6 +409,13 @@ class Weight:
         _check(lib().jk_weight_repack_tile_range(_vp(stream or 0), self._h, _vp(_ptr(gguf_dev)), _sz(gguf_len),
                                                  _sz(tile_begin), _sz(tile_end)))
 
+    @classmethod
+    def _from_handle(cls, h) -> "Weight":
+        self = cls.__new__(cls)
+        self._h = h
+        self._info()
+        return self
+
     def seal(self) -> "Weight":
         """RepackedWeight::from_tile_buffers (repack.rs:2386): every tile written, then usable."""
         _check(lib().jk_weight_seal(self._h))
@@ -426,6 +433,59 @@ class Weight:
     def __del__(self):
         try:
             self.free()
+        except Exception:
+            pass
+
+
+class GgufFileInfoC(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("n_tensors", _sz), ("n_kv", _sz), ("alignment", _sz),
+                ("data_offset", _sz), ("file_bytes", _sz)]
+
+
+class GgufTensorC(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_uint32), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4),
+                ("offset", _sz), ("nbytes", _sz), ("data", _vp)]
+
+
+class GGUF:
+    """A GGUF v2 / v3 file opened by libjk (memory-mapped): tensor records and streaming
+    loads of its weight matrices into device handles."""
+
+    def __init__(self, path: str):
+        h = _vp()
+        _check(lib().jk_gguf_open(os.fsencode(path), C.byref(h)))
+        self._h = h
+        fi = GgufFileInfoC()
+        _check(lib().jk_gguf_get_file_info(h, C.byref(fi)))
+        self.version, self.alignment, self.data_offset = fi.version, fi.alignment, fi.data_offset
+        self.n_kv, self.file_bytes = fi.n_kv, fi.file_bytes
+        self.tensors = []
+        for i in range(fi.n_tensors):
+            t = GgufTensorC()
+            _check(lib().jk_gguf_tensor_info(h, _sz(i), C.byref(t)))
+            self.tensors.append({"name": t.name.decode(), "type": t.ggml_type, "shape": list(t.ne[:t.n_dims]),
+                                 "offset": t.offset, "nbytes": t.nbytes, "data": t.data or 0})
+
+    def index(self, name: str) -> int:
+        i = _sz()
+        _check(lib().jk_gguf_find(self._h, name.encode(), C.byref(i)))
+        return int(i.value)
+
+    def load(self, tensor, stream=None, chunk_bytes: int = 0) -> Weight:
+        """The device weight of a 2D tensor (by name or index), streamed in tile-range chunks."""
+        i = self.index(tensor) if isinstance(tensor, str) else int(tensor)
+        h = _vp()
+        _check(lib().jk_gguf_load_weight(_vp(stream or 0), self._h, _sz(i), _sz(chunk_bytes), C.byref(h)))
+        return Weight._from_handle(h)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().jk_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 
