@@ -508,6 +508,42 @@ def main() -> int:
         hbm_line("lm_head Q6_K gemv, argmax", b + 4 * rows, us, f"{rows}x{cols}, logits written and re-read")
         for w in ws_lm:
             w.free()
+        # Load time: one Llama-3-8B layer's seven matrices (138 MB of GGUF bytes) in a GGUF file
+        # (page cache warm), streamed into device handles by jk_gguf_load_weight, against
+        # jk_weight_upload from host memory and the oracle's CPU repack of the same tensors (the
+        # reference repacks at load time on the host). GB/s of GGUF bytes.
+        import tempfile
+        sys.path.insert(0, os.path.join(REPO, "tests"))
+        from gguf_writer import STR, write_gguf
+        mats = [(f"blk.0.{n}.weight", q, [c, r], synth.gguf_weights(q, r, c, seed=700 + i))
+                for i, (n, q, r, c) in enumerate(synth.LLAMA3_8B_LAYER)]
+        total = sum(d.nbytes for *_, d in mats)
+        with tempfile.TemporaryDirectory() as td:
+            path = os.path.join(td, "layer.gguf")
+            write_gguf(path, mats, [("general.architecture", STR, "llama")])
+            g = jk.GGUF(path)
+            best_file = best_up = float("inf")
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ws_ = [g.load(name) for name, *_ in mats]
+                best_file = min(best_file, time.perf_counter() - t0)
+                for w in ws_:
+                    w.free()
+                t0 = time.perf_counter()
+                ws_ = [jk.Weight(jk.TensorView(n, q, ne, d), ne[1], ne[0]) for n, q, ne, d in mats]
+                torch.cuda.synchronize()
+                best_up = min(best_up, time.perf_counter() - t0)
+                for w in ws_:
+                    w.free()
+            g.close()
+        load = {"gguf_bytes": total, "gguf_load_s": round(best_file, 4),
+                "gguf_load_gbs": round(total / best_file / 1e9, 2), "upload_from_host_s": round(best_up, 4),
+                "upload_from_host_gbs": round(total / best_up / 1e9, 2),
+                "workload": "Llama-3-8B layer: Q/K/V/O/gate/up Q4_K, down Q6_K; GGUF file in the page cache"}
+        secondary["load_layer_gguf"] = load
+        load_mats = mats  # the CPU baseline below times the host repack of the same tensors
+        log(f"  load layer from GGUF {best_file * 1e3:.1f} ms ({total / best_file / 1e9:.2f} GB/s), "
+            f"upload from host {best_up * 1e3:.1f} ms")
         # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
         yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
         us = graph_us(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
@@ -529,6 +565,17 @@ def main() -> int:
     if args.cpu_seconds > 0:
         sys.path.insert(0, os.path.join(REPO, "oracle"))
         import oracle as O
+
+        if "load_layer_gguf" in secondary:  # load time on the host: the reference's CPU repack
+            t0 = time.perf_counter()
+            for n, q, ne, d in load_mats:
+                O.repack_logical(q, ne, d, ne[1], ne[0])
+            el = time.perf_counter() - t0
+            secondary["load_layer_gguf"].update({
+                "cpu_repack_s": round(el, 3),
+                "cpu_repack_gbs": round(secondary["load_layer_gguf"]["gguf_bytes"] / el / 1e9, 3),
+                "cpu_repack_kind": "port: the oracle's C restatement of the reference's repack, 1 thread"})
+            log(f"cpu repack of the layer: {el * 1e3:.0f} ms")
 
         hl = host_layers[0]
         x = synth.activations(4096, seed=5)

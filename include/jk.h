@@ -202,10 +202,12 @@ jk_status jk_gguf_get_file_info(const jk_gguf *g, jk_gguf_file_info *out);
 jk_status jk_gguf_tensor_info(const jk_gguf *g, size_t index, jk_gguf_tensor *out);
 jk_status jk_gguf_find(const jk_gguf *g, const char *name, size_t *index);
 /* RepackedWeight::from_tensor of a 2D tensor of the file, assembled as from_tile_buffers from
- * tile ranges (repack.rs:1579, 2386): rows are streamed in chunks of about chunk_bytes (0: 64
+ * tile ranges (repack.rs:1579, 2386): rows are streamed in chunks of about chunk_bytes (0: 32
  * MiB) through two pinned host buffers, copied out of the mapping by several host threads while
  * the previous chunk is transferred and repacked on stream s. The result is the handle
- * jk_weight_upload makes of the same bytes; returns once it is complete and sealed. */
+ * jk_weight_upload makes of the same bytes; returns once it is complete and sealed. The
+ * streaming buffers (2 x chunk pinned host + 2 x chunk device) stay with the file handle for
+ * the next load until jk_gguf_close; loads through one file handle are serialized. */
 jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t index, size_t chunk_bytes, jk_weight **out);
 /* dequantize_tensor_row (quant.rs:2492-2568) over output rows [row_begin, row_end):
  * out[(row - row_begin) * cols + col], bit-exact with the GGUF block dequantizers.

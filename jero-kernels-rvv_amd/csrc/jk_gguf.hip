@@ -15,6 +15,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -116,9 +117,50 @@ struct jk_gguf {
     uint32_t version = 0;
     uint64_t alignment = 32, data_start = 0, n_kv = 0;
     std::vector<TensorRec> tensors;
+    // Streaming buffers, kept from one load to the next (loads of one file are serialized):
+    // two pinned host buffers, two device staging buffers on device `device`, their events.
+    std::mutex mu;
+    size_t buf_bytes = 0;
+    int device = -1;
+    void *pinned[2] = {nullptr, nullptr}, *staging[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
 };
 
+static void release_buffers(jk_gguf *g) {
+    for (int b = 0; b < 2; ++b) {
+        if (g->ev[b]) (void)hipEventDestroy(g->ev[b]);
+        if (g->staging[b]) (void)hipFree(g->staging[b]);
+        if (g->pinned[b]) (void)hipHostFree(g->pinned[b]);
+        g->ev[b] = nullptr;
+        g->staging[b] = g->pinned[b] = nullptr;
+    }
+    g->buf_bytes = 0;
+    g->device = -1;
+}
+
+// Makes the streaming buffers hold at least bytes each, on the current device.
+static hipError_t ensure_buffers(jk_gguf *g, size_t bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (g->buf_bytes >= bytes && g->device == dev) return hipSuccess;
+    release_buffers(g);
+    for (int b = 0; b < 2 && e == hipSuccess; ++b) {
+        e = hipHostMalloc(&g->pinned[b], bytes, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc(&g->staging[b], bytes);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&g->ev[b], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        release_buffers(g);
+        return e;
+    }
+    g->buf_bytes = bytes;
+    g->device = dev;
+    return hipSuccess;
+}
+
 static void gguf_release(jk_gguf *g) {
+    if (g->buf_bytes) release_buffers(g);
     if (g->map) munmap((void *)g->map, g->size);
     if (g->fd >= 0) close(g->fd);
     delete g;
@@ -275,20 +317,17 @@ jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t ch
     JK_TRY(jk_weight_layout_for(&v, shape[1], shape[0], &L));
     jk_weight *w = nullptr;
     JK_TRY(jk_weight_create(s, &L, &w));
-    if (chunk_bytes == 0) chunk_bytes = (size_t)64 << 20;
+    if (chunk_bytes == 0) chunk_bytes = (size_t)32 << 20;
     const size_t tile_bytes = 8 * L.row_bytes;
     const size_t tiles_per_chunk = std::max<size_t>(1, chunk_bytes / tile_bytes);
     const size_t buf_bytes = std::min(tiles_per_chunk * tile_bytes, L.rows * L.row_bytes);
     hipStream_t st = (hipStream_t)s;
-    void *pinned[2] = {nullptr, nullptr}, *staging[2] = {nullptr, nullptr};
-    hipEvent_t ev[2] = {nullptr, nullptr};
+    jk_gguf *gm = const_cast<jk_gguf *>(g);  // the streaming buffers are the handle's cache
+    std::lock_guard<std::mutex> lock(gm->mu);
     jk_status rs = JK_OK;
-    hipError_t e = hipSuccess;
-    for (int b = 0; b < 2 && e == hipSuccess; ++b) {
-        e = hipHostMalloc(&pinned[b], buf_bytes, hipHostMallocDefault);
-        if (e == hipSuccess) e = hipMalloc(&staging[b], buf_bytes);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev[b], hipEventDisableTiming);
-    }
+    hipError_t e = ensure_buffers(gm, buf_bytes);
+    void *const *pinned = gm->pinned, *const *staging = gm->staging;
+    hipEvent_t *ev = gm->ev;
     const unsigned nthreads = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
     const uint8_t *src = (const uint8_t *)v.bytes;
     for (size_t t0 = 0, k = 0; e == hipSuccess && rs == JK_OK && t0 < L.n_tiles; t0 += tiles_per_chunk, ++k) {
@@ -311,13 +350,9 @@ jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t ch
         if (e == hipSuccess) rs = jk_weight_repack_tile_range(s, w, staging[b], bytes, t0, t1);
         if (e == hipSuccess && rs == JK_OK) e = hipEventRecord(ev[b], st);
     }
+    // Complete before the buffers are reused or the handle is returned.
     const hipError_t se = hipStreamSynchronize(st);
     if (e == hipSuccess) e = se;
-    for (int b = 0; b < 2; ++b) {
-        if (ev[b]) (void)hipEventDestroy(ev[b]);
-        if (staging[b]) (void)hipFree(staging[b]);
-        if (pinned[b]) (void)hipHostFree(pinned[b]);
-    }
     if (rs == JK_OK && e != hipSuccess) rs = hip_fail(e, "jk_gguf_load_weight");
     if (rs == JK_OK) rs = jk_weight_seal(w);
     if (rs != JK_OK) {
