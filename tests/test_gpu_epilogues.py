@@ -120,6 +120,10 @@ def argmax_cases():
     x = rng.standard_normal(100003).astype(np.float32)
     x[rng.random(100003) < 0.1] = np.nan
     out.append(x)
+    # more values than one pass of the largest partial grid covers (1024 x 256 x 4)
+    x = rng.standard_normal(3_000_001).astype(np.float32)
+    x[2_999_999] = x[1_048_577] = 7.5
+    out.append(x)
     return out
 
 

@@ -16,6 +16,9 @@ SHAPES = [("blk.0.attn_q.weight", jk.Q4_K, 19, 512), ("blk.0.ffn_down.weight", j
           ("blk.0.attn_k.weight", jk.Q8_0, 5, 64), ("blk.0.ffn_up.weight", jk.TQ1_0, 3, 256),
           ("blk.0.ffn_gate.weight", jk.I2_S, 12, 128), ("blk.0.x.weight", jk.Q5_0, 9, 96),
           ("blk.0.y.weight", jk.Q3_K, 17, 256), ("blk.0.z.weight", jk.IQ4_NL, 33, 64),
+          ("blk.0.q40.weight", jk.Q4_0, 21, 128), ("blk.0.q41.weight", jk.Q4_1, 10, 64),
+          ("blk.0.q51.weight", jk.Q5_1, 11, 96), ("blk.0.q2k.weight", jk.Q2_K, 16, 512),
+          ("blk.0.q5k.weight", jk.Q5_K, 7, 256), ("blk.0.tq2.weight", jk.TQ2_0, 9, 256),
           ("blk.0.big.weight", jk.Q4_K, 1000, 4096)]
 
 
