@@ -172,7 +172,9 @@ jk_status jk_weight_repack_tile_range(jk_stream s, jk_weight *w, const void *ggu
                                       size_t tile_begin, size_t tile_end);
 /* The validation half of from_tile_buffers: fails (TensorBounds) unless every tile has been
  * written, then makes the handle usable by the compute entry points (which refuse an unsealed
- * handle) and immutable (further tile writes are refused). */
+ * handle) and immutable (further tile writes are refused). The tile bookkeeping is host-side:
+ * work on another stream must wait for the streams that wrote the tiles (an event, or a
+ * synchronize), as after jk_weight_create's own stream. */
 jk_status jk_weight_seal(jk_weight *w);
 
 /* ------------------------------------------------------------------ GGUF */

@@ -8,6 +8,7 @@
 // chunk k to the device and the device repacks it (jk_weight_repack_tile_range), host threads
 // copy chunk k + 1 out of the mapped file. The bytes are handed over unchanged, exactly as a
 // TensorView over the file would hand them to the reference.
+#include <errno.h>
 #include <fcntl.h>
 #include <string.h>
 #include <sys/mman.h>

@@ -39,6 +39,7 @@
 // streaming the 54-byte blocks at full HBM bandwidth leaves.
 #pragma once
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 #include <hip/hip_runtime.h>
@@ -143,7 +144,7 @@ struct jk_weight {
     // been written. Compute entry points accept the handle only once it is sealed.
     std::mutex mu;
     std::vector<uint8_t> tile_done;
-    bool ready = false;
+    std::atomic<bool> ready{false};
 };
 
 namespace jk {
