@@ -233,19 +233,25 @@ jk_status jk_gguf_open(const char *path, jk_gguf **out) {
     jk_gguf *g = new jk_gguf();
     g->fd = open(path, O_RDONLY | O_CLOEXEC);
     struct stat st;
+    // (the error text is formed before the handle is released: release closes the file,
+    // which may change errno)
     if (g->fd < 0 || fstat(g->fd, &st) != 0) {
+        const jk_status s = fail(JK_TENSOR_BOUNDS, "gguf: cannot open %s: %s", path, strerror(errno));
         gguf_release(g);
-        return fail(JK_TENSOR_BOUNDS, "gguf: cannot open %s: %s", path, strerror(errno));
+        return s;
     }
     g->size = (uint64_t)st.st_size;
     if (g->size < 24) {
+        const jk_status s = fail(JK_TENSOR_BOUNDS, "%s: not a GGUF file (%llu bytes)", path,
+                                 (unsigned long long)g->size);
         gguf_release(g);
-        return fail(JK_TENSOR_BOUNDS, "%s: not a GGUF file (%llu bytes)", path, (unsigned long long)g->size);
+        return s;
     }
     void *m = mmap(nullptr, g->size, PROT_READ, MAP_PRIVATE, g->fd, 0);
     if (m == MAP_FAILED) {
+        const jk_status s = fail(JK_TENSOR_BOUNDS, "gguf: cannot map %s: %s", path, strerror(errno));
         gguf_release(g);
-        return fail(JK_TENSOR_BOUNDS, "gguf: cannot map %s: %s", path, strerror(errno));
+        return s;
     }
     g->map = (const uint8_t *)m;
     const jk_status s = gguf_parse(g, path);

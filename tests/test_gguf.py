@@ -116,3 +116,12 @@ def test_bad_alignment_and_offsets_fail_closed(tmp_path):
     p = tmp_path / "dims.gguf"
     write_gguf(p, [("t", jk.Q8_0, [32, 1, 1, 1, 1], np.zeros(34, np.uint8))], [])
     _raises_closed(p)
+
+
+def test_short_file_error_names_its_size(tmp_path):
+    # a file shorter than the fixed header is refused with its own size in the message (the
+    # message is formed before the handle is released)
+    p = tmp_path / "short.gguf"
+    p.write_bytes(b"GGUF" + bytes(17))
+    with pytest.raises(jk.TensorBoundsError, match=r"\(21 bytes\)"):
+        jk.GGUF(str(p))
