@@ -197,3 +197,40 @@ def test_epilogue_validation(gpu):
     with pytest.raises(jk.TensorBoundsError):  # wrong length
         jk.dev_gemv_q8_argmax(w, None, x, 255, None, idx, ws)
     torch.cuda.synchronize()
+
+
+def test_gemv_q8_argmax_graph_replays(gpu):
+    """The fused GEMV + argmax and the standalone argmax captured once in a HIP graph (no memset
+    nodes: the workspace needs no clearing) and replayed with new activations in between, eager
+    work and synchronizations between the replays; every replay's index equals the oracle's."""
+    torch = gpu
+    rows, cols = 3000, 4096
+    raw = synth.gguf_weights(jk.Q4_K, rows, cols, seed=11)
+    w = jk.Weight(jk.TensorView("lm_head", jk.Q4_K, [cols, rows], raw), rows, cols)
+    xq_dev = torch.empty(cols // 256 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device="cuda")
+    ws = torch.full((jk.argmax_workspace_bytes(rows),), 0xFF, dtype=torch.uint8, device="cuda")
+    ws2 = torch.full((jk.argmax_workspace_bytes(rows),), 0xFF, dtype=torch.uint8, device="cuda")
+    idx = torch.empty(1, dtype=torch.int32, device="cuda")
+    idx2 = torch.empty(1, dtype=torch.int32, device="cuda")
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        jk.dev_gemv_q8_argmax(w, xq_dev, None, cols // 256, y, idx, ws, side.cuda_stream)
+        jk.dev_argmax_f32(y, rows, idx2, ws2, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cs = torch.cuda.current_stream().cuda_stream
+        jk.dev_gemv_q8_argmax(w, xq_dev, None, cols // 256, y, idx, ws, cs)
+        jk.dev_argmax_f32(y, rows, idx2, ws2, cs)
+    for seed in (1, 2, 3, 4):
+        x = synth.activations(cols, 100 + seed)
+        xq = O.quantize_row_q8_k(x)
+        xq_dev.copy_(torch.from_numpy(xq.view(np.uint8).reshape(-1).copy()))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = O.argmax_f32(O.gemv_q8(jk.Q4_K, [rows, cols], raw, xq, rows))
+        assert int(idx.cpu()[0]) == ref and int(idx2.cpu()[0]) == ref, seed
