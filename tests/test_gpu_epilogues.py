@@ -234,3 +234,35 @@ def test_gemv_q8_argmax_graph_replays(gpu):
         torch.cuda.synchronize()
         ref = O.argmax_f32(O.gemv_q8(jk.Q4_K, [rows, cols], raw, xq, rows))
         assert int(idx.cpu()[0]) == ref and int(idx2.cpu()[0]) == ref, seed
+
+
+def test_gated_quantizer_graph_replays(gpu):
+    """SwiGLU fused into quantize_row_q8_k captured once and replayed with new gate / up values:
+    every replay equals the eager activation + quantizer sequence bit for bit."""
+    torch = gpu
+    n, nb = 14336, 56
+    dg = torch.empty(n, dtype=torch.float32, device="cuda")
+    du = torch.empty_like(dg)
+    q = torch.empty(nb * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        jk.dev_quantize_row_q8_k_gated(jk.ACT_SWIGLU, dg, du, n, q, nb, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        jk.dev_quantize_row_q8_k_gated(jk.ACT_SWIGLU, dg, du, n, q, nb, torch.cuda.current_stream().cuda_stream)
+    h = torch.empty_like(dg)
+    ref = torch.empty_like(q)
+    for seed in (1, 2, 3):
+        gt, ut = gate_up(n, 500 + seed)
+        dg.copy_(torch.from_numpy(gt))
+        du.copy_(torch.from_numpy(ut))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        jk.dev_swiglu_f32(dg, du, n, h)
+        jk.dev_quantize_row_q8_k(h, n, ref, nb)
+        torch.cuda.synchronize()
+        assert np.array_equal(q.cpu().numpy(), ref.cpu().numpy()), seed
