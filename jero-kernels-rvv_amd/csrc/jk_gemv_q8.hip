@@ -900,53 +900,72 @@ static jk_status launch_fast(hipStream_t s, GemvGroup &g, size_t lds) {
     return launch_fast_run<Q, LPR, F32, 8, 1>(s, g, lds, 8);
 }
 
+// One job on the global-activation kernel (caller blocks only; validated by the callers).
+template <int Q>
+static jk_status launch_global_job(hipStream_t s, const GemvJob &j) {
+    const int nwg = (j.r1 - j.r0 + 15) / 16;
+    hipLaunchKernelGGL(gemv_q8_global_kernel<Q>, dim3((unsigned)nwg), dim3(256), 0, s, j.w, j.xq, j.y, j.r0, j.r1,
+                       j.am_slots);
+    JK_TRY(check_launch("gemv_q8_global_kernel"));
+    if (j.am_slots) JK_TRY(launch_argmax_slots(s, j.am_slots, nwg, j.am_index));
+    return JK_OK;
+}
+
+// One launch of jobs whose activations all fit the LDS budget and share an activation kind.
+template <int Q>
+static jk_status launch_staged_group(hipStream_t s, GemvGroup &g) {
+    using T = QTraits<Q>;
+    int max_nb = 0;
+    for (int i = 0; i < g.njobs; ++i) max_nb = max(max_nb, g.job[i].w.nb);
+    const size_t lds = (size_t)max_nb * T::XB;
+    const bool f32 = g.job[0].xf != nullptr;
+    const bool wide = T::K && max_nb > 32;  // one wave per row for long K-quant rows
+    const int lpr = wide ? 64 : 16;
+    if ((max_nb + lpr - 1) / lpr <= kFastU<Q>) {
+        if (wide && f32) return launch_fast<Q, 64, true>(s, g, lds);
+        if (wide) return launch_fast<Q, 64, false>(s, g, lds);
+        if (f32) return launch_fast<Q, 16, true>(s, g, lds);
+        return launch_fast<Q, 16, false>(s, g, lds);
+    }
+    // full workgroups when every CU gets at least one
+    const int rpu = wide ? 1 : 4;
+    long units = 0;
+    for (int i = 0; i < g.njobs; ++i) units += (g.job[i].r1 - g.job[i].r0 + rpu - 1) / rpu;
+    const bool full = units >= (long)cu_count() * kFullWaves<Q>;
+    constexpr int FW = kFullWaves<Q>;
+    if (wide && f32) return full ? launch_group_run<Q, 64, true, FW>(s, g, lds) : launch_group_run<Q, 64, true, 4>(s, g, lds);
+    if (wide) return full ? launch_group_run<Q, 64, false, FW>(s, g, lds) : launch_group_run<Q, 64, false, 4>(s, g, lds);
+    if (f32) return full ? launch_group_run<Q, 16, true, FW>(s, g, lds) : launch_group_run<Q, 16, true, 4>(s, g, lds);
+    return full ? launch_group_run<Q, 16, false, FW>(s, g, lds) : launch_group_run<Q, 16, false, 4>(s, g, lds);
+}
+
+// Each job goes to the staged kernels when its own activation fits the LDS budget, else (caller
+// blocks only: f32 jobs beyond the budget are refused by the callers before any launch) to the
+// global-activation kernel. Staged jobs are launched together in runs of one activation kind.
 template <int Q>
 static jk_status launch_group_q(hipStream_t s, const GemvJob *jobs, int n) {
     using T = QTraits<Q>;
-    int max_nb = 0;
-    for (int i = 0; i < n; ++i) max_nb = max(max_nb, jobs[i].w.nb);
-    const size_t lds = (size_t)max_nb * T::XB;
-    if (lds > (size_t)kMaxLdsX) {
-        for (int i = 0; i < n; ++i) {
-            const GemvJob &j = jobs[i];
-            if (j.xf) return fail(JK_CAPABILITY_MISMATCH, "gemv: f32 activations need K <= %d",
-                                  kMaxLdsX / T::XB * T::XE);
-            const int nwg = (j.r1 - j.r0 + 15) / 16;
-            hipLaunchKernelGGL(gemv_q8_global_kernel<Q>, dim3((unsigned)nwg), dim3(256), 0, s, j.w, j.xq, j.y, j.r0,
-                               j.r1, j.am_slots);
-            JK_TRY(check_launch("gemv_q8_global_kernel"));
-            if (j.am_slots) JK_TRY(launch_argmax_slots(s, j.am_slots, nwg, j.am_index));
-        }
-        return JK_OK;
-    }
-    const bool wide = T::K && max_nb > 32;  // one wave per row for long K-quant rows
-    // one launch per run of jobs with the same activation kind (f32 or caller blocks)
-    int base = 0;
-    while (base < n) {
-        const bool f32 = jobs[base].xf != nullptr;
-        GemvGroup g;
-        memset(&g, 0, sizeof g);
-        while (base < n && g.njobs < kMaxGemvJobs && (jobs[base].xf != nullptr) == f32) g.job[g.njobs++] = jobs[base++];
-        const int lpr = wide ? 64 : 16;
-        if ((max_nb + lpr - 1) / lpr <= kFastU<Q>) {
-            if (wide && f32) JK_TRY((launch_fast<Q, 64, true>(s, g, lds)));
-            else if (wide) JK_TRY((launch_fast<Q, 64, false>(s, g, lds)));
-            else if (f32) JK_TRY((launch_fast<Q, 16, true>(s, g, lds)));
-            else JK_TRY((launch_fast<Q, 16, false>(s, g, lds)));
+    GemvGroup g;
+    memset(&g, 0, sizeof g);
+    for (int i = 0; i < n; ++i) {
+        const GemvJob &j = jobs[i];
+        if ((size_t)j.w.nb * T::XB > (size_t)kMaxLdsX) {
+            JK_TRY(launch_global_job<Q>(s, j));
             continue;
         }
-        // full workgroups when every CU gets at least one
-        const int rpu = wide ? 1 : 4;
-        long units = 0;
-        for (int i = 0; i < g.njobs; ++i) units += (g.job[i].r1 - g.job[i].r0 + rpu - 1) / rpu;
-        const bool full = units >= (long)cu_count() * kFullWaves<Q>;
-        constexpr int FW = kFullWaves<Q>;
-        if (wide && f32) JK_TRY(full ? (launch_group_run<Q, 64, true, FW>(s, g, lds)) : (launch_group_run<Q, 64, true, 4>(s, g, lds)));
-        else if (wide) JK_TRY(full ? (launch_group_run<Q, 64, false, FW>(s, g, lds)) : (launch_group_run<Q, 64, false, 4>(s, g, lds)));
-        else if (f32) JK_TRY(full ? (launch_group_run<Q, 16, true, FW>(s, g, lds)) : (launch_group_run<Q, 16, true, 4>(s, g, lds)));
-        else JK_TRY(full ? (launch_group_run<Q, 16, false, FW>(s, g, lds)) : (launch_group_run<Q, 16, false, 4>(s, g, lds)));
+        if (g.njobs > 0 && (g.njobs == kMaxGemvJobs || (g.job[0].xf != nullptr) != (j.xf != nullptr))) {
+            JK_TRY(launch_staged_group<Q>(s, g));
+            memset(&g, 0, sizeof g);
+        }
+        g.job[g.njobs++] = j;
     }
+    if (g.njobs > 0) JK_TRY(launch_staged_group<Q>(s, g));
     return JK_OK;
+}
+
+size_t gemv_f32_max_cols(int q) {
+    const int xb = fmt_of(q).be == 256 ? kXkBytes : kX0Bytes;
+    return (size_t)(kMaxLdsX / xb) * (size_t)fmt_of(q).be;
 }
 
 // All jobs share one weight format and have r1 > r0 (checked by the callers).

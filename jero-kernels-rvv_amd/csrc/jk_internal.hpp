@@ -195,6 +195,12 @@ jk_status launch_absmax_i8(hipStream_t s, const float *x, const float *norm_w, s
                            float eps, int8_t *q, float *scales);
 jk_status launch_gemv_q8(hipStream_t s, const WeightDev &w, const void *x, float *y, int r0, int r1);
 jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n);
+// Largest K a grouped GEMV job of device format q can take as f32 activations (the launch
+// quantizes them into LDS); caller Q8 blocks have no limit.
+size_t gemv_f32_max_cols(int q);
+// Validated GEMV + fused argmax job over all rows of w (am_slots left null).
+jk_status gemv_argmax_job(const char *what, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
+                          float *y, int32_t *index, GemvJob *out);
 jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y);
 // Token count from which jk_bitlinear_i8 uses the MFMA GEMM path.
 constexpr int kBitlinearMfmaMinTokens = 16;

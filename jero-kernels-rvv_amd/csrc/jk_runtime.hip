@@ -141,6 +141,42 @@ static float read_trailer_scale(const uint8_t *t, size_t len) {
 // Device weight limits: row and block indices are 32-bit inside the kernels.
 static const size_t kMaxRows = (size_t)1 << 30;
 
+// Compute entry points accept only a complete (sealed) handle.
+static jk_status weight_usable(const jk_weight *w, const char *what) {
+    if (!w) return fail(JK_TENSOR_BOUNDS, "%s: null weight handle", what);
+    if (!w->ready) return fail(JK_TENSOR_BOUNDS, "%s: the weight has not been sealed (jk_weight_seal)", what);
+    return JK_OK;
+}
+
+// Validation of a GEMV whose argmax is fused into its store phase (gemv_* followed by
+// argmax_f32, quant_q8.rs:1586-3273 and lib.rs:662): the job over all rows of w, with the
+// argmax slots still to be filled in by the caller.
+jk_status gemv_argmax_job(const char *what, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
+                          float *y, int32_t *index, GemvJob *out) {
+    JK_TRY(weight_usable(w, what));
+    if (!has_q8_gemv(w->quant))
+        return fail(JK_CAPABILITY_MISMATCH, "%s: %s has no quant_q8 GEMV", what, quant_name(w->quant));
+    if ((x_q8 == nullptr) == (x_f32 == nullptr))
+        return fail(JK_TENSOR_BOUNDS, "%s: exactly one of x_q8 and x_f32 must be set", what);
+    if (x_q8 ? x_len != (size_t)w->dev.nb : x_len != (size_t)w->dev.cols)
+        return fail(JK_TENSOR_BOUNDS, "%s: activation length %zu does not match the weight", what, x_len);
+    if ((uintptr_t)x_q8 % 4 || (uintptr_t)x_f32 % 16)
+        return fail(JK_TENSOR_BOUNDS, "%s: x_q8 must be 4-byte and x_f32 16-byte aligned", what);
+    if (x_f32 && (size_t)w->dev.cols > gemv_f32_max_cols(w->dev.quant))
+        return fail(JK_CAPABILITY_MISMATCH, "%s: f32 activations need K <= %zu, got %d", what,
+                    gemv_f32_max_cols(w->dev.quant), w->dev.cols);
+    if (!index) return fail(JK_TENSOR_BOUNDS, "%s: null pointer", what);
+    memset(out, 0, sizeof *out);
+    out->w = w->dev;
+    out->xq = x_q8;
+    out->xf = x_f32;
+    out->y = y;
+    out->am_index = index;
+    out->r0 = 0;
+    out->r1 = w->dev.rows;
+    return JK_OK;
+}
+
 }  // namespace jk
 
 using namespace jk;
@@ -437,12 +473,6 @@ jk_status jk_weight_seal(jk_weight *w) {
     return JK_OK;
 }
 
-// Compute entry points accept only a complete (sealed) handle.
-static jk_status weight_usable(const jk_weight *w, const char *what) {
-    if (!w) return fail(JK_TENSOR_BOUNDS, "%s: null weight handle", what);
-    if (!w->ready) return fail(JK_TENSOR_BOUNDS, "%s: the weight has not been sealed (jk_weight_seal)", what);
-    return JK_OK;
-}
 
 jk_status jk_weight_free(jk_weight *w) {
     if (!w) return JK_OK;
@@ -625,6 +655,9 @@ static jk_status gemv_job_check(const jk_gemv_job *j, size_t i, GemvJob *out) {
         return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: row range %zu..%zu out of bounds for %d rows", i,
                     j->row_begin, j->row_end, w->dev.rows);
     if (!j->y && j->row_end > j->row_begin) return fail(JK_TENSOR_BOUNDS, "gemv_q8_batch: job %zu: null output", i);
+    if (j->x_f32 && (size_t)w->dev.cols > gemv_f32_max_cols(w->dev.quant))
+        return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_batch: job %zu: f32 activations need K <= %zu, got %d", i,
+                    gemv_f32_max_cols(w->dev.quant), w->dev.cols);
     memset(out, 0, sizeof *out);
     out->w = w->dev;
     out->xq = j->x_q8;
@@ -731,27 +764,10 @@ jk_status jk_argmax_f32(jk_stream s, const float *x, size_t n, int32_t *index, v
 
 jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
                             float *y, int32_t *index, void *ws, size_t ws_bytes) {
-    JK_TRY(weight_usable(w, "gemv_q8_argmax"));
-    if (!has_q8_gemv(w->quant))
-        return fail(JK_CAPABILITY_MISMATCH, "gemv_q8_argmax: %s has no quant_q8 GEMV", quant_name(w->quant));
-    if ((x_q8 == nullptr) == (x_f32 == nullptr))
-        return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: exactly one of x_q8 and x_f32 must be set");
-    if (x_q8 ? x_len != (size_t)w->dev.nb : x_len != (size_t)w->dev.cols)
-        return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: activation length %zu does not match the weight", x_len);
-    if ((uintptr_t)x_q8 % 4 || (uintptr_t)x_f32 % 16)
-        return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: x_q8 must be 4-byte and x_f32 16-byte aligned");
-    if (!index) return fail(JK_TENSOR_BOUNDS, "gemv_q8_argmax: null pointer");
-    JK_TRY(argmax_ws_check("gemv_q8_argmax", ws, ws_bytes, (size_t)w->dev.rows));
     GemvJob j;
-    memset(&j, 0, sizeof j);
-    j.w = w->dev;
-    j.xq = x_q8;
-    j.xf = x_f32;
-    j.y = y;
+    JK_TRY(gemv_argmax_job("gemv_q8_argmax", w, x_q8, x_f32, x_len, y, index, &j));
+    JK_TRY(argmax_ws_check("gemv_q8_argmax", ws, ws_bytes, (size_t)w->dev.rows));
     j.am_slots = static_cast<unsigned long long *>(ws);
-    j.am_index = index;
-    j.r0 = 0;
-    j.r1 = w->dev.rows;
     return launch_gemv_group((hipStream_t)s, &j, 1);
 }
 

@@ -330,6 +330,41 @@ def test_gemv_q8_batch_mixed_jobs(gpu):
             assert same_bits(got, ref), mismatch(got, ref)
 
 
+def test_gemv_q8_batch_activation_beyond_lds_budget(gpu):
+    """A caller-block job whose activation exceeds the LDS budget (Q4_K, K = 51200: 200 blocks of
+    336 staged bytes > 60 KiB) runs on the global-activation kernel while small-K jobs of the same
+    format in the same call, f32 included, stay on the staged kernels; an f32 job beyond the budget
+    is refused before anything is launched (no output is written)."""
+    torch = gpu
+    specs = [(Q4_K, 40, 51200, False), (Q4_K, 96, 4096, True), (Q4_K, 24, 4096, False)]
+    jobs, expect, outs = [], [], []
+    for i, (quant, rows, cols, use_f32) in enumerate(specs):
+        raw = synth.gguf_weights(quant, rows, cols, seed=70 + i)
+        w = jk.Weight(jk.TensorView(f"w{i}", quant, [rows, cols], raw), rows, cols)
+        x = synth.activations(cols, 80 + i)
+        xq = x_blocks(quant, x)
+        y = empty(torch, 4 * rows)
+        jobs.append((w, None if use_f32 else dev(torch, xq), torch.from_numpy(x).cuda() if use_f32 else None, y, 0,
+                     rows))
+        expect.append(O.gemv_q8(quant, [rows, cols], raw, xq, rows))
+        outs.append((y, rows))
+    jk.dev_gemv_q8_batch(jobs)
+    torch.cuda.synchronize()
+    for (y, n), ref in zip(outs, expect):
+        got = host(y, np.float32, n)
+        assert same_bits(got, ref), mismatch(got, ref)
+    # the same caller-block job first, then an f32 job with K beyond the budget: refused, and the
+    # first job's output is left as it was
+    big = jobs[0]
+    xf_big = torch.from_numpy(synth.activations(51200, 90)).cuda()
+    for y, _ in outs:
+        y.fill_(7)
+    with pytest.raises(jk.CapabilityMismatch, match="f32 activations need K"):
+        jk.dev_gemv_q8_batch([big, (big[0], None, xf_big, outs[1][0], 0, 40)])
+    torch.cuda.synchronize()
+    assert bool((outs[0][0] == 7).all()) and bool((outs[1][0] == 7).all())
+
+
 def test_gemv_q8_batch_validation(gpu):
     torch = gpu
     raw = synth.gguf_weights(Q4_K, 4, 256, seed=1)
