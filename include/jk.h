@@ -343,6 +343,16 @@ jk_status jk_argmax_f32(jk_stream s, const float *x, size_t n, int32_t *index, v
  * function corresponds: gemv_* followed by argmax_f32. */
 jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
                             float *y, int32_t *index, void *workspace, size_t workspace_bytes);
+/* jk_gemv_q8_argmax without a workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc); it has no
+ * counterpart in the reference. The argmax slots live in a static array of the library, one
+ * copy per GPU (about 2 MiB, held until the process ends), so the weight may have at most
+ * 262144 output rows (JK_TENSOR_BOUNDS beyond). The call allocates nothing. Calls on one GPU
+ * share that array: calls that overlap on one GPU (other streams, unordered host threads)
+ * race and must not be issued; each call overwrites every slot it reads. Results are those of
+ * jk_gemv_q8_argmax. */
+jk_status jk_gemv_q8_argmax_noalloc(jk_stream s, const jk_weight *w, const void *x_q8, const float *x_f32,
+                                    size_t x_len, float *y, int32_t *index);
 
 /* -------------------------------------------------------------- BitLinear */
 /* bitlinear_i8_rvv (ime.rs:882-938) applied to m tokens: y[m][rows] from act[m][k]

@@ -198,6 +198,8 @@ jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n);
 // Largest K a grouped GEMV job of device format q can take as f32 activations (the launch
 // quantizes them into LDS); caller Q8 blocks have no limit.
 size_t gemv_f32_max_cols(int q);
+// Looks up this device's copy of the no-alloc entry point's static scratch (jk_noalloc.hip).
+jk_status noalloc_setup();
 // Validated GEMV + fused argmax job over all rows of w (am_slots left null).
 jk_status gemv_argmax_job(const char *what, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
                           float *y, int32_t *index, GemvJob *out);

@@ -188,7 +188,7 @@ int jk_abi_version(void) { return JK_ABI_VERSION; }
 
 jk_status jk_init(int device) {
     JK_HIP(hipSetDevice(device));
-    return JK_OK;
+    return noalloc_setup();
 }
 
 jk_status jk_stream_create(jk_stream *out) {

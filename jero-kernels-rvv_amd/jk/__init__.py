@@ -651,3 +651,9 @@ def dev_argmax_f32(x, n, index, ws, stream=None, ws_bytes=None):
 def dev_gemv_q8_argmax(w: Weight, x_q8, x_f32, x_len, y, index, ws, stream=None, ws_bytes=None):
     _check(lib().jk_gemv_q8_argmax(_vp(stream or 0), w.handle, _vp(_ptr(x_q8)), _vp(_ptr(x_f32)), _sz(x_len),
                                    _vp(_ptr(y)), _vp(_ptr(index)), _vp(_ptr(ws)), _sz(_ws_bytes(ws, ws_bytes))))
+
+
+def dev_gemv_q8_argmax_noalloc(w: Weight, x_q8, x_f32, x_len, y, index, stream=None):
+    """jk_gemv_q8_argmax with the argmax slots in the library's static device scratch."""
+    _check(lib().jk_gemv_q8_argmax_noalloc(_vp(stream or 0), w.handle, _vp(_ptr(x_q8)), _vp(_ptr(x_f32)),
+                                           _sz(x_len), _vp(_ptr(y)), _vp(_ptr(index))))
