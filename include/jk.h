@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define JK_ABI_VERSION 1
+#define JK_ABI_VERSION 2
 
 typedef enum jk_status {
     JK_OK = 0,
@@ -75,7 +75,7 @@ typedef struct jk_block_q8k {
     int16_t bsums[16];
 } jk_block_q8k;
 
-/* The fields of jero_core::TensorView the path reads (name, quant, shape, bytes). */
+/* The fields of jero_core::TensorView the path reads (name, quant, shape, bytes, offset). */
 typedef struct jk_tensor_view {
     const char *name;
     int32_t quant; /* jk_quant */
@@ -83,6 +83,7 @@ typedef struct jk_tensor_view {
     size_t ndim;
     const void *bytes; /* host memory */
     size_t byte_len;
+    size_t offset; /* TensorView::offset: the tensor's byte offset in its file (reported in errors only) */
 } jk_tensor_view;
 
 /* QuantizedActQ8 (repack.rs:462-486) on the device, as logical row-major arrays carved
@@ -106,8 +107,21 @@ typedef struct jk_weight_info {
     size_t gguf_bytes;   /* bytes of the GGUF payload it was built from */
 } jk_weight_info;
 
+/* K3Error's payload for the most recent failure on the calling thread. For JK_TENSOR_BOUNDS the
+ * fields are TensorBoundsError's (quant.rs:403-411, repack.rs:2725-2778): tensor_name, offset,
+ * byte_len, buffer_len and reason, with the values the reference puts there for the same check
+ * (0 where it reports none); for the other kinds only tensor_name and reason are set. The strings
+ * stay valid until the next failing call on the same thread. status is JK_OK when nothing failed. */
+typedef struct jk_error_info {
+    jk_status status;
+    const char *tensor_name;
+    size_t offset, byte_len, buffer_len;
+    const char *reason;
+} jk_error_info;
+
 /* ---------------------------------------------------------------- runtime */
 const char *jk_last_error(void);
+jk_status jk_last_error_info(jk_error_info *out);
 int jk_abi_version(void);
 /* Selects the device for this thread's subsequent calls. */
 jk_status jk_init(int device);
@@ -360,7 +374,37 @@ jk_status jk_gemv_q8_argmax_noalloc(jk_stream s, const jk_weight *w, const void 
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act,
                           const float *act_scales, size_t m, size_t k, float *y, size_t y_len);
 
+/* convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790) on the device over a run of block pairs: TQ2_0
+ * block k (66 bytes, crate layout: the f16 scale bits, then 64 bytes of 2-bit fields t + 1) holds
+ * the 256 trits of I2_S blocks 2k and 2k + 1 (32 bytes each). i2s_blocks must be 2 * tq2_blocks. */
+jk_status jk_convert_i2_s_to_tq2_0(jk_stream s, const void *i2s, size_t i2s_blocks, uint16_t scale_f16_bits,
+                                   void *tq2, size_t tq2_blocks);
+
 /* ------------------------------------------- host tier (synchronous mirrors) */
+/* The jk_host_* mirrors run on a per-thread stream and per-thread device scratch (grown on
+ * demand, kept until jk_host_release_thread), and keep the weights of the TensorViews they are
+ * given resident: a view is uploaded once, keyed by its byte range, format, shape and a
+ * fingerprint of sampled bytes, and later calls with it perform no upload and no allocation
+ * (tests/wave4_zero_alloc_gemv.rs:88+ is the reference's zero-allocation contract for these
+ * paths). The bytes behind a cached view must not change while it is cached: after changing or
+ * freeing them call jk_host_cache_invalidate (or jk_host_cache_clear). Entries beyond the byte
+ * limit (default 64 GiB; 0 turns the cache off) are evicted least recently used. No reference
+ * function corresponds to this control surface. */
+typedef struct jk_host_stats {
+    uint64_t weight_uploads;  /* views uploaded (cache misses, and every call with the cache off) */
+    uint64_t cache_hits;      /* calls served by a resident weight */
+    uint64_t cache_evictions;
+    uint64_t device_allocs;   /* device allocations made by the host tier (uploads and scratch growth) */
+    uint64_t cached_weights, cached_bytes, cache_limit;
+} jk_host_stats;
+jk_status jk_host_cache_set_limit(size_t bytes);
+/* Drops every cached weight whose view overlaps [bytes, bytes + len). */
+jk_status jk_host_cache_invalidate(const void *bytes, size_t len);
+jk_status jk_host_cache_clear(void);
+jk_status jk_host_get_stats(jk_host_stats *out);
+/* Frees the calling thread's host-tier stream and scratch. */
+jk_status jk_host_release_thread(void);
+
 /* quantize_row_q8_0 (quant_q8.rs:395), quantize_row_q8_k (576). */
 jk_status jk_host_quantize_row_q8_0(const float *x, size_t n, jk_block_q8_0 *out, size_t out_len);
 jk_status jk_host_quantize_row_q8_k(const float *x, size_t n, jk_block_q8k *out, size_t out_len);
@@ -414,6 +458,9 @@ jk_status jk_host_swiglu_f32(float *out, size_t out_len, const float *gate, size
 jk_status jk_host_relu_squared_gate_f32(float *out, size_t out_len, const float *gate, size_t gate_len,
                                         const float *up, size_t up_len);
 jk_status jk_host_argmax_f32(const float *x, size_t n, int64_t *index);
+/* convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790): blk0 and blk1 are 32 bytes, out 66 bytes. */
+jk_status jk_host_convert_i2_s_blocks_to_tq2_0(const uint8_t *blk0, const uint8_t *blk1, uint16_t scale_f16_bits,
+                                               uint8_t *out);
 /* bitlinear_i8_rvv (ime.rs:882-938). */
 jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view *w, const int8_t *act,
                                size_t act_len, float act_scale);

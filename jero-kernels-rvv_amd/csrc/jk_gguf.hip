@@ -319,11 +319,13 @@ jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t ch
     // TensorView over the mapped bytes: shape [ne0, ne1] = [cols, rows].
     const size_t shape[2] = {(size_t)t.ne[0], (size_t)t.ne[1]};
     jk_tensor_view v = {t.name.c_str(), (int32_t)t.type, shape, 2, g->map + g->data_start + t.rel_offset,
-                        (size_t)t.nbytes};
+                        (size_t)t.nbytes, g->data_start + t.rel_offset};
     jk_weight_layout L;
     JK_TRY(jk_weight_layout_for(&v, shape[1], shape[0], &L));
     jk_weight *w = nullptr;
     JK_TRY(jk_weight_create(s, &L, &w));
+    w->name = t.name;
+    w->offset = v.offset;
     if (chunk_bytes == 0) chunk_bytes = (size_t)32 << 20;
     const size_t tile_bytes = 8 * L.row_bytes;
     const size_t tiles_per_chunk = std::max<size_t>(1, chunk_bytes / tile_bytes);

@@ -41,6 +41,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <string>
 #include <vector>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -134,6 +135,8 @@ struct GemvGroup {
 
 struct jk_weight {
     jk::WeightDev dev = {};  // dev.quant: the device layout (dev_quant of quant)
+    std::string name;        // TensorView::name / offset of the tensor it was built from (for errors)
+    size_t offset = 0;
     int quant = 0;           // GGUF format of the uploaded tensor
     int device = 0;
     size_t device_bytes = 0;
@@ -149,8 +152,16 @@ struct jk_weight {
 
 namespace jk {
 
-// Thread-local error reporting behind jk_last_error().
+// Thread-local error reporting behind jk_last_error() / jk_last_error_info(). fail() takes the
+// tensor_name from the message's "name: " prefix; fail_tb() sets TensorBoundsError's fields.
+struct Tb {
+    const char *name;
+    size_t offset, byte_len, buffer_len;
+};
 jk_status fail(jk_status st, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+jk_status fail_tb(const Tb &t, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// The view's fields as TensorView::name / offset / byte_len / as_bytes().len() report them.
+Tb tb_view(const jk_tensor_view *w);
 jk_status hip_fail(hipError_t e, const char *what);
 void clear_error();
 
@@ -178,6 +189,8 @@ jk_status check_launch(const char *what);
 // Repacks GGUF rows [r0, r1) (gguf: exactly those rows' bytes, in device memory) into w's planes.
 jk_status launch_repack(hipStream_t s, const WeightDev &w, int gguf_quant, const uint8_t *gguf, int r0, int r1);
 jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1, float *out);
+// convert_i2_s_blocks_to_tq2_0 over n output blocks (2n I2_S blocks in, 66-byte TQ2_0 blocks out).
+jk_status launch_i2s_to_tq2(hipStream_t s, const uint8_t *i2s, size_t n, uint16_t d_bits, uint8_t *tq2);
 jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk_block_q8_0 *out);
 jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk_block_q8k *out);
 jk_status launch_quantize_act_q8(hipStream_t s, const float *x, const jk_act_q8 &a);

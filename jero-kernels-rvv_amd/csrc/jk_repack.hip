@@ -301,6 +301,40 @@ __device__ void dequant_block(const WeightDev &w, int r, int b, float *out) {
     }
 }
 
+// convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790) over n output blocks: TQ2_0 block k from I2_S
+// blocks 2k and 2k + 1. One thread per output dword: dword j (j < 16) of the 64-byte payload
+// holds elements 16j..16j+15, which lie in I2_S block (16j) / 128 at positions p..p+15 (p a
+// multiple of 16), i.e. group g = p % 32 .. +15 of field (p / 32); the thread assembles them
+// from the 16 source bytes g.. with the field's shift. Thread 16 of each block writes d.
+__global__ __launch_bounds__(256) void i2s_to_tq2_kernel(const uint8_t *__restrict__ i2s, size_t n,
+                                                         uint16_t d_bits, uint8_t *__restrict__ tq2) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t k = t / 17;
+    const int j = (int)(t % 17);
+    if (k >= n) return;
+    uint8_t *dst = tq2 + k * 66;
+    if (j == 16) {
+        dst[0] = (uint8_t)(d_bits & 0xFF);
+        dst[1] = (uint8_t)(d_bits >> 8);
+        return;
+    }
+    const int e0 = 16 * j;                      // first element of the dword
+    const uint8_t *blk = i2s + (2 * k + (size_t)(e0 / 128)) * 32;
+    const int pos = e0 % 128, field = pos / 32, g0 = pos % 32;
+    const int shift = 6 - 2 * field;            // unpack_i2_s_block_i8: t[32f + g] = (b[g] >> (6 - 2f)) & 3
+    for (int i = 0; i < 4; ++i) {
+        uint32_t byte = 0;
+        for (int q = 0; q < 4; ++q) byte |= (((uint32_t)blk[g0 + 4 * i + q] >> shift) & 3u) << (2 * q);
+        dst[2 + 4 * j + i] = (uint8_t)byte;     // the stored field is t + 1 = the I2_S field
+    }
+}
+
+jk_status launch_i2s_to_tq2(hipStream_t s, const uint8_t *i2s, size_t n, uint16_t d_bits, uint8_t *tq2) {
+    const size_t threads = n * 17;
+    hipLaunchKernelGGL(i2s_to_tq2_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, i2s, n, d_bits, tq2);
+    return check_launch("i2s_to_tq2_kernel");
+}
+
 __global__ __launch_bounds__(256) void dequant_rows_kernel(WeightDev w, int r0, int r1, float *__restrict__ out) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t total = (size_t)(r1 - r0) * (size_t)w.nb;

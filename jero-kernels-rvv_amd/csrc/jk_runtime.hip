@@ -16,23 +16,59 @@
 
 namespace jk {
 
-static thread_local std::string g_err;
+// The most recent failure on this thread: K3Error's payload (TensorBoundsError's tensor_name,
+// offset, byte_len, buffer_len and reason; the reason alone for the other kinds).
+struct ErrInfo {
+    jk_status status = JK_OK;
+    std::string name, reason;
+    size_t offset = 0, byte_len = 0, buffer_len = 0;
+};
+static thread_local ErrInfo g_err;
+
+static jk_status set_error(jk_status st, const char *name, size_t off, size_t bl, size_t buf, const char *fmt,
+                           va_list ap) {
+    char msg[512];
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    g_err.status = st;
+    g_err.reason = msg;
+    g_err.offset = off;
+    g_err.byte_len = bl;
+    g_err.buffer_len = buf;
+    if (name) {
+        g_err.name = name;
+    } else {
+        // messages name their tensor or operation first ("name: reason")
+        const char *colon = strstr(msg, ": ");
+        g_err.name = colon && !memchr(msg, ' ', (size_t)(colon - msg)) ? std::string(msg, (size_t)(colon - msg)) : "";
+    }
+    return st;
+}
 
 jk_status fail(jk_status st, const char *fmt, ...) {
-    char buf[512];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    set_error(st, nullptr, 0, 0, 0, fmt, ap);
     va_end(ap);
-    g_err = buf;
     return st;
+}
+
+jk_status fail_tb(const Tb &t, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    set_error(JK_TENSOR_BOUNDS, t.name ? t.name : "", t.offset, t.byte_len, t.buffer_len, fmt, ap);
+    va_end(ap);
+    return JK_TENSOR_BOUNDS;
+}
+
+Tb tb_view(const jk_tensor_view *w) {
+    return Tb{w->name ? w->name : "<tensor>", w->offset, w->byte_len, w->byte_len};
 }
 
 jk_status hip_fail(hipError_t e, const char *what) {
     return fail(JK_DEVICE_ERROR, "%s failed: %s", what, hipGetErrorString(e));
 }
 
-void clear_error() { g_err.clear(); }
+void clear_error() { g_err = ErrInfo(); }
 
 jk_status check_launch(const char *what) {
     hipError_t e = hipGetLastError();
@@ -79,31 +115,31 @@ jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, si
     if (!w || (!w->bytes && w->byte_len) || (w->ndim && !w->shape))
         return fail(JK_TENSOR_BOUNDS, "null tensor view");
     if (w->quant != quant)
-        return fail(JK_TENSOR_BOUNDS, "%s: expected %s quant type, got %s", tname(w),
+        return fail_tb(tb_view(w), "%s: expected %s quant type, got %s", tname(w),
                     quant_name(quant), quant_name(w->quant));
-    if (w->ndim == 0) return fail(JK_TENSOR_BOUNDS, "%s: empty tensor shape", tname(w));
+    if (w->ndim == 0) return fail_tb(tb_view(w), "%s: empty tensor shape", tname(w));
     const Fmt f = fmt_of(quant);
     if (w->ndim == 2) {
         size_t d0 = w->shape[0], d1 = w->shape[1];
         if (out_len == d0 && in_len == d1 && d1 % f.be == 0) { *rows = d0; *cols = d1; }
         else if (out_len == d1 && in_len == d0 && d0 % f.be == 0) { *rows = d1; *cols = d0; }
         else
-            return fail(JK_TENSOR_BOUNDS,
+            return fail_tb(tb_view(w),
                         "%s: matrix shape [%zu, %zu] does not match output len %zu and %s-aligned input len %zu",
                         tname(w), d0, d1, out_len, quant_name(quant), in_len);
     } else {
         size_t total = num_elements(w);
         if (in_len == 0 || out_len == 0 || in_len % f.be || out_len * in_len != total)
-            return fail(JK_TENSOR_BOUNDS, "%s: tensor elements %zu do not match output len %zu * input len %zu",
+            return fail_tb(tb_view(w), "%s: tensor elements %zu do not match output len %zu * input len %zu",
                         tname(w), total, out_len, in_len);
         *rows = out_len;
         *cols = in_len;
     }
     if (*rows == 0 || *cols == 0)
-        return fail(JK_TENSOR_BOUNDS, "%s: empty matrix [%zu, %zu]", tname(w), *rows, *cols);
+        return fail_tb(tb_view(w), "%s: empty matrix [%zu, %zu]", tname(w), *rows, *cols);
     size_t need = (*rows * *cols / f.be) * f.bb + trailer_bytes(quant);
     if (w->byte_len < need)
-        return fail(JK_TENSOR_BOUNDS, "%s: %s buffer length %zu < required %zu", tname(w),
+        return fail_tb(tb_view(w), "%s: %s buffer length %zu < required %zu", tname(w),
                     quant_name(quant), w->byte_len, need);
     return JK_OK;
 }
@@ -111,23 +147,23 @@ jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, si
 // validate_matrix_view (repack.rs:1208-1281) with validate_matrix_shape (1172-1206).
 static jk_status validate_matrix_view(const jk_tensor_view *w, size_t rows, size_t cols) {
     if (rows == 0 || cols == 0)
-        return fail(JK_TENSOR_BOUNDS, "%s: repack dimensions must be non-zero, got [%zu, %zu]", tname(w), rows, cols);
+        return fail_tb(tb_view(w), "%s: repack dimensions must be non-zero, got [%zu, %zu]", tname(w), rows, cols);
     const Fmt f = fmt_of(w->quant);
     if (cols % f.be)
-        return fail(JK_TENSOR_BOUNDS, "%s: cols %zu not a multiple of block size %d", tname(w), cols, f.be);
+        return fail_tb(tb_view(w), "%s: cols %zu not a multiple of block size %d", tname(w), cols, f.be);
     if (w->ndim == 1) {
         if (rows * cols != w->shape[0])
-            return fail(JK_TENSOR_BOUNDS, "%s: 1D shape %zu != rows * cols %zu", tname(w), w->shape[0], rows * cols);
+            return fail_tb(tb_view(w), "%s: 1D shape %zu != rows * cols %zu", tname(w), w->shape[0], rows * cols);
     } else if (w->ndim == 2) {
         size_t d0 = w->shape[0], d1 = w->shape[1];
         if (!((d0 == rows && d1 == cols) || (d0 == cols && d1 == rows)))
-            return fail(JK_TENSOR_BOUNDS, "%s: shape [%zu, %zu] does not match [%zu, %zu]", tname(w), d0, d1, rows, cols);
+            return fail_tb(tb_view(w), "%s: shape [%zu, %zu] does not match [%zu, %zu]", tname(w), d0, d1, rows, cols);
     } else {
-        return fail(JK_TENSOR_BOUNDS, "%s: expected 1D or 2D weight tensor, got %zuD", tname(w), w->ndim);
+        return fail_tb(tb_view(w), "%s: expected 1D or 2D weight tensor, got %zuD", tname(w), w->ndim);
     }
     size_t need = rows * (cols / f.be) * f.bb + trailer_bytes(w->quant);
     if (w->byte_len < need)
-        return fail(JK_TENSOR_BOUNDS, "%s: buffer length %zu < required %zu", tname(w), w->byte_len, need);
+        return fail_tb(tb_view(w), "%s: buffer length %zu < required %zu", tname(w), w->byte_len, need);
     return JK_OK;
 }
 
@@ -183,7 +219,18 @@ using namespace jk;
 
 extern "C" {
 
-const char *jk_last_error(void) { return g_err.c_str(); }
+const char *jk_last_error(void) { return g_err.reason.c_str(); }
+
+jk_status jk_last_error_info(jk_error_info *out) {
+    if (!out) return JK_TENSOR_BOUNDS;
+    out->status = g_err.status;
+    out->tensor_name = g_err.name.c_str();
+    out->offset = g_err.offset;
+    out->byte_len = g_err.byte_len;
+    out->buffer_len = g_err.buffer_len;
+    out->reason = g_err.reason.c_str();
+    return JK_OK;
+}
 int jk_abi_version(void) { return JK_ABI_VERSION; }
 
 jk_status jk_init(int device) {
@@ -358,6 +405,8 @@ jk_status jk_weight_upload(jk_stream s, const jk_tensor_view *w, size_t rows, si
                             : 0.0f;
     jk_weight *h = nullptr;
     JK_TRY(alloc_handle(w->quant, rows, cols, scale, &h));
+    h->name = tname(w);
+    h->offset = w->offset;
     const jk_status st = upload_rows((hipStream_t)s, h, (const uint8_t *)w->bytes, 0, rows, "jk_weight_upload");
     if (st != JK_OK) {
         free_handle(h);
@@ -507,18 +556,22 @@ jk_status jk_weight_dequantize_rows(jk_stream s, const jk_weight *w, size_t r0, 
 jk_status jk_quantize_row_q8_0(jk_stream s, const float *x, size_t n, jk_block_q8_0 *out, size_t out_blocks) {
     // validate_activation_quant_slice (quant_q8.rs:111-149)
     if (n == 0 || n % 32)
-        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_0: input length %zu must be a positive multiple of 32", n);
+        return fail_tb(Tb{"quantize_row_q8_0_f32", 0, n * 4, out_blocks},
+                       "quantize_row_q8_0_f32: input length %zu must be a positive multiple of 32", n);
     if (out_blocks != n / 32)
-        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_0: output block count %zu != expected %zu", out_blocks, n / 32);
+        return fail_tb(Tb{"quantize_row_q8_0_f32", 0, n * 4, out_blocks},
+                       "quantize_row_q8_0_f32: output block count %zu != expected %zu", out_blocks, n / 32);
     if (!x || !out) return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_0: null pointer");
     return launch_quantize_q8_0((hipStream_t)s, x, n / 32, out);
 }
 
 jk_status jk_quantize_row_q8_k(jk_stream s, const float *x, size_t n, jk_block_q8k *out, size_t out_blocks) {
     if (n == 0 || n % 256)
-        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: input length %zu must be a positive multiple of 256", n);
+        return fail_tb(Tb{"quantize_row_q8_k", 0, n * 4, out_blocks},
+                       "quantize_row_q8_k: input length %zu must be a positive multiple of 256", n);
     if (out_blocks != n / 256)
-        return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: output block count %zu != expected %zu", out_blocks, n / 256);
+        return fail_tb(Tb{"quantize_row_q8_k", 0, n * 4, out_blocks},
+                       "quantize_row_q8_k: output block count %zu != expected %zu", out_blocks, n / 256);
     if (!x || !out) return fail(JK_TENSOR_BOUNDS, "quantize_row_q8_k: null pointer");
     return launch_quantize_q8_k((hipStream_t)s, x, n / 256, out);
 }
@@ -592,7 +645,8 @@ static jk_status gemv_check(const jk_weight *w, int quant, const void *x, size_t
         return fail(JK_CAPABILITY_MISMATCH, "%s: %s has no quant_q8 GEMV", name, quant_name(w->quant));
     // check_q8_block_len (quant_q8.rs:1562-1578)
     if (nx != (size_t)w->dev.nb)
-        return fail(JK_TENSOR_BOUNDS, "%s: x_blocks len %zu != expected %d", name, nx, w->dev.nb);
+        return fail_tb(Tb{w->name.c_str(), w->offset, nx, (size_t)w->dev.nb}, "%s: x_blocks len %zu != expected %d",
+                       name, nx, w->dev.nb);
     if (r0 > r1 || r1 > (size_t)w->dev.rows)
         return fail(JK_TENSOR_BOUNDS, "%s: row range %zu..%zu out of bounds for %d rows", name, r0, r1, w->dev.rows);
     if (!x || (!y && r1 > r0)) return fail(JK_TENSOR_BOUNDS, "%s: null pointer", name);
@@ -771,6 +825,21 @@ jk_status jk_gemv_q8_argmax(jk_stream s, const jk_weight *w, const void *x_q8, c
     return launch_gemv_group((hipStream_t)s, &j, 1);
 }
 
+// ------------------------------------------------ I2_S -> TQ2_0 conversion
+// convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790) over a run of block pairs.
+jk_status jk_convert_i2_s_to_tq2_0(jk_stream s, const void *i2s, size_t i2s_blocks, uint16_t scale_f16_bits,
+                                   void *tq2, size_t tq2_blocks) {
+    if (i2s_blocks != 2 * tq2_blocks)
+        return fail(JK_TENSOR_BOUNDS, "convert_i2_s_blocks_to_tq2_0: %zu I2_S blocks != 2 x %zu TQ2_0 blocks",
+                    i2s_blocks, tq2_blocks);
+    if (tq2_blocks == 0) return JK_OK;
+    if (!i2s || !tq2) return fail(JK_TENSOR_BOUNDS, "convert_i2_s_blocks_to_tq2_0: null pointer");
+    if (tq2_blocks > ((size_t)1 << 31) / 17)
+        return fail(JK_TENSOR_BOUNDS, "convert_i2_s_blocks_to_tq2_0: %zu blocks exceed one launch", tq2_blocks);
+    return launch_i2s_to_tq2((hipStream_t)s, static_cast<const uint8_t *>(i2s), tq2_blocks, scale_f16_bits,
+                             static_cast<uint8_t *>(tq2));
+}
+
 // -------------------------------------------------------------- vec_dot (f32)
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
     JK_TRY(weight_usable(w, "vec_dot"));
@@ -790,12 +859,17 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
     // execute_gemm_repacked_rows (repack.rs:2725-2778)
     if (!w || !act) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null argument");
     JK_TRY(weight_usable(w, "gemm_repacked"));
+    // the reference reports the output bytes and the repacked storage (aligned_bytes) as byte_len /
+    // buffer_len; the storage here is the device layout
     if (act->k != (size_t)w->dev.cols)
-        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: activation k %zu != weight cols %d", act->k, w->dev.cols);
+        return fail_tb(Tb{"gemm_repacked", 0, y_len * 4, w->device_bytes},
+                       "gemm_repacked: activation K (%zu) != weight cols (%d)", act->k, w->dev.cols);
     if (r0 > r1 || r1 > (size_t)w->dev.rows)
-        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: row range %zu..%zu out of bounds for %d rows", r0, r1, w->dev.rows);
+        return fail_tb(Tb{"gemm_repacked", r0, r1 >= r0 ? r1 - r0 : 0, (size_t)w->dev.rows},
+                       "gemm_repacked: invalid row_range %zu..%zu for weight rows %d", r0, r1, w->dev.rows);
     if (y_len != act->m * (r1 - r0))
-        return fail(JK_TENSOR_BOUNDS, "gemm_repacked: output len %zu != %zu * %zu", y_len, act->m, r1 - r0);
+        return fail_tb(Tb{"gemm_repacked", 0, y_len * 4, act->m * (r1 - r0) * 4},
+                       "gemm_repacked: output length %zu != m (%zu) * sub_rows (%zu)", y_len, act->m, r1 - r0);
     if (r1 == r0 || act->m == 0) return JK_OK;
     if (!y) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null output");
     if (act->m > ((size_t)1 << 24))
@@ -807,7 +881,8 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
 jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
                            size_t r0, size_t r1) {
     if (act && act->m != 1)
-        return fail(JK_TENSOR_BOUNDS, "gemv_repacked requires act.m() == 1, got %zu", act->m);
+        return fail_tb(Tb{"gemv_repacked", 0, y_len * 4, w ? w->device_bytes : 0},
+                       "gemv_repacked: gemv_repacked requires act.m() == 1, got %zu", act->m);
     return jk_gemm_repacked(s, w, act, y, y_len, r0, r1);
 }
 
@@ -817,11 +892,11 @@ jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, co
     JK_TRY(weight_usable(w, "bitlinear"));
     int q = w->quant;
     // validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
-    if (!has_bitlinear(q))
-        return fail(JK_TENSOR_BOUNDS, "bitlinear: unsupported quant type %s", quant_name(q));
+    const Tb wt{w->name.c_str(), w->offset, w->gguf_bytes, w->gguf_bytes};
+    if (!has_bitlinear(q)) return fail_tb(wt, "%s: bitlinear: unsupported quant type %s", wt.name, quant_name(q));
     if (m == 0 || k != (size_t)w->dev.cols || y_len != m * (size_t)w->dev.rows)
-        return fail(JK_TENSOR_BOUNDS, "bitlinear: weights [%d, %d] do not match m=%zu k=%zu out=%zu", w->dev.rows,
-                    w->dev.cols, m, k, y_len);
+        return fail_tb(wt, "%s: bitlinear: weights [%d, %d] do not match m=%zu k=%zu out=%zu", wt.name, w->dev.rows,
+                       w->dev.cols, m, k, y_len);
     if (m >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "bitlinear: m=%zu too large", m);
     if (!act || !act_scales || !y) return fail(JK_TENSOR_BOUNDS, "bitlinear: null pointer");
     // batches of tokens run as an int8-MFMA GEMM (same per-block arithmetic and block order)

@@ -50,7 +50,17 @@ OK, TENSOR_BOUNDS, CAPABILITY_MISMATCH, DEVICE_ERROR = 0, 1, 2, 3
 
 
 class K3Error(RuntimeError):
-    """Base of the errors the reference path returns."""
+    """Base of the errors the reference path returns. TensorBoundsError's payload (tensor_name,
+    offset, byte_len, buffer_len, reason) comes from jk_last_error_info."""
+
+    def __init__(self, reason: str, tensor_name: str = "", offset: int = 0, byte_len: int = 0,
+                 buffer_len: int = 0):
+        super().__init__(reason)
+        self.reason = reason
+        self.tensor_name = tensor_name
+        self.offset = offset
+        self.byte_len = byte_len
+        self.buffer_len = buffer_len
 
 
 class TensorBoundsError(K3Error):
@@ -74,7 +84,18 @@ _vp = C.c_void_p
 
 class TensorViewC(C.Structure):
     _fields_ = [("name", C.c_char_p), ("quant", C.c_int32), ("shape", C.POINTER(_sz)), ("ndim", _sz),
-                ("bytes", _vp), ("byte_len", _sz)]
+                ("bytes", _vp), ("byte_len", _sz), ("offset", _sz)]
+
+
+class ErrorInfoC(C.Structure):
+    _fields_ = [("status", C.c_int), ("tensor_name", C.c_char_p), ("offset", _sz), ("byte_len", _sz),
+                ("buffer_len", _sz), ("reason", C.c_char_p)]
+
+
+class HostStatsC(C.Structure):
+    _fields_ = [("weight_uploads", C.c_uint64), ("cache_hits", C.c_uint64), ("cache_evictions", C.c_uint64),
+                ("device_allocs", C.c_uint64), ("cached_weights", C.c_uint64), ("cached_bytes", C.c_uint64),
+                ("cache_limit", C.c_uint64)]
 
 
 class ActQ8C(C.Structure):
@@ -125,10 +146,19 @@ def header_symbols() -> list[str]:
     return sorted(set(re.findall(r"\b(jk_[a-z0-9_]+)\s*\(", text)))
 
 
+def last_error_info() -> dict:
+    """jk_last_error_info: the payload of the calling thread's most recent failure."""
+    e = ErrorInfoC()
+    lib().jk_last_error_info(C.byref(e))
+    return {"status": e.status, "tensor_name": (e.tensor_name or b"").decode(errors="replace"), "offset": e.offset,
+            "byte_len": e.byte_len, "buffer_len": e.buffer_len, "reason": (e.reason or b"").decode(errors="replace")}
+
+
 def _check(status: int) -> None:
     if status != OK:
-        msg = lib().jk_last_error().decode(errors="replace")
-        raise _ERRORS.get(status, K3Error)(msg)
+        info = last_error_info()
+        raise _ERRORS.get(status, K3Error)(info["reason"], info["tensor_name"], info["offset"], info["byte_len"],
+                                           info["buffer_len"])
 
 
 def _ptr(x) -> int:
@@ -143,10 +173,11 @@ def _ptr(x) -> int:
 
 
 class TensorView:
-    """jero_core::TensorView fields the path reads: name, quant, shape, bytes."""
+    """jero_core::TensorView fields the path reads: name, quant, shape, bytes, offset."""
 
-    def __init__(self, name: str, quant: int, shape, data):
+    def __init__(self, name: str, quant: int, shape, data, offset: int = 0):
         self.name = name
+        self.offset = int(offset)
         self.quant = int(quant)
         self.shape = tuple(int(s) for s in shape)
         self.data = np.ascontiguousarray(np.frombuffer(memoryview(data), dtype=np.uint8)
@@ -156,7 +187,32 @@ class TensorView:
 
     def c(self) -> TensorViewC:
         return TensorViewC(self._name_b, self.quant, C.cast(self._shape_c, C.POINTER(_sz)), len(self.shape),
-                           self.data.ctypes.data, self.data.nbytes)
+                           self.data.ctypes.data, self.data.nbytes, self.offset)
+
+
+# ---------------------------------------------------------------- host-tier residency
+def host_cache_set_limit(nbytes: int) -> None:
+    _check(lib().jk_host_cache_set_limit(_sz(nbytes)))
+
+
+def host_cache_invalidate(data) -> None:
+    """Drops cached weights whose view overlaps the bytes of data (a numpy array or TensorView)."""
+    a = data.data if isinstance(data, TensorView) else data
+    _check(lib().jk_host_cache_invalidate(_vp(a.ctypes.data), _sz(a.nbytes)))
+
+
+def host_cache_clear() -> None:
+    _check(lib().jk_host_cache_clear())
+
+
+def host_stats() -> dict:
+    st = HostStatsC()
+    _check(lib().jk_host_get_stats(C.byref(st)))
+    return {name: getattr(st, name) for name, _ in HostStatsC._fields_}
+
+
+def host_release_thread() -> None:
+    _check(lib().jk_host_release_thread())
 
 
 # ---------------------------------------------------------------- host tier
@@ -352,6 +408,18 @@ def bitlinear_i8(out: np.ndarray, weights: TensorView, act_i8, act_scale: float)
     v = weights.c()
     _check(lib().jk_host_bitlinear_i8(_vp(out.ctypes.data), _sz(out.size), C.byref(v), _vp(a.ctypes.data),
                                       _sz(a.size), C.c_float(act_scale)))
+
+
+def convert_i2_s_blocks_to_tq2_0(blk0, blk1, scale_f16_bits: int) -> np.ndarray:
+    """convert_i2_s_blocks_to_tq2_0 (ime.rs:767): two 32-byte I2_S blocks -> one 66-byte TQ2_0 block."""
+    a = np.ascontiguousarray(blk0, dtype=np.uint8).reshape(-1)
+    b = np.ascontiguousarray(blk1, dtype=np.uint8).reshape(-1)
+    if a.size != 32 or b.size != 32:
+        raise TensorBoundsError("convert_i2_s_blocks_to_tq2_0: I2_S blocks are 32 bytes")
+    out = np.zeros(66, np.uint8)
+    _check(lib().jk_host_convert_i2_s_blocks_to_tq2_0(_vp(a.ctypes.data), _vp(b.ctypes.data),
+                                                      C.c_uint16(scale_f16_bits), _vp(out.ctypes.data)))
+    return out
 
 
 # ---------------------------------------------------------------- device tier
@@ -569,6 +637,11 @@ def dev_gemm_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
 def dev_gemv_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
     _check(lib().jk_gemv_repacked(_vp(stream or 0), w.handle, C.byref(act), _vp(_ptr(y)), _sz(y_len), _sz(r0),
                                   _sz(r1)))
+
+
+def dev_convert_i2_s_to_tq2_0(i2s, i2s_blocks, scale_f16_bits, tq2, tq2_blocks, stream=None):
+    _check(lib().jk_convert_i2_s_to_tq2_0(_vp(stream or 0), _vp(_ptr(i2s)), _sz(i2s_blocks),
+                                          C.c_uint16(scale_f16_bits), _vp(_ptr(tq2)), _sz(tq2_blocks)))
 
 
 def dev_bitlinear_i8(w: Weight, act, act_scales, m, k, y, y_len, stream=None):

@@ -371,6 +371,24 @@ void or_unpack_i2_s_block_i8(const uint8_t *blk, int8_t *out) {
     }
 }
 
+/* convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790): the 256 trits of two I2_S blocks (blk0 then
+ * blk1, each in unpack_i2_s_block_i8 order) re-packed as a crate-layout TQ2_0 block: the f16
+ * scale bits first, then byte i = (t[4i] + 1) | (t[4i+1] + 1) << 2 | (t[4i+2] + 1) << 4 |
+ * (t[4i+3] + 1) << 6. */
+void or_convert_i2_s_blocks_to_tq2_0(const uint8_t *blk0, const uint8_t *blk1, uint16_t scale_f16_bits,
+                                     uint8_t *out) {
+    int8_t t[256];
+    or_unpack_i2_s_block_i8(blk0, t);
+    or_unpack_i2_s_block_i8(blk1, t + 128);
+    out[0] = (uint8_t)(scale_f16_bits & 0xFF);
+    out[1] = (uint8_t)(scale_f16_bits >> 8);
+    for (int i = 0; i < 64; i++) {
+        const uint8_t q0 = (uint8_t)(t[4 * i] + 1) & 3, q1 = (uint8_t)(t[4 * i + 1] + 1) & 3;
+        const uint8_t q2 = (uint8_t)(t[4 * i + 2] + 1) & 3, q3 = (uint8_t)(t[4 * i + 3] + 1) & 3;
+        out[2 + i] = (uint8_t)(q0 | (q1 << 2) | (q2 << 4) | (q3 << 6));
+    }
+}
+
 /* quant.rs:94-102 (scale_i8_into_f32) */
 static void scale_i8_into_f32(float scale, const int8_t *q, float *out, int n) {
     if (scale == 0.0f) { for (int i = 0; i < n; i++) out[i] = 0.0f; return; }

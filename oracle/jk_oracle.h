@@ -106,6 +106,8 @@ float or_unpack_iq4_nl_block_i8(const uint8_t *blk, int8_t *out);
 void or_dequantize_iq4_nl_block(const uint8_t *blk, float *out);
 float or_unpack_tq2_0_block_i8(const uint8_t *blk, int8_t *out);
 void or_unpack_i2_s_block_i8(const uint8_t *blk, int8_t *out);
+void or_convert_i2_s_blocks_to_tq2_0(const uint8_t *blk0, const uint8_t *blk1, uint16_t scale_f16_bits,
+                                     uint8_t *out);
 void or_dequantize_i2_s_block(const uint8_t *blk, float scale, float *out);
 float or_read_i2_s_trailer_scale(const uint8_t *trailer, size_t len);
 int or_dequantize_row_bytes(int quant, const uint8_t *row, size_t row_len, size_t n_cols,

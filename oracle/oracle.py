@@ -144,6 +144,14 @@ def unpack_i2_s_block_i8(block: np.ndarray) -> np.ndarray:
     return out
 
 
+def convert_i2_s_blocks_to_tq2_0(blk0: np.ndarray, blk1: np.ndarray, scale_f16_bits: int) -> np.ndarray:
+    a = np.ascontiguousarray(blk0, dtype=np.uint8)
+    b = np.ascontiguousarray(blk1, dtype=np.uint8)
+    out = np.zeros(66, dtype=np.uint8)
+    lib().or_convert_i2_s_blocks_to_tq2_0(_p(a), _p(b), C.c_uint16(scale_f16_bits), _p(out))
+    return out
+
+
 def dequantize_i2_s_block(block: np.ndarray, scale: float) -> np.ndarray:
     b = np.ascontiguousarray(block, dtype=np.uint8)
     out = np.zeros(128, dtype=np.float32)

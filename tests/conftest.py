@@ -23,5 +23,6 @@ def gpu():
         pytest.fail("GPU test run without a visible GPU")
     jk.lib()  # raises if libjk.so is missing: no fallback path exists
     jk.init(0)
+    jk.host_cache_set_limit(4 << 30)  # the host tier's resident weights, across the whole session
     torch.cuda.init()
     return torch

@@ -16,7 +16,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert len(names) > 40
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.jk_abi_version() == 1
+    assert lib.jk_abi_version() == 2
 
 
 def test_block_struct_layouts():
@@ -149,3 +149,57 @@ def test_weight_layout_validation_fails_closed():
         jk.block_scaled_layout(jk.TensorView("w", jk.Q4_K, [512, 67], raw[:-1]), 67, 512)
     with pytest.raises(jk.TensorBoundsError):  # no inference from rows = cols = 0 (for_tensor)
         jk.block_scaled_layout(jk.TensorView("w", jk.Q4_K, [512, 67], raw), 0, 0)
+
+
+def _err(fn, *args):
+    with pytest.raises(jk.K3Error) as ei:
+        fn(*args)
+    return ei.value
+
+
+def test_tensor_bounds_error_fields():
+    """TensorBoundsError's payload (tensor_name, offset, byte_len, buffer_len, reason) as the
+    reference's validators fill it: view checks report the view (validate_quant_matvec_dimensions,
+    quant.rs:1816-1888: name, TensorView::offset, byte_len, buffer length); check_q8_block_len
+    (quant_q8.rs:1562-1578) the block counts; validate_q8_block_row_bytes (quant_q8.rs:644-664)
+    the row bytes; validate_activation_quant_slice (quant_q8.rs:111-149) the input bytes and the
+    output block count. Every check runs before any device work, so no GPU is needed."""
+    raw = np.zeros(4 * 18, np.uint8)
+    x = np.zeros(1, jk.BLOCK_Q8_0)
+    out = np.zeros(4, np.float32)
+    e = _err(jk.gemv_q8_0_q8_0, out, jk.TensorView("blk.3.ffn_up.weight", jk.Q4_0, [4, 32], raw, offset=4096), x)
+    assert isinstance(e, jk.TensorBoundsError)
+    assert (e.tensor_name, e.offset, e.byte_len, e.buffer_len) == ("blk.3.ffn_up.weight", 4096, 72, 72)
+    assert "expected Q8_0 quant type" in e.reason
+    e = _err(jk.gemv_q4_0_q8_0, out, jk.TensorView("w", jk.Q4_0, [4, 32], raw[:-1], offset=7), x)
+    assert (e.tensor_name, e.offset, e.byte_len, e.buffer_len) == ("w", 7, 71, 71)
+    assert "buffer length 71 < required 72" in e.reason
+    e = _err(jk.gemv_q4_0_q8_0, out, jk.TensorView("w", jk.Q4_0, [4, 32], raw), np.zeros(2, jk.BLOCK_Q8_0))
+    assert isinstance(e, jk.TensorBoundsError) and e.tensor_name == "w"
+    e = _err(jk.vec_dot_q4_0_q8_0, raw[:17], x)
+    assert (e.tensor_name, e.offset, e.byte_len, e.buffer_len) == ("vec_dot_q4_0_q8_0", 0, 17, 18)
+    e = _err(jk.quantize_row_q8_0, np.ones(31, np.float32))
+    assert (e.tensor_name, e.offset, e.byte_len) == ("quantize_row_q8_0_f32", 0, 124)
+    e = _err(jk.quantize_row_q8_k, np.ones(300, np.float32))
+    assert (e.tensor_name, e.byte_len) == ("quantize_row_q8_k", 1200)
+    e = _err(jk.bitlinear_i8, np.zeros(1, np.float32),
+             jk.TensorView("bw", jk.I2_S, [1, 128], np.zeros(32, np.uint8), offset=64), np.zeros(128, np.int8), 1.0)
+    assert (e.tensor_name, e.offset, e.byte_len, e.buffer_len) == ("bw", 64, 32, 32)
+    info = jk.last_error_info()
+    assert info["status"] == jk.TENSOR_BOUNDS and info["tensor_name"] == "bw" and info["reason"] == e.reason
+    e = _err(jk.dequantize_tensor_row, jk.TensorView("emb", jk.Q8_0, [32, 2], np.zeros(68, np.uint8), offset=9), 2,
+             np.zeros(32, np.float32))
+    assert (e.tensor_name, e.offset, e.byte_len) == ("emb", 9, 68) and "out of bounds" in e.reason
+
+
+def test_static_archive_exports_every_declared_symbol():
+    """libjk.a (for a Rust build.rs) holds the same entry points as libjk.so."""
+    import os
+    import subprocess
+
+    path = os.path.join(os.path.dirname(jk.LIB_PATH), "libjk.a")
+    assert os.path.exists(path), "libjk.a not built"
+    out = subprocess.run(["nm", "-g", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    defined = {line.split()[-1] for line in out.splitlines() if line.strip() and not line.endswith(":")}
+    missing = [n for n in jk.header_symbols() if n not in defined]
+    assert not missing, missing

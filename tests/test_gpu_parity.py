@@ -676,3 +676,36 @@ def test_host_tier_vec_dot_more_formats(gpu):
         f = np.zeros(7, np.float32)
         fn(f, jk.TensorView("w", quant, [1024, 7], raw), x)
         assert same_bits(f, O.vec_dot_f32(quant, [1024, 7], raw, x, 7)), quant
+
+
+# ------------------------------------------------------------ I2_S -> TQ2_0
+def test_convert_i2_s_to_tq2_0(gpu):
+    """convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790) on the device over 5000 random block pairs
+    (every byte value, I2_S field value 3 included) and through the host mirror, bit for bit
+    against the oracle; then BitLinear over the converted weights equals the oracle's TQ2_0
+    BitLinear of the same bytes."""
+    torch = gpu
+    rng = np.random.default_rng(11)
+    n = 5000
+    i2s = rng.integers(0, 256, size=(2 * n, 32), dtype=np.uint8)
+    i2s[:256, 0] = np.arange(256)
+    bits = 0x3555
+    ref = np.concatenate([O.convert_i2_s_blocks_to_tq2_0(i2s[2 * k], i2s[2 * k + 1], bits) for k in range(n)])
+    out = torch.full((n * 66,), 0xAB, dtype=torch.uint8, device="cuda")
+    jk.dev_convert_i2_s_to_tq2_0(dev(torch, i2s), 2 * n, bits, out, n)
+    torch.cuda.synchronize()
+    got = host(out, np.uint8)
+    assert np.array_equal(got, ref)
+    for k in (0, 1, 4999):
+        assert np.array_equal(jk.convert_i2_s_blocks_to_tq2_0(i2s[2 * k], i2s[2 * k + 1], bits), ref[66 * k:66 * k + 66])
+    # the converted bytes as a TQ2_0 weight of 50 rows x 25600 (trits of field value 3 included)
+    rows, cols = 50, 100 * 256
+    w = jk.Weight(jk.TensorView("tq2", TQ2_0, [rows, cols], got), rows, cols)
+    act = rng.integers(-128, 128, size=cols, dtype=np.int8)
+    y = empty(torch, 4 * rows)
+    sc = torch.tensor([0.375], dtype=torch.float32, device="cuda")
+    jk.dev_bitlinear_i8(w, dev(torch, act), sc, 1, cols, y, rows)
+    torch.cuda.synchronize()
+    assert same_bits(host(y, np.float32, rows), O.bitlinear_i8(TQ2_0, [rows, cols], ref, act, 0.375, rows))
+    with pytest.raises(jk.TensorBoundsError):
+        jk.dev_convert_i2_s_to_tq2_0(dev(torch, i2s), 3, bits, out, 1)

@@ -236,3 +236,56 @@ def test_block32_quantizer_sums():
     assert a.qs[0, 3] == 0 and a.qs[0, 7] == 0 and a.qs[0, 9] == 0
     assert abs(a.sums[0, 0] - 14.5) < 1e-5 and abs(a.sums[0, 1] - 4.0) < 1e-5
     assert np.all(a.qs[0, 40:] == 0)  # zero-padded tail
+
+
+def _i2s_kat_tensor():
+    """The I2_S weights of src/ime.rs:1243-1262 (3 rows x 256, trits from (r + gp) % 3 etc.)."""
+    rows, bpr = 3, 2
+    raw = np.zeros(rows * bpr * 32 + 32, np.uint8)
+    for r in range(rows):
+        for b in range(bpr):
+            off = (r * bpr + b) * 32
+            for gp in range(32):
+                t0, t1, t2, t3 = (r + gp) % 3, (b + gp + 1) % 3, (r + b + gp) % 3, (gp + 2) % 3
+                raw[off + gp] = (t0 << 6) | (t1 << 4) | (t2 << 2) | t3
+    raw[rows * bpr * 32:rows * bpr * 32 + 4] = list(struct.pack("<f", 0.25))
+    return raw
+
+
+def test_convert_i2_s_blocks_to_tq2_0_kat():
+    # src/ime.rs:1289-1303: the first two blocks of the test tensor with scale bits 0x3800 (0.5):
+    # the TQ2_0 unpack gives scale 0.5 and the two I2_S unpacks, in order
+    raw = _i2s_kat_tensor()
+    tq2 = O.convert_i2_s_blocks_to_tq2_0(raw[0:32], raw[32:64], 0x3800)
+    scale, t = O.unpack_tq2_0_block_i8(tq2)
+    assert abs(scale - 0.5) < 1e-6
+    assert np.array_equal(t[:128], O.unpack_i2_s_block_i8(raw[0:32]))
+    assert np.array_equal(t[128:], O.unpack_i2_s_block_i8(raw[32:64]))
+    assert list(tq2[:2]) == [0x00, 0x38]
+
+
+def test_convert_i2_s_to_tq2_0_exhaustive_bytes_and_bitlinear_round_trip():
+    # every byte value in every group position of both blocks: the unpacked trits agree with the
+    # I2_S unpack (closed form: field f of byte g is element 32 f + g); an I2_S field value of 3
+    # (not a trit, t = 2) must come out as TQ2_0 field 3 as well (the reference keeps & 0x03)
+    for v in range(256):
+        blk0 = np.full(32, v, np.uint8)
+        blk1 = np.roll(np.arange(32, dtype=np.uint8) * 7 + v, v % 32).astype(np.uint8)
+        out = O.convert_i2_s_blocks_to_tq2_0(blk0, blk1, 0x3C00)
+        _, t = O.unpack_tq2_0_block_i8(out)
+        ref = np.array([((int(b) >> (6 - 2 * f)) & 3) - 1 for blk in (blk0, blk1) for f in range(4) for b in blk],
+                       np.int8)
+        assert np.array_equal(t, ref), v
+    # BitLinear over the converted rows equals BitLinear over the I2_S rows when the f16 scale is
+    # the tensor scale exactly (0.25): same trits, same scale, same block order (two I2_S blocks
+    # per TQ2_0 block, and the reference sums each block's integer dot before scaling)
+    raw = _i2s_kat_tensor()
+    rows, cols = 3, 256
+    tq2 = np.concatenate([O.convert_i2_s_blocks_to_tq2_0(raw[64 * r:64 * r + 32], raw[64 * r + 32:64 * r + 64], 0x3400)
+                          for r in range(rows)])
+    act = np.array([(i % 15) - 7 for i in range(cols)], np.int8)
+    y_i2s = O.bitlinear_i8(I2_S, [rows, cols], raw, act, 0.5, rows)
+    y_tq2 = O.bitlinear_i8(TQ2_0, [rows, cols], tq2, act, 0.5, rows)
+    ref = np.array([sum(float(w) * (float(a) * 0.5) for w, a in
+                        zip(O.dequantize_tensor_row(I2_S, [rows, cols], raw, r, cols), act)) for r in range(rows)])
+    assert np.allclose(y_i2s, ref, atol=1e-4) and np.allclose(y_tq2, ref, atol=1e-4)
