@@ -254,8 +254,11 @@ def main() -> int:
     # ------------------------------------------------------------ prefill GEMM (Q8_0)
     # Weights rotate over 10 device copies (620 MB, beyond the 256 MB Infinity Cache); the
     # kernel is timed with HIP events on its own stream around each launch, the activation
-    # quantization (QuantizedActQ8::quantize_into) runs between the timed launches.
-    gemm, sweep = None, []
+    # quantization (QuantizedActQ8::quantize_into) runs between the timed launches. Two modes:
+    # tolerance (jk_gemm_repacked_tol: one fused multiply-add per scale group, within 1e-5 of
+    # each token's output-row L2 norm -- the bar north_star sets for f32 products; the reported
+    # line) and bit-exact (jk_gemm_repacked: the reference's separately rounded epilogue).
+    gemm, sweep, gemm_exact, sweep_exact = None, [], None, []
     s = torch.cuda.current_stream().cuda_stream
     ms_list = [args.gemm_m] if args.gemm_m > 0 else []
     ms_list += [int(v) for v in args.gemm_sweep.split(",") if v.strip() and args.gemm_m > 0]
@@ -270,43 +273,52 @@ def main() -> int:
             gstore = torch.empty(need, dtype=torch.uint8, device=dev)
             act = jk.act_q8_bind(gstore, need, M, K)
             gy = torch.empty(M * N, dtype=torch.float32, device=dev)
-            for i in range(2):
-                jk.dev_quantize_act_q8(gx, M, K, act, s)
-                jk.dev_gemm_repacked(gw[i], act, gy, M * N, 0, N, s)
-            torch.cuda.synchronize()
-            reps = 3 * ncopies
-            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            gev = []
-            g0.record()
-            for i in range(reps):
-                jk.dev_quantize_act_q8(gx, M, K, act, s)
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                jk.dev_gemm_repacked(gw[i % ncopies], act, gy, M * N, 0, N, s)
-                e1.record()
-                gev.append((e0, e1))
-            g1.record()
-            torch.cuda.synchronize()
-            ops = 2.0 * M * N * K
-            step_ms = g0.elapsed_time(g1) / reps
-            kern_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in gev]))
-            tops = ops / (kern_us * 1e-6) / 1e12
-            row = {"m": M, "kernel_us": round(kern_us, 2), "kernel_tops": round(tops, 1),
-                   "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                   "ms_per_call_incl_quantize": round(step_ms, 4)}
-            log(f"gemm Q8_0 M={M}: kernel {kern_us:.1f} us = {tops:.1f} TOPS "
-                f"({step_ms:.3f} ms/call incl. quantize)")
-            if M == args.gemm_m and gemm is None:
-                gemm = {"workload": f"Q8_0 {N}x{K} weights x {M} tokens (QuantizedActQ8 per-32 activations), "
-                                    "outputs bit-identical to the reference recipe",
-                        "ms_per_call": round(step_ms, 4), "tops": round(ops / (step_ms * 1e-3) / 1e12, 1),
+            for mode, fn in (("tolerance", jk.dev_gemm_repacked_tol), ("bit-exact", jk.dev_gemm_repacked)):
+                for i in range(2):
+                    jk.dev_quantize_act_q8(gx, M, K, act, s)
+                    fn(gw[i], act, gy, M * N, 0, N, s)
+                torch.cuda.synchronize()
+                reps = 3 * ncopies
+                g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                gev = []
+                g0.record()
+                for i in range(reps):
+                    jk.dev_quantize_act_q8(gx, M, K, act, s)
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fn(gw[i % ncopies], act, gy, M * N, 0, N, s)
+                    e1.record()
+                    gev.append((e0, e1))
+                g1.record()
+                torch.cuda.synchronize()
+                ops = 2.0 * M * N * K
+                step_ms = g0.elapsed_time(g1) / reps
+                kern_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in gev]))
+                tops = ops / (kern_us * 1e-6) / 1e12
+                row = {"m": M, "mode": mode, "kernel_us": round(kern_us, 2), "kernel_tops": round(tops, 1),
+                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                       "ms_per_call_incl_quantize": round(step_ms, 4)}
+                log(f"gemm Q8_0 M={M} {mode}: kernel {kern_us:.1f} us = {tops:.1f} TOPS "
+                    f"({step_ms:.3f} ms/call incl. quantize)")
+                kname = "gemm_tol_kernel<Q8_0>" if mode == "tolerance" else "gemm_repacked_kernel<Q8_0>"
+                line = {"workload": f"Q8_0 {N}x{K} weights x {M} tokens (QuantizedActQ8 per-32 activations), "
+                                    + ("outputs within 1e-5 of each token's output-row L2 norm of the reference "
+                                       "recipe (one fused multiply-add per scale group)" if mode == "tolerance"
+                                       else "outputs bit-identical to the reference recipe"),
+                        "mode": mode, "ms_per_call": round(step_ms, 4), "tops": round(ops / (step_ms * 1e-3) / 1e12, 1),
                         "kernel_us": row["kernel_us"], "kernel_tops": row["kernel_tops"],
                         "roofline": {"bound": "mfma", "achieved": row["kernel_tops"], "peak": INT8_PEAK_TOPS,
                                      "unit": "TOPS", "frac": row["frac_int8_peak"],
-                                     "traffic": traffic.get(f"gemm_q8_0_m{M}"),
-                                     "kernel": "gemm_repacked_kernel<Q8_0>"}}
-            else:
-                sweep.append(row)
+                                     "traffic": traffic.get(f"gemm_q8_0_m{M}" + ("_tol" if mode == "tolerance"
+                                                                                 else "")),
+                                     "kernel": kname}}
+                if M == args.gemm_m:
+                    if mode == "tolerance" and gemm is None:
+                        gemm = line
+                    elif mode == "bit-exact" and gemm_exact is None:
+                        gemm_exact = line
+                else:
+                    (sweep if mode == "tolerance" else sweep_exact).append(row)
             del gx, gstore, gy
         for w in gw:
             w.free()
@@ -670,6 +682,7 @@ def main() -> int:
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "decode_tok_s_equiv": round(1e3 / ms_per_step * args.layers / 32, 1),
         "roofline": roofline, "per_stage": per_stage, "gemm_q8_0": gemm, "gemm_q8_0_sweep": sweep,
+        "gemm_q8_0_bit_exact": gemm_exact, "gemm_q8_0_bit_exact_sweep": sweep_exact,
         "secondary": secondary,
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,

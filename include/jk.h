@@ -317,6 +317,15 @@ jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t
  * gemv_repacked_rows (repack.rs:4014-4061) is the m == 1 case. */
 jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
                            size_t y_len, size_t row_begin, size_t row_end);
+/* gemm_repacked_rows (repack.rs:4087-4094) in tolerance mode: the same arguments, validation and
+ * errors as jk_gemm_repacked, with each scale group's exact integer partial applied by one fused
+ * multiply-add (acc = fma(partial, xs * ws, acc); formats with mins add -(xsum * wm) as one more
+ * rounded step) instead of the reference's separately rounded product and sum. Every output is
+ * within 1e-5 of its token's output-row L2 norm of the bit-exact result (the tolerance the port
+ * is held to for f32 products); about three times the throughput of jk_gemm_repacked at 512
+ * tokens. No reference function has this rounding: it is the bit-exact call's alternative. */
+jk_status jk_gemm_repacked_tol(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
+                               size_t y_len, size_t row_begin, size_t row_end);
 /* gemv_repacked_view_rows (repack.rs:4045-4061): requires act->m == 1. */
 jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
                            size_t y_len, size_t row_begin, size_t row_end);

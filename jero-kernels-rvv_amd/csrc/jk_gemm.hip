@@ -66,6 +66,17 @@ template <int Q, int TN, int TM> struct GemmChunk {
     float xm[NM][TM];       // activation sum per scale group: per 32-block, or per 16 (Q2_K)
 };
 
+// Writes of 16 i8 values (K elements koff .. koff + 15 of one tile row) into a chunk's LDS
+// tiles: the i8 tiles keep them as bytes in padded rows.
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void put_a(GemmChunk<Q, TN, TM> &c, int row, int koff, uint4 v) {
+    *reinterpret_cast<uint4 *>(c.a + row * kRowB + koff) = v;
+}
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void put_b(GemmChunk<Q, TN, TM> &c, int tok, int koff, uint4 v) {
+    *reinterpret_cast<uint4 *>(c.b + tok * kRowB + koff) = v;
+}
+
 // One 16-byte global load without the streaming hint: a weight tile is read once per
 // token tile, so its lines are meant to stay in L2 for the neighbouring workgroups.
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -212,16 +223,14 @@ __device__ __forceinline__ uint4 crumb4(uint4 v, int sh) {
 // Unpack the staging registers to i8 with repack_block_scaled_range_into_i8's values
 // (repack.rs:1724-2103) and write them, with the scale (and min) of each scale group, to
 // the chunk's LDS tiles.
-template <int Q, int TN, int TM>
-__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, TM> &r, GemmChunk<Q, TN, TM> &c,
-                                            int kc) {
+template <int Q, int TN, int TM, class Chunk>
+__device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, TM> &r, Chunk &c, int kc) {
     using T = Tile<TN, TM>;
     using F = GemmFmt<Q>;
     const int t = threadIdx.x;
     {  // activations
 #pragma unroll
-        for (int i = 0; i < T::XL; ++i)
-            *reinterpret_cast<uint4 *>(c.b + ((t >> 3) + T::THREADS / 8 * i) * kRowB + 16 * (t & 7)) = r.x[i];
+        for (int i = 0; i < T::XL; ++i) put_b(c, (t >> 3) + T::THREADS / 8 * i, 16 * (t & 7), r.x[i]);
 #pragma unroll
         for (int j = 0; j < T::XS; ++j) {
             const int e = T::XS * t + j;
@@ -239,12 +248,12 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
         const int piece = t & 3;
 #pragma unroll
         for (int i = 0; i < (Q == JK_Q8_0 ? 4 : 2); ++i) {
-            uint8_t *dst = c.a + ((t >> 2) + TN / 2 * (i & 1)) * kRowB + 32 * piece;
+            const int arow = (t >> 2) + TN / 2 * (i & 1), k0 = 32 * piece;
             if constexpr (Q == JK_Q8_0) {
-                *reinterpret_cast<uint4 *>(dst + 16 * (i >> 1)) = r.w[i];
+                put_a(c, arow, k0 + 16 * (i >> 1), r.w[i]);
             } else if constexpr (Q == JK_Q4_1) {  // unpack_q4_1_block_i8 (quant.rs:117-129): the nibbles
-                *reinterpret_cast<uint4 *>(dst) = nib4(r.w[i], 0, 0u);
-                *reinterpret_cast<uint4 *>(dst + 16) = nib4(r.w[i], 4, 0u);
+                put_a(c, arow, k0, nib4(r.w[i], 0, 0u));
+                put_a(c, arow, k0 + 16, nib4(r.w[i], 4, 0u));
             } else if constexpr (Q == JK_Q5_1) {  // unpack_q5_1_block_i8 (quant.rs:168-187): nibble | 16 * bit
                 uint32_t lo[4], hi[4];
 #pragma unroll
@@ -253,8 +262,8 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                     lo[k] = (v & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (4 * k)) & 15u);
                     hi[k] = ((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (16 + 4 * k)) & 15u);
                 }
-                *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-                *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                put_a(c, arow, k0, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                put_a(c, arow, k0 + 16, make_uint4(hi[0], hi[1], hi[2], hi[3]));
             } else if constexpr (Q == JK_IQ4_NL) {  // unpack_iq4_nl_block_i8 (quant.rs:333-345)
                 uint32_t lo[4], hi[4];
 #pragma unroll
@@ -262,8 +271,8 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                     lo[k] = iq4nl_lookup(comp(r.w[i], k) & 0x0F0F0F0Fu);
                     hi[k] = iq4nl_lookup((comp(r.w[i], k) >> 4) & 0x0F0F0F0Fu);
                 }
-                *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-                *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                put_a(c, arow, k0, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                put_a(c, arow, k0 + 16, make_uint4(hi[0], hi[1], hi[2], hi[3]));
             } else if constexpr (Q == JK_Q5_0) {
                 // unpack_q5_0_block_i8 (quant.rs:139-157): (nibble | 16 * bit) - 16, bit j of
                 // the word for element j
@@ -275,11 +284,11 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                     hi[k] = (uint32_t)bytes_sub(((v >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes((qh >> (16 + 4 * k)) & 15u),
                                                 0x10101010u);
                 }
-                *reinterpret_cast<uint4 *>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-                *reinterpret_cast<uint4 *>(dst + 16) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                put_a(c, arow, k0, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                put_a(c, arow, k0 + 16, make_uint4(hi[0], hi[1], hi[2], hi[3]));
             } else {
-                *reinterpret_cast<uint4 *>(dst) = nib4(r.w[i], 0, 0x08080808u);
-                *reinterpret_cast<uint4 *>(dst + 16) = nib4(r.w[i], 4, 0x08080808u);
+                put_a(c, arow, k0, nib4(r.w[i], 0, 0x08080808u));
+                put_a(c, arow, k0 + 16, nib4(r.w[i], 4, 0x08080808u));
             }
         }
 #pragma unroll
@@ -293,7 +302,6 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
         return;
     }
     const int row = t >> 1, j = t & 1, h = kc & 1;
-    uint8_t *dst = c.a + row * kRowB;
     if constexpr (Q == JK_Q4_K) {
         // unpack_k4_scales_mins (repack.rs:1158-1170); qs planes (1 + 2c', 2 + 2c') of
         // super-block quarter c' = 2h + j hold elements 64j .. 64j + 63 of the half: low
@@ -310,8 +318,8 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
         }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh) = nib4(r.w[1], 4 * hh, 0u);
-            *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh + 16) = nib4(r.w[2], 4 * hh, 0u);
+            put_a(c, row, 64 * j + 32 * hh, nib4(r.w[1], 4 * hh, 0u));
+            put_a(c, row, 64 * j + 32 * hh + 16, nib4(r.w[2], 4 * hh, 0u));
         }
     } else if constexpr (Q == JK_Q5_K) {
         // The Q4_K arm with the Q5_K bits (repack.rs:1959-2002): quarter c' = 2h + j takes qs
@@ -337,7 +345,7 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     o[k] = ((comp(qv, k) >> (4 * hh)) & 0x0F0F0F0Fu) | (((comp(hv, k) >> (qsh + hh)) & 0x01010101u) << 4);
-                *reinterpret_cast<uint4 *>(dst + 64 * j + 32 * hh + 16 * p) = make_uint4(o[0], o[1], o[2], o[3]);
+                put_a(c, row, 64 * j + 32 * hh + 16 * p, make_uint4(o[0], o[1], o[2], o[3]));
             }
     } else if constexpr (Q == JK_Q2_K) {
         // unpack_q2_k_block_i8 (quant.rs:197-235), repack.rs:1876-1895: 16-group g = 2 jq + part of
@@ -354,9 +362,9 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                 c.ws[g][row] = d * (float)(sc & 15u);
                 c.wm[g][row] = dmin * (float)(sc >> 4);
                 const uint4 qv = r.w[1 + part];
-                *reinterpret_cast<uint4 *>(dst + 32 * jq + 16 * part) =
-                    make_uint4((qv.x >> (2 * jq)) & 0x03030303u, (qv.y >> (2 * jq)) & 0x03030303u,
-                               (qv.z >> (2 * jq)) & 0x03030303u, (qv.w >> (2 * jq)) & 0x03030303u);
+                put_a(c, row, 32 * jq + 16 * part,
+                      make_uint4((qv.x >> (2 * jq)) & 0x03030303u, (qv.y >> (2 * jq)) & 0x03030303u,
+                                 (qv.z >> (2 * jq)) & 0x03030303u, (qv.w >> (2 * jq)) & 0x03030303u));
             }
         }
     } else if constexpr (Q == JK_Q3_K) {
@@ -383,7 +391,7 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                     const uint32_t hb = (comp(hv, k) >> (4 * h + jq)) & 0x01010101u;
                     o[k] = (uint32_t)bytes_sub(v | (hb << 2), 0x04040404u);
                 }
-                *reinterpret_cast<uint4 *>(dst + 32 * jq + 16 * part) = make_uint4(o[0], o[1], o[2], o[3]);
+                put_a(c, row, 32 * jq + 16 * part, make_uint4(o[0], o[1], o[2], o[3]));
             }
         }
     } else if constexpr (Q == JK_Q6_K) {
@@ -404,7 +412,7 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
                 const uint32_t v6 = ((comp(lv, i) >> lsh) & 0x0F0F0F0Fu) | (((comp(hv, i) >> hsh) & 0x03030303u) << 4);
                 o[i] = (uint32_t)bytes_sub(v6, 0x20202020u);
             }
-            *reinterpret_cast<uint4 *>(dst + 16 * g) = make_uint4(o[0], o[1], o[2], o[3]);
+            put_a(c, row, 16 * g, make_uint4(o[0], o[1], o[2], o[3]));
         }
     } else if constexpr (Q == JK_TQ2_0) {
         // plane 2h + j: its dword k holds elements 64j + 16k .. 64j + 16k + 15, the 2-bit
@@ -415,17 +423,17 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t wv = comp(r.w[0], k);
-            *reinterpret_cast<uint4 *>(dst + 64 * j + 16 * k) =
-                make_uint4((uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
-                           (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
-                           (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
-                           (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u));
+            put_a(c, row, 64 * j + 16 * k,
+                  make_uint4((uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
+                             (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
+                             (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
+                             (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u)));
         }
     } else {  // JK_I2_S: 32-group g is 2-bit field g (shift 6 - 2g) of planes 0 (first 16) and 1
         c.ws[2 * j][row] = w.tensor_scale;
         c.ws[2 * j + 1][row] = w.tensor_scale;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) *reinterpret_cast<uint4 *>(dst + 32 * g + 16 * j) = crumb4(r.w[0], 6 - 2 * g);
+        for (int g = 0; g < 4; ++g) put_a(c, row, 32 * g + 16 * j, crumb4(r.w[0], 6 - 2 * g));
     }
 }
 
@@ -433,7 +441,12 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
 // one epilogue per step); for BitLinear (one scale per token and per weight block: 256
 // elements for TQ2_0, 128 for I2_S, 32 for Q8_0) the block's MFMAs accumulate in i32 and the
 // epilogue runs once per block.
-template <int Q, int GB, int TN, int TM>
+// TOL: tolerance mode -- each group's exact integer partial enters the accumulator through one
+// fused multiply-add, acc = fma(f32(c), xs * ws, acc), and formats with mins add -(xsum * wm) with
+// the K = 1 outer-product MFMA accumulating into the accumulators (one rounding each), instead of
+// the reference's separately rounded products and sums. The 1e-5-of-the-row-L2-norm tolerance
+// the port is held to for f32 products allows it; the bit-exact kernel is TOL = false.
+template <int Q, int GB, int TN, int TM, bool TOL = false>
 __global__ __launch_bounds__(2 * TN) __attribute__((amdgpu_waves_per_eu(Tile<TN, TM>::WPE))) void
 gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
     using F = GemmFmt<Q>;
@@ -462,6 +475,7 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
+    v32f tacc = v32f{0};  // TOL: both 32-row blocks' accumulators in the outer product's layout
 
     v16i cacc[NT];  // i32 partials of the current scale block (GB > 1)
 #pragma unroll
@@ -508,6 +522,16 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
             // of block nt in element 16 nt + v.
             const int g = (32 / F::GK) * st + gg;
             const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][srow], xs, v32f{0}, 0, 0, 0);
+            if constexpr (TOL) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        tacc[16 * nt + v] = __builtin_fmaf((float)c[nt][v], p[16 * nt + v], tacc[16 * nt + v]);
+                if constexpr (F::MINS && F::GK == 32)
+                    tacc = __builtin_amdgcn_mfma_f32_32x32x1f32(-cs.wm[st][srow], xsum32, tacc, 0, 0, 0);
+                continue;
+            }
             v32f pm;
             // mins: per 32-group with the 32-block activation sum, or per 16-group (Q2_K) with
             // the 16-element sum (accumulate_scaled_tile_scalar, repack.rs:3061-3077)
@@ -553,7 +577,7 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int n = n0 + RW * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
-                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = acc[nt][v];
+                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = TOL ? tacc[16 * nt + v] : acc[nt][v];
             }
     }
 }
@@ -668,24 +692,26 @@ __global__ __launch_bounds__(64) void gemm16_kernel(WeightDev w, jk_act_q8 a, fl
 static int gemm_tile(int quant, long rows, long m) {
     const long ncu = cu_count();
     auto tiles = [&](long tn, long tm) { return (rows + tn - 1) / tn * ((m + tm - 1) / tm); };
-    // (Q2_K's 16-element mins do not fit the 128 x 64 tile's register budget without spills)
-    if (tiles(128, 64) >= 2 * ncu && quant != JK_Q2_K) return 0;
+    // (the 16-element-group formats do not fit the 128 x 64 tile's register budget without spills)
+    if (tiles(128, 64) >= 2 * ncu && quant != JK_Q2_K && quant != JK_Q3_K && quant != JK_Q6_K) return 0;
     if (tiles(64, 64) >= 2 * ncu) return 1;
     if (tiles(32, 32) >= 2 * ncu || quant == JK_Q6_K || quant == JK_Q3_K || quant == JK_Q2_K) return 2;
     return 3;
 }
 
-template <int Q, int GB, int TN, int TM>
+template <int Q, int GB, int TN, int TM, bool TOL = false>
 static void launch_tile(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     const size_t ntn = (size_t)(r1 - r0 + TN - 1) / TN, ntm = (a.m + TM - 1) / TM;
     const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(Tile<TN, TM>::THREADS);
-    hipLaunchKernelGGL((gemm_repacked_kernel<Q, GB, TN, TM>), grid, block, 0, s, w, a, y, r0, r1);
+    hipLaunchKernelGGL((gemm_repacked_kernel<Q, GB, TN, TM, TOL>), grid, block, 0, s, w, a, y, r0, r1);
 }
 
 template <int Q, int GB>
 static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
-    case 0: launch_tile<Q, GB, 128, 64>(s, w, a, y, r0, r1); break;
+    case 0:
+        if constexpr (GemmFmt<Q>::GK == 32) launch_tile<Q, GB, 128, 64>(s, w, a, y, r0, r1);
+        break;
     case 1: launch_tile<Q, GB, 64, 64>(s, w, a, y, r0, r1); break;
     case 2: launch_tile<Q, GB, 32, 32>(s, w, a, y, r0, r1); break;
     default:
@@ -699,6 +725,43 @@ static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 
         break;
     }
     return check_launch("gemm_repacked_kernel");
+}
+
+// Tolerance-mode launch: the bit-exact launch's tile choice; the 32 x 16 single-wave tiles
+// (VALU scale products) are replaced by 32 x 32 tiles.
+template <int Q>
+static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    // The 16-element-group formats keep the bit-exact kernel (their two groups per step do not fit
+    // the tolerance kernel's register budget); its results are within the tolerance by definition.
+    if constexpr (GemmFmt<Q>::GK == 16) {
+        return launch_gemm<Q, 1>(s, w, a, y, r0, r1);
+    } else {
+        switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
+        case 0: launch_tile<Q, 1, 128, 64, true>(s, w, a, y, r0, r1); break;
+        case 1: launch_tile<Q, 1, 64, 64, true>(s, w, a, y, r0, r1); break;
+        default: launch_tile<Q, 1, 32, 32, true>(s, w, a, y, r0, r1); break;
+        }
+        return check_launch("gemm_repacked_kernel");
+    }
+}
+
+jk_status launch_gemm_repacked_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    switch (w.quant) {
+    case JK_Q8_0: return launch_gemm_tol<JK_Q8_0>(s, w, a, y, r0, r1);
+    case JK_Q4_0: return launch_gemm_tol<JK_Q4_0>(s, w, a, y, r0, r1);
+    case JK_Q5_0: return launch_gemm_tol<JK_Q5_0>(s, w, a, y, r0, r1);
+    case JK_Q4_K: return launch_gemm_tol<JK_Q4_K>(s, w, a, y, r0, r1);
+    case JK_Q5_K: return launch_gemm_tol<JK_Q5_K>(s, w, a, y, r0, r1);
+    case JK_Q4_1: return launch_gemm_tol<JK_Q4_1>(s, w, a, y, r0, r1);
+    case JK_Q5_1: return launch_gemm_tol<JK_Q5_1>(s, w, a, y, r0, r1);
+    case JK_IQ4_NL: return launch_gemm_tol<JK_IQ4_NL>(s, w, a, y, r0, r1);
+    case JK_Q2_K: return launch_gemm_tol<JK_Q2_K>(s, w, a, y, r0, r1);
+    case JK_Q3_K: return launch_gemm_tol<JK_Q3_K>(s, w, a, y, r0, r1);
+    case JK_Q6_K: return launch_gemm_tol<JK_Q6_K>(s, w, a, y, r0, r1);
+    case JK_TQ2_0: return launch_gemm_tol<JK_TQ2_0>(s, w, a, y, r0, r1);
+    case JK_I2_S: return launch_gemm_tol<JK_I2_S>(s, w, a, y, r0, r1);
+    default: return fail(JK_CAPABILITY_MISMATCH, "gemm: unsupported quant %d", w.quant);
+    }
 }
 
 // bitlinear_i8_rvv (ime.rs:882-938) for m tokens on int8 MFMA: the activation rows act[m][k]

@@ -854,9 +854,11 @@ jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t
 }
 
 // ------------------------------------------------------------ repacked GEMM
-jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
-                           size_t r0, size_t r1) {
-    // execute_gemm_repacked_rows (repack.rs:2725-2778)
+// execute_gemm_repacked_rows (repack.rs:2725-2778) validation, shared by both GEMM modes. *run
+// is false for an empty row range or token count (nothing to launch).
+static jk_status gemm_check(const jk_weight *w, const jk_act_q8 *act, const float *y, size_t y_len, size_t r0,
+                            size_t r1, bool *run) {
+    *run = false;
     if (!w || !act) return fail(JK_TENSOR_BOUNDS, "gemm_repacked: null argument");
     JK_TRY(weight_usable(w, "gemm_repacked"));
     // the reference reports the output bytes and the repacked storage (aligned_bytes) as byte_len /
@@ -875,9 +877,25 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
     if (act->m > ((size_t)1 << 24))
         return fail(JK_TENSOR_BOUNDS, "gemm_repacked: %zu tokens exceed the 2^24 per call this device path tiles",
                     act->m);
+    *run = true;
+    return JK_OK;
+}
+
+jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
+                           size_t r0, size_t r1) {
+    bool run;
+    JK_TRY(gemm_check(w, act, y, y_len, r0, r1, &run));
+    if (!run) return JK_OK;
     return launch_gemm_repacked((hipStream_t)s, w->dev, *act, y, (int)r0, (int)r1);
 }
 
+jk_status jk_gemm_repacked_tol(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
+                               size_t r0, size_t r1) {
+    bool run;
+    JK_TRY(gemm_check(w, act, y, y_len, r0, r1, &run));
+    if (!run) return JK_OK;
+    return launch_gemm_repacked_tol((hipStream_t)s, w->dev, *act, y, (int)r0, (int)r1);
+}
 jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y, size_t y_len,
                            size_t r0, size_t r1) {
     if (act && act->m != 1)

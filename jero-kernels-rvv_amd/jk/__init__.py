@@ -634,6 +634,12 @@ def dev_gemm_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
                                   _sz(r1)))
 
 
+def dev_gemm_repacked_tol(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
+    """Tolerance-mode repacked GEMM (one fused multiply-add per scale group)."""
+    _check(lib().jk_gemm_repacked_tol(_vp(stream or 0), w.handle, C.byref(act), _vp(_ptr(y)), _sz(y_len), _sz(r0),
+                                      _sz(r1)))
+
+
 def dev_gemv_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
     _check(lib().jk_gemv_repacked(_vp(stream or 0), w.handle, C.byref(act), _vp(_ptr(y)), _sz(y_len), _sz(r0),
                                   _sz(r1)))
