@@ -503,14 +503,11 @@ __device__ __forceinline__ void stage_finish(XRegs<NW, F32, Q> &xr, const GemvJo
     }
 }
 
-// Job of workgroup blockIdx.x (jobs are ordered by first workgroup; unused wg0 entries
-// hold INT_MAX).
-__device__ __forceinline__ int job_of_block(const GemvGroup &grp) {
-    int j = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxGemvJobs; ++i) j += (int)blockIdx.x >= grp.wg0[i];
-    return j;
-}
+// Grid of a group launch: blockIdx.y is the job, blockIdx.x the workgroup within it (the
+// grid is as wide as the largest job; workgroups past a job's own count exit at once). The
+// job is known from the dispatch itself, so a workgroup's first scalar load already fetches
+// its job's fields: a lookup table of first workgroups would cost a second dependent load
+// round trip before the first weight load (about 0.5 us per launch on MI355X).
 
 // ------------------------------------------------------------------ kernel
 // Work unit of a wave: RPU output rows (4 with LPR 16, 1 with LPR 64) over all their
@@ -589,7 +586,8 @@ gemv_q8_group_kernel(GemvGroup grp) {
     extern __shared__ __align__(16) uint8_t s_x[];
     __shared__ __align__(16) float s_red[LPR == 64 ? NW : 1][64];
 
-    const GemvJob &job = grp.job[job_of_block(grp)];
+    const GemvJob &job = grp.job[blockIdx.y];
+    if ((int)blockIdx.x >= job.nwg) return;  // (uniform over the workgroup)
     const WeightDev &w = job.w;
 
     // wave index as a scalar: the unit loop below must be wave-uniform control flow
@@ -615,7 +613,7 @@ gemv_q8_group_kernel(GemvGroup grp) {
     //    loads. A batch position past the last unit re-reads batch A's own addresses (lines
     //    already requested), so the dummy loads neither add traffic nor pile onto one row;
     //    a wave without any unit reads a row of its own index.
-    int ua = ((int)blockIdx.x - job.wg0) * NW + wave, ia = 0;
+    int ua = (int)blockIdx.x * NW + wave, ia = 0;
     int ub = ua, ib = ia;
     wk.next(ub, ib);
     WReg<Q> A[T::U], B[T::U];
@@ -668,7 +666,7 @@ gemv_q8_group_kernel(GemvGroup grp) {
     }
     if (job.am_slots) {
         __shared__ unsigned long long s_keys[NW];
-        argmax_store_wg(key, job.am_slots + ((int)blockIdx.x - job.wg0), s_keys, NW);
+        argmax_store_wg(key, job.am_slots + blockIdx.x, s_keys, NW);
     }
 }
 
@@ -688,13 +686,14 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     extern __shared__ __align__(16) uint8_t s_x[];
     __shared__ __align__(16) float s_red[LPR == 64 ? NW : 1][64];
 
-    const GemvJob &job = grp.job[job_of_block(grp)];
+    const GemvJob &job = grp.job[blockIdx.y];
+    if ((int)blockIdx.x >= job.nwg) return;  // (uniform over the workgroup)
     const WeightDev &w = job.w;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int sub = lane / LPR, p = lane % LPR;
     const int nb = w.nb, nit = (nb + LPR - 1) / LPR;  // nit <= UF
     const int r0 = job.r0, r1 = job.r1;
-    const int g0 = ((int)blockIdx.x - job.wg0) * job.upg;
+    const int g0 = (int)blockIdx.x * job.upg;
     const int units = min((r1 - r0 + RPU - 1) / RPU, g0 + job.upg);  // end of this workgroup's units
     const int base = g0 + wave;                                          // unit q: base + NW * q
 
@@ -766,7 +765,7 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     }
     if (job.am_slots) {
         __shared__ unsigned long long s_keys[NW];
-        argmax_store_wg(key, job.am_slots + ((int)blockIdx.x - job.wg0), s_keys, NW);
+        argmax_store_wg(key, job.am_slots + blockIdx.x, s_keys, NW);
     }
 }
 
@@ -857,29 +856,61 @@ static jk_status launch_group_run(hipStream_t s, GemvGroup &g, size_t lds) {
     int wgs = 0;
     for (int i = 0; i < g.njobs; ++i) {
         const int units = (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
-        g.job[i].wg0 = g.wg0[i] = wgs;
         g.job[i].nwg = (units + NW * upw - 1) / (NW * upw);
-        wgs += g.job[i].nwg;
+        wgs = max(wgs, g.job[i].nwg);
     }
-    for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
-    hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * NW), lds, s, g);
+    hipLaunchKernelGGL(kern, dim3((unsigned)wgs, (unsigned)g.njobs), dim3(64 * NW), lds, s, g);
     JK_TRY(check_launch("gemv_q8_group_kernel"));
     return launch_group_argmax(s, g);
+}
+
+// Jobs of unequal size leave part of a group launch's grid empty (its width is the largest
+// job's workgroup count), and an empty workgroup still costs a dispatch. A group whose jobs
+// differ in size is therefore re-cut, when it fits in kMaxGemvJobs, into jobs of the
+// smallest job's workgroup count: row ranges of rpw rows per workgroup, each writing its
+// own part of the original output (argmax jobs keep their shape: their slots are indexed by
+// workgroup).
+static void even_out_jobs(GemvGroup &g, int rpw) {
+    if (g.njobs < 2) return;
+    int min_wg = INT_MAX, max_wg = 0, pieces = 0;
+    for (int i = 0; i < g.njobs; ++i) {
+        if (g.job[i].am_slots) return;
+        const int n = (g.job[i].r1 - g.job[i].r0 + rpw - 1) / rpw;
+        min_wg = min(min_wg, n);
+        max_wg = max(max_wg, n);
+    }
+    if (max_wg == min_wg) return;
+    const int span = min_wg * rpw;  // rows of one piece
+    for (int i = 0; i < g.njobs; ++i) pieces += (g.job[i].r1 - g.job[i].r0 + span - 1) / span;
+    if (pieces > kMaxGemvJobs) return;
+    GemvGroup out = g;
+    out.njobs = 0;
+    for (int i = 0; i < g.njobs; ++i) {
+        const GemvJob &j = g.job[i];
+        for (int r = j.r0; r < j.r1; r += span) {
+            GemvJob p = j;
+            p.r0 = r;
+            p.r1 = min(j.r1, r + span);
+            if (j.y) p.y = j.y + (r - j.r0);
+            out.job[out.njobs++] = p;
+        }
+    }
+    g = out;
 }
 
 template <int Q, int LPR, bool F32, int NW, int QPW>
 static jk_status launch_fast_run(hipStream_t s, GemvGroup &g, size_t lds, int upg) {
     constexpr int RPU = 64 / LPR;
+    even_out_jobs(g, upg * RPU);
     int wgs = 0;
     for (int i = 0; i < g.njobs; ++i) {
         const int units = (g.job[i].r1 - g.job[i].r0 + RPU - 1) / RPU;
-        g.job[i].wg0 = g.wg0[i] = wgs;
         g.job[i].upg = upg;
         g.job[i].nwg = (units + upg - 1) / upg;
-        wgs += g.job[i].nwg;
+        wgs = max(wgs, g.job[i].nwg);
     }
-    for (int i = g.njobs; i < kMaxGemvJobs; ++i) g.wg0[i] = INT_MAX;
-    hipLaunchKernelGGL((gemv_q8_fast_kernel<Q, LPR, F32, NW, QPW>), dim3((unsigned)wgs), dim3(64 * NW), lds, s, g);
+    hipLaunchKernelGGL((gemv_q8_fast_kernel<Q, LPR, F32, NW, QPW>), dim3((unsigned)wgs, (unsigned)g.njobs), dim3(64 * NW),
+                       lds, s, g);
     JK_TRY(check_launch("gemv_q8_fast_kernel"));
     return launch_group_argmax(s, g);
 }

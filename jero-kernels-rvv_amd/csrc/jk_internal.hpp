@@ -109,8 +109,7 @@ struct WeightDev {
 
 // One product of a grouped quant_q8 GEMV launch: y[row - r0] for rows [r0, r1) of w,
 // against pre-quantized activation blocks xq or f32 activations xf (quantized in the
-// launch). wg0 / nwg are the job's first workgroup and workgroup count, filled in by the
-// launcher.
+// launch). nwg (the job's workgroup count) and upg are filled in by the launcher.
 constexpr int kMaxGemvJobs = 8;
 struct GemvJob {
     WeightDev w;
@@ -119,13 +118,12 @@ struct GemvJob {
     float *y;                       // may be null when am_slots is set (argmax only)
     unsigned long long *am_slots;   // argmax of the job's outputs: one key per workgroup, or null
     int32_t *am_index;              // where the reduction of the slots writes the index
-    int r0, r1, wg0, nwg;
-    int upg;  // units per workgroup (fast kernel)
-    int pad;
+    int r0, r1;  // output rows [r0, r1)
+    int nwg;     // workgroups of the job (the columns of its grid row that do work)
+    int upg;     // units per workgroup (fast kernel)
 };
 struct GemvGroup {
-    int wg0[kMaxGemvJobs];  // first workgroup of each job (one scalar load for the lookup)
-    GemvJob job[kMaxGemvJobs];
+    GemvJob job[kMaxGemvJobs];  // job blockIdx.y of a group launch
     int njobs;
     int upw;      // units per wave (upper bound), sizes the per-wave result slots in LDS
     int out_off;  // byte offset of the result slots in dynamic LDS

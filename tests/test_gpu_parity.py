@@ -330,6 +330,32 @@ def test_gemv_q8_batch_mixed_jobs(gpu):
             assert same_bits(got, ref), mismatch(got, ref)
 
 
+@pytest.mark.parametrize("use_f32", [True, False])
+def test_gemv_q8_batch_uneven_jobs(gpu, use_f32):
+    """Jobs of very different sizes in one call (the Q/K/V shape: 4096 + 1024 + 1024 rows, here
+    with a sliced job and a row count that is no multiple of a workgroup's rows), which the
+    launcher re-cuts into equal row ranges, == the oracle per matrix, bit for bit."""
+    torch = gpu
+    cols = 4096
+    specs = [(4096, 5, 4000), (1024, 0, 1024), (1000, 0, 1000), (1024, 17, 1024)]
+    x = synth.activations(cols, 77)
+    xq = x_blocks(Q4_K, x)
+    dxf, dxq = torch.from_numpy(x).cuda(), dev(torch, xq)
+    jobs, expect, outs = [], [], []
+    for i, (rows, r0, r1) in enumerate(specs):
+        raw = synth.gguf_weights(Q4_K, rows, cols, seed=90 + i)
+        w = jk.Weight(jk.TensorView(f"w{i}", Q4_K, [rows, cols], raw), rows, cols)
+        y = empty(torch, 4 * (r1 - r0))
+        jobs.append((w, None if use_f32 else dxq, dxf if use_f32 else None, y, r0, r1))
+        expect.append(O.gemv_q8(Q4_K, [rows, cols], raw, xq, rows)[r0:r1])
+        outs.append((y, r1 - r0))
+    jk.dev_gemv_q8_batch(jobs)
+    torch.cuda.synchronize()
+    for i, ((y, n), ref) in enumerate(zip(outs, expect)):
+        got = host(y, np.float32, n)
+        assert same_bits(got, ref), (i, mismatch(got, ref))
+
+
 def test_gemv_q8_batch_activation_beyond_lds_budget(gpu):
     """A caller-block job whose activation exceeds the LDS budget (Q4_K, K = 51200: 200 blocks of
     336 staged bytes > 60 KiB) runs on the global-activation kernel while small-K jobs of the same
