@@ -16,8 +16,11 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <exception>
 #include <mutex>
+#include <new>
 #include <string>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -36,19 +39,28 @@ struct TensorRec {
     uint64_t nbytes = 0;      // 0 when the type's size is not known here
 };
 
+constexpr uint64_t kBytesOverflow = UINT64_MAX;  // type_bytes: the byte count does not fit 64 bits
+
 // Bytes of n elements of ggml type t (the block formats this library reads, plus the dense
-// types a model file commonly holds), 0 when unknown or not a whole number of blocks.
+// types a model file commonly holds), 0 when unknown or not a whole number of blocks,
+// kBytesOverflow when the count does not fit in 64 bits.
 uint64_t type_bytes(uint32_t t, uint64_t n) {
+    uint64_t unit = 0, count = n, extra = 0;
     switch (t) {
-    case 0: return n * 4;   // F32
-    case 1: return n * 2;   // F16
-    case 30: return n * 2;  // BF16
-    default: break;
+    case 0: unit = 4; break;   // F32
+    case 1: unit = 2; break;   // F16
+    case 30: unit = 2; break;  // BF16
+    default: {
+        if (!fmt_known((int)t)) return 0;
+        const Fmt f = fmt_of((int)t);
+        if (n % (uint64_t)f.be) return 0;
+        unit = (uint64_t)f.bb;
+        count = n / (uint64_t)f.be;
+        extra = trailer_bytes((int)t);
     }
-    if (!fmt_known((int)t)) return 0;
-    const Fmt f = fmt_of((int)t);
-    if (n % (uint64_t)f.be) return 0;
-    return n / (uint64_t)f.be * (uint64_t)f.bb + trailer_bytes((int)t);
+    }
+    if (count > (UINT64_MAX - extra) / unit) return kBytesOverflow;
+    return count * unit + extra;
 }
 
 // Bounds-checked little-endian cursor over the mapped file.
@@ -193,9 +205,11 @@ static jk_status gguf_parse(jk_gguf *g, const char *path) {
     }
     if (n_tensors > (g->size - c.pos) / 24)  // every tensor record holds at least 24 bytes
         return fail(JK_TENSOR_BOUNDS, "%s: tensor count %llu exceeds the file", path, (unsigned long long)n_tensors);
-    g->tensors.resize(n_tensors);
+    // (records are appended as they are read: the count is only bounded by the file size)
+    g->tensors.reserve((size_t)std::min<uint64_t>(n_tensors, 4096));
     for (uint64_t i = 0; i < n_tensors; ++i) {
-        TensorRec &t = g->tensors[i];
+        g->tensors.emplace_back();
+        TensorRec &t = g->tensors.back();
         c.str(&t.name);
         t.n_dims = c.u32();
         if (c.ok && (t.n_dims == 0 || t.n_dims > 4))
@@ -214,6 +228,8 @@ static jk_status gguf_parse(jk_gguf *g, const char *path) {
             return fail(JK_TENSOR_BOUNDS, "%s: tensor %s offset %llu is not %llu-aligned", path, t.name.c_str(),
                         (unsigned long long)t.rel_offset, (unsigned long long)g->alignment);
         t.nbytes = type_bytes(t.type, n);
+        if (t.nbytes == kBytesOverflow)
+            return fail(JK_TENSOR_BOUNDS, "%s: tensor %s byte count overflows 64 bits", path, t.name.c_str());
     }
     g->data_start = (c.pos + g->alignment - 1) / g->alignment * g->alignment;
     for (const TensorRec &t : g->tensors) {
@@ -224,44 +240,63 @@ static jk_status gguf_parse(jk_gguf *g, const char *path) {
     return JK_OK;
 }
 
+// C++ exceptions (an allocation that fails, a thread that cannot start) never cross the C
+// ABI: the extern "C" entries below that allocate turn them into an error status.
+template <class F>
+static jk_status no_throw(const char *what, F &&f) {
+    try {
+        return f();
+    } catch (const std::exception &e) {
+        return fail(JK_TENSOR_BOUNDS, "%s: %s", what, e.what());
+    } catch (...) {
+        return fail(JK_TENSOR_BOUNDS, "%s: unexpected exception", what);
+    }
+}
+
+static jk_status gguf_open(const char *path, jk_gguf **out);
+static jk_status gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t chunk_bytes, jk_weight **out);
+
 extern "C" {
 
 jk_status jk_gguf_open(const char *path, jk_gguf **out) {
+    return no_throw("jk_gguf_open", [&] { return gguf_open(path, out); });
+}
+
+jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t chunk_bytes, jk_weight **out) {
+    return no_throw("jk_gguf_load_weight", [&] { return gguf_load_weight(s, g, i, chunk_bytes, out); });
+}
+
+}  // extern "C"
+
+static jk_status gguf_open(const char *path, jk_gguf **out) {
     if (!out) return fail(JK_TENSOR_BOUNDS, "gguf: null out-pointer");
     *out = nullptr;
     if (!path) return fail(JK_TENSOR_BOUNDS, "gguf: null path");
-    jk_gguf *g = new jk_gguf();
+    // the handle is released on every way out but success, exceptions included
+    struct Guard {
+        jk_gguf *g;
+        ~Guard() {
+            if (g) gguf_release(g);
+        }
+    } guard{new jk_gguf()};
+    jk_gguf *g = guard.g;
     g->fd = open(path, O_RDONLY | O_CLOEXEC);
     struct stat st;
-    // (the error text is formed before the handle is released: release closes the file,
-    // which may change errno)
-    if (g->fd < 0 || fstat(g->fd, &st) != 0) {
-        const jk_status s = fail(JK_TENSOR_BOUNDS, "gguf: cannot open %s: %s", path, strerror(errno));
-        gguf_release(g);
-        return s;
-    }
+    if (g->fd < 0 || fstat(g->fd, &st) != 0)
+        return fail(JK_TENSOR_BOUNDS, "gguf: cannot open %s: %s", path, strerror(errno));
     g->size = (uint64_t)st.st_size;
-    if (g->size < 24) {
-        const jk_status s = fail(JK_TENSOR_BOUNDS, "%s: not a GGUF file (%llu bytes)", path,
-                                 (unsigned long long)g->size);
-        gguf_release(g);
-        return s;
-    }
+    if (g->size < 24)
+        return fail(JK_TENSOR_BOUNDS, "%s: not a GGUF file (%llu bytes)", path, (unsigned long long)g->size);
     void *m = mmap(nullptr, g->size, PROT_READ, MAP_PRIVATE, g->fd, 0);
-    if (m == MAP_FAILED) {
-        const jk_status s = fail(JK_TENSOR_BOUNDS, "gguf: cannot map %s: %s", path, strerror(errno));
-        gguf_release(g);
-        return s;
-    }
+    if (m == MAP_FAILED) return fail(JK_TENSOR_BOUNDS, "gguf: cannot map %s: %s", path, strerror(errno));
     g->map = (const uint8_t *)m;
-    const jk_status s = gguf_parse(g, path);
-    if (s != JK_OK) {
-        gguf_release(g);
-        return s;
-    }
+    JK_TRY(gguf_parse(g, path));
     *out = g;
+    guard.g = nullptr;
     return JK_OK;
 }
+
+extern "C" {
 
 jk_status jk_gguf_close(jk_gguf *g) {
     if (g) gguf_release(g);
@@ -304,7 +339,9 @@ jk_status jk_gguf_find(const jk_gguf *g, const char *name, size_t *index) {
     return fail(JK_TENSOR_BOUNDS, "gguf: no tensor named %s", name);
 }
 
-jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t chunk_bytes, jk_weight **out) {
+}  // extern "C"
+
+static jk_status gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t chunk_bytes, jk_weight **out) {
     if (!out) return fail(JK_TENSOR_BOUNDS, "gguf: null weight out-pointer");
     *out = nullptr;
     if (!g) return fail(JK_TENSOR_BOUNDS, "gguf: null file");
@@ -338,6 +375,11 @@ jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t ch
     void *const *pinned = gm->pinned, *const *staging = gm->staging;
     hipEvent_t *ev = gm->ev;
     const unsigned nthreads = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> th;
+    try {
+        th.reserve(nthreads);  // (no reallocation below; without it every part is copied here)
+    } catch (const std::bad_alloc &) {
+    }
     const uint8_t *src = (const uint8_t *)v.bytes;
     for (size_t t0 = 0, k = 0; e == hipSuccess && rs == JK_OK && t0 < L.n_tiles; t0 += tiles_per_chunk, ++k) {
         const size_t t1 = std::min(L.n_tiles, t0 + tiles_per_chunk);
@@ -346,14 +388,21 @@ jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t ch
         const int b = (int)(k & 1);
         if (k >= 2) e = hipEventSynchronize(ev[b]);  // the DMA of chunk k - 2 has read this buffer
         if (e != hipSuccess) break;
-        // host threads copy the chunk out of the mapping (page faults and all) in parallel
-        std::vector<std::thread> th;
+        // host threads copy the chunk out of the mapping (page faults and all) in parallel; a
+        // thread that cannot be started leaves its part (and the later ones) to this thread
         const size_t part = (bytes + nthreads - 1) / nthreads;
-        for (unsigned p = 0; p < nthreads && p * part < bytes; ++p)
-            th.emplace_back([&, p] {
-                const size_t o = p * part, n = std::min(part, bytes - o);
-                memcpy((uint8_t *)pinned[b] + o, src + r0 * L.row_bytes + o, n);
-            });
+        auto copy_part = [&](unsigned p) {
+            const size_t o = p * part, n = std::min(part, bytes - o);
+            memcpy((uint8_t *)pinned[b] + o, src + r0 * L.row_bytes + o, n);
+        };
+        th.clear();
+        unsigned started = 0;
+        try {
+            for (; started < th.capacity() && started < nthreads && started * part < bytes; ++started)
+                th.emplace_back(copy_part, started);
+        } catch (const std::system_error &) {
+        }
+        for (unsigned p = started; p < nthreads && p * part < bytes; ++p) copy_part(p);
         for (auto &x : th) x.join();
         e = hipMemcpyAsync(staging[b], pinned[b], bytes, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) rs = jk_weight_repack_tile_range(s, w, staging[b], bytes, t0, t1);
@@ -372,4 +421,3 @@ jk_status jk_gguf_load_weight(jk_stream s, const jk_gguf *g, size_t i, size_t ch
     return JK_OK;
 }
 
-}  // extern "C"

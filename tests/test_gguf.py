@@ -118,6 +118,20 @@ def test_bad_alignment_and_offsets_fail_closed(tmp_path):
     _raises_closed(p)
 
 
+def test_wrapping_byte_count_fails_closed(tmp_path):
+    # 32 x 542551296285575048 Q8_0 elements: the element count fits 64 bits, the byte count
+    # (34 bytes per 32) wraps to 16 -- refused at open, not reported as a 16-byte tensor
+    p = tmp_path / "wrap.gguf"
+    write_gguf(p, [("w", jk.Q8_0, [32, 542551296285575048], np.zeros(34, np.uint8))], [])
+    with pytest.raises(jk.TensorBoundsError, match="overflows"):
+        jk.GGUF(str(p))
+    # the same for a dense type: F32 with 2^62 elements
+    p = tmp_path / "wrap_f32.gguf"
+    write_gguf(p, [("f", 0, [1 << 31, 1 << 31], np.zeros(16, np.uint8))], [])
+    with pytest.raises(jk.TensorBoundsError, match="overflows"):
+        jk.GGUF(str(p))
+
+
 def test_short_file_error_names_its_size(tmp_path):
     # a file shorter than the fixed header is refused with its own size in the message (the
     # message is formed before the handle is released)

@@ -87,6 +87,63 @@ def test_quantize_row_q8_k_gated(gpu, n):
             assert np.array_equal(q2.cpu().numpy(), ref)
 
 
+# Bound of a SwiGLU-fused quantizer against the oracle. The device SwiGLU is within
+# max(1e-6, 1e-5 |h|) of the oracle's (glibc expf), so a block maximum -- and the scale
+# d = amax / 127 -- moves by at most 1e-5 relative plus 1e-6 / 127, and h * 127 / amax by at
+# most 127 * 2e-5 + 1e-6 * 127 / amax < 0.01 for the blocks here (amax > 0.5): a quant can
+# only cross a rounding boundary, i.e. move by one level.
+def assert_scale_close(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 1e-6 / 127), np.max(np.abs(got - ref) / np.abs(ref))
+
+
+@pytest.mark.parametrize("n", [256, 14336, 256 * 57])
+def test_quantize_row_q8_k_swiglu_vs_oracle(gpu, n):
+    """SwiGLU fused into quantize_row_q8_k vs the oracle's quantize_row_q8_k of the oracle's SwiGLU:
+    d within 1e-5 relative, every quant within one level, bsums the sums of the device's own quants
+    (so within 16 of the oracle's)."""
+    torch = gpu
+    g, u = gate_up(n, n + 2)
+    nb = n // 256
+    q = torch.empty(nb * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device="cuda")
+    jk.dev_quantize_row_q8_k_gated(jk.ACT_SWIGLU, dev(torch, g), dev(torch, u), n, q, nb)
+    torch.cuda.synchronize()
+    got = q.cpu().numpy().view(jk.BLOCK_Q8K)
+    ref = O.quantize_row_q8_k(O.swiglu_f32(g, u))
+    assert np.all(np.abs(ref["d"]) * 127 > 0.5)  # the premise of the bound
+    assert_scale_close(got["d"], ref["d"])
+    dq = got["qs"].astype(np.int32) - ref["qs"].astype(np.int32)
+    assert np.abs(dq).max() <= 1
+    own = got["qs"].astype(np.int32).reshape(nb, 16, 16).sum(axis=2)
+    assert np.array_equal(got["bsums"].astype(np.int32), own)
+    assert np.abs(own - ref["bsums"].astype(np.int32)).max() <= 16
+    assert np.mean(dq == 0) > 0.99  # a level moves only next to a rounding boundary
+
+
+@pytest.mark.parametrize("m,k", [(1, 14336), (7, 4096)])
+def test_quantize_act_q8_swiglu_vs_oracle(gpu, m, k):
+    """SwiGLU fused into quantize_act_q8 vs the oracle's quantize of the oracle's SwiGLU: the 32-element
+    scales within 1e-5 relative and quants within one level. (The derived sums of given quants and
+    scales are pinned bit for bit by the non-fused quantizer's oracle test and the gated == two-call
+    test below.)"""
+    torch = gpu
+    g, u = gate_up(m * k, m + k + 3)
+    need = jk.act_q8_bytes(m, k)
+    st = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    a = jk.act_q8_bind(st, need, m, k)
+    jk.dev_quantize_act_q8_gated(jk.ACT_SWIGLU, dev(torch, g), dev(torch, u), m, k, a)
+    torch.cuda.synchronize()
+    raw, base = st.cpu().numpy(), st.data_ptr()
+    ref = O.ActQ8(O.swiglu_f32(g, u), m, k)
+    qs = raw[a.qs - base: a.qs - base + m * a.k_padded].view(np.int8).reshape(m, -1)
+    sc = raw[a.scales - base: a.scales - base + 4 * ref.scales.size].view(np.float32).reshape(ref.scales.shape)
+    live = ref.scales != 0
+    assert np.array_equal(sc[~live], ref.scales[~live])
+    assert np.all(np.abs(ref.scales[live]) * 127 > 0.5)
+    assert_scale_close(sc[live], ref.scales[live])
+    assert np.abs(qs.astype(np.int32) - ref.qs.astype(np.int32)).max() <= 1
+
+
 @pytest.mark.parametrize("m,k", [(1, 14336), (7, 4096), (3, 300)])
 def test_quantize_act_q8_gated(gpu, m, k):
     torch = gpu

@@ -178,6 +178,27 @@ def test_upload_and_dequantize_rows(gpu, quant):
         assert same_bits(got[r], ref), (r, mismatch(got[r], ref))
 
 
+def test_dequantize_every_f16_scale(gpu):
+    """Device f16 scale decode on all 65,536 bit patterns: Q8_0 block i carries d = i (normal,
+    subnormal, +-0, Inf and NaN patterns alike) and quants spanning -128..127, and its dequantized
+    row is the oracle's bit for bit (f16_to_f32_finite, lib.rs:676-717: NaN/Inf -> 0)."""
+    torch = gpu
+    rows, cols = 2048, 1024  # 32 blocks per row: 65,536 blocks
+    blk = np.zeros(65536, dtype=[("d", "<u2"), ("qs", "i1", 32)])
+    blk["d"] = np.arange(65536, dtype=np.uint16)
+    blk["qs"] = np.int8([1, -1, 127, -128, 0, 2, -2, 3, 5, -7, 11, -13, 64, -64, 100, -100,
+                         17, -19, 23, -29, 31, -37, 41, -43, 47, -53, 59, -61, 67, -71, 73, -79])
+    raw = blk.view(np.uint8).reshape(-1)
+    w = jk.Weight(jk.TensorView("w", Q8_0, [rows, cols], raw), rows, cols)
+    dy = empty(torch, 4 * rows * cols)
+    jk.dev_dequantize_rows(w, 0, rows, dy, rows * cols)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, rows * cols).reshape(rows, cols)
+    for r in range(rows):
+        ref = O.dequantize_tensor_row(Q8_0, [rows, cols], raw, r, cols)
+        assert same_bits(got[r], ref), (r, mismatch(got[r], ref))
+
+
 # ------------------------------------------------------------------ quant_q8 GEMV
 @pytest.mark.parametrize("quant", GEMV_FORMATS)
 @pytest.mark.parametrize("rows,cols", [(1, 256), (3, 512), (5, 4352), (17, 1024), (33, 7168), (64, 2560)])
