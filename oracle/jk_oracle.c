@@ -1267,6 +1267,229 @@ int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t
 }
 
 /* ------------------------------------------------------------------------- */
+/* PackedNibbleMatrix GEMM (the compact 4-bit path, repack.rs:4216-5397)      */
+/* ------------------------------------------------------------------------- */
+
+enum { NIB_TILE_N = 8, NIB_TILE_M = 8, NIB_TILE_K = 16 }; /* ime.rs:40-48 */
+
+/* PackedNibbleMatrix (repack.rs:4216-4229): tiles[nt][b32] of 128 bytes (bytes 0..63 hold
+ * columns 0..15, 64..127 columns 16..31; within each half, 16-byte segment `pair` holds row
+ * 2*pair in the low nibbles and row 2*pair+1 in the high nibbles), plus the per-format
+ * metadata of PackedNibbleMeta (repack.rs:4185-4210). */
+typedef struct {
+    size_t rows, cols, k_blocks32, n_tiles;
+    int quant;
+    uint8_t *tiles;
+    uint16_t *scales_f16, *mins_f16; /* [nt][b32][j] (Q4_0, IQ4_NL; Q4_1 both) */
+    uint8_t *headers;                /* [nt][sb][j][16] raw Q4_K headers */
+} nibble_matrix;
+
+static void nibble_free(nibble_matrix *nm) {
+    free(nm->tiles); free(nm->scales_f16); free(nm->mins_f16); free(nm->headers);
+}
+
+/* pack_pair_split_nibbles_into_tile, scalar arm (repack.rs:4297-4305): column k of the even
+ * and odd rows' 16 bytes (low nibbles = columns 0..15, high nibbles = columns 16..31). */
+static void nibble_pack_pair(const uint8_t *e, const uint8_t *o, uint8_t *tile, int pair) {
+    for (int k = 0; k < 16; k++) {
+        tile[pair * 16 + k] = (uint8_t)((e[k] & 0x0F) | ((o[k] & 0x0F) << 4));
+        tile[64 + pair * 16 + k] = (uint8_t)((e[k] >> 4) | (o[k] & 0xF0));
+    }
+}
+
+/* pack_q4k_pair_chunk32_into_tiles, scalar arm (repack.rs:4379-4394): the 32 qs bytes of a
+ * Q4_K 64-element chunk; low nibbles go to tile lo (b32 = 2c), high nibbles to tile hi. */
+static void nibble_pack_q4k_chunk(const uint8_t *e, const uint8_t *o, uint8_t *lo, uint8_t *hi, int pair) {
+    for (int k = 0; k < 16; k++) {
+        lo[pair * 16 + k] = (uint8_t)((e[k] & 0x0F) | ((o[k] & 0x0F) << 4));
+        hi[pair * 16 + k] = (uint8_t)((e[k] >> 4) | (o[k] & 0xF0));
+        lo[64 + pair * 16 + k] = (uint8_t)((e[16 + k] & 0x0F) | ((o[16 + k] & 0x0F) << 4));
+        hi[64 + pair * 16 + k] = (uint8_t)((e[16 + k] >> 4) | (o[16 + k] & 0xF0));
+    }
+}
+
+/* PackedNibbleMatrix::from_tensor (repack.rs:4788-4865) via repack_nibble_into_tile_range over
+ * every tile (repack.rs:4414-4644). Q4_0 / IQ4_NL blocks whose scale decodes to 0 keep a zero
+ * scale and zero nibbles. */
+static int nibble_pack(const or_tensor_view *w, size_t rows, size_t cols, nibble_matrix *nm) {
+    memset(nm, 0, sizeof *nm);
+    int q = w->quant;
+    if (q != OR_Q4_0 && q != OR_Q4_K && q != OR_Q4_1 && q != OR_IQ4_NL) return OR_CAPABILITY_MISMATCH;
+    int st = validate_matrix_view(w, rows, cols);
+    if (st) return st;
+    size_t bb = or_block_bytes(q), row_bytes = cols / or_block_elements(q) * bb;
+    nm->rows = rows; nm->cols = cols; nm->quant = q;
+    nm->k_blocks32 = cols / 32;
+    nm->n_tiles = (rows + NIB_TILE_N - 1) / NIB_TILE_N;
+    size_t kb = nm->k_blocks32, nt_n = nm->n_tiles, n_sblks = cols / 256;
+    nm->tiles = calloc(nt_n * kb, 128);
+    if (q == OR_Q4_K) nm->headers = calloc(nt_n * n_sblks * NIB_TILE_N, 16);
+    else nm->scales_f16 = calloc(nt_n * kb * NIB_TILE_N, 2);
+    if (q == OR_Q4_1) nm->mins_f16 = calloc(nt_n * kb * NIB_TILE_N, 2);
+    if (!nm->tiles || (q == OR_Q4_K ? !nm->headers : !nm->scales_f16) || (q == OR_Q4_1 && !nm->mins_f16)) {
+        nibble_free(nm);
+        return OR_TENSOR_BOUNDS;
+    }
+    static const uint8_t zero[32] = {0};
+    for (size_t nt = 0; nt < nt_n; nt++) {
+        uint8_t *ts = nm->tiles + nt * kb * 128;
+        for (int pair = 0; pair < 4; pair++) {
+            size_t re = nt * NIB_TILE_N + 2 * (size_t)pair;
+            if (re >= rows) break;
+            int has_odd = re + 1 < rows;
+            const uint8_t *er = w->bytes + re * row_bytes, *orr = has_odd ? er + row_bytes : 0;
+            if (q == OR_Q4_0 || q == OR_IQ4_NL) {
+                for (size_t b = 0; b < kb; b++) {
+                    const uint8_t *be = er + b * 18;
+                    uint16_t eb = rd16(be);
+                    int ez = or_f16_to_f32_finite(eb) == 0.0f;
+                    nm->scales_f16[(nt * kb + b) * NIB_TILE_N + 2 * pair] = ez ? 0 : eb;
+                    int oz = 1;
+                    const uint8_t *no = zero;
+                    if (has_odd) {
+                        const uint8_t *bo = orr + b * 18;
+                        uint16_t ob = rd16(bo);
+                        oz = or_f16_to_f32_finite(ob) == 0.0f;
+                        nm->scales_f16[(nt * kb + b) * NIB_TILE_N + 2 * pair + 1] = oz ? 0 : ob;
+                        if (!oz) no = bo + 2;
+                    }
+                    const uint8_t *ne = ez ? zero : be + 2;
+                    if (!ez || !oz) nibble_pack_pair(ne, no, ts + b * 128, pair);
+                }
+            } else if (q == OR_Q4_1) {
+                for (size_t b = 0; b < kb; b++) {
+                    const uint8_t *be = er + b * 20;
+                    size_t ie = (nt * kb + b) * NIB_TILE_N + 2 * pair;
+                    nm->scales_f16[ie] = rd16(be);
+                    nm->mins_f16[ie] = rd16(be + 2);
+                    const uint8_t *no = zero;
+                    if (has_odd) {
+                        const uint8_t *bo = orr + b * 20;
+                        nm->scales_f16[ie + 1] = rd16(bo);
+                        nm->mins_f16[ie + 1] = rd16(bo + 2);
+                        no = bo + 4;
+                    }
+                    nibble_pack_pair(be + 4, no, ts + b * 128, pair);
+                }
+            } else { /* Q4_K */
+                for (size_t sb = 0; sb < n_sblks; sb++) {
+                    const uint8_t *be = er + sb * 144, *bo = has_odd ? orr + sb * 144 : 0;
+                    memcpy(nm->headers + ((nt * n_sblks + sb) * NIB_TILE_N + 2 * pair) * 16, be, 16);
+                    if (bo) memcpy(nm->headers + ((nt * n_sblks + sb) * NIB_TILE_N + 2 * pair + 1) * 16, bo, 16);
+                    for (int c = 0; c < 4; c++) {
+                        size_t blo = sb * 8 + 2 * (size_t)c;
+                        nibble_pack_q4k_chunk(be + 16 + 32 * c, bo ? bo + 16 + 32 * c : zero, ts + blo * 128,
+                                              ts + (blo + 1) * 128, pair);
+                    }
+                }
+            }
+        }
+    }
+    return OR_OK;
+}
+
+/* PackedNibbleMatrix::decode_tile_scales (repack.rs:5044-5090): per (b32, j) scale and min of
+ * tile nt; returns whether the format has mins. */
+static int nibble_decode_tile_scales(const nibble_matrix *nm, size_t nt, float *sc, float *mn) {
+    size_t len = nm->k_blocks32 * NIB_TILE_N, base = nt * len;
+    if (nm->quant == OR_Q4_0 || nm->quant == OR_IQ4_NL) {
+        for (size_t i = 0; i < len; i++) sc[i] = or_f16_to_f32_finite(nm->scales_f16[base + i]);
+        return 0;
+    }
+    if (nm->quant == OR_Q4_1) {
+        for (size_t i = 0; i < len; i++) {
+            sc[i] = or_f16_to_f32_finite(nm->scales_f16[base + i]);
+            float m = or_f16_to_f32_finite(nm->mins_f16[base + i]);
+            mn[i] = m == 0.0f ? 0.0f : -m;
+        }
+        return 1;
+    }
+    size_t n_sblks = nm->k_blocks32 / 8;
+    for (size_t sb = 0; sb < n_sblks; sb++)
+        for (int j = 0; j < NIB_TILE_N; j++) {
+            const uint8_t *h = nm->headers + ((nt * n_sblks + sb) * NIB_TILE_N + (size_t)j) * 16;
+            float d = or_f16_to_f32_finite(rd16(h)), dmin = or_f16_to_f32_finite(rd16(h + 2));
+            uint8_t s8[8], m8[8];
+            unpack_k4_scales_mins(h + 4, s8, m8);
+            for (int is = 0; is < 8; is++) {
+                size_t idx = (sb * 8 + (size_t)is) * NIB_TILE_N + (size_t)j;
+                sc[idx] = d * (float)s8[is];
+                mn[idx] = dmin * (float)m8[is];
+            }
+        }
+    return 1;
+}
+
+/* unpack_nibble_tile_to_chunks (repack.rs:5093-5130): ch[0] = columns 0..15, ch[1] = columns
+ * 16..31, each [row j][16]; Q4_0 subtracts 8, IQ4_NL looks up KVALUES_IQ4NL, Q4_1 / Q4_K keep
+ * the nibble. */
+static void nibble_unpack(const uint8_t *t, int quant, int8_t ch[2][128]) {
+    for (int pair = 0; pair < 4; pair++)
+        for (int k = 0; k < 16; k++) {
+            uint8_t b0 = t[pair * 16 + k], b1 = t[64 + pair * 16 + k];
+            int v[4] = {b0 & 0x0F, b0 >> 4, b1 & 0x0F, b1 >> 4};
+            for (int i = 0; i < 4; i++) v[i] = quant == OR_Q4_0 ? v[i] - 8 : quant == OR_IQ4_NL ? kvalues_iq4nl[v[i]] : v[i];
+            ch[0][(2 * pair) * NIB_TILE_K + k] = (int8_t)v[0];
+            ch[0][(2 * pair + 1) * NIB_TILE_K + k] = (int8_t)v[1];
+            ch[1][(2 * pair) * NIB_TILE_K + k] = (int8_t)v[2];
+            ch[1][(2 * pair + 1) * NIB_TILE_K + k] = (int8_t)v[3];
+        }
+}
+
+/* execute_nibble_gemm_rows (repack.rs:5181-5397), the host (non-RISC-V) arm: per 8-row tile and
+ * 8-token tile, acc starts at 0.0; per 32-element block, the i8 tile dot of the activation chunks
+ * with the unpacked nibble chunks (tile_dot_scalar_rows, ime.rs:127-148) is folded in by
+ * accumulate_scaled_tile_scalar with two chunks per scale (repack.rs:3045-3093). The activation
+ * tiles are read through the logical qs[m][k_padded] (the same elements). */
+int or_nibble_gemm_rows(float *out, size_t out_len, const or_tensor_view *w, size_t rows, size_t cols,
+                        const or_act_q8 *act, size_t r0, size_t r1) {
+    nibble_matrix nm;
+    int st = nibble_pack(w, rows, cols, &nm);
+    if (st) return st;
+    st = OR_TENSOR_BOUNDS;
+    size_t m = act->m, sub = r1 - r0, kb = nm.k_blocks32;
+    float *sc = malloc(kb * NIB_TILE_N * sizeof(float)), *mn = malloc(kb * NIB_TILE_N * sizeof(float));
+    if (act->k != cols || r0 > r1 || r1 > rows || out_len != m * sub || !sc || !mn) goto done;
+    st = OR_OK;
+    if (sub == 0) goto done;
+    for (size_t nt = r0 / NIB_TILE_N; nt <= (r1 - 1) / NIB_TILE_N; nt++) {
+        size_t j0 = r0 > nt * NIB_TILE_N ? r0 - nt * NIB_TILE_N : 0;
+        size_t j1 = r1 - nt * NIB_TILE_N < NIB_TILE_N ? r1 - nt * NIB_TILE_N : NIB_TILE_N;
+        int has_mins = nibble_decode_tile_scales(&nm, nt, sc, mn);
+        for (size_t mt = 0; mt * NIB_TILE_M < m; mt++) {
+            size_t active = m - mt * NIB_TILE_M < NIB_TILE_M ? m - mt * NIB_TILE_M : NIB_TILE_M;
+            float acc[NIB_TILE_M * NIB_TILE_N] = {0};
+            for (size_t b = 0; b < kb; b++) {
+                int8_t ch[2][128];
+                nibble_unpack(nm.tiles + (nt * kb + b) * 128, nm.quant, ch);
+                for (size_t i = 0; i < active; i++) {
+                    size_t gm = mt * NIB_TILE_M + i;
+                    const int8_t *xq = act->qs + gm * act->k_padded + 32 * b;
+                    float xs = act->scales[gm * act->k_blocks32 + b];
+                    float xsm = has_mins ? act->sums[gm * act->k_blocks32 + b] : 0.0f;
+                    for (size_t j = j0; j < j1; j++) {
+                        int32_t c = 0;
+                        for (int h = 0; h < 2; h++)
+                            for (int k = 0; k < NIB_TILE_K; k++)
+                                c += (int32_t)xq[16 * h + k] * (int32_t)ch[h][j * NIB_TILE_K + (size_t)k];
+                        float ws = sc[b * NIB_TILE_N + j];
+                        if (has_mins) acc[i * NIB_TILE_N + j] += (float)c * (xs * ws) - xsm * mn[b * NIB_TILE_N + j];
+                        else acc[i * NIB_TILE_N + j] += (float)c * (xs * ws);
+                    }
+                }
+            }
+            for (size_t i = 0; i < active; i++)
+                for (size_t j = j0; j < j1; j++)
+                    out[(mt * NIB_TILE_M + i) * sub + (nt * NIB_TILE_N + j - r0)] = acc[i * NIB_TILE_N + j];
+        }
+    }
+done:
+    free(sc); free(mn);
+    nibble_free(&nm);
+    return st;
+}
+
+/* ------------------------------------------------------------------------- */
 /* BitLinear: bitlinear_i8_rvv (ime.rs:882-938)                               */
 /* ------------------------------------------------------------------------- */
 

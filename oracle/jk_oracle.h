@@ -193,6 +193,10 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
                       int *has_mins_out, int *chunks_per_scale_out);
 int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t rows,
                      size_t cols, const or_act_q8 *act, size_t r0, size_t r1);
+/* PackedNibbleMatrix::gemm_rows (repack.rs:5181-5397): the compact 4-bit path for Q4_0, Q4_1,
+ * IQ4_NL and Q4_K (packing, tile-scale decode and the host arm's tile dot and accumulation). */
+int or_nibble_gemm_rows(float *out, size_t out_len, const or_tensor_view *w, size_t rows, size_t cols,
+                        const or_act_q8 *act, size_t r0, size_t r1);
 
 /* ---- gated activations, argmax ---- */
 int or_swiglu_f32(float *out, const float *gate, const float *up, size_t n);

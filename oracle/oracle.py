@@ -290,6 +290,15 @@ def gemm_repacked(quant: int, shape, data: np.ndarray, rows: int, cols: int, act
     return out.reshape(act.m, r1 - r0)
 
 
+def nibble_gemm_rows(quant: int, shape, data: np.ndarray, rows: int, cols: int, act: ActQ8, r0: int, r1: int):
+    """PackedNibbleMatrix::gemm_rows restated (Q4_0, Q4_1, IQ4_NL, Q4_K)."""
+    v = View(quant, shape, data)
+    out = np.zeros(act.m * (r1 - r0), dtype=np.float32)
+    _ok(lib().or_nibble_gemm_rows(_p(out), _sz(out.size), C.byref(v.c), _sz(rows), _sz(cols), C.byref(act.c),
+                                  _sz(r0), _sz(r1)), "nibble_gemm_rows")
+    return out.reshape(act.m, r1 - r0)
+
+
 # ----------------------------------------------------------------- BitLinear
 def bitlinear_i8(quant: int, shape, data: np.ndarray, act: np.ndarray, act_scale: float, out_len: int):
     v = View(quant, shape, data)
