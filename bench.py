@@ -89,7 +89,7 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch the step eagerly instead of a HIP graph")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the per-kernel lines of the other workloads (C1, C2, C5, vec_dot f32, quantizers)")
-    ap.add_argument("--ffn", choices=("swiglu", "synthetic"), default="synthetic",
+    ap.add_argument("--ffn", choices=("swiglu", "synthetic"), default="swiglu",
                     help="ffn_down input of the timed step: a fixed synthetic activation quantized to Q8_K, or "
                          "SwiGLU of the layer's gate / up outputs fused into its Q8_K quantizer (a Llama "
                          "feed-forward block; also reported as a secondary line)")
@@ -256,7 +256,7 @@ def main() -> int:
     # kernel is timed with HIP events on its own stream around each launch, the activation
     # quantization (QuantizedActQ8::quantize_into) runs between the timed launches. Two modes:
     # tolerance (jk_gemm_repacked_tol: one fused multiply-add per scale group, within 1e-5 of
-    # each token's output-row L2 norm -- the bar north_star sets for f32 products; the reported
+    # each token's output-row L2 norm -- the bar for f32 products; the reported
     # line) and bit-exact (jk_gemm_repacked: the reference's separately rounded epilogue).
     gemm, sweep, gemm_exact, sweep_exact = None, [], None, []
     s = torch.cuda.current_stream().cuda_stream
@@ -399,6 +399,22 @@ def main() -> int:
             hbm_line(name, b, us, f"{rows}x{cols}, Q8_0 activation blocks")
             for w in ws:
                 w.free()
+        # Repacked GEMV (the m <= 2 route of the repacked GEMM, repack.rs:2892): one token's
+        # QuantizedActQ8 against the block-scaled weights, at the C1 shape and the C3 gate shape
+        for name, quant, rows, cols in (("gemv_repacked Q8_0 4096x4096 M=1", jk.Q8_0, 4096, 4096),
+                                        ("gemv_repacked Q4_0 4096x4096 M=1", jk.Q4_0, 4096, 4096),
+                                        ("gemv_repacked Q4_K 14336x4096 M=1", jk.Q4_K, 14336, 4096)):
+            ws = copies(quant, rows, cols, 550 + quant)
+            need = jk.act_q8_bytes(1, cols)
+            store = torch.empty(need, dtype=torch.uint8, device=dev)
+            act1 = jk.act_q8_bind(store, need, 1, cols)
+            jk.dev_quantize_act_q8(acts["x"], 1, cols, act1)
+            y = torch.empty(rows, dtype=torch.float32, device=dev)
+            us = graph_us(lambda i, st: jk.dev_gemv_repacked(ws[i % len(ws)], act1, y, rows, 0, rows, st), len(ws))
+            b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + need + 4 * rows
+            hbm_line(name, b, us, f"{rows}x{cols}, one token's QuantizedActQ8")
+            for w in ws:
+                w.free()
         # Q5_0 / Q5_K / TQ1_0 quant_q8 GEMV with caller blocks (GGUF bytes; TQ1_0 streams its
         # 66-byte device blocks, 22% more than the 54 GGUF bytes counted here)
         for name, quant, rows, cols in (("gemv_q5_0_q8_0 4096x4096", jk.Q5_0, 4096, 4096),
@@ -466,8 +482,9 @@ def main() -> int:
                 for w in ws:
                     w.free()
         # Repacked GEMM of every other weight format at the prefill shape (14336x4096, 512
-        # tokens; the activation quantized once beforehand), kernel-only, graph-timed over 4
-        # weight copies: compute-bound at this token count, so the copies need not exceed the cache
+        # tokens; the activation quantized once beforehand), kernel-only, graph-timed over weight
+        # copies of >= 600 MB in all (beyond the 256 MB Infinity Cache: every launch streams its
+        # weights from HBM)
         M, N, K = 512, 14336, 4096
         xin = torch.randn(M, K, generator=gen).to(dev)
         need = jk.act_q8_bytes(M, K)
@@ -477,8 +494,7 @@ def main() -> int:
         y = torch.empty(M * N, dtype=torch.float32, device=dev)
         for quant in (jk.Q4_0, jk.Q4_1, jk.Q5_0, jk.Q5_1, jk.IQ4_NL, jk.Q4_K, jk.Q5_K, jk.Q6_K, jk.Q2_K, jk.Q3_K,
                       jk.TQ1_0):
-            data = synth.gguf_weights(quant, N, K, seed=900 + quant)
-            ws = [jk.Weight(jk.TensorView(f"g{i}", quant, (N, K), data), N, K) for i in range(4)]
+            ws = copies(quant, N, K, 900 + quant)
             us = graph_us(lambda i, st: jk.dev_gemm_repacked(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
             tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
             name = f"gemm_repacked {jk.QUANT_NAMES[quant]} M=512"

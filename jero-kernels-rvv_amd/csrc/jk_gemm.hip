@@ -112,7 +112,7 @@ template <int TN, int TM> struct Stage {
 // past r1 are read clamped to r1 - 1 and never stored.
 template <int Q, int TN, int TM>
 __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage<TN, TM> &r) {
-    const int nb = w.nb, t = threadIdx.x;
+    const int nb = w.nb, t = (int)threadIdx.x % Tile<TN, TM>::THREADS;
     if constexpr (GemmFmt<Q>::B32) {
         constexpr int HW = fmt_of(Q).h_len / 4;  // words per block in the word plane
         const int b = min(4 * kc + (t & 3), nb - 1);
@@ -174,7 +174,7 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
 template <int Q, int TN, int TM>
 __device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage<TN, TM> &r) {
     using T = Tile<TN, TM>;
-    const int t = threadIdx.x;
+    const int t = (int)threadIdx.x % T::THREADS;
     int k = kKC * kc + 16 * (t & 7);
     if (k >= (int)a.k_padded) k = 0;  // past the row end (partial chunk): in bounds, unused
 #pragma unroll
@@ -227,7 +227,7 @@ template <int Q, int TN, int TM, class Chunk>
 __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, TM> &r, Chunk &c, int kc) {
     using T = Tile<TN, TM>;
     using F = GemmFmt<Q>;
-    const int t = threadIdx.x;
+    const int t = (int)threadIdx.x % T::THREADS;
     {  // activations
 #pragma unroll
         for (int i = 0; i < T::XL; ++i) put_b(c, (t >> 3) + T::THREADS / 8 * i, 16 * (t & 7), r.x[i]);
@@ -686,6 +686,133 @@ __global__ __launch_bounds__(64) void gemm16_kernel(WeightDev w, jk_act_q8 a, fl
     }
 }
 
+// One or two tokens (the reference's m <= 2 GEMV route, repack.rs:2892): the same per-group
+// arithmetic without MFMA, shaped for streaming. A workgroup owns 32 weight rows and all of K;
+// its NW waves take the 128-element chunks round-robin (wave v: chunks v, v + NW, ...), each
+// staging its chunk through the GEMM's loads (kGemvDepth chunks in flight) and unpacking into a
+// chunk of LDS of its own.
+// Each lane evaluates the terms of half the chunk's scale groups for one row and every token,
+//     term = f32(sum xq * wq) * (xs * ws)  [- xsum * wm],
+// the reference's per-group addend (accumulate_scaled_tile_scalar, repack.rs:3045-3093), into
+// an LDS table; after a barrier, wave 0 (lane: row l % 32 of token l / 32) adds the round's
+// terms to its accumulator in K order. Each output is therefore the same sum, in the same
+// order, as the GEMM's.
+constexpr int kGemvNW = 8;     // waves per workgroup (chunk LDS plus term tables: 99-142 KB of the 160 KB)
+constexpr int kGemvDepth = 2;  // chunks in flight per wave (4 measured slower: register pressure)
+
+template <int Q>
+__global__ __launch_bounds__(64 * kGemvNW) void gemv_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
+                                                                     int r0, int r1) {
+    using F = GemmFmt<Q>;
+    using Ch = GemmChunk<Q, 32, 16>;
+    constexpr int NW = kGemvNW, NG = F::NG, GPL = NG / 2;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    Ch &cs = reinterpret_cast<Ch *>(smem)[wave];
+    float *terms = reinterpret_cast<float *>(smem + NW * sizeof(Ch));  // [2 rounds][2 tokens][NW][NG][32]
+    const int n0 = r0 + 32 * (int)blockIdx.x;
+    const int M = (int)a.m;
+    const int steps = w.cols / 32, nchunks = (steps + kSteps - 1) / kSteps, rounds = (nchunks + NW - 1) / NW;
+    const int row = lane & 31, hs = lane >> 5;
+    float acc = 0.0f;  // wave 0: row n0 + row of token hs
+
+    // kGemvDepth chunks in flight per wave: round rd's chunk is staged in set rd % kGemvDepth
+    // (the loop is unrolled so that each staging set is a fixed set of registers)
+    Stage<32, 16> rg[kGemvDepth];
+#pragma unroll
+    for (int d = 0; d < kGemvDepth; ++d)
+        if (wave + NW * d < nchunks) chunk_load<Q>(rg[d], w, a, n0, r1, 0, M, wave + NW * d);
+    auto round = [&](int rd, Stage<32, 16> &stg) {
+        const int kc = NW * rd + wave;  // wave-uniform
+        float *tb = terms + (rd & 1) * (2 * NW * NG * 32);
+        if (kc < nchunks) {
+            chunk_store<Q>(w, stg, cs, kc);
+            wave_lds_sync();
+            if (kc + kGemvDepth * NW < nchunks) chunk_load<Q>(stg, w, a, n0, r1, 0, M, kc + kGemvDepth * NW);
+            const int ng = min(kSteps, steps - kSteps * kc) * 32 / F::GK;  // groups of this chunk
+            for (int m = 0; m < M; ++m) {
+#pragma unroll
+                for (int q = 0; q < GPL; ++q) {
+                    const int g = GPL * hs + q, st = g * F::GK / 32;
+                    if (g < ng) {
+                        const uint8_t *pa = cs.a + row * kRowB + F::GK * g, *pb = cs.b + m * kRowB + F::GK * g;
+                        int c = 0;
+#pragma unroll
+                        for (int i = 0; i < F::GK / 16; ++i) {
+                            const uint4 va = *reinterpret_cast<const uint4 *>(pa + 16 * i);
+                            const uint4 vb = *reinterpret_cast<const uint4 *>(pb + 16 * i);
+                            c = dot4((int)va.x, (int)vb.x, c);
+                            c = dot4((int)va.y, (int)vb.y, c);
+                            c = dot4((int)va.z, (int)vb.z, c);
+                            c = dot4((int)va.w, (int)vb.w, c);
+                        }
+                        float term = (float)c * (cs.xs[st][m] * cs.ws[g][row]);
+                        if constexpr (F::MINS && F::GK == 32) term = term - cs.xm[st][m] * cs.wm[st][row];
+                        if constexpr (F::MINS && F::GK == 16) term = term - cs.xm[g][m] * cs.wm[g][row];
+                        tb[((m * NW + wave) * NG + g) * 32 + row] = term;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0 && hs < M) {
+            // every term of the round read first (independent LDS reads in flight together),
+            // then added in K order; slots past the last chunk are read but never added
+            float t[NW * NG];
+#pragma unroll
+            for (int i = 0; i < NW * NG; ++i) t[i] = tb[(hs * NW * NG + i) * 32 + row];
+#pragma unroll
+            for (int v = 0; v < NW; ++v) {
+                const int kv = NW * rd + v;
+                const int ng = kv < nchunks ? min(kSteps, steps - kSteps * kv) * 32 / F::GK : 0;
+#pragma unroll
+                for (int g = 0; g < NG; ++g)
+                    if (g < ng) acc += t[v * NG + g];
+            }
+        }
+    };
+    for (int rd = 0; rd < rounds; rd += kGemvDepth) {
+#pragma unroll
+        for (int d = 0; d < kGemvDepth; ++d)
+            if (rd + d < rounds) round(rd + d, rg[d]);
+    }
+    if (wave == 0 && hs < M && n0 + row < r1) y[(size_t)hs * (size_t)(r1 - r0) + (size_t)(n0 + row - r0)] = acc;
+}
+
+template <int Q>
+static jk_status launch_gemv_repacked_q(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0,
+                                        int r1) {
+    constexpr size_t lds =
+        kGemvNW * sizeof(GemmChunk<Q, 32, 16>) + 2 * 2 * kGemvNW * GemmFmt<Q>::NG * 32 * sizeof(float);
+    static_assert(lds <= 160 * 1024, "GEMV LDS budget (160 KB per workgroup on gfx950)");
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_repacked_kernel<Q>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return hip_fail(attr, "gemv_repacked_kernel LDS");
+    hipLaunchKernelGGL(gemv_repacked_kernel<Q>, dim3((unsigned)((r1 - r0 + 31) / 32)), dim3(64 * kGemvNW), lds, s, w, a,
+                       y, r0, r1);
+    return check_launch("gemv_repacked_kernel");
+}
+
+// m <= 2 of the repacked GEMM entry points (both modes: the result is the bit-exact one).
+static jk_status launch_gemv_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    switch (w.quant) {
+    case JK_Q8_0: return launch_gemv_repacked_q<JK_Q8_0>(s, w, a, y, r0, r1);
+    case JK_Q4_0: return launch_gemv_repacked_q<JK_Q4_0>(s, w, a, y, r0, r1);
+    case JK_Q5_0: return launch_gemv_repacked_q<JK_Q5_0>(s, w, a, y, r0, r1);
+    case JK_Q4_K: return launch_gemv_repacked_q<JK_Q4_K>(s, w, a, y, r0, r1);
+    case JK_Q5_K: return launch_gemv_repacked_q<JK_Q5_K>(s, w, a, y, r0, r1);
+    case JK_Q4_1: return launch_gemv_repacked_q<JK_Q4_1>(s, w, a, y, r0, r1);
+    case JK_Q5_1: return launch_gemv_repacked_q<JK_Q5_1>(s, w, a, y, r0, r1);
+    case JK_IQ4_NL: return launch_gemv_repacked_q<JK_IQ4_NL>(s, w, a, y, r0, r1);
+    case JK_Q2_K: return launch_gemv_repacked_q<JK_Q2_K>(s, w, a, y, r0, r1);
+    case JK_Q3_K: return launch_gemv_repacked_q<JK_Q3_K>(s, w, a, y, r0, r1);
+    case JK_Q6_K: return launch_gemv_repacked_q<JK_Q6_K>(s, w, a, y, r0, r1);
+    case JK_TQ2_0: return launch_gemv_repacked_q<JK_TQ2_0>(s, w, a, y, r0, r1);
+    case JK_I2_S: return launch_gemv_repacked_q<JK_I2_S>(s, w, a, y, r0, r1);
+    default: return fail(JK_CAPABILITY_MISMATCH, "gemm: unsupported quant %d", w.quant);
+    }
+}
+
 // Tile shape of a launch: the largest tile that still gives every CU two workgroups, down to the
 // 32 x 16 single-wave tiles (not for Q6_K). (Four 32 x 32 tiles per CU beat the 32 x 16 tiles
 // with the weights cold in HBM: those re-read every weight tile twice as often.)
@@ -746,6 +873,7 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
 }
 
 jk_status launch_gemm_repacked_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    if (a.m <= 2) return launch_gemv_repacked(s, w, a, y, r0, r1);
     switch (w.quant) {
     case JK_Q8_0: return launch_gemm_tol<JK_Q8_0>(s, w, a, y, r0, r1);
     case JK_Q4_0: return launch_gemm_tol<JK_Q4_0>(s, w, a, y, r0, r1);
@@ -785,6 +913,7 @@ jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t 
 }
 
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    if (a.m <= 2) return launch_gemv_repacked(s, w, a, y, r0, r1);
     switch (w.quant) {
     case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, r0, r1);
     case JK_Q4_0: return launch_gemm<JK_Q4_0, 1>(s, w, a, y, r0, r1);

@@ -486,6 +486,34 @@ def test_gemm_repacked(gpu, quant, m, rows, cols):
 
 
 @pytest.mark.parametrize("quant", ALL_FORMATS)
+@pytest.mark.parametrize("m,rows,cols", [(1, 37, 512), (2, 100, 4096), (1, 33, 768), (2, 9, 160), (1, 4100, 1280),
+                                         (2, 70, 14336)])
+def test_gemv_repacked_one_or_two_tokens(gpu, quant, m, rows, cols):
+    """m <= 2 runs the GEMV kernel (K split over the waves of a 32-row workgroup, terms folded in K
+    order): every repacked entry point == the oracle bit for bit -- one and several rounds of
+    chunks, a partial last round and a partial last chunk (160 = 5 steps of 32), a partial last
+    row tile, row slices, both GEMM modes and jk_gemv_repacked."""
+    torch = gpu
+    if cols % jk.BLOCK_ELEMENTS[quant]:
+        pytest.skip("shape not block aligned")
+    raw = synth.random_weights(quant, rows, cols, seed=7 * m + quant + rows, specials=True)
+    x = np.random.default_rng(m + cols).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, O.ActQ8(x, m, cols), 0, rows)
+    got = gpu_gemm(torch, w, x, m)
+    assert same_bits(got, ref), mismatch(got, ref)
+    r0, r1 = min(3, rows - 1), rows - min(5, rows - 4)
+    assert same_bits(gpu_gemm(torch, w, x, m, r0, r1), ref[:, r0:r1])
+    assert same_bits(gpu_gemm_tol(torch, w, x, m), ref)
+    if m == 1:
+        storage, act = gpu_act(torch, x, m, cols)
+        dy = empty(torch, 4 * rows)
+        jk.dev_gemv_repacked(w, act, dy, rows, 0, rows)
+        torch.cuda.synchronize()
+        assert same_bits(host(dy, np.float32, rows).reshape(1, rows), ref)
+
+
+@pytest.mark.parametrize("quant", ALL_FORMATS)
 @pytest.mark.parametrize("m", [500, 250, 128, 30])
 def test_gemm_tile_shapes(gpu, quant, m):
     """8200 rows: 500 tokens launch 128x64 tiles, 250 tokens 64x64, 128 tokens 32x32, 30
@@ -514,7 +542,7 @@ def gpu_gemm_tol(torch, w, x, m, r0=0, r1=None):
 
 
 def assert_within_row_norm(got, ref, tol=1e-5):
-    """north_star's bar for f32 products: every output within tol of its token's output-row L2 norm."""
+    """The bar for f32 products: every output within tol of its token's output-row L2 norm."""
     ref64 = ref.astype(np.float64)
     norms = np.linalg.norm(ref64, axis=1)
     err = np.abs(got.astype(np.float64) - ref64).max(axis=1)
