@@ -26,6 +26,7 @@ namespace jk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kKC = 128;      // K elements per chunk
@@ -53,7 +54,8 @@ template <int TN, int TM> struct Tile {
     static constexpr int XS = 4 * TM / THREADS;   // activation scales per thread and chunk
     static constexpr int XS16 = 8 * TM / THREADS; // activation 16-sums per thread and chunk (Q2_K)
     static constexpr int WPE = TN == 128 ? 3 : 2;  // waves per SIMD the register budget allows
-    static_assert(WR * WM == WAVES && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
+    // (a wave covers 32 tokens, or 64 in the tolerance kernel's 128 x 128 tiles)
+    static_assert((WR * WM) % WAVES == 0 && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
 };
 
 template <int Q, int TN, int TM> struct GemmChunk {
@@ -475,7 +477,10 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[nt][v] = 0.0f;
-    v32f tacc = v32f{0};  // TOL: both 32-row blocks' accumulators in the outer product's layout
+    v16f tacc[NT];  // TOL: the accumulators of each 32-row block, in the MFMA result layout
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) tacc[nt] = v16f{0};
+    static_assert(!TOL || (F::GK == 32 && GB == 1), "tolerance mode: 32-element groups, one per step");
 
     v16i cacc[NT];  // i32 partials of the current scale block (GB > 1)
 #pragma unroll
@@ -486,6 +491,27 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
     auto step = [&](int kc, int st) {
         const float xs = cs.xs[st][tok];
         const float xsum32 = F::MINS && F::GK == 32 ? cs.xm[st][tok] : 0.0f;
+        if constexpr (TOL) {
+            // One 32-row block at a time: its integer partial, its scale products as a K = 2 f32
+            // outer product (lanes 32..63 supply the zero second column, so each is the single
+            // rounded product xs * ws), then one fused multiply-add per output; formats with mins
+            // add -(xsum * wm) through the same outer product accumulating into the block.
+            const v4i bq = *reinterpret_cast<const v4i *>(cs.b + tok * kRowB + 32 * st + 16 * hl);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int r = RW * wn + 32 * nt + jl;
+                const v4i aq = *reinterpret_cast<const v4i *>(cs.a + r * kRowB + 32 * st + 16 * hl);
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+                const v16f p =
+                    __builtin_amdgcn_mfma_f32_32x32x2f32(hl ? 0.0f : cs.ws[st][r], hl ? 0.0f : xs, v16f{0}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) tacc[nt][v] = __builtin_fmaf((float)c[v], p[v], tacc[nt][v]);
+                if constexpr (F::MINS)
+                    tacc[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(hl ? 0.0f : -cs.wm[st][r], hl ? 0.0f : xsum32,
+                                                                    tacc[nt], 0, 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (int gg = 0; gg < 32 / F::GK; ++gg) {
             v16i c[NT];
@@ -522,16 +548,6 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
             // of block nt in element 16 nt + v.
             const int g = (32 / F::GK) * st + gg;
             const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[g][srow], xs, v32f{0}, 0, 0, 0);
-            if constexpr (TOL) {
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        tacc[16 * nt + v] = __builtin_fmaf((float)c[nt][v], p[16 * nt + v], tacc[16 * nt + v]);
-                if constexpr (F::MINS && F::GK == 32)
-                    tacc = __builtin_amdgcn_mfma_f32_32x32x1f32(-cs.wm[st][srow], xsum32, tacc, 0, 0, 0);
-                continue;
-            }
             v32f pm;
             // mins: per 32-group with the 32-block activation sum, or per 16-group (Q2_K) with
             // the 16-element sum (accumulate_scaled_tile_scalar, repack.rs:3061-3077)
@@ -577,9 +593,285 @@ gemm_repacked_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, in
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int n = n0 + RW * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
-                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = TOL ? tacc[16 * nt + v] : acc[nt][v];
+                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = TOL ? tacc[nt][v] : acc[nt][v];
             }
     }
+}
+
+// Tolerance-mode prefill tiles for the 32-element-group formats: a workgroup computes 128
+// weight rows x 128 tokens with four waves, each 64 rows x 64 tokens (2 x 2 blocks of 32 x 32),
+// at two waves per SIMD. Per scale group a wave issues four integer MFMAs, one two-block f32
+// outer product of the scale products per token block (each the single rounded xs * ws), and
+// one fused multiply-add per output, acc = fma(f32(c), xs * ws, acc); formats with mins add
+// -(xsum * wm) through an outer product accumulating into the accumulators. Against the
+// 128 x 64 tiles at three waves per SIMD the tile count halves (a 512-token launch fits the
+// GPU's 512 resident workgroups in one round instead of 1.17) and each staged weight byte
+// feeds twice the MFMAs.
+template <int Q>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gemm_tol_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+    using F = GemmFmt<Q>;
+    constexpr int TN = 128, TM = 128;
+    static_assert(F::GK == 32, "32-element scale groups");
+    __shared__ __align__(16) GemmChunk<Q, TN, TM> cs;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wn = wave & 1, wmi = wave >> 1;  // wave tile: rows 64 wn .., tokens 64 wmi ..
+    // tile order as gemm_repacked_kernel: a row tile's token tiles on one XCD
+    const int ntn = (r1 - r0 + TN - 1) / TN, ntm = ((int)a.m + TM - 1) / TM;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;
+    const int n0 = r0 + tn * TN, m0 = tm * TM;
+    const int M = (int)a.m;
+    const int steps = w.cols / 32;
+    const int nchunks = (steps + kSteps - 1) / kSteps;
+    const int hl = lane >> 5, jl = lane & 31;
+    const int arow = 64 * wn + jl;  // A operand row of block 0 (block 1: + 32)
+
+    v32f tacc[2];  // [token block]: both 32-row blocks, element 16 nt + v
+    tacc[0] = tacc[1] = v32f{0};
+    // A step's MFMA operands, read from LDS one step ahead of their use (the scales are read
+    // where they are used)
+    struct Ops {
+        v4i aq[2], bq[2];
+    };
+    auto load_ops = [&](int st) {
+        Ops o;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            o.aq[nt] = *reinterpret_cast<const v4i *>(cs.a + (arow + 32 * nt) * kRowB + 32 * st + 16 * hl);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+            o.bq[tb] = *reinterpret_cast<const v4i *>(cs.b + (64 * wmi + 32 * tb + jl) * kRowB + 32 * st + 16 * hl);
+        return o;
+    };
+    auto compute = [&](const Ops &o, int st) {
+        const float ws = cs.ws[st][64 * wn + lane];  // lane l: row of block l / 32
+        [[maybe_unused]] const float wm = F::MINS ? -cs.wm[st][64 * wn + lane] : 0.0f;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const int tok = 64 * wmi + 32 * tb + jl;
+            v16i c[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.aq[nt], o.bq[tb], v16i{0}, 0, 0, 0);
+            const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, cs.xs[st][tok], v32f{0}, 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    tacc[tb][16 * nt + v] = __builtin_fmaf((float)c[nt][v], p[16 * nt + v], tacc[tb][16 * nt + v]);
+            if constexpr (F::MINS) tacc[tb] = __builtin_amdgcn_mfma_f32_32x32x1f32(wm, cs.xm[st][tok], tacc[tb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // the four steps of a whole chunk, unrolled, each step's operands read during the previous one
+    // (a loop, not unrolled: unrolled, the register allocation of the four steps spills)
+    auto chunk4 = [&]() {
+        Ops cur = load_ops(0);
+#pragma unroll 1
+        for (int st = 0; st < kSteps; ++st) {
+            const Ops nxt = load_ops(st + 1 < kSteps ? st + 1 : st);
+            compute(cur, st);
+            cur = nxt;
+        }
+    };
+
+    Stage<TN, TM> rg;
+    chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
+    chunk_store<Q>(w, rg, cs, 0);
+    __syncthreads();
+    for (int kc = 0; kc < nchunks; ++kc) {
+        const bool more = kc + 1 < nchunks;
+        if (more) chunk_load<Q>(rg, w, a, n0, r1, m0, M, kc + 1);
+        chunk4();  // (K is a multiple of 128 on this kernel)
+        if (more) {
+            __syncthreads();
+            chunk_store<Q>(w, rg, cs, kc + 1);
+            __syncthreads();
+        }
+    }
+
+    const size_t ld = (size_t)(r1 - r0);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+        const int m = m0 + 64 * wmi + 32 * tb + jl;
+        if (m >= M) continue;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int n = n0 + 64 * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
+                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = tacc[tb][16 * nt + v];
+            }
+    }
+}
+
+// Q8_0 tolerance-mode prefill, the same tiles and arithmetic as gemm_tol_kernel with its loads
+// made asynchronous: Q8_0 quants need no unpacking, so every tile goes from global memory
+// straight into LDS (global_load_lds: lane l of a load writes bytes 16 l.. of a 1 KB LDS
+// span), two chunk stages deep, with no staging registers. While chunk kc is evaluated from
+// one stage, chunk kc + 1 streams into the other. The stages are separate LDS objects, so
+// the compiler's dependency tracking keeps the reads of one stage free of the loads into the
+// other; each wave waits for its own loads of a stage (vmcnt) before a barrier publishes it.
+// A stage (35 KB): weights [row][8 x 16 B] and activation quants [token][8 x 16 B] with the
+// 16-byte piece p of row r at slot p ^ (r & 7) (the 32 rows or tokens an MFMA operand read
+// covers then fall on distinct banks in every group of 8 lanes), the f16 scales of the
+// chunk's four blocks per row, and the f32 activation scales per token.
+template <int TN> struct alignas(16) Q8Stage {
+    uint8_t a[TN * 128];
+    uint8_t x[128 * 128];
+    uint16_t ws[TN * 4];
+    float xs[128 * 4];
+};
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+// s_waitcnt vmcnt(n) (GFX9 encoding; expcnt and lgkmcnt left unconstrained)
+#define JK_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | (7 << 4) | (15 << 8))
+// loads per wave and stage (NW = TN / 32 waves): 4 weight, 16 / NW activation, 1 scale, 8 / NW act scale
+template <int TN> constexpr int kQ8DmaPerWave = 4 + 16 / (TN / 32) + 1 + 8 / (TN / 32);
+
+// Workgroup barrier between the stage phases with the waits made explicit: a wave has already
+// waited for its own loads into the stage (vmcnt) and waits here for its own LDS reads (lgkmcnt);
+// the compiler-only fences keep memory accesses on their side of the barrier. (A release fence
+// would also wait for the loads into the other stage: LDS-bound loads count as LDS writes.)
+__device__ __forceinline__ void stage_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int TN>
+__device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_act_q8 &a, float *__restrict__ y, int r0,
+                                                  int r1) {
+    constexpr int TM = 128, NW = TN / 32, WR = TN / 64;  // waves; waves along the rows (64 rows each)
+    constexpr int XPW = 16 / NW, SPW = 8 / NW;          // activation / activation-scale loads per wave
+    __shared__ Q8Stage<TN> sA;
+    __shared__ Q8Stage<TN> sB;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wn = wave % WR, wmi = wave / WR;  // wave tile: rows 64 wn .., tokens 64 wmi ..
+    const int ntn = (r1 - r0 + TN - 1) / TN, ntm = ((int)a.m + TM - 1) / TM;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;
+    const int n0 = r0 + tn * TN, m0 = tm * TM;
+    const int M = (int)a.m, nb = w.nb;
+    const int nchunks = w.cols / 128;  // (K is a multiple of 128 on this kernel)
+    const int hl = lane >> 5, jl = lane & 31;
+    const size_t pstride = (size_t)w.rows * (size_t)nb * 16;
+
+    // this lane's share of a stage's loads (addresses of chunk 0; chunk kc adds a fixed offset)
+    const int rr = lane >> 3, slot = lane & 7;
+    const uint8_t *asrc[4];
+    const uint8_t *xsrc[XPW];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = 8 * (4 * wave + i) + rr, p = slot ^ (n & 7);
+        const int gn = min(n0 + n, r1 - 1);
+        asrc[i] = w.planes + (size_t)(p & 1) * pstride + ((size_t)gn * (size_t)nb + (size_t)(p >> 1)) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) {
+        const int t = 8 * (XPW * wave + i) + rr, q = slot ^ (t & 7);
+        const int gt = min(m0 + t, M - 1);
+        xsrc[i] = reinterpret_cast<const uint8_t *>(a.qs) + (size_t)gt * a.k_padded + (size_t)(16 * q);
+    }
+    const int wsd = 64 * wave + lane;  // dword of the scale span: row wsd / 2, blocks 2 (wsd % 2) ..
+    const uint8_t *wssrc = reinterpret_cast<const uint8_t *>(w.dplane) +
+                           ((size_t)min(n0 + (wsd >> 1), r1 - 1) * (size_t)nb + (size_t)(2 * (wsd & 1))) * 2;
+    const uint8_t *xssrc[SPW];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+        const int d = 64 * (SPW * wave + i) + lane;  // token d / 4, block d % 4
+        xssrc[i] = reinterpret_cast<const uint8_t *>(a.scales) +
+                   ((size_t)min(m0 + (d >> 2), M - 1) * a.k_blocks32 + (size_t)(d & 3)) * 4;
+    }
+    auto issue = [&](Q8Stage<TN> &S, int kc) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(asrc[i] + (size_t)kc * 64, (lds_void_t *)((lds_u8_t *)S.a + 1024 * (4 * wave + i)),
+                                             16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < XPW; ++i)
+            __builtin_amdgcn_global_load_lds(xsrc[i] + (size_t)kc * 128,
+                                             (lds_void_t *)((lds_u8_t *)S.x + 1024 * (XPW * wave + i)), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(wssrc + (size_t)kc * 8, (lds_void_t *)((lds_u8_t *)S.ws + 256 * wave), 4, 0, 0);
+#pragma unroll
+        for (int i = 0; i < SPW; ++i)
+            __builtin_amdgcn_global_load_lds(xssrc[i] + (size_t)kc * 16,
+                                             (lds_void_t *)((lds_u8_t *)S.xs + 256 * (SPW * wave + i)), 4, 0, 0);
+    };
+
+    v32f tacc[2];
+    tacc[0] = tacc[1] = v32f{0};
+    const int arow = 64 * wn + jl;
+    auto chunk = [&](const Q8Stage<TN> &S) {
+#pragma unroll 1
+        for (int st = 0; st < kSteps; ++st) {
+            const int pc = 2 * st + hl;  // 16-byte piece: block st, half hl
+            v4i aq[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int r = arow + 32 * nt;
+                aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ (r & 7)) << 4));
+            }
+            const float ws = f16_finite(S.ws[(64 * wn + lane) * 4 + st]);  // lane l: row of block l / 32
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const int t = 64 * wmi + 32 * tb + jl;
+                const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ (t & 7)) << 4));
+                v16i c[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, v16i{0}, 0, 0, 0);
+                const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, S.xs[t * 4 + st], v32f{0}, 0, 0, 0);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        tacc[tb][16 * nt + v] = __builtin_fmaf((float)c[nt][v], pr[16 * nt + v], tacc[tb][16 * nt + v]);
+            }
+        }
+    };
+
+    issue(sA, 0);
+    if (nchunks > 1) issue(sB, 1);
+    for (int kc = 0; kc < nchunks; kc += 2) {
+        if (kc + 1 < nchunks) JK_WAIT_VMCNT(kQ8DmaPerWave<TN>);
+        else JK_WAIT_VMCNT(0);
+        stage_barrier();
+        chunk(sA);
+        stage_barrier();
+        if (kc + 2 < nchunks) issue(sA, kc + 2);
+        if (kc + 1 >= nchunks) break;
+        if (kc + 2 < nchunks) JK_WAIT_VMCNT(kQ8DmaPerWave<TN>);
+        else JK_WAIT_VMCNT(0);
+        stage_barrier();
+        chunk(sB);
+        stage_barrier();
+        if (kc + 3 < nchunks) issue(sB, kc + 3);
+    }
+
+    const size_t ld = (size_t)(r1 - r0);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+        const int m = m0 + 64 * wmi + 32 * tb + jl;
+        if (m >= M) continue;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int n = n0 + 64 * wn + 32 * nt + 8 * (v >> 2) + 4 * hl + (v & 3);
+                if (n < r1) y[(size_t)m * ld + (size_t)(n - r0)] = tacc[tb][16 * nt + v];
+            }
+    }
+}
+
+// (a plain kernel around the body: the host stub of a kernel template with this body is not
+// emitted)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gemm_q8_0_tol_dma_128(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+    gemm_q8_0_tol_dma<128>(w, a, y, r0, r1);
 }
 
 static long cu_count() {
@@ -863,6 +1155,20 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
     if constexpr (GemmFmt<Q>::GK == 16) {
         return launch_gemm<Q, 1>(s, w, a, y, r0, r1);
     } else {
+        const long ncu = cu_count();
+        const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
+        if (t128 >= ncu && w.cols % 128 == 0) {  // at least one 128 x 128 tile per CU; whole chunks
+            const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
+            if constexpr (Q == JK_Q8_0) {
+                // (256-row tiles, one workgroup per CU, measured slower at 512 and 2048 tokens)
+                hipLaunchKernelGGL(gemm_q8_0_tol_dma_128, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
+                                   a, y, r0, r1);
+                return check_launch("gemm_q8_0_tol_dma");
+            }
+            hipLaunchKernelGGL(gemm_tol_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w, a, y,
+                               r0, r1);
+            return check_launch("gemm_tol_kernel");
+        }
         switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
         case 0: launch_tile<Q, 1, 128, 64, true>(s, w, a, y, r0, r1); break;
         case 1: launch_tile<Q, 1, 64, 64, true>(s, w, a, y, r0, r1); break;
