@@ -723,8 +723,19 @@ template <int TN> struct alignas(16) Q8Stage {
     uint16_t ws[TN * 4];
     float xs[128 * 4];
 };
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+// One global-to-LDS load of 16 (or 4) bytes per lane into the LDS span starting at byte lds
+// (M0). Written as inline asm so that the compiler's wait insertion, which cannot tell the two
+// stages' loads apart across the loop, does not drain the other stage's loads before every
+// read of this one; the kernel waits for its own loads explicitly (vmcnt) instead. No
+// compiler-issued global load shares the loop, so those explicit counts are exact.
+__device__ __forceinline__ void lds_dma16(const void *src, const lds_u8_t *lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"((unsigned)(size_t)lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *src, const lds_u8_t *lds) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"((unsigned)(size_t)lds) : "memory");
+}
 
 // s_waitcnt vmcnt(n) (GFX9 encoding; expcnt and lgkmcnt left unconstrained)
 #define JK_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | (7 << 4) | (15 << 8))
@@ -789,18 +800,12 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
     }
     auto issue = [&](Q8Stage<TN> &S, int kc) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(asrc[i] + (size_t)kc * 64, (lds_void_t *)((lds_u8_t *)S.a + 1024 * (4 * wave + i)),
-                                             16, 0, 0);
+        for (int i = 0; i < 4; ++i) lds_dma16(asrc[i] + (size_t)kc * 64, (lds_u8_t *)S.a + 1024 * (4 * wave + i));
 #pragma unroll
-        for (int i = 0; i < XPW; ++i)
-            __builtin_amdgcn_global_load_lds(xsrc[i] + (size_t)kc * 128,
-                                             (lds_void_t *)((lds_u8_t *)S.x + 1024 * (XPW * wave + i)), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(wssrc + (size_t)kc * 8, (lds_void_t *)((lds_u8_t *)S.ws + 256 * wave), 4, 0, 0);
+        for (int i = 0; i < XPW; ++i) lds_dma16(xsrc[i] + (size_t)kc * 128, (lds_u8_t *)S.x + 1024 * (XPW * wave + i));
+        lds_dma4(wssrc + (size_t)kc * 8, (lds_u8_t *)S.ws + 256 * wave);
 #pragma unroll
-        for (int i = 0; i < SPW; ++i)
-            __builtin_amdgcn_global_load_lds(xssrc[i] + (size_t)kc * 16,
-                                             (lds_void_t *)((lds_u8_t *)S.xs + 256 * (SPW * wave + i)), 4, 0, 0);
+        for (int i = 0; i < SPW; ++i) lds_dma4(xssrc[i] + (size_t)kc * 16, (lds_u8_t *)S.xs + 256 * (SPW * wave + i));
     };
 
     v32f tacc[2];
