@@ -300,7 +300,10 @@ def main() -> int:
                        "ms_per_call_incl_quantize": round(step_ms, 4)}
                 log(f"gemm Q8_0 M={M} {mode}: kernel {kern_us:.1f} us = {tops:.1f} TOPS "
                     f"({step_ms:.3f} ms/call incl. quantize)")
-                kname = "gemm_tol_kernel<Q8_0>" if mode == "tolerance" else "gemm_repacked_kernel<Q8_0>"
+                t128 = -(-N // 128) * -(-M // 128)  # 128 x 128 tolerance tiles (one per CU at least)
+                kname = (("gemm_q8_0_tol_dma_128 (128x128 tiles, LDS-bound loads)" if t128 >= 256
+                          else "gemm_repacked_kernel<Q8_0, tolerance>") if mode == "tolerance"
+                         else "gemm_repacked_kernel<Q8_0>")
                 line = {"workload": f"Q8_0 {N}x{K} weights x {M} tokens (QuantizedActQ8 per-32 activations), "
                                     + ("outputs within 1e-5 of each token's output-row L2 norm of the reference "
                                        "recipe (one fused multiply-add per scale group)" if mode == "tolerance"
