@@ -322,8 +322,10 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
  * multiply-add (acc = fma(partial, xs * ws, acc); formats with mins add -(xsum * wm) as one more
  * rounded step) instead of the reference's separately rounded product and sum. Every output is
  * within 1e-5 of its token's output-row L2 norm of the bit-exact result (the tolerance the port
- * is held to for f32 products); about three times the throughput of jk_gemm_repacked at 512
- * tokens. No reference function has this rounding: it is the bit-exact call's alternative. */
+ * is held to for f32 products). From one 128 x 128 tile per CU on (14336 rows: 512 tokens), the
+ * 32-element-group formats run larger tiles with fewer VALU operations per scale group, about
+ * 1.2x the throughput of jk_gemm_repacked; Q2_K, Q3_K and Q6_K run the bit-exact kernel. No
+ * reference function has this rounding: it is the bit-exact call's alternative. */
 jk_status jk_gemm_repacked_tol(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
                                size_t y_len, size_t row_begin, size_t row_end);
 /* gemv_repacked_view_rows (repack.rs:4045-4061): requires act->m == 1. */
