@@ -55,7 +55,7 @@ template <int TN, int TM> struct Tile {
     static constexpr int XS16 = 8 * TM / THREADS; // activation 16-sums per thread and chunk (Q2_K)
     static constexpr int WPE = TN == 128 ? 3 : 2;  // waves per SIMD the register budget allows
     // (a wave covers 32 tokens, or 64 in the tolerance kernel's 128 x 128 tiles)
-    static_assert((WR * WM) % WAVES == 0 && XL >= 1 && XS >= 1 && XS <= 2, "tile shape");
+    static_assert((WR * WM) % WAVES == 0 && XL >= 1 && XS >= 1 && XS <= 4, "tile shape");
 };
 
 template <int Q, int TN, int TM> struct GemmChunk {
@@ -1110,6 +1110,159 @@ static jk_status launch_gemv_repacked(hipStream_t s, const WeightDev &w, const j
     }
 }
 
+// Tolerance-mode products of a few tokens (3 up to a few hundred) for the 32-element-group
+// formats, where the tiled kernels have too few tiles to fill the GPU: K is split instead. A
+// workgroup owns 32 weight rows x TM tokens (TM = 32 or 64) and all of K; its NW waves take the
+// 128-element chunks round-robin (wave v: chunks v, v + NW, ...). Each wave stages its chunks
+// through the GEMM's coalesced loads and unpacking into an LDS chunk of its own -- two chunks in
+// flight per wave, no barrier with the other waves -- and accumulates a partial tile; the NW
+// partial tiles are added in wave order through LDS at the end. Per 32-element step: one
+// integer MFMA per 32-token block; the scale products from one two-block f32 outer product
+// (TM = 64: the two token blocks; TM = 32: two steps, held in the two halves of the partial tile
+// until the end); one fused multiply-add per output; formats with mins add -(xsum * wm) through
+// a second outer product accumulating into the partial tile.
+template <int Q, int TM, int NW> union SplitkSmem {
+    GemmChunk<Q, 32, TM> cs[NW];  // while the chunks are evaluated: one per wave
+    float red[NW][TM][33];        // then the partial tiles [wave][token][row], rows padded to 33
+};
+
+template <int Q, int TM>
+__device__ __forceinline__ void sk_compute(const GemmChunk<Q, 32, TM> &cs, v32f &acc, int lane) {
+    constexpr bool MINS = GemmFmt<Q>::MINS;
+    const int hl = lane >> 5, jl = lane & 31;
+    const uint8_t *pa = cs.a + jl * kRowB + 16 * hl;
+    if constexpr (TM == 64) {
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            const v4i aq = *reinterpret_cast<const v4i *>(pa + 32 * st);
+            // lane l: row jl and token l (token block l / 32)
+            const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[st][jl], cs.xs[st][lane], v32f{0}, 0, 0, 0);
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const v4i bq = *reinterpret_cast<const v4i *>(cs.b + (32 * tb + jl) * kRowB + 32 * st + 16 * hl);
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[16 * tb + v] = __builtin_fmaf((float)c[v], p[16 * tb + v], acc[16 * tb + v]);
+                __builtin_amdgcn_sched_barrier(0);  // (interleaving the steps' MFMAs spills)
+            }
+            if constexpr (MINS)
+                acc = __builtin_amdgcn_mfma_f32_32x32x1f32(-cs.wm[st][jl], cs.xm[st][lane], acc, 0, 0, 0);
+        }
+    } else {
+        const uint8_t *pb = cs.b + jl * kRowB + 16 * hl;
+#pragma unroll
+        for (int st = 0; st < kSteps; st += 2) {
+            // lanes 0..31 carry step st, lanes 32..63 step st + 1 into the outer products
+            const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[st + hl][jl], cs.xs[st + hl][jl], v32f{0}, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const v4i aq = *reinterpret_cast<const v4i *>(pa + 32 * (st + e));
+                const v4i bq = *reinterpret_cast<const v4i *>(pb + 32 * (st + e));
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[16 * e + v] = __builtin_fmaf((float)c[v], p[16 * e + v], acc[16 * e + v]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (MINS)
+                acc = __builtin_amdgcn_mfma_f32_32x32x1f32(-cs.wm[st + hl][jl], cs.xm[st + hl][jl], acc, 0, 0, 0);
+        }
+    }
+}
+
+template <int Q, int TM, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
+                                                                  int r0, int r1) {
+    static_assert(GemmFmt<Q>::GK == 32 && (TM == 32 || TM == 64), "32-element groups; 32 or 64 tokens");
+    __shared__ __align__(16) SplitkSmem<Q, TM, NW> sm;
+    // (wave read as a scalar: the chunk loop's branches are then uniform, not exec-masked)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hl = lane >> 5, jl = lane & 31;
+    // tile order as gemm_repacked_kernel: a row tile's token tiles on one XCD
+    const int ntn = (r1 - r0 + 31) / 32, ntm = ((int)a.m + TM - 1) / TM;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;  // workgroup-uniform: the whole workgroup leaves before any barrier
+    const int n0 = r0 + 32 * tn, m0 = TM * tm, M = (int)a.m;
+    const int nchunks = w.cols / kKC;
+    GemmChunk<Q, 32, TM> &cs = sm.cs[wave];
+
+    v32f acc = v32f{0};
+    // Chunks of this wave: wave, wave + NW, ... Every load is unconditional (a chunk past the
+    // wave's last is read as its last again, from L2) so that the loads in flight are the same on
+    // every path and each staging buffer's wait leaves the other buffer's loads in flight.
+    const int cnt = (nchunks - wave + NW - 1) / NW;
+    if (cnt > 0) {
+        const int last = wave + NW * (cnt - 1);
+        auto ck = [&](int i) { return min(wave + NW * i, last); };
+        Stage<32, TM> ra, rb;
+        // (the scheduling barriers keep each phase in place: the waits count loads in issue order,
+        // so a buffer loaded out of turn -- here or in the loop -- would drain the other one too)
+        chunk_load<Q>(ra, w, a, n0, r1, m0, M, ck(0));
+        __builtin_amdgcn_sched_barrier(0);
+        chunk_load<Q>(rb, w, a, n0, r1, m0, M, ck(1));
+        __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < cnt; i += 2) {
+            chunk_store<Q>(w, ra, cs, ck(i));
+            wave_lds_sync();
+            __builtin_amdgcn_sched_barrier(0);
+            chunk_load<Q>(ra, w, a, n0, r1, m0, M, ck(i + 2));
+            __builtin_amdgcn_sched_barrier(0);
+            sk_compute(cs, acc, lane);
+            wave_lds_sync();  // the chunk's LDS reads are done before the next store
+            __builtin_amdgcn_sched_barrier(0);
+            chunk_store<Q>(w, rb, cs, ck(i + 1));
+            wave_lds_sync();
+            __builtin_amdgcn_sched_barrier(0);
+            chunk_load<Q>(rb, w, a, n0, r1, m0, M, ck(i + 3));
+            __builtin_amdgcn_sched_barrier(0);
+            if (i + 1 < cnt) sk_compute(cs, acc, lane);
+            wave_lds_sync();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    __syncthreads();  // every wave is done with its chunk before the partial tiles overwrite them
+    // element v of block e: row 8 (v / 4) + 4 hl + v % 4; token jl of token block e (TM = 64)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = 8 * (v >> 2) + 4 * hl + (v & 3);
+        if constexpr (TM == 64) {
+            sm.red[wave][jl][row] = acc[v];
+            sm.red[wave][32 + jl][row] = acc[16 + v];
+        } else {
+            sm.red[wave][jl][row] = acc[v] + acc[16 + v];
+        }
+    }
+    __syncthreads();
+    const size_t ld = (size_t)(r1 - r0);
+    for (int o = (int)threadIdx.x; o < TM * 32; o += 64 * NW) {
+        const int tok = o >> 5, row = o & 31;
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) s += sm.red[v][tok][row];
+        if (m0 + tok < M && n0 + row < r1) y[(size_t)(m0 + tok) * ld + (size_t)(n0 + row - r0)] = s;
+    }
+}
+
+// waves per workgroup (K = 4096: 32 chunks, 8 per wave): two workgroups per CU by registers, and
+// eight waves per workgroup measured slower (their 1.75 rounds over the CUs against one)
+constexpr int kSplitkNW = 4;
+
+template <int Q>
+static jk_status launch_splitk(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    const size_t ntn = (size_t)(r1 - r0 + 31) / 32;
+    if (a.m <= 32) {
+        const size_t ntm = (a.m + 31) / 32;
+        hipLaunchKernelGGL((gemm_tol_splitk_kernel<Q, 32, kSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+                           dim3(64 * kSplitkNW), 0, s, w, a, y, r0, r1);
+    } else {
+        const size_t ntm = (a.m + 63) / 64;
+        hipLaunchKernelGGL((gemm_tol_splitk_kernel<Q, 64, kSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+                           dim3(64 * kSplitkNW), 0, s, w, a, y, r0, r1);
+    }
+    return check_launch("gemm_tol_splitk_kernel");
+}
+
 // Tile shape of a launch: the largest tile that still gives every CU two workgroups, down to the
 // 32 x 16 single-wave tiles (not for Q6_K). (Four 32 x 32 tiles per CU beat the 32 x 16 tiles
 // with the weights cold in HBM: those re-read every weight tile twice as often.)
@@ -1174,6 +1327,9 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
                                r0, r1);
             return check_launch("gemm_tol_kernel");
         }
+        // where the tiled launch would fall back to single-wave 32-row tiles (Q8_0 14336 rows:
+        // up to 128 tokens), K is split instead
+        if (w.cols % 128 == 0 && gemm_tile(Q, r1 - r0, (long)a.m) >= 2) return launch_splitk<Q>(s, w, a, y, r0, r1);
         switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
         case 0: launch_tile<Q, 1, 128, 64, true>(s, w, a, y, r0, r1); break;
         case 1: launch_tile<Q, 1, 64, 64, true>(s, w, a, y, r0, r1); break;

@@ -597,6 +597,37 @@ def test_gemm_tol_tile_shapes(gpu, quant, m):
     w.free()
 
 
+SPLITK_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S]
+
+
+@pytest.mark.parametrize("quant", SPLITK_FORMATS)
+@pytest.mark.parametrize("m,chunks", [(3, 1), (17, 3), (32, 5), (33, 6), (64, 13), (100, 10)])
+def test_gemm_tol_split_k(gpu, quant, m, chunks):
+    """Tolerance-mode GEMM of a few tokens, where K is split over the waves of a workgroup: K of
+    1 to 13 chunks of 128 (waves with no chunk, with one more chunk than the others), 32- and
+    64-token tiles with a partial last one, 200 rows (a partial last row tile) and a row slice.
+    Held within 1e-5 of each token's output-row L2 norm of the bit-exact GPU output over the whole
+    matrix and of the oracle on a row window."""
+    torch = gpu
+    block = 256 if quant in (Q4_K, Q5_K, TQ2_0) else 128  # K-quant super-blocks, I2_S blocks of 128
+    cols = max(block, 128 * chunks // block * block)
+    rows = 200
+    raw = synth.random_weights(quant, rows, cols, seed=7 * m + chunks + quant, specials=True)
+    x = np.random.default_rng(m + chunks).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m)
+    assert_within_row_norm(tol, exact)
+    act = O.ActQ8(x, m, cols)
+    ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, act, 150, 200)
+    assert same_bits(exact[:, 150:200], ref)
+    norms = np.linalg.norm(exact.astype(np.float64), axis=1)
+    assert np.all(np.abs(tol[:, 150:200] - ref).max(axis=1) <= 1e-5 * norms)
+    sl = gpu_gemm_tol(torch, w, x, m, 5, 171)
+    assert_within_row_norm(sl, exact[:, 5:171])
+    w.free()
+
+
 # ------------------------------------------------------------------ BitLinear
 @pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S, Q8_0])
 @pytest.mark.parametrize("m,rows,cols", [(1, 7, 256), (3, 64, 2560), (2, 2560, 6912),
