@@ -1263,6 +1263,120 @@ static jk_status launch_splitk(hipStream_t s, const WeightDev &w, const jk_act_q
     return check_launch("gemm_tol_splitk_kernel");
 }
 
+// Bit-exact block-scaled products with few row tiles (BitLinear at 16 or more tokens: TQ2_0 with
+// GB = 8 32-element steps per weight block, I2_S with GB = 4), K split over the waves of a
+// workgroup with the reference's order of additions kept. A workgroup owns 32 weight rows x 32
+// tokens; the weight blocks go round-robin to its NW waves (round r: wave v takes block NW r + v).
+// Per block a wave stages the block's chunks through the GEMM's coalesced loads (two chunks in
+// flight), accumulates the exact i32 dot over its GB steps with MFMA, and writes the block's
+// addend f32(dot) * (ws * xs) -- the scale product the single rounded f32 product, from an
+// outer-product MFMA -- to an LDS table. After a barrier every thread adds the round's addends,
+// for its outputs, in wave order, i.e. in block order, to an accumulator that started at 0.0:
+// the same sum in the same order as gemm_repacked_kernel, bit for bit. The table is kept per
+// round parity, so one barrier per round suffices.
+template <int Q, int GB, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_block_splitk_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
+                                                                    int r0, int r1) {
+    static_assert(GemmFmt<Q>::GK == 32 && !GemmFmt<Q>::MINS && (GB == 4 || GB == 8), "blocks of 4 or 8 steps");
+    constexpr int UC = GB / 4;  // chunks per weight block
+    __shared__ __align__(16) GemmChunk<Q, 32, 32> css[NW];
+    __shared__ float tab[2][NW][32][33];  // [round parity][wave][token][row], rows padded to 33
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hl = lane >> 5, jl = lane & 31;
+    const int ntn = (r1 - r0 + 31) / 32, ntm = ((int)a.m + 31) / 32;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;  // workgroup-uniform: the whole workgroup leaves before any barrier
+    const int n0 = r0 + 32 * tn, m0 = 32 * tm, M = (int)a.m;
+    const int nblocks = w.cols / (32 * GB), rounds = (nblocks + NW - 1) / NW;
+    GemmChunk<Q, 32, 32> &cs = css[wave];
+
+    // This wave's chunks in order: block wave + NW i, chunk c of it. Every wave loads, stages and
+    // evaluates a block in every round -- past its last block (or with none: K below NW blocks)
+    // it repeats a valid one whose addend is not used -- so that the loads in flight are the same
+    // on every path and each staging buffer's wait leaves the other buffer's loads in flight.
+    const int nmine = (nblocks - wave + NW - 1) / NW, lastq = max(nmine * UC - 1, 0);
+    auto kc_of = [&](int q) {
+        q = min(q, lastq);
+        return nmine > 0 ? (wave + NW * (q / UC)) * UC + q % UC : q % UC;
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // outputs threadIdx.x + 64 NW i of the tile
+    Stage<32, 32> ra, rb;
+    chunk_load<Q>(ra, w, a, n0, r1, m0, M, kc_of(0));
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_load<Q>(rb, w, a, n0, r1, m0, M, kc_of(1));
+    __builtin_amdgcn_sched_barrier(0);
+    v16i cacc = v16i{0};
+    // one chunk: staged from r (which then loads chunk q + 2), its GB / UC = 4 steps added to cacc
+    auto chunk = [&](Stage<32, 32> &r, int q) {
+        chunk_store<Q>(w, r, cs, kc_of(q));
+        wave_lds_sync();
+        __builtin_amdgcn_sched_barrier(0);
+        chunk_load<Q>(r, w, a, n0, r1, m0, M, kc_of(q + 2));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            const v4i aq = *reinterpret_cast<const v4i *>(cs.a + jl * kRowB + 32 * st + 16 * hl);
+            const v4i bq = *reinterpret_cast<const v4i *>(cs.b + jl * kRowB + 32 * st + 16 * hl);
+            cacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, cacc, 0, 0, 0);
+        }
+    };
+    // round rd: this wave's block NW rd + wave (chunks rd UC .. rd UC + UC - 1), then the ordered
+    // addition; the staging buffer of chunk q is ra when q is even, so the caller passes the
+    // buffers in chunk order (fixed registers on every path)
+    auto round = [&](int rd, Stage<32, 32> &b0, Stage<32, 32> &b1) {
+        chunk(b0, rd * UC);
+        if constexpr (UC == 2) chunk(b1, rd * UC + 1);
+        if (NW * rd + wave < nblocks) {  // wave-uniform; false only in the last round
+            // the block's addend: lane l supplies the scale of row jl and of token jl (both halves
+            // repeat them), so p[v] = ws(row 8 (v / 4) + 4 hl + v % 4) * xs(token jl)
+            const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[kSteps - 1][jl], cs.xs[kSteps - 1][jl], v32f{0}, 0,
+                                                                0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                tab[rd & 1][wave][jl][8 * (v >> 2) + 4 * hl + (v & 3)] = (float)cacc[v] * p[v];
+        }
+        cacc = v16i{0};
+        // LDS wait and barrier without a fence: the chunk loads in flight stay in flight
+        stage_barrier();
+        const int nv = min(NW, nblocks - NW * rd);  // blocks of this round
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int o = (int)threadIdx.x + 64 * NW * i, tok = o >> 5, row = o & 31;
+            if (o < 32 * 32)
+                for (int v = 0; v < nv; ++v) acc[i] += tab[rd & 1][v][tok][row];
+        }
+    };
+    if constexpr (UC == 2) {
+        for (int rd = 0; rd < rounds; ++rd) round(rd, ra, rb);
+    } else {
+        // (pairs of rounds, the odd last one after the loop: the loop's back edge then always
+        // follows the same loads, so the waits at its head stay exact)
+        int rd = 0;
+        for (; rd + 1 < rounds; rd += 2) {
+            round(rd, ra, rb);
+            round(rd + 1, rb, ra);
+        }
+        if (rd < rounds) round(rd, ra, rb);
+    }
+    const size_t ld = (size_t)(r1 - r0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int o = (int)threadIdx.x + 64 * NW * i, tok = o >> 5, row = o & 31;
+        if (o < 32 * 32 && m0 + tok < M && n0 + row < r1) y[(size_t)(m0 + tok) * ld + (size_t)(n0 + row - r0)] = acc[i];
+    }
+}
+
+constexpr int kBlockSplitkNW = 4;  // (8 waves measured slower on both 128-token BitLinear shapes)
+
+template <int Q, int GB>
+static jk_status launch_block_splitk(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    const size_t ntn = (size_t)(r1 - r0 + 31) / 32, ntm = (a.m + 31) / 32;
+    hipLaunchKernelGGL((gemm_block_splitk_kernel<Q, GB, kBlockSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+                       dim3(64 * kBlockSplitkNW), 0, s, w, a, y, r0, r1);
+    return check_launch("gemm_block_splitk_kernel");
+}
+
 // Tile shape of a launch: the largest tile that still gives every CU two workgroups, down to the
 // 32 x 16 single-wave tiles (not for Q6_K). (Four 32 x 32 tiles per CU beat the 32 x 16 tiles
 // with the weights cold in HBM: those re-read every weight tile twice as often.)
@@ -1371,9 +1485,14 @@ jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t 
     a.k_blocks32 = 1;
     a.qs = const_cast<int8_t *>(act);
     a.scales = const_cast<float *>(act_scales);
+    // where the tiled launch would fall back to single-wave 32-row tiles (2560 x 6912 and
+    // 6912 x 2560 at 128 tokens), K is split over the waves of a workgroup instead
+    const bool split = gemm_tile(w.quant, w.rows, m) >= 2;
     switch (w.quant) {
-    case JK_TQ2_0: return launch_gemm<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows);
-    case JK_I2_S: return launch_gemm<JK_I2_S, 4>(s, w, a, y, 0, w.rows);
+    case JK_TQ2_0: return split ? launch_block_splitk<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows)
+                                : launch_gemm<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows);
+    case JK_I2_S: return split ? launch_block_splitk<JK_I2_S, 4>(s, w, a, y, 0, w.rows)
+                               : launch_gemm<JK_I2_S, 4>(s, w, a, y, 0, w.rows);
     case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, 0, w.rows);
     default: return fail(JK_CAPABILITY_MISMATCH, "bitlinear: unsupported quant %d", w.quant);
     }
