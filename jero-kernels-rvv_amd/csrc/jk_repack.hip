@@ -341,10 +341,8 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(WeightDev w, int r0, 
     if (idx >= total) return;
     const int r = r0 + (int)(idx / (size_t)w.nb), b = (int)(idx % (size_t)w.nb);
     const Fmt f = fmt_of(w.quant);
-    float buf[256];
-    dequant_block(w, r, b, buf);
-    float *dst = out + (size_t)(r - r0) * (size_t)w.cols + (size_t)b * f.be;
-    for (int i = 0; i < f.be; ++i) dst[i] = buf[i];
+    // (straight into the output row: a per-thread staging array of a block's values lived in scratch)
+    dequant_block(w, r, b, out + (size_t)(r - r0) * (size_t)w.cols + (size_t)b * f.be);
 }
 
 jk_status launch_dequant_rows(hipStream_t s, const WeightDev &w, int r0, int r1, float *out) {
