@@ -112,7 +112,8 @@ template <int TN, int TM> struct Stage {
 
 // Blocks past the row end (a partial last chunk) are read clamped and never used; rows
 // past r1 are read clamped to r1 - 1 and never stored.
-template <int Q, int TN, int TM>
+// XV (whole chunks, nb % 4 == 0): the two f16 scales of a thread's blocks in one 4-byte load.
+template <int Q, int TN, int TM, bool XV = false>
 __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1, int kc, Stage<TN, TM> &r) {
     const int nb = w.nb, t = (int)threadIdx.x % Tile<TN, TM>::THREADS;
     if constexpr (GemmFmt<Q>::B32) {
@@ -126,11 +127,17 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
             if constexpr (Q == JK_Q5_1) r.wh[i] = w.hplane[((size_t)n * (size_t)nb + (size_t)b) * 2 + 1];
         }
         const size_t srow = (size_t)min(n0 + (t >> 1), r1 - 1) * (size_t)nb;
+        if constexpr (XV && Q != JK_Q4_1 && Q != JK_Q5_1) {
+            const uint32_t dd = *reinterpret_cast<const uint32_t *>(w.dplane + srow + (size_t)(4 * kc + 2 * (t & 1)));
+            r.wd[0] = dd & 0xFFFFu;
+            r.wd[1] = dd >> 16;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const size_t blk = srow + (size_t)min(4 * kc + 2 * (t & 1) + j, nb - 1);
-            if constexpr (Q == JK_Q4_1 || Q == JK_Q5_1) r.wd[j] = w.hplane[blk * HW];  // d | m << 16
-            else r.wd[j] = w.dplane[blk];
+            for (int j = 0; j < 2; ++j) {
+                const size_t blk = srow + (size_t)min(4 * kc + 2 * (t & 1) + j, nb - 1);
+                if constexpr (Q == JK_Q4_1 || Q == JK_Q5_1) r.wd[j] = w.hplane[blk * HW];  // d | m << 16
+                else r.wd[j] = w.dplane[blk];
+            }
         }
     } else {
         const int n = min(n0 + (t >> 1), r1 - 1), j = t & 1;
@@ -173,7 +180,10 @@ __device__ __forceinline__ void chunk_w_load(const WeightDev &w, int n0, int r1,
     }
 }
 
-template <int Q, int TN, int TM>
+// XV: a thread's XS (2 or 4) scale entries are consecutive blocks of one token, read with one
+// 8- or 16-byte load per array instead of XS loads that each touch a different line per lane.
+// The caller guarantees whole chunks, k_blocks32 % 4 == 0 and 16-byte aligned scales / sums.
+template <int Q, int TN, int TM, bool XV = false>
 __device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, int kc, Stage<TN, TM> &r) {
     using T = Tile<TN, TM>;
     const int t = (int)threadIdx.x % T::THREADS;
@@ -184,13 +194,41 @@ __device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, 
         const int m = min(m0 + (t >> 3) + T::THREADS / 8 * i, M - 1);
         r.x[i] = ldg16(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + k);
     }
+    constexpr bool SUMS = GemmFmt<Q>::MINS && GemmFmt<Q>::GK == 32;
+    if constexpr (XV && (T::XS == 2 || T::XS == 4)) {
+        const int e = T::XS * t;
+        const size_t sidx = (size_t)min(m0 + (e >> 2), M - 1) * a.k_blocks32 + (size_t)(4 * kc + (e & 3));
+        if constexpr (T::XS == 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(a.scales + sidx);
+            r.xd[0][0] = __float_as_uint(v.x), r.xd[0][1] = __float_as_uint(v.y);
+            r.xd[0][2] = __float_as_uint(v.z), r.xd[0][3] = __float_as_uint(v.w);
+            if constexpr (SUMS) {
+                const float4 u = *reinterpret_cast<const float4 *>(a.sums + sidx);
+                r.xd[1][0] = __float_as_uint(u.x), r.xd[1][1] = __float_as_uint(u.y);
+                r.xd[1][2] = __float_as_uint(u.z), r.xd[1][3] = __float_as_uint(u.w);
+            } else {
 #pragma unroll
-    for (int j = 0; j < T::XS; ++j) {
-        const int e = T::XS * t + j;
-        const size_t sidx =
-            (size_t)min(m0 + (e >> 2), M - 1) * a.k_blocks32 + (size_t)min(4 * kc + (e & 3), (int)a.k_blocks32 - 1);
-        r.xd[0][j] = __float_as_uint(a.scales[sidx]);
-        r.xd[1][j] = GemmFmt<Q>::MINS && GemmFmt<Q>::GK == 32 ? __float_as_uint(a.sums[sidx]) : 0u;
+                for (int j = 0; j < 4; ++j) r.xd[1][j] = 0u;
+            }
+        } else {
+            const float2 v = *reinterpret_cast<const float2 *>(a.scales + sidx);
+            r.xd[0][0] = __float_as_uint(v.x), r.xd[0][1] = __float_as_uint(v.y);
+            if constexpr (SUMS) {
+                const float2 u = *reinterpret_cast<const float2 *>(a.sums + sidx);
+                r.xd[1][0] = __float_as_uint(u.x), r.xd[1][1] = __float_as_uint(u.y);
+            } else {
+                r.xd[1][0] = r.xd[1][1] = 0u;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < T::XS; ++j) {
+            const int e = T::XS * t + j;
+            const size_t sidx =
+                (size_t)min(m0 + (e >> 2), M - 1) * a.k_blocks32 + (size_t)min(4 * kc + (e & 3), (int)a.k_blocks32 - 1);
+            r.xd[0][j] = __float_as_uint(a.scales[sidx]);
+            r.xd[1][j] = SUMS ? __float_as_uint(a.sums[sidx]) : 0u;
+        }
     }
     if constexpr (GemmFmt<Q>::MINS && GemmFmt<Q>::GK == 16) {  // x_sums_16 (repack.rs:3061-3066)
 #pragma unroll
@@ -204,11 +242,11 @@ __device__ __forceinline__ void chunk_x_load(const jk_act_q8 &a, int m0, int M, 
 }
 
 // Global loads of chunk kc into this thread's staging registers.
-template <int Q, int TN, int TM>
+template <int Q, bool XV = false, int TN, int TM>
 __device__ __forceinline__ void chunk_load(Stage<TN, TM> &r, const WeightDev &w, const jk_act_q8 &a, int n0, int r1,
                                            int m0, int M, int kc) {
-    chunk_w_load<Q>(w, n0, r1, kc, r);
-    chunk_x_load<Q>(a, m0, M, kc, r);
+    chunk_w_load<Q, TN, TM, XV>(w, n0, r1, kc, r);
+    chunk_x_load<Q, TN, TM, XV>(a, m0, M, kc, r);
 }
 
 __device__ __forceinline__ uint4 nib4(uint4 v, int sh, uint32_t bias) {
@@ -1169,7 +1207,7 @@ __device__ __forceinline__ void sk_compute(const GemmChunk<Q, 32, TM> &cs, v32f 
     }
 }
 
-template <int Q, int TM, int NW>
+template <int Q, int TM, int NW, bool XV>
 __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
                                                                   int r0, int r1) {
     static_assert(GemmFmt<Q>::GK == 32 && (TM == 32 || TM == 64), "32-element groups; 32 or 64 tokens");
@@ -1197,15 +1235,15 @@ __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, j
         Stage<32, TM> ra, rb;
         // (the scheduling barriers keep each phase in place: the waits count loads in issue order,
         // so a buffer loaded out of turn -- here or in the loop -- would drain the other one too)
-        chunk_load<Q>(ra, w, a, n0, r1, m0, M, ck(0));
+        chunk_load<Q, XV>(ra, w, a, n0, r1, m0, M, ck(0));
         __builtin_amdgcn_sched_barrier(0);
-        chunk_load<Q>(rb, w, a, n0, r1, m0, M, ck(1));
+        chunk_load<Q, XV>(rb, w, a, n0, r1, m0, M, ck(1));
         __builtin_amdgcn_sched_barrier(0);
         for (int i = 0; i < cnt; i += 2) {
             chunk_store<Q>(w, ra, cs, ck(i));
             wave_lds_sync();
             __builtin_amdgcn_sched_barrier(0);
-            chunk_load<Q>(ra, w, a, n0, r1, m0, M, ck(i + 2));
+            chunk_load<Q, XV>(ra, w, a, n0, r1, m0, M, ck(i + 2));
             __builtin_amdgcn_sched_barrier(0);
             sk_compute(cs, acc, lane);
             wave_lds_sync();  // the chunk's LDS reads are done before the next store
@@ -1213,7 +1251,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, j
             chunk_store<Q>(w, rb, cs, ck(i + 1));
             wave_lds_sync();
             __builtin_amdgcn_sched_barrier(0);
-            chunk_load<Q>(rb, w, a, n0, r1, m0, M, ck(i + 3));
+            chunk_load<Q, XV>(rb, w, a, n0, r1, m0, M, ck(i + 3));
             __builtin_amdgcn_sched_barrier(0);
             if (i + 1 < cnt) sk_compute(cs, acc, lane);
             wave_lds_sync();
@@ -1248,17 +1286,26 @@ __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, j
 // eight waves per workgroup measured slower (their 1.75 rounds over the CUs against one)
 constexpr int kSplitkNW = 4;
 
+template <int Q, int TM, bool XV>
+static void launch_splitk_t(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    const size_t ntn = (size_t)(r1 - r0 + 31) / 32, ntm = (a.m + TM - 1) / TM;
+    hipLaunchKernelGGL((gemm_tol_splitk_kernel<Q, TM, kSplitkNW, XV>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+                       dim3(64 * kSplitkNW), 0, s, w, a, y, r0, r1);
+}
+
+// (w.cols % 128 == 0, checked by the caller)
 template <int Q>
 static jk_status launch_splitk(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    const size_t ntn = (size_t)(r1 - r0 + 31) / 32;
+    // one load per thread for its chunk's activation scales (and sums), and one for its two weight
+    // scales, when the rows allow it (w.nb % 4 == 0 follows from whole chunks)
+    const bool xv = a.k_blocks32 % 4 == 0 && (uintptr_t)a.scales % 16 == 0 && (uintptr_t)a.sums % 16 == 0 &&
+                    (uintptr_t)w.dplane % 4 == 0;
     if (a.m <= 32) {
-        const size_t ntm = (a.m + 31) / 32;
-        hipLaunchKernelGGL((gemm_tol_splitk_kernel<Q, 32, kSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
-                           dim3(64 * kSplitkNW), 0, s, w, a, y, r0, r1);
+        if (xv) launch_splitk_t<Q, 32, true>(s, w, a, y, r0, r1);
+        else launch_splitk_t<Q, 32, false>(s, w, a, y, r0, r1);
     } else {
-        const size_t ntm = (a.m + 63) / 64;
-        hipLaunchKernelGGL((gemm_tol_splitk_kernel<Q, 64, kSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
-                           dim3(64 * kSplitkNW), 0, s, w, a, y, r0, r1);
+        if (xv) launch_splitk_t<Q, 64, true>(s, w, a, y, r0, r1);
+        else launch_splitk_t<Q, 64, false>(s, w, a, y, r0, r1);
     }
     return check_launch("gemm_tol_splitk_kernel");
 }
