@@ -8,13 +8,12 @@
 
 namespace jk {
 
-// f16_to_f32_finite (lib.rs:676-717): exact decode, NaN/Inf -> +0.0, signed zero kept.
+// f16_to_f32_finite (lib.rs:676-717): exact decode, NaN/Inf -> +0.0, signed zero kept. The low
+// 16 bits of h are the f16. The hardware conversion is exact for every f16, subnormals included
+// (the kernels run with f16 denormals preserved), so the decode is one conversion and a select.
 __device__ __forceinline__ float f16_finite(uint32_t h) {
-    // straight-line selects: no branch that would wait on the load feeding h
-    const uint32_t e = (h >> 10) & 31u, m = h & 1023u, s = (h & 0x8000u) << 16;
-    const float sub = __uint_as_float(s | __float_as_uint((float)m * 0x1p-24f));
-    const float nrm = __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
-    return e == 31u ? 0.0f : (e == 0u ? sub : nrm);
+    const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    return __builtin_isfinite(f) ? f : 0.0f;
 }
 
 // Signed 4 x i8 dot product accumulated into c (v_dot4_i32_i8).
