@@ -29,6 +29,24 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
+// Integer MFMA results as f32 without a conversion instruction: the accumulator starts at the
+// bit pattern of 1.5 * 2^23, so the i32 sum adds the group's dot product d to that float's
+// mantissa. |d| <= 32 * 128 * 128 < 2^22 keeps it in the binade [2^23, 2^24), where the float
+// is exactly 1.5 * 2^23 + d, and one exact subtraction recovers d -- cheaper to issue than
+// v_cvt_f32_i32 (about 0.6 of its cost on MI355X). The bias registers are never written (the
+// MFMA's result goes elsewhere), at 16 VGPRs: used where the epilogue's issue time dominates
+// and registers allow (the 512-token tolerance tiles; measured slower in the split-K and the
+// bit-exact tiles, whose register budgets it crowds).
+constexpr int kMagicBits = 0x4B400000;
+constexpr float kMagicF = 12582912.0f;  // 1.5 * 2^23
+__device__ __forceinline__ v16i magic_acc() {
+    v16i m;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) m[v] = kMagicBits;
+    return m;
+}
+__device__ __forceinline__ float unbias(int c) { return __int_as_float(c) - kMagicF; }
+
 constexpr int kKC = 128;      // K elements per chunk
 constexpr int kSteps = 4;     // 32-element steps per chunk
 constexpr int kRowB = 144;    // padded LDS bytes per 128-byte row
@@ -848,6 +866,7 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
 
     v32f tacc[2];
     tacc[0] = tacc[1] = v32f{0};
+    const v16i bias = magic_acc();
     const int arow = 64 * wn + jl;
     auto chunk = [&](const Q8Stage<TN> &S) {
 #pragma unroll 1
@@ -866,13 +885,13 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
                 const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ (t & 7)) << 4));
                 v16i c[2];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, v16i{0}, 0, 0, 0);
+                for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, bias, 0, 0, 0);
                 const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, S.xs[t * 4 + st], v32f{0}, 0, 0, 0);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        tacc[tb][16 * nt + v] = __builtin_fmaf((float)c[nt][v], pr[16 * nt + v], tacc[tb][16 * nt + v]);
+                        tacc[tb][16 * nt + v] = __builtin_fmaf(unbias(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
             }
         }
     };

@@ -597,6 +597,33 @@ def test_gemm_tol_tile_shapes(gpu, quant, m):
     w.free()
 
 
+def test_gemm_tol_extreme_group_dots(gpu):
+    """The 512-token tolerance tiles read each group's integer dot product out of a biased
+    accumulator; its range must hold the largest |dot| a Q8_0 group can reach, 32 * 128 * 127 (-128
+    weight quants against +-127 activation quants). Weights of +-128 / +127 quants with d = 1.0,
+    activations of +-1.0 (quants +-127), 8192 rows x 512 tokens (the 128 x 128 tiles): equal to the
+    bit-exact output within the tolerance, and the bit-exact output equal to the oracle."""
+    torch = gpu
+    rows, cols, m = 8192, 256, 512
+    blk = np.dtype([("d", "<f2"), ("qs", "i1", (32,))])
+    w_blocks = np.zeros((rows, cols // 32), dtype=blk)
+    w_blocks["d"] = 1.0
+    w_blocks["qs"][0::2] = -128
+    w_blocks["qs"][1::2] = 127
+    raw = np.frombuffer(w_blocks.tobytes(), dtype=np.uint8)
+    x = np.where((np.arange(m) % 3 == 0)[:, None], -1.0, 1.0).astype(np.float32) * np.ones((m, cols), np.float32)
+    w = jk.Weight(jk.TensorView("w", Q8_0, [rows, cols], raw), rows, cols)
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m)
+    assert_within_row_norm(tol, exact)
+    act = O.ActQ8(x, m, cols)
+    ref = O.gemm_repacked(Q8_0, [rows, cols], raw, rows, cols, act, 4000, 4040)
+    assert same_bits(exact[:, 4000:4040], ref)
+    # every group dot is +-520192 or +-516128, i.e. -4096 / +4064 times 127; 8 groups per row
+    assert np.allclose(exact[1, 0:2], [8 * -4096.0, 8 * 4064.0], rtol=1e-6)
+    w.free()
+
+
 SPLITK_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S]
 
 
