@@ -896,22 +896,22 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
         }
     };
 
+    // One barrier per chunk: the barrier that publishes chunk kc (every wave has waited for its own
+    // loads into the stage) also shows every wave done with chunk kc - 1, whose stage is then
+    // refilled with chunk kc + 1 while chunk kc is evaluated.
     issue(sA, 0);
     if (nchunks > 1) issue(sB, 1);
     for (int kc = 0; kc < nchunks; kc += 2) {
-        if (kc + 1 < nchunks) JK_WAIT_VMCNT(kQ8DmaPerWave<TN>);
+        if (kc == 0 && nchunks > 1) JK_WAIT_VMCNT(kQ8DmaPerWave<TN>);  // chunk 1 stays in flight
         else JK_WAIT_VMCNT(0);
         stage_barrier();
+        if (kc >= 2 && kc + 1 < nchunks) issue(sB, kc + 1);
         chunk(sA);
+        if (kc + 1 >= nchunks) break;
+        JK_WAIT_VMCNT(0);
         stage_barrier();
         if (kc + 2 < nchunks) issue(sA, kc + 2);
-        if (kc + 1 >= nchunks) break;
-        if (kc + 2 < nchunks) JK_WAIT_VMCNT(kQ8DmaPerWave<TN>);
-        else JK_WAIT_VMCNT(0);
-        stage_barrier();
         chunk(sB);
-        stage_barrier();
-        if (kc + 3 < nchunks) issue(sB, kc + 3);
     }
 
     const size_t ld = (size_t)(r1 - r0);
