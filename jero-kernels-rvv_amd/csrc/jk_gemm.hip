@@ -33,10 +33,10 @@ typedef float v32f __attribute__((ext_vector_type(32)));
 // bit pattern of 1.5 * 2^23, so the i32 sum adds the group's dot product d to that float's
 // mantissa. |d| <= 32 * 128 * 128 < 2^22 keeps it in the binade [2^23, 2^24), where the float
 // is exactly 1.5 * 2^23 + d, and one exact subtraction recovers d -- cheaper to issue than
-// v_cvt_f32_i32 (about 0.6 of its cost on MI355X). The bias registers are never written (the
-// MFMA's result goes elsewhere), at 16 VGPRs: used where the epilogue's issue time dominates
-// and registers allow (the 512-token tolerance tiles; measured slower in the split-K and the
-// bit-exact tiles, whose register budgets it crowds).
+// v_cvt_f32_i32. The bias registers are never written (the MFMA's result goes elsewhere), at
+// 16 VGPRs: used where the epilogue's issue time dominates and registers allow (the 512-token
+// tolerance tiles; measured slower in the split-K and the bit-exact tiles, whose register
+// budgets it crowds).
 constexpr int kMagicBits = 0x4B400000;
 constexpr float kMagicF = 12582912.0f;  // 1.5 * 2^23
 __device__ __forceinline__ v16i magic_acc() {
