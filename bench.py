@@ -403,15 +403,17 @@ def main() -> int:
             for w in ws:
                 w.free()
         # Repacked GEMV (the m <= 2 route of the repacked GEMM, repack.rs:2892): one token's
-        # QuantizedActQ8 against the block-scaled weights, at the C1 shape and the C3 gate shape
+        # QuantizedActQ8 against the block-scaled weights, at the C1 shape and the C3 gate and
+        # down shapes
         for name, quant, rows, cols in (("gemv_repacked Q8_0 4096x4096 M=1", jk.Q8_0, 4096, 4096),
                                         ("gemv_repacked Q4_0 4096x4096 M=1", jk.Q4_0, 4096, 4096),
-                                        ("gemv_repacked Q4_K 14336x4096 M=1", jk.Q4_K, 14336, 4096)):
+                                        ("gemv_repacked Q4_K 14336x4096 M=1", jk.Q4_K, 14336, 4096),
+                                        ("gemv_repacked Q6_K 4096x14336 M=1", jk.Q6_K, 4096, 14336)):
             ws = copies(quant, rows, cols, 550 + quant)
             need = jk.act_q8_bytes(1, cols)
             store = torch.empty(need, dtype=torch.uint8, device=dev)
             act1 = jk.act_q8_bind(store, need, 1, cols)
-            jk.dev_quantize_act_q8(acts["x"], 1, cols, act1)
+            jk.dev_quantize_act_q8(acts["x" if cols == 4096 else "h"], 1, cols, act1)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
             us = graph_us(lambda i, st: jk.dev_gemv_repacked(ws[i % len(ws)], act1, y, rows, 0, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + need + 4 * rows

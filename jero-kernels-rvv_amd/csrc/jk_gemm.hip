@@ -1149,6 +1149,8 @@ static jk_status launch_gemv_repacked_q(hipStream_t s, const WeightDev &w, const
 
 // m <= 2 of the repacked GEMM entry points (both modes: the result is the bit-exact one).
 static jk_status launch_gemv_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    if (gemv_repacked_fast_ok(w.quant, a.m, a.k_padded, a.k_blocks32))
+        return launch_gemv_repacked_fast(s, w, a, y, r0, r1);
     switch (w.quant) {
     case JK_Q8_0: return launch_gemv_repacked_q<JK_Q8_0>(s, w, a, y, r0, r1);
     case JK_Q4_0: return launch_gemv_repacked_q<JK_Q4_0>(s, w, a, y, r0, r1);

@@ -769,6 +769,228 @@ gemv_q8_fast_kernel(GemvGroup grp) {
     }
 }
 
+// ------------------------------------------------------------------ repacked GEMV, 1-2 tokens
+// gemm_repacked's recipe for one or two tokens (the reference's m <= 2 route, repack.rs:2892),
+// shaped like the quant_q8 GEMV: 16 lanes per output row, lane p taking blocks p, p + 16, ... of
+// the row from the planes into registers (two blocks in flight). A block's scale groups give their
+// terms (accumulate_scaled_tile_scalar, repack.rs:3045-3093)
+//     f32(sum xq * wq) * (xs * ws)  [- xsum * wm]
+// with the weight values, scales and mins of repack_block_scaled_range_into_i8 (repack.rs:
+// 1724-2103), and each block's terms are folded, in K order, onto the running sum passed from
+// the lane of the previous block (the chain_add steps with a block's terms per step): every
+// output is the GEMM's sum, in the GEMM's order, starting from 0.0. The activation quants are
+// staged in LDS once per workgroup (their loads issued before the weight loads); scales and sums
+// are read per lane.
+constexpr int kRpNW = 4;        // waves per workgroup: 16 rows
+constexpr int kRpMaxLoads = 8;  // 16-byte activation loads per thread: MT * k_padded <= 32 KB
+
+template <int Q> constexpr int kRpGroups = Q == JK_Q4_K ? 8 : Q == JK_Q6_K ? 16 : 1;  // scale groups per block
+// LDS padding after each block's activation quants: the 16 lanes of a row read 16 consecutive
+// blocks at once, and at 256 bytes a block they would all fall on the same banks; 16 more bytes
+// a block put consecutive lanes on consecutive 16-byte bank groups. (32-byte blocks already do.)
+template <int Q> constexpr int kRpPad = fmt_of(Q).be >= 256 ? 16 : 0;
+static size_t rp_lds_row(int quant, size_t k_padded) {
+    const size_t be = quant == JK_Q4_K || quant == JK_Q6_K ? 256 : 32;
+    return k_padded + (quant == JK_Q4_K || quant == JK_Q6_K ? k_padded / be * 16 : 0);
+}
+
+// The terms of block b of the lane's row for one token (its quants of the block in LDS, its
+// scales and sums in LDS).
+template <int Q>
+__device__ __forceinline__ void rp_terms(const WReg<Q> &wr, const uint8_t *xq, const float *xs, const float *xm,
+                                         float (&t)[kRpGroups<Q>]) {
+    const int *xi = reinterpret_cast<const int *>(xq);
+    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
+        const float ws = f16_finite(wr.d);  // repack.rs:1735-1760: the block's d
+        int s = 0;
+        if constexpr (Q == JK_Q8_0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = dot4((int)comp(wr.c[i >> 2], i & 3), xi[i], s);
+        } else {  // nibbles biased by +8: sum((n - 8) x) = sum(n x) - 8 sum(x), exactly
+            int sx = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s = dot4((int)(comp(wr.c[0], i) & 0x0F0F0F0Fu), xi[i], s);
+                s = dot4((int)((comp(wr.c[0], i) >> 4) & 0x0F0F0F0Fu), xi[4 + i], s);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sx = dot4(xi[i], 0x01010101, sx);
+            s -= 8 * sx;
+        }
+        t[0] = (float)s * (xs[0] * ws);
+    } else if constexpr (Q == JK_Q4_K) {
+        // sub-block g (elements 32 g ..): quarter g / 2, low (g even) or high nibbles of planes
+        // 1 + g / 2 * 2 and 2 + g / 2 * 2; scale / min unpack_k4_scales_mins (repack.rs:1158-1170)
+        const uint4 h = wr.c[0];
+        const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
+        const uint32_t sc[2] = {h.y & 0x3F3F3F3Fu, (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u)};
+        const uint32_t mv[2] = {h.z & 0x3F3F3F3Fu, ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int c = g >> 1, sh = 4 * (g & 1);
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t wd = comp(i < 4 ? wr.c[1 + 2 * c] : wr.c[2 + 2 * c], i & 3);
+                s = dot4((int)((wd >> sh) & 0x0F0F0F0Fu), xi[8 * g + i], s);
+            }
+            const float ws = d * (float)byte_of(sc[g >> 2], g & 3);
+            const float wm = dmin * (float)byte_of(mv[g >> 2], g & 3);
+            t[g] = (float)s * (xs[g] * ws) - xm[g] * wm;
+        }
+    } else {  // JK_Q6_K
+        // 16-group g of half h (elements 128 h + 16 g ..): ql plane 4 h + g % 2 + 2 (g / 2 % 2),
+        // nibble g / 4, qh plane 8 + 2 h + g % 2, field g / 2; scale 8 h + g (repack.rs:1861-1874)
+        const float d = f16_finite(wr.d);
+        const uint4 scv = wr.c[12];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const int j = g & 1, qq = g >> 1, js = 8 * hh + g;
+                const uint4 lv = wr.c[4 * hh + j + 2 * (qq & 1)], hv = wr.c[8 + 2 * hh + j];
+                const int lsh = qq < 2 ? 0 : 4, hsh = 2 * qq;
+                int s = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t v6 =
+                        ((comp(lv, i) >> lsh) & 0x0F0F0F0Fu) | (((comp(hv, i) >> hsh) & 0x03030303u) << 4);
+                    s = dot4(bytes_sub(v6, 0x20202020u), xi[32 * hh + 4 * g + i], s);
+                }
+                const float ws = d * (float)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
+                t[8 * hh + g] = (float)s * (xs[4 * hh + (g >> 1)] * ws);
+            }
+    }
+}
+
+template <int Q, int MT>
+__global__ __launch_bounds__(64 * kRpNW) __attribute__((amdgpu_waves_per_eu(2))) void
+gemv_repacked_fast_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+    constexpr int G = kRpGroups<Q>, BE = fmt_of(Q).be, NT = 64 * kRpNW, PAD = kRpPad<Q>;
+    constexpr bool SUMS = Q == JK_Q4_K;
+    // LDS: activation quants [MT][k_padded / BE][BE + PAD] (k_padded a multiple of BE when PAD is
+    // not 0), then scales [MT][k_blocks32] (and sums, Q4_K)
+    extern __shared__ __align__(16) uint8_t s_xq[];
+    if (MT == 1 && blockIdx.y > 0) {  // one token per workgroup row of the grid: token blockIdx.y
+        a.qs += blockIdx.y * a.k_padded;
+        a.scales += blockIdx.y * a.k_blocks32;
+        a.sums += blockIdx.y * a.k_blocks32;
+        y += blockIdx.y * (size_t)(r1 - r0);
+    }
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int p = lane & 15, sub = lane >> 4;
+    const int row = r0 + 16 * (int)blockIdx.x + 4 * wave + sub;
+    const int r = min(row, r1 - 1);
+    const int nb = w.nb, nit = (nb + 15) / 16;
+    const int kp = (int)a.k_padded, kb = (int)a.k_blocks32;
+    const int kpp = kp + kp / BE * PAD;  // one token's padded quants
+    float *s_xs = reinterpret_cast<float *>(s_xq + MT * kpp);
+    float *s_xm = s_xs + MT * kb;
+
+    // 1. the activation -- quants in 16-byte loads, scales (and sums) in 4-byte loads -- issued
+    //    first (clamped, unconditional), so that it does not queue behind the weight stream
+    const int n16 = MT * kp / 16, n4 = MT * kb;
+    u32x4 xr[kRpMaxLoads];  // (a plain vector type: an array of uint4 is kept in scratch)
+    float sr[kRpMaxLoads], mr[kRpMaxLoads];
+#pragma unroll
+    for (int i = 0; i < kRpMaxLoads; ++i) {
+        const int k = min(tid + NT * i, n16 - 1);
+        const int m = k / (kp / 16), o = k - m * (kp / 16);
+        xr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + 16 * o);
+        const int e = min(tid + NT * i, n4 - 1);  // scales of token m at a.scales + m * kb
+        sr[i] = a.scales[e];
+        mr[i] = SUMS ? a.sums[e] : 0.0f;
+    }
+    // 2. the lane's first two blocks
+    WReg<Q> W[2];
+    wload<Q>(W[0], w, r, min(p, nb - 1));
+    wload<Q>(W[1], w, r, min(16 + p, nb - 1));
+    // 3. the activation into LDS: every store unconditional, at the index its load was clamped to
+    //    (a clamped store rewrites the last element with its own value), so the stores stay one
+    //    straight-line sequence
+#pragma unroll
+    for (int i = 0; i < kRpMaxLoads; ++i) {
+        const int k = min(tid + NT * i, n16 - 1);  // 16-byte piece k: block k / (BE / 16) of all MT
+        *reinterpret_cast<u32x4 *>(s_xq + 16 * k + PAD * (k / (BE / 16))) = xr[i];
+        const int e = min(tid + NT * i, n4 - 1);
+        s_xs[e] = sr[i];
+        if constexpr (SUMS) s_xm[e] = mr[i];
+    }
+    lds_barrier();
+
+    // 4. blocks in order, two in flight: block it is folded while block it + 1 loads, then block
+    //    it + 2 is issued into the buffer just consumed (clamped past the row end: the loads stay
+    //    unconditional, which keeps the double buffer's waits exact -- branching around them
+    //    measured slower)
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+    auto fold_block = [&](const WReg<Q> &wr, int it) {
+        const int b = 16 * it + p;
+        const bool live = b < nb;
+        const int bb = live ? b : 0;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float t[G];
+            rp_terms<Q>(wr, s_xq + m * kpp + bb * (BE + PAD), s_xs + m * kb + bb * (BE / 32), s_xm + m * kb + bb * (BE / 32), t);
+#pragma unroll
+            for (int g = 0; g < G; ++g) t[g] = live ? t[g] : -0.0f;  // -0.0: the identity of the fold
+            // the chain: in step s the lane of block 16 it + s folds its terms onto the sum passed
+            // from the lane before it (after the 16 steps lane 15 holds the sum through the block)
+#pragma unroll
+            for (int st = 0; st < 16; ++st) {
+                float run = row_ror1(acc[m]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) run = run + t[g];
+                acc[m] = run;
+            }
+        }
+    };
+    for (int it = 0; it < nit; it += 2) {
+        fold_block(W[0], it);
+        wload<Q>(W[0], w, r, min(16 * (it + 2) + p, nb - 1));
+        if (it + 1 >= nit) break;
+        fold_block(W[1], it + 1);
+        wload<Q>(W[1], w, r, min(16 * (it + 3) + p, nb - 1));
+    }
+    if (p == 15 && row < r1)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) y[(size_t)m * (size_t)(r1 - r0) + (size_t)(row - r0)] = acc[m];
+}
+
+template <int Q>
+static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    // Q6_K takes two tokens as two rows of one-token workgroups (both tokens in one wave need more
+    // registers than it has); the second token's weight reads then mostly hit the caches
+    const bool split = Q == JK_Q6_K && a.m == 2;
+    const size_t mt = split ? 1 : a.m;
+    const size_t lds = mt * rp_lds_row(Q, a.k_padded) + (Q == JK_Q4_K ? 2 : 1) * mt * a.k_blocks32 * sizeof(float);
+    const dim3 grid((unsigned)((r1 - r0 + 15) / 16), split ? 2u : 1u), block(64 * kRpNW);
+    if (mt == 1) hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 1>), grid, block, lds, s, w, a, y, r0, r1);
+    else if constexpr (Q != JK_Q6_K)
+        hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 2>), grid, block, lds, s, w, a, y, r0, r1);
+    return check_launch("gemv_repacked_fast_kernel");
+}
+
+bool gemv_repacked_fast_ok(int quant, size_t m, size_t k_padded, size_t k_blocks32) {
+    const bool fmt = quant == JK_Q8_0 || quant == JK_Q4_0 || quant == JK_Q4_K || quant == JK_Q6_K;
+    const size_t nt = 64 * kRpNW * kRpMaxLoads;  // activation loads of a workgroup
+    const bool padded = quant == JK_Q4_K || quant == JK_Q6_K;
+    return fmt && m >= 1 && m <= 2 && k_padded % (padded ? 256 : 16) == 0 && m * k_padded / 16 <= nt &&
+           m * k_blocks32 <= nt;
+}
+
+// (checked by the caller with gemv_repacked_fast_ok)
+jk_status launch_gemv_repacked_fast(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    switch (w.quant) {
+    case JK_Q8_0: return launch_rp_fast_q<JK_Q8_0>(s, w, a, y, r0, r1);
+    case JK_Q4_0: return launch_rp_fast_q<JK_Q4_0>(s, w, a, y, r0, r1);
+    case JK_Q4_K: return launch_rp_fast_q<JK_Q4_K>(s, w, a, y, r0, r1);
+    case JK_Q6_K: return launch_rp_fast_q<JK_Q6_K>(s, w, a, y, r0, r1);
+    default: return fail(JK_CAPABILITY_MISMATCH, "gemv_repacked_fast: unsupported quant %d", w.quant);
+    }
+}
+
 // ------------------------------------------------------------------ global-x fallback
 // Activations read from global memory (matrices whose activation exceeds the LDS budget).
 template <int Q>

@@ -209,6 +209,10 @@ jk_status launch_gemv_group(hipStream_t s, const GemvJob *jobs, int n);
 // Largest K a grouped GEMV job of device format q can take as f32 activations (the launch
 // quantizes them into LDS); caller Q8 blocks have no limit.
 size_t gemv_f32_max_cols(int q);
+// Repacked GEMV for one or two tokens on the GEMV-shaped kernel (jk_gemv_q8.hip): the formats and
+// activation sizes it takes, and the launch (bit-identical to the GEMM's m <= 2 route).
+bool gemv_repacked_fast_ok(int quant, size_t m, size_t k_padded, size_t k_blocks32);
+jk_status launch_gemv_repacked_fast(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1);
 // Looks up this device's copy of the no-alloc entry point's static scratch (jk_noalloc.hip).
 jk_status noalloc_setup();
 // Validated GEMV + fused argmax job over all rows of w (am_slots left null).

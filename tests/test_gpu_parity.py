@@ -487,12 +487,15 @@ def test_gemm_repacked(gpu, quant, m, rows, cols):
 
 @pytest.mark.parametrize("quant", ALL_FORMATS)
 @pytest.mark.parametrize("m,rows,cols", [(1, 37, 512), (2, 100, 4096), (1, 33, 768), (2, 9, 160), (1, 4100, 1280),
-                                         (2, 70, 14336)])
+                                         (2, 70, 14336), (2, 21, 33024)])
 def test_gemv_repacked_one_or_two_tokens(gpu, quant, m, rows, cols):
-    """m <= 2 runs the GEMV kernel (K split over the waves of a 32-row workgroup, terms folded in K
-    order): every repacked entry point == the oracle bit for bit -- one and several rounds of
-    chunks, a partial last round and a partial last chunk (160 = 5 steps of 32), a partial last
-    row tile, row slices, both GEMM modes and jk_gemv_repacked."""
+    """m <= 2 runs a GEMV kernel (Q8_0 / Q4_0 / Q4_K / Q6_K: 16 lanes per row, block b on lane
+    b % 16, terms chained across the lanes in K order; the other formats, and activations beyond
+    the 32 KB staged in LDS (33024 columns at two tokens), the 32-row kernel whose waves split K):
+    every repacked entry point == the oracle bit for bit -- one and several rounds of blocks, a
+    partial last round and a partial last chunk (160 = 5 steps of 32), a partial last row tile, row
+    slices (the two-token Q6_K launch offsets each token's output), both GEMM modes and
+    jk_gemv_repacked."""
     torch = gpu
     if cols % jk.BLOCK_ELEMENTS[quant]:
         pytest.skip("shape not block aligned")
