@@ -1196,14 +1196,19 @@ __device__ __forceinline__ void sk_compute(const GemmChunk<Q, 32, TM> &cs, v32f 
             const v4i aq = *reinterpret_cast<const v4i *>(pa + 32 * st);
             // lane l: row jl and token l (token block l / 32)
             const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.ws[st][jl], cs.xs[st][lane], v32f{0}, 0, 0, 0);
+            // both token blocks' MFMAs ahead of their rescaling (one more v16i live: 236 VGPRs);
+            // across steps the MFMAs stay in order (interleaving them spills)
+            v16i c[2];
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
                 const v4i bq = *reinterpret_cast<const v4i *>(cs.b + (32 * tb + jl) * kRowB + 32 * st + 16 * hl);
-                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[16 * tb + v] = __builtin_fmaf((float)c[v], p[16 * tb + v], acc[16 * tb + v]);
-                __builtin_amdgcn_sched_barrier(0);  // (interleaving the steps' MFMAs spills)
+                c[tb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq, bq, v16i{0}, 0, 0, 0);
             }
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[16 * tb + v] = __builtin_fmaf((float)c[tb][v], p[16 * tb + v], acc[16 * tb + v]);
+            __builtin_amdgcn_sched_barrier(0);
             if constexpr (MINS)
                 acc = __builtin_amdgcn_mfma_f32_32x32x1f32(-cs.wm[st][jl], cs.xm[st][lane], acc, 0, 0, 0);
         }
@@ -1486,18 +1491,23 @@ static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 
     return check_launch("gemm_repacked_kernel");
 }
 
-// Tolerance-mode launch: the bit-exact launch's tile choice; the 32 x 16 single-wave tiles
-// (VALU scale products) are replaced by 32 x 32 tiles.
+// Tolerance-mode launch. The bit-exact kernels' results are within the tolerance by definition,
+// so the launch takes whichever measured faster: 128 x 128 tolerance tiles with at least 1.5
+// tiles per CU, K split over the waves where the tiled launch would fall back to single-wave
+// 32-row tiles, the bit-exact launch for the 128 x 64 and 64 x 64 tiles (Q8_0 / Q4_0 / Q4_K
+// 14336 x 4096 at 160 to 384 tokens: 6-19% faster than those tiles' tolerance variant, and
+// than 128 x 128 tiles at 1.3 per CU), and 32 x 32 tolerance tiles in place of the
+// 32 x 16 single-wave ones (VALU scale products).
 template <int Q>
 static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     // The 16-element-group formats keep the bit-exact kernel (their two groups per step do not fit
-    // the tolerance kernel's register budget); its results are within the tolerance by definition.
+    // the tolerance kernel's register budget).
     if constexpr (GemmFmt<Q>::GK == 16) {
         return launch_gemm<Q, 1>(s, w, a, y, r0, r1);
     } else {
         const long ncu = cu_count();
         const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
-        if (t128 >= ncu && w.cols % 128 == 0) {  // at least one 128 x 128 tile per CU; whole chunks
+        if (2 * t128 >= 3 * ncu && w.cols % 128 == 0) {  // at least 1.5 128 x 128 tiles per CU; whole chunks
             const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
             if constexpr (Q == JK_Q8_0) {
                 // (256-row tiles, one workgroup per CU, measured slower at 512 and 2048 tokens)
@@ -1512,11 +1522,8 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
         // where the tiled launch would fall back to single-wave 32-row tiles (Q8_0 14336 rows:
         // up to 128 tokens), K is split instead
         if (w.cols % 128 == 0 && gemm_tile(Q, r1 - r0, (long)a.m) >= 2) return launch_splitk<Q>(s, w, a, y, r0, r1);
-        switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
-        case 0: launch_tile<Q, 1, 128, 64, true>(s, w, a, y, r0, r1); break;
-        case 1: launch_tile<Q, 1, 64, 64, true>(s, w, a, y, r0, r1); break;
-        default: launch_tile<Q, 1, 32, 32, true>(s, w, a, y, r0, r1); break;
-        }
+        if (gemm_tile(Q, r1 - r0, (long)a.m) < 2) return launch_gemm<Q, 1>(s, w, a, y, r0, r1);
+        launch_tile<Q, 1, 32, 32, true>(s, w, a, y, r0, r1);
         return check_launch("gemm_repacked_kernel");
     }
 }
