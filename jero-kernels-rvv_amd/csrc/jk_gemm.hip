@@ -1440,6 +1440,104 @@ __global__ __launch_bounds__(64 * NW) void gemm_block_splitk_kernel(WeightDev w,
     }
 }
 
+// BitLinear token batches, one wave per 32 weight rows x 32 tokens with all of K in block order:
+// each output has one owner, so the reference's order of additions needs no table or barrier.
+// Per block the wave loads its rows' plane bytes and its tokens' activation bytes straight into
+// registers (two blocks in flight; loads clamped past the ends and unconditional), unpacks each
+// step's weight operand in registers (TQ2_0: dword 2 (st % 2) + hl of plane 2 (st / 4) +
+// (st % 4) / 2 holds the step's 16 values of half hl, the 2-bit fields of its bytes in order;
+// I2_S: field 6 - 2 st of plane hl), accumulates the exact i32 dot over the block's GB steps with
+// MFMA and adds f32(dot) * (xs * ws) -- the scale product from an outer-product MFMA, a single
+// rounded f32 product -- to an accumulator that started at 0.0 (ime.rs:882-938). Activations are
+// the MFMA's A operand and weights its B operand, so a lane holds one weight row and a store
+// instruction writes 32 consecutive rows of two tokens.
+template <int Q> struct BlRegs {
+    u32x4 w[Q == JK_TQ2_0 ? 4 : 1];  // TQ2_0: the block's four planes; I2_S: plane hl
+    u32x4 x[Q == JK_TQ2_0 ? 8 : 4];  // step st: token jl's bytes 32 st + 16 hl ..
+    uint32_t d;                      // TQ2_0: the block's f16 scale
+};
+
+template <int Q>
+__global__ __launch_bounds__(64) void bitlinear_wave_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0,
+                                                            int r1) {
+    static_assert(Q == JK_TQ2_0 || Q == JK_I2_S, "ternary formats");
+    constexpr int GB = Q == JK_TQ2_0 ? 8 : 4, BE = 32 * GB;  // steps and elements per weight block
+    const int lane = threadIdx.x & 63, hl = lane >> 5, jl = lane & 31;
+    const int ntn = (r1 - r0 + 31) / 32, ntm = ((int)a.m + 31) / 32;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;
+    const int n0 = r0 + 32 * tn, m0 = 32 * tm, M = (int)a.m, nb = w.nb;
+    const int row = min(n0 + jl, r1 - 1), tok = min(m0 + jl, M - 1);
+    const uint8_t *xrow = reinterpret_cast<const uint8_t *>(a.qs) + (size_t)tok * a.k_padded + 16 * hl;
+    const float xs = a.scales[(size_t)tok * a.k_blocks32];  // the token's scale (k_blocks32 = 1)
+    auto load = [&](BlRegs<Q> &R, int b) {
+        b = min(b, nb - 1);
+        if constexpr (Q == JK_TQ2_0) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) R.w[p] = *reinterpret_cast<const u32x4 *>(plane_ptr(w, p, row, b));
+            R.d = w.dplane[(size_t)row * (size_t)nb + (size_t)b];
+        } else {
+            R.w[0] = *reinterpret_cast<const u32x4 *>(plane_ptr(w, hl, row, b));
+        }
+#pragma unroll
+        for (int st = 0; st < GB; ++st) R.x[st] = *reinterpret_cast<const u32x4 *>(xrow + (size_t)b * BE + 32 * st);
+    };
+    float acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    auto block = [&](const BlRegs<Q> &R) {
+        v16i c = v16i{0};
+#pragma unroll
+        for (int st = 0; st < GB; ++st) {
+            u32x4 wq;
+            if constexpr (Q == JK_TQ2_0) {
+                const uint32_t wv = R.w[2 * (st >> 2) + ((st & 3) >> 1)][2 * (st & 1) + hl];
+                wq = u32x4{(uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
+                           (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
+                           (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
+                           (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u)};
+            } else {
+                const int sh = 6 - 2 * st;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) wq[k] = (uint32_t)bytes_sub((R.w[0][k] >> sh) & 0x03030303u, 0x01010101u);
+            }
+            c = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, R.x[st]), __builtin_bit_cast(v4i, wq), c, 0,
+                                                      0, 0);
+        }
+        const float ws = Q == JK_TQ2_0 ? f16_finite(R.d) : w.tensor_scale;
+        // p[v] = xs(token 8 (v / 4) + 4 hl + v % 4) * ws(row jl)
+        const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(xs, ws, v32f{0}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] += (float)c[v] * p[v];
+    };
+    BlRegs<Q> R0, R1;
+    load(R0, 0);
+    load(R1, 1);
+    for (int b = 0; b < nb; b += 2) {
+        block(R0);
+        load(R0, b + 2);
+        if (b + 1 >= nb) break;
+        block(R1);
+        load(R1, b + 3);
+    }
+    const size_t ld = (size_t)(r1 - r0);
+    if (n0 + jl < r1)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int m = m0 + 8 * (v >> 2) + 4 * hl + (v & 3);
+            if (m < M) y[(size_t)m * ld + (size_t)(n0 + jl - r0)] = acc[v];
+        }
+}
+
+template <int Q>
+static jk_status launch_bitlinear_wave(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y) {
+    const size_t ntn = (size_t)(w.rows + 31) / 32, ntm = (a.m + 31) / 32;
+    hipLaunchKernelGGL(bitlinear_wave_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64), 0, s, w, a, y, 0,
+                       w.rows);
+    return check_launch("bitlinear_wave_kernel");
+}
+
 constexpr int kBlockSplitkNW = 4;  // (8 waves measured slower on both 128-token BitLinear shapes)
 
 template <int Q, int GB>
@@ -1561,13 +1659,21 @@ jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t 
     a.qs = const_cast<int8_t *>(act);
     a.scales = const_cast<float *>(act_scales);
     // where the tiled launch would fall back to single-wave 32-row tiles (2560 x 6912 and
-    // 6912 x 2560 at 128 tokens), K is split over the waves of a workgroup instead
+    // 6912 x 2560 at 128 tokens): one wave per 32 x 32 tile over all of K when those tiles give
+    // every CU two waves (6912 x 2560: 864 tiles; TQ2_0 19.3 -> 15.1 us, I2_S 21.6 -> 14.2 us), and
+    // otherwise K split over the waves of a workgroup (2560 x 6912: 320 tiles of 27 blocks, where
+    // the single-wave chains took 25.0 us against 20.8 us). The wave kernel reads the activation
+    // rows with 16-byte loads, so it takes 16-byte aligned ones.
     const bool split = gemm_tile(w.quant, w.rows, m) >= 2;
+    const long tiles = (long)(w.rows + 31) / 32 * (long)((m + 31) / 32);
+    const bool wave = split && tiles >= 2 * cu_count() && (uintptr_t)act % 16 == 0;
     switch (w.quant) {
-    case JK_TQ2_0: return split ? launch_block_splitk<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows)
-                                : launch_gemm<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows);
-    case JK_I2_S: return split ? launch_block_splitk<JK_I2_S, 4>(s, w, a, y, 0, w.rows)
-                               : launch_gemm<JK_I2_S, 4>(s, w, a, y, 0, w.rows);
+    case JK_TQ2_0: return wave    ? launch_bitlinear_wave<JK_TQ2_0>(s, w, a, y)
+                          : split ? launch_block_splitk<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows)
+                                  : launch_gemm<JK_TQ2_0, 8>(s, w, a, y, 0, w.rows);
+    case JK_I2_S: return wave    ? launch_bitlinear_wave<JK_I2_S>(s, w, a, y)
+                         : split ? launch_block_splitk<JK_I2_S, 4>(s, w, a, y, 0, w.rows)
+                                 : launch_gemm<JK_I2_S, 4>(s, w, a, y, 0, w.rows);
     case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, 0, w.rows);
     default: return fail(JK_CAPABILITY_MISMATCH, "bitlinear: unsupported quant %d", w.quant);
     }

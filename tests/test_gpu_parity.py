@@ -704,6 +704,27 @@ def test_bitlinear_few_tokens_paths(gpu, quant, m, rows, cols, offset):
         assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
 
 
+@pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S])
+def test_bitlinear_wave_tiles_partial(gpu, quant):
+    """The one-wave-per-tile BitLinear launch (enough 32 x 32 tiles for two waves per CU) with a
+    partial last row tile (6900 = 215 x 32 + 20) and a partial last token tile (100 = 3 x 32 + 4):
+    every token against the oracle, bit for bit."""
+    torch = gpu
+    m, rows, cols = 100, 6900, 2560
+    raw = synth.gguf_weights(quant, rows, cols, seed=quant + 5)
+    rng = np.random.default_rng(quant)
+    a = rng.integers(-128, 128, (m, cols)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    dy = empty(torch, 4 * m * rows)
+    jk.dev_bitlinear_i8(w, dev(torch, a), dev(torch, sc), m, cols, dy, m * rows)
+    torch.cuda.synchronize()
+    got = host(dy, np.float32, m * rows).reshape(m, rows)
+    for i in range(m):
+        ref = O.bitlinear_i8(quant, [rows, cols], raw, a[i], float(sc[i]), rows)
+        assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
+
+
 @pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S, Q8_0])
 @pytest.mark.parametrize("m", [500, 250, 128, 30])
 def test_bitlinear_tile_shapes(gpu, quant, m):
