@@ -487,7 +487,7 @@ def test_gemm_repacked(gpu, quant, m, rows, cols):
 
 @pytest.mark.parametrize("quant", ALL_FORMATS)
 @pytest.mark.parametrize("m,rows,cols", [(1, 37, 512), (2, 100, 4096), (1, 33, 768), (2, 9, 160), (1, 4100, 1280),
-                                         (2, 70, 14336), (2, 21, 33024)])
+                                         (2, 70, 14336), (2, 21, 33024), (1, 9, 32768), (2, 5, 16384)])
 def test_gemv_repacked_one_or_two_tokens(gpu, quant, m, rows, cols):
     """m <= 2 runs a GEMV kernel (Q8_0 / Q4_0 / Q4_K / Q6_K: 16 lanes per row, block b on lane
     b % 16, terms chained across the lanes in K order; the other formats, and activations beyond
@@ -495,7 +495,8 @@ def test_gemv_repacked_one_or_two_tokens(gpu, quant, m, rows, cols):
     every repacked entry point == the oracle bit for bit -- one and several rounds of blocks, a
     partial last round and a partial last chunk (160 = 5 steps of 32), a partial last row tile, row
     slices (the two-token Q6_K launch offsets each token's output), both GEMM modes and
-    jk_gemv_repacked."""
+    jk_gemv_repacked. 32768 columns at one token and 16384 at two fill the LDS-staged activation
+    exactly (every thread's eight 16-byte pieces distinct)."""
     torch = gpu
     if cols % jk.BLOCK_ELEMENTS[quant]:
         pytest.skip("shape not block aligned")
