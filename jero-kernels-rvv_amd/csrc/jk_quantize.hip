@@ -34,30 +34,47 @@ jk_status launch_quantize_q8_0(hipStream_t s, const float *x, size_t nblocks, jk
 
 // quantize_block_q8_k_scalar (quant_q8.rs:447-475): one wave per block, 4 elements per lane,
 // bsums[j] = sum of the 16 quants of lanes 4j..4j+3. With ACT != 0 the input element is the
-// gated activation gated<ACT>(x[i], up[i]) (SwiGLU or ReLU^2), computed in the load.
-template <int ACT>
+// gated activation gated<ACT>(x[i], up[i]) (SwiGLU or ReLU^2), computed in the load. V4: the inputs
+// are 16-byte aligned and a lane reads its four elements with one load each. The block maximum and
+// the bsums are DPP reductions (a maximum and an integer sum: exact in any order), with no LDS
+// round trip on the launch's critical path.
+template <int ACT, bool V4>
 __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restrict__ x, const float *__restrict__ up,
                                                             size_t nblocks, jk_block_q8k *__restrict__ out) {
     const size_t blk = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int l = threadIdx.x & 63;
     const bool live = blk < nblocks;
+    const size_t e0 = min(blk, nblocks - 1) * 256 + 4 * l;  // (clamped: in bounds for every lane)
+    float g[4], u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (V4) {
+        const float4 gv = *reinterpret_cast<const float4 *>(x + e0);
+        g[0] = gv.x, g[1] = gv.y, g[2] = gv.z, g[3] = gv.w;
+        if constexpr (ACT != 0) {
+            const float4 uv = *reinterpret_cast<const float4 *>(up + e0);
+            u[0] = uv.x, u[1] = uv.y, u[2] = uv.z, u[3] = uv.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g[i] = x[e0 + i];
+            if constexpr (ACT != 0) u[i] = up[e0 + i];
+        }
+    }
     float v[4];
     float a = 0.0f;
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const size_t e = blk * 256 + 4 * l + i;
-        v[i] = live ? gated<ACT>(x[e], ACT ? up[e] : 0.0f) : 0.0f;
+        v[i] = live ? gated<ACT>(g[i], u[i]) : 0.0f;
         a = fmaxf(a, __builtin_isfinite(v[i]) ? fabsf(v[i]) : 0.0f);
     }
-    const float amax = wave_max<64>(a);
+    const float amax = wave_max64_dpp(a);
     int q[4] = {0, 0, 0, 0};
     const bool zero = amax == 0.0f || !__builtin_isfinite(amax);
     if (!zero) {
         const float inv = 127.0f / amax;
         for (int i = 0; i < 4; ++i) q[i] = round_scaled_to_i8(v[i], inv);
     }
-    int part = q[0] + q[1] + q[2] + q[3];
-    part += __shfl_xor(part, 1, 64);
-    part += __shfl_xor(part, 2, 64);
+    const int part = sum4_dpp(q[0] + q[1] + q[2] + q[3]);
     if (!live) return;
     uint32_t packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
                       ((uint32_t)(q[3] & 255) << 24);
@@ -73,9 +90,17 @@ jk_status launch_quantize_q8_k(hipStream_t s, const float *x, size_t nblocks, jk
 jk_status launch_quantize_q8_k_gated(hipStream_t s, int act, const float *x, const float *up, size_t nblocks,
                                      jk_block_q8k *out) {
     const dim3 grid((unsigned)((nblocks * 64 + 255) / 256)), block(256);
-    if (act == kActSwiglu) hipLaunchKernelGGL(quantize_q8_k_kernel<kActSwiglu>, grid, block, 0, s, x, up, nblocks, out);
-    else if (act == kActRelu2) hipLaunchKernelGGL(quantize_q8_k_kernel<kActRelu2>, grid, block, 0, s, x, up, nblocks, out);
-    else hipLaunchKernelGGL(quantize_q8_k_kernel<kActNone>, grid, block, 0, s, x, up, nblocks, out);
+    const bool v4 = (uintptr_t)x % 16 == 0 && (act == kActNone || (uintptr_t)up % 16 == 0);
+    if (act == kActSwiglu) {
+        if (v4) hipLaunchKernelGGL((quantize_q8_k_kernel<kActSwiglu, true>), grid, block, 0, s, x, up, nblocks, out);
+        else hipLaunchKernelGGL((quantize_q8_k_kernel<kActSwiglu, false>), grid, block, 0, s, x, up, nblocks, out);
+    } else if (act == kActRelu2) {
+        if (v4) hipLaunchKernelGGL((quantize_q8_k_kernel<kActRelu2, true>), grid, block, 0, s, x, up, nblocks, out);
+        else hipLaunchKernelGGL((quantize_q8_k_kernel<kActRelu2, false>), grid, block, 0, s, x, up, nblocks, out);
+    } else {
+        if (v4) hipLaunchKernelGGL((quantize_q8_k_kernel<kActNone, true>), grid, block, 0, s, x, up, nblocks, out);
+        else hipLaunchKernelGGL((quantize_q8_k_kernel<kActNone, false>), grid, block, 0, s, x, up, nblocks, out);
+    }
     return check_launch("quantize_q8_k_kernel");
 }
 

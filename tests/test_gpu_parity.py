@@ -89,7 +89,10 @@ def test_quantize_row_q8_0(gpu, n):
 
 
 @pytest.mark.parametrize("n", [256, 4096, 14336, 256 * 77])
-def test_quantize_row_q8_k(gpu, n):
+@pytest.mark.parametrize("offset", [0, 1])
+def test_quantize_row_q8_k(gpu, n, offset):
+    """offset 1: the input one float past a 16-byte boundary (element-wise loads instead of one
+    16-byte load per lane)."""
     torch = gpu
     rng = np.random.default_rng(n + 1)
     x = (rng.standard_normal(n) * rng.choice([1e-3, 1, 50], n)).astype(np.float32)
@@ -97,7 +100,9 @@ def test_quantize_row_q8_k(gpu, n):
     x[:256] = np.nan
     ref = O.quantize_row_q8_k(x)
     dy = empty(torch, ref.nbytes)
-    jk.dev_quantize_row_q8_k(dev(torch, x), n, dy, n // 256)
+    dx = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    dx[offset:offset + n] = torch.from_numpy(x).cuda()
+    jk.dev_quantize_row_q8_k(dx[offset:], n, dy, n // 256)
     torch.cuda.synchronize()
     got = host(dy, jk.BLOCK_Q8K, ref.size)
     assert same_bits(got["d"], ref["d"])
