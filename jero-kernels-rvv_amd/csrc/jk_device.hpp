@@ -69,6 +69,11 @@ __device__ __forceinline__ int bytes_sub(uint32_t a, uint32_t k) {
     return (int)(((a | 0x80808080u) - k) ^ 0x80808080u);
 }
 
+// Four 2-bit fields f (one per byte, values 0..3) to the signed bytes f - 1 by one byte permute:
+// selector byte f picks byte f of 0x020100FF (v_perm_b32 reads selectors 0..3 from its second
+// operand).
+__device__ __forceinline__ uint32_t crumbs_minus1(uint32_t f) { return __builtin_amdgcn_perm(0u, 0x020100FFu, f); }
+
 // Bits 0..3 of n moved to bit 4 of bytes 0..3 (the four shifted copies of n occupy
 // disjoint bit ranges, so the multiply has no carries): the fifth bit of four 5-bit quants.
 __device__ __forceinline__ uint32_t bit4_of_bytes(uint32_t n) { return ((n * 0x00204081u) & 0x01010101u) << 4; }

@@ -272,10 +272,8 @@ __device__ __forceinline__ uint4 nib4(uint4 v, int sh, uint32_t bias) {
                       (uint32_t)bytes_sub((v.z >> sh) & 0x0F0F0F0Fu, bias), (uint32_t)bytes_sub((v.w >> sh) & 0x0F0F0F0Fu, bias));
 }
 __device__ __forceinline__ uint4 crumb4(uint4 v, int sh) {
-    return make_uint4((uint32_t)bytes_sub((v.x >> sh) & 0x03030303u, 0x01010101u),
-                      (uint32_t)bytes_sub((v.y >> sh) & 0x03030303u, 0x01010101u),
-                      (uint32_t)bytes_sub((v.z >> sh) & 0x03030303u, 0x01010101u),
-                      (uint32_t)bytes_sub((v.w >> sh) & 0x03030303u, 0x01010101u));
+    return make_uint4(crumbs_minus1((v.x >> sh) & 0x03030303u), crumbs_minus1((v.y >> sh) & 0x03030303u),
+                      crumbs_minus1((v.z >> sh) & 0x03030303u), crumbs_minus1((v.w >> sh) & 0x03030303u));
 }
 
 // Unpack the staging registers to i8 with repack_block_scaled_range_into_i8's values
@@ -482,10 +480,8 @@ __device__ __forceinline__ void chunk_store(const WeightDev &w, const Stage<TN, 
         for (int k = 0; k < 4; ++k) {
             const uint32_t wv = comp(r.w[0], k);
             put_a(c, row, 64 * j + 16 * k,
-                  make_uint4((uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
-                             (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
-                             (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
-                             (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u)));
+                  make_uint4(crumbs_minus1(wv & 0x03030303u), crumbs_minus1((wv >> 2) & 0x03030303u),
+                             crumbs_minus1((wv >> 4) & 0x03030303u), crumbs_minus1((wv >> 6) & 0x03030303u)));
         }
     } else {  // JK_I2_S: 32-group g is 2-bit field g (shift 6 - 2g) of planes 0 (first 16) and 1
         c.ws[2 * j][row] = w.tensor_scale;
@@ -1471,17 +1467,20 @@ __global__ __launch_bounds__(64) void bitlinear_wave_kernel(WeightDev w, jk_act_
     const int row = min(n0 + jl, r1 - 1), tok = min(m0 + jl, M - 1);
     const uint8_t *xrow = reinterpret_cast<const uint8_t *>(a.qs) + (size_t)tok * a.k_padded + 16 * hl;
     const float xs = a.scales[(size_t)tok * a.k_blocks32];  // the token's scale (k_blocks32 = 1)
+    // the row's planes (TQ2_0: all four; I2_S: plane hl) and scales, advanced by the block index
+    constexpr int NP = Q == JK_TQ2_0 ? 4 : 1;
+    const uint8_t *pbase[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) pbase[p] = plane_ptr(w, Q == JK_TQ2_0 ? p : hl, row, 0);
+    const uint16_t *dbase = Q == JK_TQ2_0 ? w.dplane + (size_t)row * (size_t)nb : nullptr;
     auto load = [&](BlRegs<Q> &R, int b) {
         b = min(b, nb - 1);
-        if constexpr (Q == JK_TQ2_0) {
 #pragma unroll
-            for (int p = 0; p < 4; ++p) R.w[p] = *reinterpret_cast<const u32x4 *>(plane_ptr(w, p, row, b));
-            R.d = w.dplane[(size_t)row * (size_t)nb + (size_t)b];
-        } else {
-            R.w[0] = *reinterpret_cast<const u32x4 *>(plane_ptr(w, hl, row, b));
-        }
+        for (int p = 0; p < NP; ++p) R.w[p] = *reinterpret_cast<const u32x4 *>(pbase[p] + 16 * b);
+        if constexpr (Q == JK_TQ2_0) R.d = dbase[b];
+        const uint8_t *xb = xrow + (size_t)b * BE;
 #pragma unroll
-        for (int st = 0; st < GB; ++st) R.x[st] = *reinterpret_cast<const u32x4 *>(xrow + (size_t)b * BE + 32 * st);
+        for (int st = 0; st < GB; ++st) R.x[st] = *reinterpret_cast<const u32x4 *>(xb + 32 * st);
     };
     float acc[16];
 #pragma unroll
@@ -1493,14 +1492,12 @@ __global__ __launch_bounds__(64) void bitlinear_wave_kernel(WeightDev w, jk_act_
             u32x4 wq;
             if constexpr (Q == JK_TQ2_0) {
                 const uint32_t wv = R.w[2 * (st >> 2) + ((st & 3) >> 1)][2 * (st & 1) + hl];
-                wq = u32x4{(uint32_t)bytes_sub(wv & 0x03030303u, 0x01010101u),
-                           (uint32_t)bytes_sub((wv >> 2) & 0x03030303u, 0x01010101u),
-                           (uint32_t)bytes_sub((wv >> 4) & 0x03030303u, 0x01010101u),
-                           (uint32_t)bytes_sub((wv >> 6) & 0x03030303u, 0x01010101u)};
+                wq = u32x4{crumbs_minus1(wv & 0x03030303u), crumbs_minus1((wv >> 2) & 0x03030303u),
+                           crumbs_minus1((wv >> 4) & 0x03030303u), crumbs_minus1((wv >> 6) & 0x03030303u)};
             } else {
                 const int sh = 6 - 2 * st;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) wq[k] = (uint32_t)bytes_sub((R.w[0][k] >> sh) & 0x03030303u, 0x01010101u);
+                for (int k = 0; k < 4; ++k) wq[k] = crumbs_minus1((R.w[0][k] >> sh) & 0x03030303u);
             }
             c = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, R.x[st]), __builtin_bit_cast(v4i, wq), c, 0,
                                                       0, 0);
