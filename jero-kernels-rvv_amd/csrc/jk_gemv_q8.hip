@@ -781,8 +781,9 @@ gemv_q8_fast_kernel(GemvGroup grp) {
 // output is the GEMM's sum, in the GEMM's order, starting from 0.0. The activation quants are
 // staged in LDS once per workgroup (their loads issued before the weight loads); scales and sums
 // are read per lane.
-constexpr int kRpNW = 4;        // waves per workgroup: 16 rows
-constexpr int kRpMaxLoads = 8;  // 16-byte activation loads per thread: MT * k_padded <= 32 KB
+constexpr int kRpNW = 4;        // waves per workgroup: 4 rows a wave
+constexpr int kRpMaxLoads = 8;  // 16-byte activation loads per thread and staging round
+constexpr int kRpMaxPieces = 2048;  // staged activation: MT * k_padded <= 32 KB, MT * k_blocks32 <= 2048
 
 template <int Q> constexpr int kRpGroups = Q == JK_Q4_K ? 8 : Q == JK_Q6_K ? 16 : 1;  // scale groups per block
 // LDS padding after each block's activation quants: the 16 lanes of a row read 16 consecutive
@@ -879,7 +880,7 @@ gemv_repacked_fast_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r
     }
     const int tid = (int)threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = lane & 15, sub = lane >> 4;
-    const int row = r0 + 16 * (int)blockIdx.x + 4 * wave + sub;
+    const int row = r0 + 4 * kRpNW * (int)blockIdx.x + 4 * wave + sub;
     const int r = min(row, r1 - 1);
     const int nb = w.nb, nit = (nb + 15) / 16;
     const int kp = (int)a.k_padded, kb = (int)a.k_blocks32;
@@ -887,34 +888,47 @@ gemv_repacked_fast_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r
     float *s_xs = reinterpret_cast<float *>(s_xq + MT * kpp);
     float *s_xm = s_xs + MT * kb;
 
-    // 1. the activation -- quants in 16-byte loads, scales (and sums) in 4-byte loads -- issued
-    //    first (clamped, unconditional), so that it does not queue behind the weight stream
+    // 1. the activation -- quants in 16-byte loads, scales (and sums) in 4-byte loads -- in rounds
+    //    of kRpMaxLoads per thread; round 0 is issued first (clamped, unconditional), so that it
+    //    does not queue behind the weight stream
     const int n16 = MT * kp / 16, n4 = MT * kb;
+    const int rounds = (max(n16, n4) + NT * kRpMaxLoads - 1) / (NT * kRpMaxLoads);
     u32x4 xr[kRpMaxLoads];  // (a plain vector type: an array of uint4 is kept in scratch)
     float sr[kRpMaxLoads], mr[kRpMaxLoads];
+    auto stage_load = [&](int rd) {
 #pragma unroll
-    for (int i = 0; i < kRpMaxLoads; ++i) {
-        const int k = min(tid + NT * i, n16 - 1);
-        const int m = k / (kp / 16), o = k - m * (kp / 16);
-        xr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded + 16 * o);
-        const int e = min(tid + NT * i, n4 - 1);  // scales of token m at a.scales + m * kb
-        sr[i] = a.scales[e];
-        mr[i] = SUMS ? a.sums[e] : 0.0f;
-    }
+        for (int i = 0; i < kRpMaxLoads; ++i) {
+            const int k = min(NT * (kRpMaxLoads * rd + i) + tid, n16 - 1);
+            const int m = k / (kp / 16), o = k - m * (kp / 16);
+            xr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint8_t *>(a.qs) + (size_t)m * a.k_padded +
+                                                     16 * o);
+            const int e = min(NT * (kRpMaxLoads * rd + i) + tid, n4 - 1);  // token m's scales at a.scales + m * kb
+            sr[i] = a.scales[e];
+            mr[i] = SUMS ? a.sums[e] : 0.0f;
+        }
+    };
+    // every store unconditional, at the index its load was clamped to (a clamped store rewrites
+    // the last element with its own value), so the stores stay one straight-line sequence
+    auto stage_store = [&](int rd) {
+#pragma unroll
+        for (int i = 0; i < kRpMaxLoads; ++i) {
+            const int k = min(NT * (kRpMaxLoads * rd + i) + tid, n16 - 1);  // piece k: block k / (BE / 16) of all MT
+            *reinterpret_cast<u32x4 *>(s_xq + 16 * k + PAD * (k / (BE / 16))) = xr[i];
+            const int e = min(NT * (kRpMaxLoads * rd + i) + tid, n4 - 1);
+            s_xs[e] = sr[i];
+            if constexpr (SUMS) s_xm[e] = mr[i];
+        }
+    };
+    stage_load(0);
     // 2. the lane's first two blocks
     WReg<Q> W[2];
     wload<Q>(W[0], w, r, min(p, nb - 1));
     wload<Q>(W[1], w, r, min(16 + p, nb - 1));
-    // 3. the activation into LDS: every store unconditional, at the index its load was clamped to
-    //    (a clamped store rewrites the last element with its own value), so the stores stay one
-    //    straight-line sequence
-#pragma unroll
-    for (int i = 0; i < kRpMaxLoads; ++i) {
-        const int k = min(tid + NT * i, n16 - 1);  // 16-byte piece k: block k / (BE / 16) of all MT
-        *reinterpret_cast<u32x4 *>(s_xq + 16 * k + PAD * (k / (BE / 16))) = xr[i];
-        const int e = min(tid + NT * i, n4 - 1);
-        s_xs[e] = sr[i];
-        if constexpr (SUMS) s_xm[e] = mr[i];
+    // 3. the activation into LDS (further rounds behind the weight loads)
+    stage_store(0);
+    for (int rd = 1; rd < rounds; ++rd) {
+        stage_load(rd);
+        stage_store(rd);
     }
     lds_barrier();
 
@@ -965,7 +979,7 @@ static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_ac
     const bool split = Q == JK_Q6_K && a.m == 2;
     const size_t mt = split ? 1 : a.m;
     const size_t lds = mt * rp_lds_row(Q, a.k_padded) + (Q == JK_Q4_K ? 2 : 1) * mt * a.k_blocks32 * sizeof(float);
-    const dim3 grid((unsigned)((r1 - r0 + 15) / 16), split ? 2u : 1u), block(64 * kRpNW);
+    const dim3 grid((unsigned)((r1 - r0 + 4 * kRpNW - 1) / (4 * kRpNW)), split ? 2u : 1u), block(64 * kRpNW);
     if (mt == 1) hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 1>), grid, block, lds, s, w, a, y, r0, r1);
     else if constexpr (Q != JK_Q6_K)
         hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 2>), grid, block, lds, s, w, a, y, r0, r1);
@@ -974,10 +988,9 @@ static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_ac
 
 bool gemv_repacked_fast_ok(int quant, size_t m, size_t k_padded, size_t k_blocks32) {
     const bool fmt = quant == JK_Q8_0 || quant == JK_Q4_0 || quant == JK_Q4_K || quant == JK_Q6_K;
-    const size_t nt = 64 * kRpNW * kRpMaxLoads;  // activation loads of a workgroup
     const bool padded = quant == JK_Q4_K || quant == JK_Q6_K;
-    return fmt && m >= 1 && m <= 2 && k_padded % (padded ? 256 : 16) == 0 && m * k_padded / 16 <= nt &&
-           m * k_blocks32 <= nt;
+    return fmt && m >= 1 && m <= 2 && k_padded % (padded ? 256 : 16) == 0 && m * k_padded / 16 <= kRpMaxPieces &&
+           m * k_blocks32 <= kRpMaxPieces;
 }
 
 // (checked by the caller with gemv_repacked_fast_ok)
