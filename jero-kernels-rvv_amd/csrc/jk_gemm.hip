@@ -1347,6 +1347,7 @@ template <int Q, int GB, int NW>
 __global__ __launch_bounds__(64 * NW) void gemm_block_splitk_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
                                                                     int r0, int r1) {
     static_assert(GemmFmt<Q>::GK == 32 && !GemmFmt<Q>::MINS && (GB == 4 || GB == 8), "blocks of 4 or 8 steps");
+    static_assert(NW >= 4, "each thread adds four of the tile's 32 x 32 outputs");
     constexpr int UC = GB / 4;  // chunks per weight block
     __shared__ __align__(16) GemmChunk<Q, 32, 32> css[NW];
     __shared__ float tab[2][NW][32][33];  // [round parity][wave][token][row], rows padded to 33
