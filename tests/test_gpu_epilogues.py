@@ -66,20 +66,26 @@ def test_gated_host_tier(gpu):
 
 
 @pytest.mark.parametrize("n", [256, 14336, 256 * 57])
-def test_quantize_row_q8_k_gated(gpu, n):
+@pytest.mark.parametrize("offset", [0, 1])
+def test_quantize_row_q8_k_gated(gpu, n, offset):
     """Fused activation + quantize_row_q8_k == the activation kernel followed by the quantizer
-    (bit for bit), and for ReLU^2 == the oracle's quantize of the oracle's activation."""
+    (bit for bit), and for ReLU^2 == the oracle's quantize of the oracle's activation. offset 1:
+    the fused call's gate and up rows one float past a 16-byte boundary (element-wise loads)."""
     torch = gpu
     g, u = gate_up(n, n + 1)
     dg, du = dev(torch, g), dev(torch, u)
     nb = n // 256
+    ug, uu = torch.zeros(n + 4, dtype=torch.float32, device="cuda"), torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    ug[offset:offset + n] = dg
+    uu[offset:offset + n] = du
+    fg, fu = ug[offset:], uu[offset:]
     for act in (jk.ACT_SWIGLU, jk.ACT_RELU2):
         h = torch.empty(n, dtype=torch.float32, device="cuda")
         (jk.dev_swiglu_f32 if act == jk.ACT_SWIGLU else jk.dev_relu_squared_gate_f32)(dg, du, n, h)
         q1 = torch.empty(nb * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device="cuda")
         q2 = torch.empty_like(q1)
         jk.dev_quantize_row_q8_k(h, n, q1, nb)
-        jk.dev_quantize_row_q8_k_gated(act, dg, du, n, q2, nb)
+        jk.dev_quantize_row_q8_k_gated(act, fg, fu, n, q2, nb)
         torch.cuda.synchronize()
         assert np.array_equal(q1.cpu().numpy(), q2.cpu().numpy()), act
         if act == jk.ACT_RELU2:
