@@ -758,6 +758,119 @@ gemm_tol_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1)
     }
 }
 
+// Tolerance-mode prefill for Q6_K (16-element scale groups, no mins): the tiles, staging and loop
+// of gemm_tol_kernel. A 32-element step holds two groups of one weight block with integer scales
+// sc0, sc1 and the block's d (dequantize_q6_k_block, quant.rs:594-648: y = d * sc * (q - 32)).
+// Each group's exact i32 dot comes from a K = 16 MFMA; with tokens as the MFMA's A operand and
+// weights as its B operand a lane holds one weight row, so the two groups combine in integers,
+// sc0 * c0 + sc1 * c1 (24-bit multiplies: |c| <= 16 * 32 * 127 and |sc| <= 128, so the sum stays
+// below 2^24 and converts to f32 exactly), and enter the accumulator through one fused
+// multiply-add by xs * d -- four VALU instructions per output and step where the reference's
+// recipe takes six. Outputs are within the tolerance of the bit-exact recipe as for the other
+// tolerance kernels (the group's scale product is rounded once instead of twice).
+template <int Q>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gemm_tol16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+    static_assert(Q == JK_Q6_K, "Q6_K");
+    constexpr int TN = 128, TM = 128;
+    __shared__ __align__(16) GemmChunk<Q, TN, TM> cs;
+    __shared__ int s_sc[8][TN];  // the chunk's 8 group scales per row
+    __shared__ float s_d[TN];    // the rows' block scale d
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wn = wave & 1, wmi = wave >> 1;  // wave tile: rows 64 wn .., tokens 64 wmi ..
+    const int ntn = (r1 - r0 + TN - 1) / TN, ntm = ((int)a.m + TM - 1) / TM;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;
+    const int n0 = r0 + tn * TN, m0 = tm * TM;
+    const int M = (int)a.m;
+    const int nchunks = w.cols / kKC;  // (K is a multiple of 128 on this kernel)
+    const int hl = lane >> 5, jl = lane & 31;
+
+    v32f tacc[2];  // [token block]: rows of block nt at element 16 nt + v (lane: row jl of the block)
+    tacc[0] = tacc[1] = v32f{0};
+    // the scales of the staged chunk kc: thread t has row t / 2, half j = t % 2 of the chunk's
+    // groups (g = j + 2 qq), as chunk_store unpacks them
+    auto store_scales = [&](const Stage<TN, TM> &r, int kc) {
+        const int t = (int)threadIdx.x, row = t >> 1, j = t & 1, h = kc & 1;
+        const uint4 scv = r.w[3];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const int g = j + 2 * qq, js = 8 * h + g;
+            s_sc[g][row] = (int)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
+        }
+        if (j == 0) s_d[row] = f16_finite(r.wd[0]);
+    };
+    auto step = [&](int st) {
+        // lane l (half hl) supplies token jl's scale (A) and the d of row 64 wn + 32 hl + jl (B):
+        // p[16 nt + v] = xs(token 8 (v / 4) + 4 hl + v % 4 of the token block) * d(row jl of block nt)
+        const float dr = s_d[64 * wn + 32 * hl + jl];
+        int sc[2][2];  // [nt][group]
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) sc[nt][gg] = s_sc[2 * st + gg][64 * wn + 32 * nt + jl];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const int tok = 64 * wmi + 32 * tb + jl;
+            const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.xs[st][tok], dr, v32f{0}, 0, 0, 0);
+            long bq[2];
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg)
+                bq[gg] = *reinterpret_cast<const long *>(cs.b + tok * kRowB + 32 * st + 16 * gg + 8 * hl);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int arow = 64 * wn + 32 * nt + jl;
+                v16i c[2];
+#pragma unroll
+                for (int gg = 0; gg < 2; ++gg) {
+                    const long aq = *reinterpret_cast<const long *>(cs.a + arow * kRowB + 32 * st + 16 * gg + 8 * hl);
+                    c[gg] = __builtin_amdgcn_mfma_i32_32x32x16_i8(bq[gg], aq, v16i{0}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int comb = __mul24(c[0][v], sc[nt][0]) + __mul24(c[1][v], sc[nt][1]);
+                    tacc[tb][16 * nt + v] = __builtin_fmaf((float)comb, p[16 * nt + v], tacc[tb][16 * nt + v]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    Stage<TN, TM> rg;
+    chunk_load<Q>(rg, w, a, n0, r1, m0, M, 0);
+    chunk_store<Q>(w, rg, cs, 0);
+    store_scales(rg, 0);
+    __syncthreads();
+    for (int kc = 0; kc < nchunks; ++kc) {
+        const bool more = kc + 1 < nchunks;
+        if (more) chunk_load<Q>(rg, w, a, n0, r1, m0, M, kc + 1);
+#pragma unroll 1
+        for (int st = 0; st < kSteps; ++st) step(st);
+        if (more) {
+            __syncthreads();
+            chunk_store<Q>(w, rg, cs, kc + 1);
+            store_scales(rg, kc + 1);
+            __syncthreads();
+        }
+    }
+
+    // element v of block nt: token 8 (v / 4) + 4 hl + v % 4 of token block tb, row jl of block nt
+    const size_t ld = (size_t)(r1 - r0);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int n = n0 + 64 * wn + 32 * nt + jl;
+            if (n >= r1) continue;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + 64 * wmi + 32 * tb + 8 * (v >> 2) + 4 * hl + (v & 3);
+                if (m < M) y[(size_t)m * ld + (size_t)(n - r0)] = tacc[tb][16 * nt + v];
+            }
+        }
+}
+
 // Q8_0 tolerance-mode prefill, the same tiles and arithmetic as gemm_tol_kernel with its loads
 // made asynchronous: Q8_0 quants need no unpacking, so every tile goes from global memory
 // straight into LDS (global_load_lds: lane l of a load writes bytes 16 l.. of a 1 KB LDS
@@ -1596,9 +1709,18 @@ static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 
 // 32 x 16 single-wave ones (VALU scale products).
 template <int Q>
 static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    // The 16-element-group formats keep the bit-exact kernel (their two groups per step do not fit
-    // the tolerance kernel's register budget).
+    // The 16-element-group formats keep the bit-exact kernel, except Q6_K on enough 128 x 128 tiles.
     if constexpr (GemmFmt<Q>::GK == 16) {
+        if constexpr (Q == JK_Q6_K) {
+            const long ncu = cu_count();
+            const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
+            if (2 * t128 >= 3 * ncu && w.cols % 128 == 0) {
+                const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
+                hipLaunchKernelGGL(gemm_tol16_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
+                                   a, y, r0, r1);
+                return check_launch("gemm_tol16_kernel");
+            }
+        }
         return launch_gemm<Q, 1>(s, w, a, y, r0, r1);
     } else {
         const long ncu = cu_count();

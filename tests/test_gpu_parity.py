@@ -606,6 +606,52 @@ def test_gemm_tol_tile_shapes(gpu, quant, m):
     w.free()
 
 
+def test_gemm_tol_q6_k_tiles(gpu):
+    """Q6_K in tolerance mode on 128 x 128 tiles (14300 rows, a partial last row tile; 500 tokens, a
+    partial last token tile; weights with special scales): the two 16-element groups of a step
+    combined in integers with their scales, then one fused multiply-add. Within 1e-5 of each
+    token's output-row L2 norm of the bit-exact GPU output over the whole matrix and of the
+    oracle on a row window; a row slice within the same bar."""
+    torch = gpu
+    rows, cols, m = 14300, 512, 500
+    raw = synth.random_weights(Q6_K, rows, cols, seed=61, specials=True)
+    x = np.random.default_rng(62).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", Q6_K, [rows, cols], raw), rows, cols)
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m)
+    assert_within_row_norm(tol, exact)
+    ref = O.gemm_repacked(Q6_K, [rows, cols], raw, rows, cols, O.ActQ8(x, m, cols), 14250, 14300)
+    assert same_bits(exact[:, 14250:], ref)
+    norms = np.linalg.norm(exact.astype(np.float64), axis=1)
+    assert np.all(np.abs(tol[:, 14250:] - ref).max(axis=1) <= 1e-5 * norms)
+    assert_within_row_norm(gpu_gemm_tol(torch, w, x, m, 3, rows - 5), exact[:, 3:rows - 5])
+    w.free()
+
+
+def test_gemm_tol_q6_k_extreme_combination(gpu):
+    """The Q6_K tolerance tiles add sc0 * c0 + sc1 * c1 in integers before converting: the largest
+    magnitude a step can reach is 2 * 16 * 32 * 127 * 128 = 16,646,144, just under 2^24 (exact in
+    f32). Every weight at q - 32 = -32 with scales -128 and d = 1.0, activations +1.0 (quants 127),
+    12288 rows x 512 tokens: within the tolerance of the bit-exact output, which equals the
+    oracle."""
+    torch = gpu
+    rows, cols, m = 12288, 256, 512
+    blk = np.dtype([("ql", "u1", (128,)), ("qh", "u1", (64,)), ("scales", "i1", (16,)), ("d", "<f2")])
+    wb = np.zeros((rows, cols // 256), dtype=blk)
+    wb["scales"] = -128
+    wb["d"] = 1.0
+    raw = np.frombuffer(wb.tobytes(), dtype=np.uint8)
+    x = np.ones((m, cols), np.float32)
+    w = jk.Weight(jk.TensorView("w", Q6_K, [rows, cols], raw), rows, cols)
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m)
+    assert_within_row_norm(tol, exact)
+    ref = O.gemm_repacked(Q6_K, [rows, cols], raw, rows, cols, O.ActQ8(x[:2], 2, cols), 100, 140)
+    assert same_bits(exact[:2, 100:140], ref)
+    assert exact[0, 0] == 2 * 8 * 16 * 32 * 127 * 128 / 127.0  # 16 groups of (-32 * -128) * 16 * 127, xs = 1/127
+    w.free()
+
+
 def test_gemm_tol_extreme_group_dots(gpu):
     """The 512-token tolerance tiles read each group's integer dot product out of a biased
     accumulator; its range must hold the largest |dot| a Q8_0 group can reach, 32 * 128 * 127 (-128
