@@ -758,9 +758,10 @@ gemm_tol_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1)
     }
 }
 
-// Tolerance-mode prefill for Q6_K (16-element scale groups, no mins): the tiles, staging and loop
-// of gemm_tol_kernel. A 32-element step holds two groups of one weight block with integer scales
-// sc0, sc1 and the block's d (dequantize_q6_k_block, quant.rs:594-648: y = d * sc * (q - 32)).
+// Tolerance-mode prefill for Q6_K and Q3_K (16-element scale groups, no mins): the tiles, staging
+// and loop of gemm_tol_kernel. A 32-element step holds two groups of one weight block with integer
+// scales sc0, sc1 and the block's d (dequantize_q6_k_block, quant.rs:594-648: y = d * sc * (q - 32);
+// dequantize_q3_k_block, quant.rs:320-331: y = d * (scale - 32) * q3).
 // Each group's exact i32 dot comes from a K = 16 MFMA; with tokens as the MFMA's A operand and
 // weights as its B operand a lane holds one weight row, so the two groups combine in integers,
 // sc0 * c0 + sc1 * c1 (24-bit multiplies: |c| <= 16 * 32 * 127 and |sc| <= 128, so the sum stays
@@ -771,7 +772,7 @@ gemm_tol_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1)
 template <int Q>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 gemm_tol16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
-    static_assert(Q == JK_Q6_K, "Q6_K");
+    static_assert(Q == JK_Q6_K || Q == JK_Q3_K, "Q6_K, Q3_K");
     constexpr int TN = 128, TM = 128;
     __shared__ __align__(16) GemmChunk<Q, TN, TM> cs;
     __shared__ int s_sc[8][TN];  // the chunk's 8 group scales per row
@@ -793,13 +794,28 @@ gemm_tol16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r
     // groups (g = j + 2 qq), as chunk_store unpacks them
     auto store_scales = [&](const Stage<TN, TM> &r, int kc) {
         const int t = (int)threadIdx.x, row = t >> 1, j = t & 1, h = kc & 1;
-        const uint4 scv = r.w[3];
+        if constexpr (Q == JK_Q6_K) {
+            const uint4 scv = r.w[3];
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-            const int g = j + 2 * qq, js = 8 * h + g;
-            s_sc[g][row] = (int)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
+            for (int qq = 0; qq < 4; ++qq) {
+                const int g = j + 2 * qq, js = 8 * h + g;
+                s_sc[g][row] = (int)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
+            }
+            if (j == 0) s_d[row] = f16_finite(r.wd[0]);
+        } else {  // Q3_K: 6-bit scale 8h + g minus 32, d in the tail (repack.rs:1896-1911)
+            const uint4 tail = r.w[4];
+#pragma unroll
+            for (int jo = 0; jo < 2; ++jo)
+#pragma unroll
+                for (int part = 0; part < 2; ++part) {
+                    const int g = 2 * (2 * j + jo) + part, is = 8 * h + g;
+                    const uint32_t lb = (comp(tail, (is & 7) >> 2) >> (8 * (is & 3))) & 255u;
+                    const uint32_t lo = is < 8 ? (lb & 15u) : (lb >> 4);
+                    const uint32_t hi = (((tail.z >> (8 * (is & 3))) & 255u) >> (2 * (is >> 2))) & 3u;
+                    s_sc[g][row] = (int)(lo | (hi << 4)) - 32;
+                }
+            if (j == 0) s_d[row] = f16_finite(tail.w & 0xFFFFu);
         }
-        if (j == 0) s_d[row] = f16_finite(r.wd[0]);
     };
     auto step = [&](int st) {
         // lane l (half hl) supplies token jl's scale (A) and the d of row 64 wn + 32 hl + jl (B):
@@ -1709,9 +1725,10 @@ static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 
 // 32 x 16 single-wave ones (VALU scale products).
 template <int Q>
 static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    // The 16-element-group formats keep the bit-exact kernel, except Q6_K on enough 128 x 128 tiles.
+    // The 16-element-group formats keep the bit-exact kernel, except Q6_K and Q3_K on enough 128 x 128
+    // tiles.
     if constexpr (GemmFmt<Q>::GK == 16) {
-        if constexpr (Q == JK_Q6_K) {
+        if constexpr (Q == JK_Q6_K || Q == JK_Q3_K) {
             const long ncu = cu_count();
             const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
             if (2 * t128 >= 3 * ncu && w.cols % 128 == 0) {

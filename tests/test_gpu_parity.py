@@ -606,21 +606,22 @@ def test_gemm_tol_tile_shapes(gpu, quant, m):
     w.free()
 
 
-def test_gemm_tol_q6_k_tiles(gpu):
-    """Q6_K in tolerance mode on 128 x 128 tiles (14300 rows, a partial last row tile; 500 tokens, a
+@pytest.mark.parametrize("quant", [Q6_K, Q3_K])
+def test_gemm_tol_q6_k_tiles(gpu, quant):
+    """Q6_K / Q3_K in tolerance mode on 128 x 128 tiles (14300 rows, a partial last row tile; 500 tokens, a
     partial last token tile; weights with special scales): the two 16-element groups of a step
     combined in integers with their scales, then one fused multiply-add. Within 1e-5 of each
     token's output-row L2 norm of the bit-exact GPU output over the whole matrix and of the
     oracle on a row window; a row slice within the same bar."""
     torch = gpu
     rows, cols, m = 14300, 512, 500
-    raw = synth.random_weights(Q6_K, rows, cols, seed=61, specials=True)
+    raw = synth.random_weights(quant, rows, cols, seed=61 + quant, specials=True)
     x = np.random.default_rng(62).standard_normal((m, cols)).astype(np.float32)
-    w = jk.Weight(jk.TensorView("w", Q6_K, [rows, cols], raw), rows, cols)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
     exact = gpu_gemm(torch, w, x, m)
     tol = gpu_gemm_tol(torch, w, x, m)
     assert_within_row_norm(tol, exact)
-    ref = O.gemm_repacked(Q6_K, [rows, cols], raw, rows, cols, O.ActQ8(x, m, cols), 14250, 14300)
+    ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, O.ActQ8(x, m, cols), 14250, 14300)
     assert same_bits(exact[:, 14250:], ref)
     norms = np.linalg.norm(exact.astype(np.float64), axis=1)
     assert np.all(np.abs(tol[:, 14250:] - ref).max(axis=1) <= 1e-5 * norms)
