@@ -758,12 +758,13 @@ def test_bitlinear_few_tokens_paths(gpu, quant, m, rows, cols, offset):
 
 
 @pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S])
-def test_bitlinear_wave_tiles_partial(gpu, quant):
+@pytest.mark.parametrize("m,rows,cols", [(100, 6900, 2560), (16, 16400, 256)])
+def test_bitlinear_wave_tiles_partial(gpu, quant, m, rows, cols):
     """The one-wave-per-tile BitLinear launch (enough 32 x 32 tiles for two waves per CU) with a
-    partial last row tile (6900 = 215 x 32 + 20) and a partial last token tile (100 = 3 x 32 + 4):
+    partial last row tile (6900 = 215 x 32 + 20) and a partial last token tile (100 = 3 x 32 + 4),
+    and with one half-empty token tile (16 tokens, 16400 rows: 513 tiles, one weight block a row):
     every token against the oracle, bit for bit."""
     torch = gpu
-    m, rows, cols = 100, 6900, 2560
     raw = synth.gguf_weights(quant, rows, cols, seed=quant + 5)
     rng = np.random.default_rng(quant)
     a = rng.integers(-128, 128, (m, cols)).astype(np.int8)
