@@ -758,6 +758,36 @@ gemm_tol_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1)
     }
 }
 
+// The integer scales of a staged 16-element-group chunk kc (Q6_K: int8 scale 8h + g; Q3_K: 6-bit
+// scale 8h + g minus 32) and the block's d, as chunk_store unpacks them: staging thread t has row
+// t / 2 and half j = t % 2 of the chunk's 8 groups.
+template <int Q, int TN, int TM>
+__device__ __forceinline__ void tol16_scales(const Stage<TN, TM> &r, int kc, int t, int (*sc)[TN], float *d) {
+    const int row = t >> 1, j = t & 1, h = kc & 1;
+    if constexpr (Q == JK_Q6_K) {
+        const uint4 scv = r.w[3];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const int g = j + 2 * qq, js = 8 * h + g;
+            sc[g][row] = (int)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
+        }
+        if (j == 0) d[row] = f16_finite(r.wd[0]);
+    } else {  // Q3_K (repack.rs:1896-1911)
+        const uint4 tail = r.w[4];
+#pragma unroll
+        for (int jo = 0; jo < 2; ++jo)
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+                const int g = 2 * (2 * j + jo) + part, is = 8 * h + g;
+                const uint32_t lb = (comp(tail, (is & 7) >> 2) >> (8 * (is & 3))) & 255u;
+                const uint32_t lo = is < 8 ? (lb & 15u) : (lb >> 4);
+                const uint32_t hi = (((tail.z >> (8 * (is & 3))) & 255u) >> (2 * (is >> 2))) & 3u;
+                sc[g][row] = (int)(lo | (hi << 4)) - 32;
+            }
+        if (j == 0) d[row] = f16_finite(tail.w & 0xFFFFu);
+    }
+}
+
 // Tolerance-mode prefill for Q6_K and Q3_K (16-element scale groups, no mins): the tiles, staging
 // and loop of gemm_tol_kernel. A 32-element step holds two groups of one weight block with integer
 // scales sc0, sc1 and the block's d (dequantize_q6_k_block, quant.rs:594-648: y = d * sc * (q - 32);
@@ -792,31 +822,7 @@ gemm_tol16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r
     tacc[0] = tacc[1] = v32f{0};
     // the scales of the staged chunk kc: thread t has row t / 2, half j = t % 2 of the chunk's
     // groups (g = j + 2 qq), as chunk_store unpacks them
-    auto store_scales = [&](const Stage<TN, TM> &r, int kc) {
-        const int t = (int)threadIdx.x, row = t >> 1, j = t & 1, h = kc & 1;
-        if constexpr (Q == JK_Q6_K) {
-            const uint4 scv = r.w[3];
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq) {
-                const int g = j + 2 * qq, js = 8 * h + g;
-                s_sc[g][row] = (int)(int8_t)(comp(scv, js >> 2) >> (8 * (js & 3)));
-            }
-            if (j == 0) s_d[row] = f16_finite(r.wd[0]);
-        } else {  // Q3_K: 6-bit scale 8h + g minus 32, d in the tail (repack.rs:1896-1911)
-            const uint4 tail = r.w[4];
-#pragma unroll
-            for (int jo = 0; jo < 2; ++jo)
-#pragma unroll
-                for (int part = 0; part < 2; ++part) {
-                    const int g = 2 * (2 * j + jo) + part, is = 8 * h + g;
-                    const uint32_t lb = (comp(tail, (is & 7) >> 2) >> (8 * (is & 3))) & 255u;
-                    const uint32_t lo = is < 8 ? (lb & 15u) : (lb >> 4);
-                    const uint32_t hi = (((tail.z >> (8 * (is & 3))) & 255u) >> (2 * (is >> 2))) & 3u;
-                    s_sc[g][row] = (int)(lo | (hi << 4)) - 32;
-                }
-            if (j == 0) s_d[row] = f16_finite(tail.w & 0xFFFFu);
-        }
-    };
+    auto store_scales = [&](const Stage<TN, TM> &r, int kc) { tol16_scales<Q>(r, kc, (int)threadIdx.x, s_sc, s_d); };
     auto step = [&](int st) {
         // lane l (half hl) supplies token jl's scale (A) and the d of row 64 wn + 32 hl + jl (B):
         // p[16 nt + v] = xs(token 8 (v / 4) + 4 hl + v % 4 of the token block) * d(row jl of block nt)
@@ -1358,11 +1364,51 @@ __device__ __forceinline__ void sk_compute(const GemmChunk<Q, 32, TM> &cs, v32f 
     }
 }
 
+// sk_compute for the 16-element-group formats without mins (Q6_K, Q3_K), 64 tokens: the two
+// groups of a step each get their exact i32 dot from a K = 16 MFMA with the tokens as the A operand
+// and the weights as the B operand (a lane holds weight row jl), combine in integers with the row's
+// scales (below 2^24, exact in f32), and enter the accumulator through one fused multiply-add by
+// xs * d. acc[16 tb + v]: token 32 tb + 8 (v / 4) + 4 hl + v % 4, row jl.
+template <int Q>
+__device__ __forceinline__ void sk16_compute(const GemmChunk<Q, 32, 64> &cs, const int (*sc)[32], const float *d,
+                                             v32f &acc, int lane) {
+    const int hl = lane >> 5, jl = lane & 31;
+    const float dr = d[jl];
+#pragma unroll 1
+    for (int st = 0; st < kSteps; ++st) {  // (rolled: unrolled, the steps' registers spill)
+        const int sc0 = sc[2 * st][jl], sc1 = sc[2 * st + 1][jl];
+        // block b of the outer product: token 32 b + i (lane 32 b + i supplies its scale) times row jl's d
+        const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(cs.xs[st][lane], dr, v32f{0}, 0, 0, 0);
+        long aq[2];
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) aq[gg] = *reinterpret_cast<const long *>(cs.a + jl * kRowB + 32 * st + 16 * gg + 8 * hl);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            v16i c[2];
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) {
+                const long bq = *reinterpret_cast<const long *>(cs.b + (32 * tb + jl) * kRowB + 32 * st + 16 * gg + 8 * hl);
+                c[gg] = __builtin_amdgcn_mfma_i32_32x32x16_i8(bq, aq[gg], v16i{0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                acc[16 * tb + v] =
+                    __builtin_fmaf((float)(__mul24(c[0][v], sc0) + __mul24(c[1][v], sc1)), p[16 * tb + v], acc[16 * tb + v]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
 template <int Q, int TM, int NW, bool XV>
 __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y,
                                                                   int r0, int r1) {
-    static_assert(GemmFmt<Q>::GK == 32 && (TM == 32 || TM == 64), "32-element groups; 32 or 64 tokens");
+    // 16-element groups (Q6_K, Q3_K) combine a step's two groups in integers: 64-token tiles
+    constexpr bool G16 = GemmFmt<Q>::GK == 16;
+    static_assert((TM == 32 || TM == 64) && (!G16 || (TM == 64 && !GemmFmt<Q>::MINS)),
+                  "32-element groups on 32 or 64 tokens; 16-element groups without mins on 64");
     __shared__ __align__(16) SplitkSmem<Q, TM, NW> sm;
+    __shared__ int s_sc16[G16 ? NW : 1][8][32];  // (G16) each wave's chunk: group scales per row
+    __shared__ float s_d16[G16 ? NW : 1][32];    // and the rows' block scale d
     // (wave read as a scalar: the chunk loop's branches are then uniform, not exec-masked)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hl = lane >> 5, jl = lane & 31;
@@ -1390,21 +1436,29 @@ __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, j
         __builtin_amdgcn_sched_barrier(0);
         chunk_load<Q, XV>(rb, w, a, n0, r1, m0, M, ck(1));
         __builtin_amdgcn_sched_barrier(0);
+        auto store = [&](const Stage<32, TM> &r, int kc) {
+            chunk_store<Q>(w, r, cs, kc);
+            if constexpr (G16) tol16_scales<Q>(r, kc, lane, s_sc16[wave], s_d16[wave]);
+        };
+        auto compute = [&]() {
+            if constexpr (G16) sk16_compute<Q>(cs, s_sc16[wave], s_d16[wave], acc, lane);
+            else sk_compute(cs, acc, lane);
+        };
         for (int i = 0; i < cnt; i += 2) {
-            chunk_store<Q>(w, ra, cs, ck(i));
+            store(ra, ck(i));
             wave_lds_sync();
             __builtin_amdgcn_sched_barrier(0);
             chunk_load<Q, XV>(ra, w, a, n0, r1, m0, M, ck(i + 2));
             __builtin_amdgcn_sched_barrier(0);
-            sk_compute(cs, acc, lane);
+            compute();
             wave_lds_sync();  // the chunk's LDS reads are done before the next store
             __builtin_amdgcn_sched_barrier(0);
-            chunk_store<Q>(w, rb, cs, ck(i + 1));
+            store(rb, ck(i + 1));
             wave_lds_sync();
             __builtin_amdgcn_sched_barrier(0);
             chunk_load<Q, XV>(rb, w, a, n0, r1, m0, M, ck(i + 3));
             __builtin_amdgcn_sched_barrier(0);
-            if (i + 1 < cnt) sk_compute(cs, acc, lane);
+            if (i + 1 < cnt) compute();
             wave_lds_sync();
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1415,7 +1469,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_tol_splitk_kernel(WeightDev w, j
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int row = 8 * (v >> 2) + 4 * hl + (v & 3);
-        if constexpr (TM == 64) {
+        if constexpr (G16) {  // element 16 tb + v: token 32 tb + 8 (v / 4) + 4 hl + v % 4, row jl
+            sm.red[wave][row][jl] = acc[v];
+            sm.red[wave][32 + row][jl] = acc[16 + v];
+        } else if constexpr (TM == 64) {
             sm.red[wave][jl][row] = acc[v];
             sm.red[wave][32 + jl][row] = acc[16 + v];
         } else {
@@ -1729,6 +1786,14 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
     // tiles.
     if constexpr (GemmFmt<Q>::GK == 16) {
         if constexpr (Q == JK_Q6_K || Q == JK_Q3_K) {
+            // few tokens: K split over the waves of a workgroup (Q3_K's heavier unpack loses to the
+            // bit-exact tiles at 128 tokens: 104.7 against 101.3 us on 14336 x 4096)
+            if (a.m <= (Q == JK_Q6_K ? 128 : 64) && w.cols % 128 == 0) {
+                const bool xv = a.k_blocks32 % 4 == 0 && (uintptr_t)a.scales % 16 == 0;
+                if (xv) launch_splitk_t<Q, 64, true>(s, w, a, y, r0, r1);
+                else launch_splitk_t<Q, 64, false>(s, w, a, y, r0, r1);
+                return check_launch("gemm_tol_splitk_kernel");
+            }
             const long ncu = cu_count();
             const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
             if (2 * t128 >= 3 * ncu && w.cols % 128 == 0) {

@@ -680,7 +680,7 @@ def test_gemm_tol_extreme_group_dots(gpu):
     w.free()
 
 
-SPLITK_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S]
+SPLITK_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S, Q6_K, Q3_K]
 
 
 @pytest.mark.parametrize("quant", SPLITK_FORMATS)
@@ -688,11 +688,12 @@ SPLITK_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S]
 def test_gemm_tol_split_k(gpu, quant, m, chunks):
     """Tolerance-mode GEMM of a few tokens, where K is split over the waves of a workgroup: K of
     1 to 13 chunks of 128 (waves with no chunk, with one more chunk than the others), 32- and
-    64-token tiles with a partial last one, 200 rows (a partial last row tile) and a row slice.
+    64-token tiles with a partial last one (Q6_K / Q3_K: 64-token tiles, the two 16-element groups of
+    a step combined in integers), 200 rows (a partial last row tile) and a row slice.
     Held within 1e-5 of each token's output-row L2 norm of the bit-exact GPU output over the whole
     matrix and of the oracle on a row window."""
     torch = gpu
-    block = 256 if quant in (Q4_K, Q5_K, TQ2_0) else 128  # K-quant super-blocks, I2_S blocks of 128
+    block = 256 if quant in (Q4_K, Q5_K, TQ2_0, Q6_K, Q3_K) else 128  # K-quant super-blocks, I2_S blocks of 128
     cols = max(block, 128 * chunks // block * block)
     rows = 200
     raw = synth.random_weights(quant, rows, cols, seed=7 * m + chunks + quant, specials=True)
