@@ -1782,18 +1782,11 @@ static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 
 // 32 x 16 single-wave ones (VALU scale products).
 template <int Q>
 static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
-    // The 16-element-group formats keep the bit-exact kernel, except Q6_K and Q3_K on enough 128 x 128
-    // tiles.
+    // The 16-element-group formats: Q6_K and Q3_K combine a step's two groups in integers (128 x 128
+    // tiles from 1.5 per CU, K split over the waves of a workgroup below); Q2_K, and Q3_K between 64
+    // tokens and the tiles, run the bit-exact kernel.
     if constexpr (GemmFmt<Q>::GK == 16) {
         if constexpr (Q == JK_Q6_K || Q == JK_Q3_K) {
-            // few tokens: K split over the waves of a workgroup (Q3_K's heavier unpack loses to the
-            // bit-exact tiles at 128 tokens: 104.7 against 101.3 us on 14336 x 4096)
-            if (a.m <= (Q == JK_Q6_K ? 128 : 64) && w.cols % 128 == 0) {
-                const bool xv = a.k_blocks32 % 4 == 0 && (uintptr_t)a.scales % 16 == 0;
-                if (xv) launch_splitk_t<Q, 64, true>(s, w, a, y, r0, r1);
-                else launch_splitk_t<Q, 64, false>(s, w, a, y, r0, r1);
-                return check_launch("gemm_tol_splitk_kernel");
-            }
             const long ncu = cu_count();
             const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
             if (2 * t128 >= 3 * ncu && w.cols % 128 == 0) {
@@ -1801,6 +1794,16 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
                 hipLaunchKernelGGL(gemm_tol16_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
                                    a, y, r0, r1);
                 return check_launch("gemm_tol16_kernel");
+            }
+            // below that, K split over the waves of a workgroup: Q6_K at every token count (14336 x 4096
+            // at 192 / 256 / 384 tokens 122.9 / 145.9 / 220.0 us against 146.6 / 162.6 / 245.1 us for
+            // the bit-exact tiles), Q3_K up to 64 tokens (its heavier unpack lost at 128 tokens: 104.7
+            // against 101.3 us)
+            if ((Q == JK_Q6_K || a.m <= 64) && w.cols % 128 == 0) {
+                const bool xv = a.k_blocks32 % 4 == 0 && (uintptr_t)a.scales % 16 == 0;
+                if (xv) launch_splitk_t<Q, 64, true>(s, w, a, y, r0, r1);
+                else launch_splitk_t<Q, 64, false>(s, w, a, y, r0, r1);
+                return check_launch("gemm_tol_splitk_kernel");
             }
         }
         return launch_gemm<Q, 1>(s, w, a, y, r0, r1);

@@ -684,7 +684,7 @@ SPLITK_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S,
 
 
 @pytest.mark.parametrize("quant", SPLITK_FORMATS)
-@pytest.mark.parametrize("m,chunks", [(3, 1), (17, 3), (32, 5), (33, 6), (64, 13), (100, 10)])
+@pytest.mark.parametrize("m,chunks", [(3, 1), (17, 3), (32, 5), (33, 6), (64, 13), (100, 10), (200, 4)])
 def test_gemm_tol_split_k(gpu, quant, m, chunks):
     """Tolerance-mode GEMM of a few tokens, where K is split over the waves of a workgroup: K of
     1 to 13 chunks of 128 (waves with no chunk, with one more chunk than the others), 32- and
