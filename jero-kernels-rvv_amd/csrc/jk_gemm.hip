@@ -798,7 +798,8 @@ __device__ __forceinline__ void tol16_scales(const Stage<TN, TM> &r, int kc, int
 // below 2^24 and converts to f32 exactly), and enter the accumulator through one fused
 // multiply-add by xs * d -- four VALU instructions per output and step where the reference's
 // recipe takes six. Outputs are within the tolerance of the bit-exact recipe as for the other
-// tolerance kernels (the group's scale product is rounded once instead of twice).
+// tolerance kernels: per step the scale product xs * d and the fused multiply-add round once
+// each, where the reference rounds two products and a sum per group (d * sc is exact either way).
 template <int Q>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 gemm_tol16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
