@@ -408,6 +408,7 @@ def main() -> int:
         for name, quant, rows, cols in (("gemv_repacked Q8_0 4096x4096 M=1", jk.Q8_0, 4096, 4096),
                                         ("gemv_repacked Q4_0 4096x4096 M=1", jk.Q4_0, 4096, 4096),
                                         ("gemv_repacked Q4_K 14336x4096 M=1", jk.Q4_K, 14336, 4096),
+                                        ("gemv_repacked Q5_K 14336x4096 M=1", jk.Q5_K, 14336, 4096),
                                         ("gemv_repacked Q6_K 4096x14336 M=1", jk.Q6_K, 4096, 14336)):
             ws = copies(quant, rows, cols, 550 + quant)
             need = jk.act_q8_bytes(1, cols)

@@ -785,14 +785,14 @@ constexpr int kRpNW = 4;        // waves per workgroup: 4 rows a wave
 constexpr int kRpMaxLoads = 8;  // 16-byte activation loads per thread and staging round
 constexpr int kRpMaxPieces = 2048;  // staged activation: MT * k_padded <= 32 KB, MT * k_blocks32 <= 2048
 
-template <int Q> constexpr int kRpGroups = Q == JK_Q4_K ? 8 : Q == JK_Q6_K ? 16 : 1;  // scale groups per block
+template <int Q> constexpr int kRpGroups = Q == JK_Q4_K || Q == JK_Q5_K ? 8 : Q == JK_Q6_K ? 16 : 1;  // scale groups per block
 // LDS padding after each block's activation quants: the 16 lanes of a row read 16 consecutive
 // blocks at once, and at 256 bytes a block they would all fall on the same banks; 16 more bytes
 // a block put consecutive lanes on consecutive 16-byte bank groups. (32-byte blocks already do.)
 template <int Q> constexpr int kRpPad = fmt_of(Q).be >= 256 ? 16 : 0;
+static bool rp_kquant(int quant) { return quant == JK_Q4_K || quant == JK_Q5_K || quant == JK_Q6_K; }
 static size_t rp_lds_row(int quant, size_t k_padded) {
-    const size_t be = quant == JK_Q4_K || quant == JK_Q6_K ? 256 : 32;
-    return k_padded + (quant == JK_Q4_K || quant == JK_Q6_K ? k_padded / be * 16 : 0);
+    return k_padded + (rp_kquant(quant) ? k_padded / 256 * 16 : 0);
 }
 
 // The terms of block b of the lane's row for one token (its quants of the block in LDS, its
@@ -819,9 +819,10 @@ __device__ __forceinline__ void rp_terms(const WReg<Q> &wr, const uint8_t *xq, c
             s -= 8 * sx;
         }
         t[0] = (float)s * (xs[0] * ws);
-    } else if constexpr (Q == JK_Q4_K) {
+    } else if constexpr (Q == JK_Q4_K || Q == JK_Q5_K) {
         // sub-block g (elements 32 g ..): quarter g / 2, low (g even) or high nibbles of planes
-        // 1 + g / 2 * 2 and 2 + g / 2 * 2; scale / min unpack_k4_scales_mins (repack.rs:1158-1170)
+        // 1 + g / 2 * 2 and 2 + g / 2 * 2 (Q5_K: planes 3 + ..., 4 + ..., and bit g of the qh bytes
+        // in planes 1 and 2 as the fifth bit); scale / min unpack_k4_scales_mins (repack.rs:1158-1170)
         const uint4 h = wr.c[0];
         const float d = f16_finite(h.x & 0xFFFFu), dmin = f16_finite(h.x >> 16);
         const uint32_t sc[2] = {h.y & 0x3F3F3F3Fu, (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u)};
@@ -832,8 +833,11 @@ __device__ __forceinline__ void rp_terms(const WReg<Q> &wr, const uint8_t *xq, c
             int s = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t wd = comp(i < 4 ? wr.c[1 + 2 * c] : wr.c[2 + 2 * c], i & 3);
-                s = dot4((int)((wd >> sh) & 0x0F0F0F0Fu), xi[8 * g + i], s);
+                constexpr int P = Q == JK_Q5_K ? 3 : 1;  // first quant plane
+                const uint32_t wd = comp(i < 4 ? wr.c[P + 2 * c] : wr.c[P + 1 + 2 * c], i & 3);
+                uint32_t v = (wd >> sh) & 0x0F0F0F0Fu;
+                if constexpr (Q == JK_Q5_K) v |= ((comp(wr.c[1 + (i >> 2)], i & 3) >> g) & 0x01010101u) << 4;
+                s = dot4((int)v, xi[8 * g + i], s);
             }
             const float ws = d * (float)byte_of(sc[g >> 2], g & 3);
             const float wm = dmin * (float)byte_of(mv[g >> 2], g & 3);
@@ -868,7 +872,7 @@ template <int Q, int MT>
 __global__ __launch_bounds__(64 * kRpNW) __attribute__((amdgpu_waves_per_eu(2))) void
 gemv_repacked_fast_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
     constexpr int G = kRpGroups<Q>, BE = fmt_of(Q).be, NT = 64 * kRpNW, PAD = kRpPad<Q>;
-    constexpr bool SUMS = Q == JK_Q4_K;
+    constexpr bool SUMS = Q == JK_Q4_K || Q == JK_Q5_K;
     // LDS: activation quants [MT][k_padded / BE][BE + PAD] (k_padded a multiple of BE when PAD is
     // not 0), then scales [MT][k_blocks32] (and sums, Q4_K)
     extern __shared__ __align__(16) uint8_t s_xq[];
@@ -978,7 +982,7 @@ static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_ac
     // registers than it has); the second token's weight reads then mostly hit the caches
     const bool split = Q == JK_Q6_K && a.m == 2;
     const size_t mt = split ? 1 : a.m;
-    const size_t lds = mt * rp_lds_row(Q, a.k_padded) + (Q == JK_Q4_K ? 2 : 1) * mt * a.k_blocks32 * sizeof(float);
+    const size_t lds = mt * rp_lds_row(Q, a.k_padded) + (Q == JK_Q4_K || Q == JK_Q5_K ? 2 : 1) * mt * a.k_blocks32 * sizeof(float);
     const dim3 grid((unsigned)((r1 - r0 + 4 * kRpNW - 1) / (4 * kRpNW)), split ? 2u : 1u), block(64 * kRpNW);
     if (mt == 1) hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 1>), grid, block, lds, s, w, a, y, r0, r1);
     else if constexpr (Q != JK_Q6_K)
@@ -987,8 +991,8 @@ static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_ac
 }
 
 bool gemv_repacked_fast_ok(int quant, size_t m, size_t k_padded, size_t k_blocks32) {
-    const bool fmt = quant == JK_Q8_0 || quant == JK_Q4_0 || quant == JK_Q4_K || quant == JK_Q6_K;
-    const bool padded = quant == JK_Q4_K || quant == JK_Q6_K;
+    const bool fmt = quant == JK_Q8_0 || quant == JK_Q4_0 || rp_kquant(quant);
+    const bool padded = rp_kquant(quant);
     return fmt && m >= 1 && m <= 2 && k_padded % (padded ? 256 : 16) == 0 && m * k_padded / 16 <= kRpMaxPieces &&
            m * k_blocks32 <= kRpMaxPieces;
 }
@@ -999,6 +1003,7 @@ jk_status launch_gemv_repacked_fast(hipStream_t s, const WeightDev &w, const jk_
     case JK_Q8_0: return launch_rp_fast_q<JK_Q8_0>(s, w, a, y, r0, r1);
     case JK_Q4_0: return launch_rp_fast_q<JK_Q4_0>(s, w, a, y, r0, r1);
     case JK_Q4_K: return launch_rp_fast_q<JK_Q4_K>(s, w, a, y, r0, r1);
+    case JK_Q5_K: return launch_rp_fast_q<JK_Q5_K>(s, w, a, y, r0, r1);
     case JK_Q6_K: return launch_rp_fast_q<JK_Q6_K>(s, w, a, y, r0, r1);
     default: return fail(JK_CAPABILITY_MISMATCH, "gemv_repacked_fast: unsupported quant %d", w.quant);
     }

@@ -494,7 +494,7 @@ def test_gemm_repacked(gpu, quant, m, rows, cols):
 @pytest.mark.parametrize("m,rows,cols", [(1, 37, 512), (2, 100, 4096), (1, 33, 768), (2, 9, 160), (1, 4100, 1280),
                                          (2, 70, 14336), (2, 21, 33024), (1, 9, 32768), (2, 5, 16384)])
 def test_gemv_repacked_one_or_two_tokens(gpu, quant, m, rows, cols):
-    """m <= 2 runs a GEMV kernel (Q8_0 / Q4_0 / Q4_K / Q6_K: 16 lanes per row, block b on lane
+    """m <= 2 runs a GEMV kernel (Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K: 16 lanes per row, block b on lane
     b % 16, terms chained across the lanes in K order; the other formats, and activations beyond
     the 32 KB staged in LDS (33024 columns at two tokens), the 32-row kernel whose waves split K):
     every repacked entry point == the oracle bit for bit -- one and several rounds of blocks, a
