@@ -801,12 +801,29 @@ template <int Q>
 __device__ __forceinline__ void rp_terms(const WReg<Q> &wr, const uint8_t *xq, const float *xs, const float *xm,
                                          float (&t)[kRpGroups<Q>]) {
     const int *xi = reinterpret_cast<const int *>(xq);
-    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0) {
+    if constexpr (Q == JK_Q8_0 || Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_IQ4_NL) {
         const float ws = f16_finite(wr.d);  // repack.rs:1735-1760: the block's d
         int s = 0;
         if constexpr (Q == JK_Q8_0) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) s = dot4((int)comp(wr.c[i >> 2], i & 3), xi[i], s);
+        } else if constexpr (Q == JK_Q5_0) {  // (nibble | 16 bit) - 16, element j's bit j of the word (repack.rs:1830)
+            int sx = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t wd = comp(wr.c[0], i);
+                s = dot4((int)((wd & 0x0F0F0F0Fu) | bit4_of_bytes((wr.h >> (4 * i)) & 15u)), xi[i], s);
+                s = dot4((int)(((wd >> 4) & 0x0F0F0F0Fu) | bit4_of_bytes((wr.h >> (16 + 4 * i)) & 15u)), xi[4 + i], s);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sx = dot4(xi[i], 0x01010101, sx);
+            s -= 16 * sx;
+        } else if constexpr (Q == JK_IQ4_NL) {  // KVALUES_IQ4NL[nibble] (repack.rs:1861)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s = dot4((int)iq4nl_lookup(comp(wr.c[0], i) & 0x0F0F0F0Fu), xi[i], s);
+                s = dot4((int)iq4nl_lookup((comp(wr.c[0], i) >> 4) & 0x0F0F0F0Fu), xi[4 + i], s);
+            }
         } else {  // nibbles biased by +8: sum((n - 8) x) = sum(n x) - 8 sum(x), exactly
             int sx = 0;
 #pragma unroll
@@ -991,7 +1008,7 @@ static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_ac
 }
 
 bool gemv_repacked_fast_ok(int quant, size_t m, size_t k_padded, size_t k_blocks32) {
-    const bool fmt = quant == JK_Q8_0 || quant == JK_Q4_0 || rp_kquant(quant);
+    const bool fmt = quant == JK_Q8_0 || quant == JK_Q4_0 || quant == JK_Q5_0 || quant == JK_IQ4_NL || rp_kquant(quant);
     const bool padded = rp_kquant(quant);
     return fmt && m >= 1 && m <= 2 && k_padded % (padded ? 256 : 16) == 0 && m * k_padded / 16 <= kRpMaxPieces &&
            m * k_blocks32 <= kRpMaxPieces;
@@ -1002,6 +1019,8 @@ jk_status launch_gemv_repacked_fast(hipStream_t s, const WeightDev &w, const jk_
     switch (w.quant) {
     case JK_Q8_0: return launch_rp_fast_q<JK_Q8_0>(s, w, a, y, r0, r1);
     case JK_Q4_0: return launch_rp_fast_q<JK_Q4_0>(s, w, a, y, r0, r1);
+    case JK_Q5_0: return launch_rp_fast_q<JK_Q5_0>(s, w, a, y, r0, r1);
+    case JK_IQ4_NL: return launch_rp_fast_q<JK_IQ4_NL>(s, w, a, y, r0, r1);
     case JK_Q4_K: return launch_rp_fast_q<JK_Q4_K>(s, w, a, y, r0, r1);
     case JK_Q5_K: return launch_rp_fast_q<JK_Q5_K>(s, w, a, y, r0, r1);
     case JK_Q6_K: return launch_rp_fast_q<JK_Q6_K>(s, w, a, y, r0, r1);
