@@ -55,6 +55,43 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def graph_us(torch, launch, n, reps=5) -> float:
+    """Per-launch time of n launches captured back to back in a HIP graph, replayed `reps`
+    times with HIP events on the capturing stream (includes the graph's inter-launch gap)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n):
+            launch(i, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cs = torch.cuda.current_stream().cuda_stream
+        for i in range(n):
+            launch(i, cs)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+
+def stream_read_us(torch, jk, buf, sink, nbytes) -> float:
+    """jk_measure_stream_read of nbytes, graph-timed like the GEMV stages: back-to-back launches
+    over distinct spans of buf (>= 600 MB in all where buf allows, beyond the 256 MB Infinity
+    Cache), so every launch reads from HBM."""
+    span = (nbytes + 65535) // 65536 * 65536
+    n = max(1, min(buf.numel() // span, max(8, -(-600_000_000 // span))))
+    base = buf.data_ptr()
+    return graph_us(torch, lambda i, st: jk.dev_measure_stream_read(base + (i % n) * span, nbytes, sink, st), n)
+
+
 def gemv_bytes(quant, rows, cols, jk) -> int:
     nb = cols // jk.BLOCK_ELEMENTS[quant]
     return rows * nb * jk.BLOCK_BYTES[quant] + (cols // 256) * jk.BLOCK_Q8K.itemsize + rows * 4
@@ -243,12 +280,34 @@ def main() -> int:
                             "gbs": round(b / (dur_us * 1e-6) / 1e9, 1)}
         log(f"  {stage:12s} {b:>10d} B: {dur_us:.2f} us/launch, {per_stage[stage]['gbs']} GB/s")
         del g
+    # Streaming-read ceiling of each stage: a plain read of the stage's algorithmic byte count
+    # (jk_measure_stream_read), timed the same way, and the stage's time as a fraction of it;
+    # plus one 1 GiB read for the asymptotic HBM read rate of this GPU.
+    rd_buf = torch.empty(2_400_000_000, dtype=torch.uint8, device=dev)
+    rd_sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    stream_ceiling = {}
+    for stage, rec_ in per_stage.items():
+        us = stream_read_us(torch, jk, rd_buf, rd_sink, rec_["bytes"])
+        rec_["stream_read_us"] = round(us, 3)
+        rec_["stream_read_gbs"] = round(rec_["bytes"] / (us * 1e-6) / 1e9, 1)
+        rec_["frac_of_stream_read"] = round(us / rec_["us"], 4)
+        stream_ceiling[stage] = {"bytes": rec_["bytes"], "us": round(us, 3), "gbs": rec_["stream_read_gbs"]}
+        log(f"  stream read {rec_['bytes']:>10d} B: {us:.2f} us/launch, {rec_['stream_read_gbs']} GB/s "
+            f"({stage} at {100 * us / rec_['us']:.1f}% of it)")
+    big = 1 << 30
+    us = stream_read_us(torch, jk, rd_buf, rd_sink, big)
+    stream_ceiling["1 GiB"] = {"bytes": big, "us": round(us, 3), "gbs": round(big / (us * 1e-6) / 1e9, 1)}
+    log(f"  stream read {big:>10d} B: {us:.2f} us/launch, {stream_ceiling['1 GiB']['gbs']} GB/s")
+    stream_ceiling["kernel"] = ("jk_measure_stream_read: 256-thread workgroups of 32 KB, eight coalesced 16-byte "
+                                "non-temporal loads per lane, nothing written")
+    del rd_buf
     dom = per_stage["ffn_gate_up"]
     traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic.get("ffn_gate_up"),
                 "kernel": "gemv_q8_fast_kernel<Q4_K> (ffn_gate + ffn_up, 2 x 14336x4096, f32 activation)",
                 "avg_launch_us": dom["us"], "bytes_per_launch": dom["bytes"],
+                "stream_read_us": dom["stream_read_us"], "frac_of_stream_read": dom["frac_of_stream_read"],
                 "traffic_source": os.path.relpath(TRAFFIC_FILE, REPO)}
 
     # ------------------------------------------------------------ prefill GEMM (Q8_0)
@@ -259,6 +318,7 @@ def main() -> int:
     # each token's output-row L2 norm -- the bar for f32 products; the reported
     # line) and bit-exact (jk_gemm_repacked: the reference's separately rounded epilogue).
     gemm, sweep, gemm_exact, sweep_exact = None, [], None, []
+    gemm_host = None
     s = torch.cuda.current_stream().cuda_stream
     ms_list = [args.gemm_m] if args.gemm_m > 0 else []
     ms_list += [int(v) for v in args.gemm_sweep.split(",") if v.strip() and args.gemm_m > 0]
@@ -269,6 +329,8 @@ def main() -> int:
         gw = [jk.Weight(jk.TensorView(f"ffn_gate.{i}", jk.Q8_0, (N, K), gdata), N, K) for i in range(ncopies)]
         for M in ms_list:
             gx = torch.randn(M, K, generator=gen).to(dev)
+            if M == args.gemm_m:
+                gemm_host = (gdata, gx.cpu().numpy(), M, N, K)
             need = jk.act_q8_bytes(M, K)
             gstore = torch.empty(need, dtype=torch.uint8, device=dev)
             act = jk.act_q8_bind(gstore, need, M, K)
@@ -300,10 +362,8 @@ def main() -> int:
                        "ms_per_call_incl_quantize": round(step_ms, 4)}
                 log(f"gemm Q8_0 M={M} {mode}: kernel {kern_us:.1f} us = {tops:.1f} TOPS "
                     f"({step_ms:.3f} ms/call incl. quantize)")
-                t128 = -(-N // 128) * -(-M // 128)  # 128 x 128 tolerance tiles (one per CU at least)
-                kname = (("gemm_q8_0_tol_dma_128 (128x128 tiles, LDS-bound loads)" if t128 >= 256
-                          else "gemm_repacked_kernel<Q8_0, tolerance>") if mode == "tolerance"
-                         else "gemm_repacked_kernel<Q8_0>")
+                kname = jk.gemm_plan(gw[0], act, 0, N, mode == "tolerance")  # the kernel this call launches
+                row["kernel"] = kname
                 line = {"workload": f"Q8_0 {N}x{K} weights x {M} tokens (QuantizedActQ8 per-32 activations), "
                                     + ("outputs within 1e-5 of each token's output-row L2 norm of the reference "
                                        "recipe (one fused multiply-add per scale group)" if mode == "tolerance"
@@ -332,6 +392,7 @@ def main() -> int:
     # a HIP graph and timed with HIP events on the capturing stream (per-launch time includes
     # the graph's inter-launch gap). Bytes are algorithmic (weight bytes + activation + output).
     secondary = {}
+    cpu_jobs = []  # (kind, line, ...): the same tensors and inputs, timed on the host by the CPU leg
     if not args.no_secondary and graph is not None:
         # The same step with ffn_down's input computed as in a Llama feed-forward block:
         # SwiGLU(gate, up) of the layer's own outputs, fused into the Q8_K quantizer.
@@ -354,32 +415,12 @@ def main() -> int:
                         + ("SwiGLU(gate, up) fused into its quantizer" if other == "swiglu" else "synthetic")}
         log(f"  decode step, ffn_down input {other}: {ms2:.4f} ms/step")
     if not args.no_secondary:
-        def graph_us(launch, n, reps=5):
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for i in range(n):
-                    launch(i, side.cuda_stream)
-            torch.cuda.current_stream().wait_stream(side)
-            torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                cs = torch.cuda.current_stream().cuda_stream
-                for i in range(n):
-                    launch(i, cs)
-            g.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(reps):
-                g.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            del g
-            return e0.elapsed_time(e1) * 1e3 / (reps * n)
+        def gus(launch, n, reps=5):
+            return graph_us(torch, launch, n, reps)
 
         def copies(quant, rows, cols, seed):
             data = synth.gguf_weights(quant, rows, cols, seed=seed)
+            copies.data = data
             n = max(4, int(600e6 // data.nbytes) + 1)
             return [jk.Weight(jk.TensorView(f"w{i}", quant, (rows, cols), data), rows, cols) for i in range(n)]
 
@@ -397,9 +438,10 @@ def main() -> int:
             xq = torch.empty(cols // 32 * jk.BLOCK_Q8_0.itemsize, dtype=torch.uint8, device=dev)
             jk.dev_quantize_row_q8_0(acts["x"], cols, xq, cols // 32)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
-            us = graph_us(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 32, y, rows, st), len(ws))
+            us = gus(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 32, y, rows, st), len(ws))
             b = gemv_bytes_q80(quant, rows, cols, jk)
             hbm_line(name, b, us, f"{rows}x{cols}, Q8_0 activation blocks")
+            cpu_jobs.append(("gemv", name, quant, rows, cols, copies.data, acts["x"].cpu().numpy(), b))
             for w in ws:
                 w.free()
         # Repacked GEMV (the m <= 2 route of the repacked GEMM, repack.rs:2892): one token's
@@ -416,7 +458,7 @@ def main() -> int:
             act1 = jk.act_q8_bind(store, need, 1, cols)
             jk.dev_quantize_act_q8(acts["x" if cols == 4096 else "h"], 1, cols, act1)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
-            us = graph_us(lambda i, st: jk.dev_gemv_repacked(ws[i % len(ws)], act1, y, rows, 0, rows, st), len(ws))
+            us = gus(lambda i, st: jk.dev_gemv_repacked(ws[i % len(ws)], act1, y, rows, 0, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + need + 4 * rows
             hbm_line(name, b, us, f"{rows}x{cols}, one token's QuantizedActQ8")
             for w in ws:
@@ -438,7 +480,7 @@ def main() -> int:
             else:
                 jk.dev_quantize_row_q8_k(xin, cols, xq, cols // 256)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
-            us = graph_us(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // be, y, rows, st), len(ws))
+            us = gus(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // be, y, rows, st), len(ws))
             b = (gemv_bytes_q80 if small else gemv_bytes)(quant, rows, cols, jk)
             hbm_line(name, b, us, f"{rows}x{cols}, {'Q8_0' if small else 'Q8_K'} activation blocks")
             for w in ws:
@@ -448,7 +490,7 @@ def main() -> int:
                                             ("vec_dot_q6_k f32", jk.Q6_K, 4096, 14336, "h")):
             ws = copies(quant, rows, cols, 600 + quant)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
-            us = graph_us(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts[xa], cols, y, rows, st), len(ws))
+            us = gus(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts[xa], cols, y, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + 4 * cols + 4 * rows
             hbm_line(name, b, us, f"{rows}x{cols}, f32 activation")
             for w in ws:
@@ -463,7 +505,7 @@ def main() -> int:
                     xin = torch.randn(cols, generator=gen).to(dev)
                     jk.dev_quantize_row_q8_k(xin, cols, xq, cols // 256)
                     y = torch.empty(rows, dtype=torch.float32, device=dev)
-                    us = graph_us(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 256, y, rows, st), len(ws))
+                    us = gus(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 256, y, rows, st), len(ws))
                     hbm_line(f"gemv_tq2_0_q8_k {rows}x{cols}", wbytes + cols // 256 * 292 + 4 * rows, us,
                              "C5, Q8_K activation blocks")
                 for m in (1, 128):
@@ -472,10 +514,13 @@ def main() -> int:
                     asc = torch.empty(m, dtype=torch.float32, device=dev)
                     jk.dev_quantize_absmax_i8(xin, m, cols, aq, asc)
                     y = torch.empty(m * rows, dtype=torch.float32, device=dev)
-                    us = graph_us(lambda i, st: jk.dev_bitlinear_i8(ws[i % len(ws)], aq, asc, m, cols, y, m * rows, st),
+                    us = gus(lambda i, st: jk.dev_bitlinear_i8(ws[i % len(ws)], aq, asc, m, cols, y, m * rows, st),
                                   len(ws))
                     b = wbytes + m * (cols + 4) + 4 * m * rows
                     name = f"bitlinear_{qname} {rows}x{cols} M={m}"
+                    if quant in (jk.TQ2_0, jk.I2_S):
+                        cpu_jobs.append(("bitlinear", name, quant, rows, cols, copies.data, aq.cpu().numpy(),
+                                         asc.cpu().numpy(), m, b))
                     if m == 1:
                         hbm_line(name, b, us, "C5, per-token absmax i8 activation")
                     else:
@@ -501,14 +546,14 @@ def main() -> int:
         for quant in (jk.Q4_0, jk.Q4_1, jk.Q5_0, jk.Q5_1, jk.IQ4_NL, jk.Q4_K, jk.Q5_K, jk.Q6_K, jk.Q2_K, jk.Q3_K,
                       jk.TQ1_0):
             ws = copies(quant, N, K, 900 + quant)
-            us = graph_us(lambda i, st: jk.dev_gemm_repacked(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
+            us = gus(lambda i, st: jk.dev_gemm_repacked(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
             tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
             name = f"gemm_repacked {jk.QUANT_NAMES[quant]} M=512"
             secondary[name] = {"us": round(us, 3), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                                "bound": "mfma", "workload": f"{N}x{K} weights x {M} tokens, kernel only"}
             log(f"  {name:28s} {us:8.2f} us  {tops:7.2f} TOPS")
             if quant in (jk.Q4_K, jk.Q6_K, jk.Q3_K):  # tolerance mode of the K-quant prefill formats
-                us = graph_us(lambda i, st: jk.dev_gemm_repacked_tol(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
+                us = gus(lambda i, st: jk.dev_gemm_repacked_tol(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
                 tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
                 name = f"gemm_repacked_tol {jk.QUANT_NAMES[quant]} M=512"
                 secondary[name] = {"us": round(us, 3), "tops": round(tops, 2),
@@ -524,7 +569,7 @@ def main() -> int:
             rows, cols = 4096, 4096
             ws = copies(quant, rows, cols, 950 + quant)
             y = torch.empty(rows, dtype=torch.float32, device=dev)
-            us = graph_us(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts["x"], cols, y, rows, st), len(ws))
+            us = gus(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts["x"], cols, y, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + 4 * cols + 4 * rows
             hbm_line(f"vec_dot_{jk.QUANT_NAMES[quant].lower()} f32", b, us, f"{rows}x{cols}, f32 activation")
             for w in ws:
@@ -539,7 +584,7 @@ def main() -> int:
         amw = torch.empty(jk.argmax_workspace_bytes(rows), dtype=torch.uint8, device=dev)
         idx = torch.empty(1, dtype=torch.int32, device=dev)
         b = gemv_bytes(jk.Q6_K, rows, cols, jk)
-        us = graph_us(lambda i, st: jk.dev_gemv_q8_argmax(ws_lm[i % len(ws_lm)], xq, None, cols // 256, None, idx, amw, st),
+        us = gus(lambda i, st: jk.dev_gemv_q8_argmax(ws_lm[i % len(ws_lm)], xq, None, cols // 256, None, idx, amw, st),
                       len(ws_lm))
         hbm_line("lm_head Q6_K gemv+argmax", b - 4 * rows, us, f"{rows}x{cols}, fused argmax, no logits written")
 
@@ -547,7 +592,7 @@ def main() -> int:
             jk.dev_gemv_q8(ws_lm[i % len(ws_lm)], xq, cols // 256, y, rows, st)
             jk.dev_argmax_f32(y, rows, idx, amw, st)
 
-        us = graph_us(two, len(ws_lm))
+        us = gus(two, len(ws_lm))
         hbm_line("lm_head Q6_K gemv, argmax", b + 4 * rows, us, f"{rows}x{cols}, logits written and re-read")
         for w in ws_lm:
             w.free()
@@ -622,7 +667,7 @@ def main() -> int:
         del hraw, hv
         # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
         yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
-        us = graph_us(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
+        us = gus(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
         secondary["quantize_row_q8_k 14336"] = {"us": round(us, 3), "bound": "latency",
                                                 "workload": "ffn_down input, 56 blocks"}
         log(f"  {'quantize_row_q8_k 14336':28s} {us:8.2f} us")
@@ -631,7 +676,7 @@ def main() -> int:
         need = jk.act_q8_bytes(M, K)
         store = torch.empty(need, dtype=torch.uint8, device=dev)
         act = jk.act_q8_bind(store, need, M, K)
-        us = graph_us(lambda i, st: jk.dev_quantize_act_q8(xin, M, K, act, st), 32)
+        us = gus(lambda i, st: jk.dev_quantize_act_q8(xin, M, K, act, st), 32)
         b = M * K * 4 + M * K + M * (K // 32) * 8
         hbm_line("quantize_act_q8 512x4096", b, us, "QuantizedActQ8::quantize_into for the prefill GEMM")
         del xin, store
@@ -698,6 +743,68 @@ def main() -> int:
                              f"{ncores} threads (row_range partitioning)"}
         log(f"cpu baseline, {ncores} threads: {cpu_all_gbs:.3f} GB/s ({reps} layer passes)")
 
+        # The same scalar restatement beside every other GPU figure: the prefill GEMM (TOPS over the
+        # 64-row x all-token slices done; the load-time repack is not timed, as in the reference,
+        # which repacks once), the C1 / C2 GEMVs and the C5 BitLinear lines. One thread, then the
+        # rows (GEMV, GEMM, one-token BitLinear) or tokens (128-token BitLinear) split over the cores.
+        def attach(target, unit, scale, one, alln, what):
+            (u1, el1, c1), (un, eln, cn) = one, alln
+            target["cpu_baseline"] = {"value": round(u1 / el1 / scale, 4), "unit": unit, "cores": 1, "kind": "port",
+                                      "sample": f"{c1} {what} in {el1:.1f} s, oracle C restatement of the scalar "
+                                                "fallback, -O3 -march=x86-64, 1 thread"}
+            target["cpu_baseline_all_cores"] = {"value": round(un / eln / scale, 4), "unit": unit, "cores": ncores,
+                                                "kind": "port", "sample": f"{cn} {what} in {eln:.1f} s on {ncores} threads"}
+            log(f"cpu baseline {unit}: {u1 / el1 / scale:.4g} (1 thread), {un / eln / scale:.4g} ({ncores} threads)")
+
+        if gemm_host is not None and (gemm is not None or gemm_exact is not None):
+            gd, gxh, M, N, K = gemm_host
+            q, sc, mn, cps = O.repack_logical(jk.Q8_0, (N, K), gd, N, K)
+            gact = O.ActQ8(gxh, M, K)
+            R = 64
+            sl = [(lambda r0=r0: O.gemm_logical_rows(q, sc, mn, cps, K, gact, 0, M, r0, min(N, r0 + R)),
+                   2.0 * M * (min(N, r0 + R) - r0) * K) for r0 in range(0, N, R)]
+            gsec = max(2.0, args.cpu_seconds)
+            res = (cpu_rate(sl, gsec, 1), cpu_rate(sl, max(1.0, gsec / 3), ncores))
+            for line in (gemm, gemm_exact):
+                if line is not None:
+                    attach(line, "TOPS", 1e12, *res, f"slices of {R} weight rows x {M} tokens of the same GEMM")
+            del q, sc, mn, gact
+        for job in cpu_jobs:
+            sec = secondary.get(job[1])
+            if sec is None:
+                continue
+            if job[0] == "gemv":
+                _, name, quant, rows, cols, data, xh, b = job
+                xb = O.quantize_row_q8_0(xh)
+                one = [(lambda: O.gemv_q8(quant, (rows, cols), data, xb, rows), b)]
+                step = -(-rows // ncores)
+                par = [(lambda r0=r0: O.gemv_rows(quant, data, rows, cols, xb, r0, min(rows, r0 + step)),
+                        b * (min(rows, r0 + step) - r0) / rows) for r0 in range(0, rows, step)]
+                attach(sec, "GB/s", 1e9, cpu_rate(one, 2.0, 1), cpu_rate(par, 1.0, ncores),
+                       f"GEMVs (or row slices) of the {rows}x{cols} matrix")
+            else:
+                _, name, quant, rows, cols, data, aqh, asch, m, b = job
+                ops = 2.0 * rows * cols
+                if m == 1:  # rows split over the cores: row-range views of the same tensor
+                    one = [(lambda: O.bitlinear_i8(quant, (rows, cols), data, aqh, float(asch[0]), rows), b)]
+                    rb = cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[quant]
+                    tail = data[rows * rb:]  # the I2_S tensor trailer (empty for TQ2_0)
+                    step = -(-rows // ncores)
+                    par = []
+                    for r0 in range(0, rows, step):
+                        r1 = min(rows, r0 + step)
+                        part = np.concatenate([data[r0 * rb:r1 * rb], tail])
+                        par.append((lambda part=part, n=r1 - r0: O.bitlinear_i8(quant, (n, cols), part, aqh,
+                                                                                float(asch[0]), n), b * (r1 - r0) / rows))
+                    attach(sec, "GB/s", 1e9, cpu_rate(one, 2.0, 1), cpu_rate(par, 1.0, ncores),
+                           f"one-token BitLinear products (or row slices) of the {rows}x{cols} matrix")
+                else:  # one token per call
+                    aq2 = aqh.reshape(m, cols)
+                    sl = [(lambda t=t: O.bitlinear_i8(quant, (rows, cols), data, aq2[t], float(asch[t]), rows), ops)
+                          for t in range(m)]
+                    attach(sec, "TOPS", 1e12, cpu_rate(sl, 2.0, 1), cpu_rate(sl, 1.0, ncores),
+                           f"tokens of the {m}-token BitLinear over the {rows}x{cols} matrix")
+
     rec = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
@@ -720,6 +827,32 @@ def main() -> int:
     }
     print(json.dumps(rec), flush=True)
     return 0
+
+
+def cpu_rate(slices, seconds, threads=1):
+    """Runs the (callable, work units) slices in order, cyclically, until `seconds` have
+    passed: one at a time on one thread, or `threads` at a time on a thread pool (ctypes
+    releases the GIL during each oracle call). Returns (units done, elapsed s, calls)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    done, calls, i = 0.0, 0, 0
+    t0 = time.perf_counter()
+    if threads == 1:
+        while True:
+            fn, u = slices[i % len(slices)]
+            fn()
+            done, calls, i = done + u, calls + 1, i + 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return done, el, calls
+    with ThreadPoolExecutor(threads) as ex:
+        while True:
+            batch = [slices[(i + j) % len(slices)] for j in range(threads)]
+            list(ex.map(lambda sl: sl[0](), batch))
+            done, calls, i = done + sum(u for _, u in batch), calls + threads, i + threads
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return done, el, calls
 
 
 def _cpu_model() -> str:

@@ -476,6 +476,25 @@ jk_status jk_host_convert_i2_s_blocks_to_tq2_0(const uint8_t *blk0, const uint8_
 jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view *w, const int8_t *act,
                                size_t act_len, float act_scale);
 
+/* ---------------------------------------------------------------- measurement */
+
+/* A plain streaming read of `bytes` (a non-zero multiple of 16, 16-byte aligned) of device
+ * memory: coalesced 16-byte non-temporal loads, one-shot 256-thread workgroups of 32 KB each,
+ * nothing written (sink is a 4-byte device word that is stored only if the xor of everything
+ * read equals a fixed constant). It is the ceiling the GEMV launches are measured against:
+ * the same byte count read once on the same launch path. No counterpart in the reference. */
+jk_status jk_measure_stream_read(jk_stream s, const void *buf, size_t bytes, uint32_t *sink);
+
+/* Which kernel a call would launch, as a static string in *kernel, found by running the
+ * launcher with the launch recorded instead of made (nothing is enqueued; the arguments are
+ * validated as the call itself validates them). jk_gemm_plan: jk_gemm_repacked (tolerance 0)
+ * or jk_gemm_repacked_tol (1) of `act` against rows [row_begin, row_end) of w (*kernel NULL
+ * for an empty range). jk_bitlinear_plan: jk_bitlinear_i8 of m tokens whose rows start at act.
+ * For tests and benchmarks; no counterpart in the reference. */
+jk_status jk_gemm_plan(const jk_weight *w, const jk_act_q8 *act, size_t row_begin, size_t row_end, int tolerance,
+                       const char **kernel);
+jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, const char **kernel);
+
 #ifdef __cplusplus
 }
 #endif

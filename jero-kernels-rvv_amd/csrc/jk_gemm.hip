@@ -1271,6 +1271,10 @@ static jk_status launch_gemv_repacked_q(hipStream_t s, const WeightDev &w, const
     constexpr size_t lds =
         kGemvNW * sizeof(GemmChunk<Q, 32, 16>) + 2 * 2 * kGemvNW * GemmFmt<Q>::NG * 32 * sizeof(float);
     static_assert(lds <= 160 * 1024, "GEMV LDS budget (160 KB per workgroup on gfx950)");
+    if (t_plan.dry) {
+        t_plan.kernel = "gemv_repacked_kernel";
+        return JK_OK;
+    }
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_repacked_kernel<Q>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return hip_fail(attr, "gemv_repacked_kernel LDS");
@@ -1498,7 +1502,8 @@ constexpr int kSplitkNW = 4;
 template <int Q, int TM, bool XV>
 static void launch_splitk_t(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     const size_t ntn = (size_t)(r1 - r0 + 31) / 32, ntm = (a.m + TM - 1) / TM;
-    hipLaunchKernelGGL((gemm_tol_splitk_kernel<Q, TM, kSplitkNW, XV>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+    JK_LAUNCH(TM == 32 ? "gemm_tol_splitk_kernel<32 tokens>" : "gemm_tol_splitk_kernel<64 tokens>",
+              (gemm_tol_splitk_kernel<Q, TM, kSplitkNW, XV>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
                        dim3(64 * kSplitkNW), 0, s, w, a, y, r0, r1);
 }
 
@@ -1718,7 +1723,7 @@ __global__ __launch_bounds__(64) void bitlinear_wave_kernel(WeightDev w, jk_act_
 template <int Q>
 static jk_status launch_bitlinear_wave(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y) {
     const size_t ntn = (size_t)(w.rows + 31) / 32, ntm = (a.m + 31) / 32;
-    hipLaunchKernelGGL(bitlinear_wave_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64), 0, s, w, a, y, 0,
+    JK_LAUNCH("bitlinear_wave_kernel", bitlinear_wave_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64), 0, s, w, a, y, 0,
                        w.rows);
     return check_launch("bitlinear_wave_kernel");
 }
@@ -1728,7 +1733,7 @@ constexpr int kBlockSplitkNW = 4;  // (8 waves measured slower on both 128-token
 template <int Q, int GB>
 static jk_status launch_block_splitk(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     const size_t ntn = (size_t)(r1 - r0 + 31) / 32, ntm = (a.m + 31) / 32;
-    hipLaunchKernelGGL((gemm_block_splitk_kernel<Q, GB, kBlockSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+    JK_LAUNCH("gemm_block_splitk_kernel", (gemm_block_splitk_kernel<Q, GB, kBlockSplitkNW>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
                        dim3(64 * kBlockSplitkNW), 0, s, w, a, y, r0, r1);
     return check_launch("gemm_block_splitk_kernel");
 }
@@ -1746,11 +1751,19 @@ static int gemm_tile(int quant, long rows, long m) {
     return 3;
 }
 
+static const char *tile_kernel_name(int tn, int tm, bool tol) {
+    if (tol) return tn == 32 ? "gemm_repacked_kernel<32x32, tolerance>" : "gemm_repacked_kernel<tolerance>";
+    if (tn == 128) return "gemm_repacked_kernel<128x64>";
+    if (tn == 64) return "gemm_repacked_kernel<64x64>";
+    return tm == 32 ? "gemm_repacked_kernel<32x32>" : "gemm_repacked_kernel<32x16>";
+}
+
 template <int Q, int GB, int TN, int TM, bool TOL = false>
 static void launch_tile(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     const size_t ntn = (size_t)(r1 - r0 + TN - 1) / TN, ntm = (a.m + TM - 1) / TM;
     const dim3 grid((unsigned)((ntn + 7) / 8 * 8 * ntm)), block(Tile<TN, TM>::THREADS);
-    hipLaunchKernelGGL((gemm_repacked_kernel<Q, GB, TN, TM, TOL>), grid, block, 0, s, w, a, y, r0, r1);
+    JK_LAUNCH(tile_kernel_name(TN, TM, TOL), (gemm_repacked_kernel<Q, GB, TN, TM, TOL>), grid, block, 0, s, w, a, y,
+              r0, r1);
 }
 
 template <int Q, int GB>
@@ -1764,7 +1777,7 @@ static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 
     default:
         if constexpr (GemmFmt<Q>::GK == 32) {
             const size_t ntn = (size_t)(r1 - r0 + 31) / 32, ntm = (a.m + 15) / 16;
-            hipLaunchKernelGGL((gemm16_kernel<Q, GB>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64), 0, s, w,
+            JK_LAUNCH("gemm16_kernel", (gemm16_kernel<Q, GB>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64), 0, s, w,
                                a, y, r0, r1);
         } else {
             launch_tile<Q, GB, 32, 32>(s, w, a, y, r0, r1);  // not chosen for 16-element groups
@@ -1792,7 +1805,7 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
             const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
             if (2 * t128 >= 3 * ncu && w.cols % 128 == 0) {
                 const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
-                hipLaunchKernelGGL(gemm_tol16_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
+                JK_LAUNCH("gemm_tol16_kernel", gemm_tol16_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
                                    a, y, r0, r1);
                 return check_launch("gemm_tol16_kernel");
             }
@@ -1815,11 +1828,11 @@ static jk_status launch_gemm_tol(hipStream_t s, const WeightDev &w, const jk_act
             const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
             if constexpr (Q == JK_Q8_0) {
                 // (256-row tiles, one workgroup per CU, measured slower at 512 and 2048 tokens)
-                hipLaunchKernelGGL(gemm_q8_0_tol_dma_128, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
+                JK_LAUNCH("gemm_q8_0_tol_dma_128", gemm_q8_0_tol_dma_128, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w,
                                    a, y, r0, r1);
                 return check_launch("gemm_q8_0_tol_dma");
             }
-            hipLaunchKernelGGL(gemm_tol_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w, a, y,
+            JK_LAUNCH("gemm_tol_kernel", gemm_tol_kernel<Q>, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(256), 0, s, w, a, y,
                                r0, r1);
             return check_launch("gemm_tol_kernel");
         }

@@ -466,9 +466,9 @@ static jk_status launch_bl_ternary(hipStream_t s, const WeightDev &w, const int8
                                    int m, float *y) {
     const dim3 grid((unsigned)((w.rows + RW - 1) / RW), (unsigned)m), block(16 * RW);
     const size_t lds = (size_t)w.nb * (kBlBE<Q> + 16) + (size_t)w.nb * 4;
-    if (w.nb <= 16) hipLaunchKernelGGL((bitlinear_ternary_kernel<Q, 1, RW>), grid, block, lds, s, w, act, act_scales, y);
-    else if (w.nb <= 32) hipLaunchKernelGGL((bitlinear_ternary_kernel<Q, 2, RW>), grid, block, lds, s, w, act, act_scales, y);
-    else hipLaunchKernelGGL((bitlinear_ternary_kernel<Q, 4, RW>), grid, block, lds, s, w, act, act_scales, y);
+    if (w.nb <= 16) JK_LAUNCH("bitlinear_ternary_kernel", (bitlinear_ternary_kernel<Q, 1, RW>), grid, block, lds, s, w, act, act_scales, y);
+    else if (w.nb <= 32) JK_LAUNCH("bitlinear_ternary_kernel", (bitlinear_ternary_kernel<Q, 2, RW>), grid, block, lds, s, w, act, act_scales, y);
+    else JK_LAUNCH("bitlinear_ternary_kernel", (bitlinear_ternary_kernel<Q, 4, RW>), grid, block, lds, s, w, act, act_scales, y);
     return check_launch("bitlinear_ternary_kernel");
 }
 
@@ -485,7 +485,7 @@ jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act,
         return narrow ? launch_bl_ternary<JK_I2_S, 4>(s, w, act, act_scales, m, y)
                       : launch_bl_ternary<JK_I2_S, 8>(s, w, act, act_scales, m, y);
     }
-    hipLaunchKernelGGL(bitlinear_kernel, dim3((unsigned)((w.rows + 15) / 16), (unsigned)m), dim3(256), 0, s, w, act,
+    JK_LAUNCH("bitlinear_kernel", bitlinear_kernel, dim3((unsigned)((w.rows + 15) / 16), (unsigned)m), dim3(256), 0, s, w, act,
                        act_scales, y);
     return check_launch("bitlinear_kernel");
 }

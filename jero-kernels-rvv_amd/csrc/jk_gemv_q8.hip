@@ -1001,9 +1001,9 @@ static jk_status launch_rp_fast_q(hipStream_t s, const WeightDev &w, const jk_ac
     const size_t mt = split ? 1 : a.m;
     const size_t lds = mt * rp_lds_row(Q, a.k_padded) + (Q == JK_Q4_K || Q == JK_Q5_K ? 2 : 1) * mt * a.k_blocks32 * sizeof(float);
     const dim3 grid((unsigned)((r1 - r0 + 4 * kRpNW - 1) / (4 * kRpNW)), split ? 2u : 1u), block(64 * kRpNW);
-    if (mt == 1) hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 1>), grid, block, lds, s, w, a, y, r0, r1);
+    if (mt == 1) JK_LAUNCH("gemv_repacked_fast_kernel<1 token>", (gemv_repacked_fast_kernel<Q, 1>), grid, block, lds, s, w, a, y, r0, r1);
     else if constexpr (Q != JK_Q6_K)
-        hipLaunchKernelGGL((gemv_repacked_fast_kernel<Q, 2>), grid, block, lds, s, w, a, y, r0, r1);
+        JK_LAUNCH("gemv_repacked_fast_kernel<2 tokens>", (gemv_repacked_fast_kernel<Q, 2>), grid, block, lds, s, w, a, y, r0, r1);
     return check_launch("gemv_repacked_fast_kernel");
 }
 

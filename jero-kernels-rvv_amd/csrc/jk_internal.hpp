@@ -182,6 +182,22 @@ jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, si
 // Checks the last kernel launch on the current thread.
 jk_status check_launch(const char *what);
 
+// Launch plans: with t_plan.dry set, the GEMM / BitLinear launchers record the kernel they
+// would launch (its name) instead of launching it. jk_gemm_plan / jk_bitlinear_plan use this
+// to report a shape's kernel, so tests and the bench can check which kernel a call runs.
+struct LaunchPlan {
+    bool dry = false;
+    const char *kernel = nullptr;
+};
+extern thread_local LaunchPlan t_plan;
+#define JK_LAUNCH(NAME, ...)                   \
+    do {                                       \
+        if (::jk::t_plan.dry)                  \
+            ::jk::t_plan.kernel = (NAME);      \
+        else                                   \
+            hipLaunchKernelGGL(__VA_ARGS__);   \
+    } while (0)
+
 // Kernel launchers (device tier internals). All arguments are validated by callers.
 // gguf_quant: the GGUF format of the staged payload (w.quant is its device layout).
 // Repacks GGUF rows [r0, r1) (gguf: exactly those rows' bytes, in device memory) into w's planes.

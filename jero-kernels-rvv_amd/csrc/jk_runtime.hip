@@ -70,6 +70,8 @@ jk_status hip_fail(hipError_t e, const char *what) {
 
 void clear_error() { g_err = ErrInfo(); }
 
+thread_local LaunchPlan t_plan;
+
 jk_status check_launch(const char *what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, what);
@@ -904,6 +906,24 @@ jk_status jk_gemv_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
     return jk_gemm_repacked(s, w, act, y, y_len, r0, r1);
 }
 
+// Which kernel a jk_gemm_repacked (tolerance = 0) or jk_gemm_repacked_tol (1) call with these
+// arguments launches: the launcher runs with its launch recorded instead of made.
+jk_status jk_gemm_plan(const jk_weight *w, const jk_act_q8 *act, size_t r0, size_t r1, int tolerance,
+                       const char **kernel) {
+    if (!kernel) return fail(JK_TENSOR_BOUNDS, "gemm_plan: null kernel");
+    *kernel = nullptr;
+    bool run;
+    float dummy;
+    JK_TRY(gemm_check(w, act, &dummy, act ? act->m * (r1 - r0) : 0, r0, r1, &run));
+    if (!run) return JK_OK;
+    t_plan = LaunchPlan{true, nullptr};
+    const jk_status st = tolerance ? launch_gemm_repacked_tol(nullptr, w->dev, *act, &dummy, (int)r0, (int)r1)
+                                   : launch_gemm_repacked(nullptr, w->dev, *act, &dummy, (int)r0, (int)r1);
+    *kernel = t_plan.kernel;
+    t_plan = LaunchPlan{};
+    return st;
+}
+
 // ---------------------------------------------------------------- BitLinear
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
                           size_t k, float *y, size_t y_len) {
@@ -920,6 +940,24 @@ jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, co
     // batches of tokens run as an int8-MFMA GEMM (same per-block arithmetic and block order)
     if (m >= (size_t)kBitlinearMfmaMinTokens) return launch_bitlinear_mfma((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
     return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
+}
+
+// Which kernel a jk_bitlinear_i8 call of m tokens on w launches, for activation rows at `act`
+// (their alignment can choose the kernel).
+jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, const char **kernel) {
+    if (!kernel) return fail(JK_TENSOR_BOUNDS, "bitlinear_plan: null kernel");
+    *kernel = nullptr;
+    JK_TRY(weight_usable(w, "bitlinear"));
+    if (!has_bitlinear(w->quant)) return fail(JK_CAPABILITY_MISMATCH, "bitlinear_plan: unsupported quant %d", w->quant);
+    if (m == 0 || m >= kMaxRows || !act) return fail(JK_TENSOR_BOUNDS, "bitlinear_plan: m=%zu", m);
+    float dummy;
+    t_plan = LaunchPlan{true, nullptr};
+    const jk_status st = m >= (size_t)kBitlinearMfmaMinTokens
+                             ? launch_bitlinear_mfma(nullptr, w->dev, act, &dummy, (int)m, &dummy)
+                             : launch_bitlinear(nullptr, w->dev, act, &dummy, (int)m, &dummy);
+    *kernel = t_plan.kernel;
+    t_plan = LaunchPlan{};
+    return st;
 }
 
 }  // extern "C"

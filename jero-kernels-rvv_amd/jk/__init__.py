@@ -736,3 +736,23 @@ def dev_gemv_q8_argmax_noalloc(w: Weight, x_q8, x_f32, x_len, y, index, stream=N
     """jk_gemv_q8_argmax with the argmax slots in the library's static device scratch."""
     _check(lib().jk_gemv_q8_argmax_noalloc(_vp(stream or 0), w.handle, _vp(_ptr(x_q8)), _vp(_ptr(x_f32)),
                                            _sz(x_len), _vp(_ptr(y)), _vp(_ptr(index))))
+
+
+def dev_measure_stream_read(buf, nbytes, sink, stream=None):
+    """jk_measure_stream_read: a plain streaming read of nbytes of device memory (the roofline
+    the GEMV launches are placed against)."""
+    _check(lib().jk_measure_stream_read(_vp(stream or 0), _vp(_ptr(buf)), _sz(nbytes), _vp(_ptr(sink))))
+
+
+def gemm_plan(w: Weight, act: ActQ8C, r0: int, r1: int, tolerance: bool) -> str | None:
+    """jk_gemm_plan: the kernel jk_gemm_repacked(_tol) launches for this activation and row range."""
+    k = C.c_char_p()
+    _check(lib().jk_gemm_plan(w.handle, C.byref(act), _sz(r0), _sz(r1), C.c_int(int(tolerance)), C.byref(k)))
+    return k.value.decode() if k.value else None
+
+
+def bitlinear_plan(w: Weight, act, m: int) -> str:
+    """jk_bitlinear_plan: the kernel jk_bitlinear_i8 launches for m tokens whose rows start at act."""
+    k = C.c_char_p()
+    _check(lib().jk_bitlinear_plan(w.handle, _vp(_ptr(act)), _sz(m), C.byref(k)))
+    return k.value.decode()

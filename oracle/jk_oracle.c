@@ -1222,7 +1222,41 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
 
 /* execute_gemm_repacked_rows (repack.rs:2718-3042) on the scalar arm with
  * tile_dot_scalar_rows (ime.rs:127-148) and accumulate_scaled_tile_scalar
- * (repack.rs:3045-3093): acc starts at 0.0 and adds one term per scale group in order. */
+ * (repack.rs:3045-3093), over weights already in the logical repacked form (the reference
+ * repacks once at load time, RepackedWeight::repack, repack.rs:2255): tokens [m0, m1) x rows
+ * [r0, r1), acc starts at 0.0 and adds one term per scale group in order. out is
+ * [m1 - m0][r1 - r0]. */
+int or_gemm_logical_rows(float *out, const int8_t *q, const float *sc, const float *mn, size_t cols, size_t sg,
+                         int cps, const or_act_q8 *act, size_t m0, size_t m1, size_t r0, size_t r1) {
+    if (act->k != cols || m0 > m1 || m1 > act->m || r0 > r1) return OR_TENSOR_BOUNDS;
+    size_t kp = (cols + 31) / 32 * 32, sub = r1 - r0;
+    size_t gl = 16 * (size_t)cps;
+    for (size_t i = m0; i < m1; i++) {
+        const int8_t *xq = act->qs + i * act->k_padded;
+        for (size_t r = r0; r < r1; r++) {
+            const int8_t *wq = q + r * kp;
+            float acc = 0.0f;
+            for (size_t g = 0; g < sg; g++) {
+                int32_t c = 0;
+                for (size_t k = g * gl; k < (g + 1) * gl; k++) c += xq[k] * wq[k];
+                size_t b32 = cps == 2 ? g : g / 2;
+                float xs = act->scales[i * act->k_blocks32 + b32];
+                float ws = sc[r * sg + g];
+                if (mn) {
+                    float xsm = cps == 2 ? act->sums[i * act->k_blocks32 + b32] : act->sums16[i * act->k_chunks + g];
+                    acc += (float)c * (xs * ws) - xsm * mn[r * sg + g];
+                } else {
+                    acc += (float)c * (xs * ws);
+                }
+            }
+            out[(i - m0) * sub + (r - r0)] = acc;
+        }
+    }
+    return OR_OK;
+}
+
+/* The same product from the GGUF bytes: repack (or_repack_logical) then or_gemm_logical_rows
+ * over every token. */
 int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t rows, size_t cols,
                      const or_act_q8 *act, size_t r0, size_t r1) {
     size_t sg;
@@ -1240,30 +1274,9 @@ int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t
     float *mn = has_mins ? malloc(rows * sg * sizeof(float)) : 0;
     if (!q || !sc || (has_mins && !mn)) { free(q); free(sc); free(mn); return OR_TENSOR_BOUNDS; }
     or_repack_logical(w, rows, cols, q, sc, mn, 0, 0, 0);
-    size_t gl = 16 * (size_t)cps;
-    for (size_t i = 0; i < m; i++) {
-        const int8_t *xq = act->qs + i * act->k_padded;
-        for (size_t r = r0; r < r1; r++) {
-            const int8_t *wq = q + r * kp;
-            float acc = 0.0f;
-            for (size_t g = 0; g < sg; g++) {
-                int32_t c = 0;
-                for (size_t k = g * gl; k < (g + 1) * gl; k++) c += xq[k] * wq[k];
-                size_t b32 = cps == 2 ? g : g / 2;
-                float xs = act->scales[i * act->k_blocks32 + b32];
-                float ws = sc[r * sg + g];
-                if (has_mins) {
-                    float xsm = cps == 2 ? act->sums[i * act->k_blocks32 + b32] : act->sums16[i * act->k_chunks + g];
-                    acc += (float)c * (xs * ws) - xsm * mn[r * sg + g];
-                } else {
-                    acc += (float)c * (xs * ws);
-                }
-            }
-            out[i * sub + (r - r0)] = acc;
-        }
-    }
+    st = or_gemm_logical_rows(out, q, sc, mn, cols, sg, cps, act, 0, m, r0, r1);
     free(q); free(sc); free(mn);
-    return OR_OK;
+    return st;
 }
 
 /* ------------------------------------------------------------------------- */

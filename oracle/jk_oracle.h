@@ -193,6 +193,11 @@ int or_repack_logical(const or_tensor_view *w, size_t rows, size_t cols, int8_t 
                       int *has_mins_out, int *chunks_per_scale_out);
 int or_gemm_repacked(float *out, size_t out_len, const or_tensor_view *w, size_t rows,
                      size_t cols, const or_act_q8 *act, size_t r0, size_t r1);
+/* The product over weights already repacked by or_repack_logical (q [rows][kp], scales and
+ * mins [rows][sg]; mins NULL for formats without): tokens [m0, m1) x rows [r0, r1) into out
+ * [m1 - m0][r1 - r0]. */
+int or_gemm_logical_rows(float *out, const int8_t *q, const float *sc, const float *mn, size_t cols, size_t sg,
+                         int cps, const or_act_q8 *act, size_t m0, size_t m1, size_t r0, size_t r1);
 /* PackedNibbleMatrix::gemm_rows (repack.rs:5181-5397): the compact 4-bit path for Q4_0, Q4_1,
  * IQ4_NL and Q4_K (packing, tile-scale decode and the host arm's tile dot and accumulation). */
 int or_nibble_gemm_rows(float *out, size_t out_len, const or_tensor_view *w, size_t rows, size_t cols,

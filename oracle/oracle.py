@@ -290,6 +290,17 @@ def gemm_repacked(quant: int, shape, data: np.ndarray, rows: int, cols: int, act
     return out.reshape(act.m, r1 - r0)
 
 
+def gemm_logical_rows(q: np.ndarray, sc: np.ndarray, mn, cps: int, cols: int, act: ActQ8, m0: int, m1: int,
+                      r0: int, r1: int) -> np.ndarray:
+    """Tokens [m0, m1) x rows [r0, r1) of the repacked GEMM over weights already repacked by
+    repack_logical (the reference repacks once at load time; the product is what a call costs)."""
+    out = np.zeros((m1 - m0) * (r1 - r0), dtype=np.float32)
+    _ok(lib().or_gemm_logical_rows(_p(out), _p(q), _p(sc), _p(mn) if mn is not None else None, _sz(cols),
+                                   _sz(sc.shape[1]), C.c_int(cps), C.byref(act.c), _sz(m0), _sz(m1), _sz(r0),
+                                   _sz(r1)), "gemm_logical_rows")
+    return out.reshape(m1 - m0, r1 - r0)
+
+
 def nibble_gemm_rows(quant: int, shape, data: np.ndarray, rows: int, cols: int, act: ActQ8, r0: int, r1: int):
     """PackedNibbleMatrix::gemm_rows restated (Q4_0, Q4_1, IQ4_NL, Q4_K)."""
     v = View(quant, shape, data)

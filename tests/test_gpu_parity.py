@@ -541,9 +541,14 @@ def test_gemm_tile_shapes(gpu, quant, m):
         assert same_bits(got[:, r0:r0 + 45], ref), (r0, mismatch(got[:, r0:r0 + 45], ref))
 
 
-def gpu_gemm_tol(torch, w, x, m, r0=0, r1=None):
+def gpu_gemm_tol(torch, w, x, m, r0=0, r1=None, expect=None):
+    """Tolerance-mode GEMM; with `expect`, first checks (jk_gemm_plan) that the call launches
+    that kernel, so a change of the launch rules cannot leave the test on another one."""
     r1 = w.rows if r1 is None else r1
     storage, act = gpu_act(torch, x, m, w.cols)
+    if expect is not None:
+        kernel = jk.gemm_plan(w, act, r0, r1, True)
+        assert kernel == expect, f"{m} tokens x rows {r0}..{r1} launch {kernel}, not {expect}"
     dy = empty(torch, 4 * m * (r1 - r0))
     jk.dev_gemm_repacked_tol(w, act, dy, m * (r1 - r0), r0, r1)
     torch.cuda.synchronize()
@@ -657,10 +662,11 @@ def test_gemm_tol_extreme_group_dots(gpu):
     """The 512-token tolerance tiles read each group's integer dot product out of a biased
     accumulator; its range must hold the largest |dot| a Q8_0 group can reach, 32 * 128 * 127 (-128
     weight quants against +-127 activation quants). Weights of +-128 / +127 quants with d = 1.0,
-    activations of +-1.0 (quants +-127), 8192 rows x 512 tokens (the 128 x 128 tiles): equal to the
-    bit-exact output within the tolerance, and the bit-exact output equal to the oracle."""
+    activations of +-1.0 (quants +-127), 14336 rows x 512 tokens (448 128 x 128 tiles, which the
+    launch plan confirms run gemm_q8_0_tol_dma_128): equal to the bit-exact output within the
+    tolerance, and the bit-exact output equal to the oracle."""
     torch = gpu
-    rows, cols, m = 8192, 256, 512
+    rows, cols, m = 14336, 256, 512
     blk = np.dtype([("d", "<f2"), ("qs", "i1", (32,))])
     w_blocks = np.zeros((rows, cols // 32), dtype=blk)
     w_blocks["d"] = 1.0
@@ -670,13 +676,67 @@ def test_gemm_tol_extreme_group_dots(gpu):
     x = np.where((np.arange(m) % 3 == 0)[:, None], -1.0, 1.0).astype(np.float32) * np.ones((m, cols), np.float32)
     w = jk.Weight(jk.TensorView("w", Q8_0, [rows, cols], raw), rows, cols)
     exact = gpu_gemm(torch, w, x, m)
-    tol = gpu_gemm_tol(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m, expect="gemm_q8_0_tol_dma_128")
     assert_within_row_norm(tol, exact)
     act = O.ActQ8(x, m, cols)
     ref = O.gemm_repacked(Q8_0, [rows, cols], raw, rows, cols, act, 4000, 4040)
     assert same_bits(exact[:, 4000:4040], ref)
     # every group dot is +-520192 or +-516128, i.e. -4096 / +4064 times 127; 8 groups per row
     assert np.allclose(exact[1, 0:2], [8 * -4096.0, 8 * 4064.0], rtol=1e-6)
+    w.free()
+
+
+TOL128_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S]
+
+
+@pytest.mark.parametrize("quant", TOL128_FORMATS)
+def test_gemm_tol_128_tiles(gpu, quant):
+    """Tolerance-mode 128 x 128 tiles of every 32-element-group format (gemm_tol_kernel; Q8_0 its
+    DMA variant): 14300 rows x 500 tokens is 448 tiles, above the launch's 1.5 tiles per CU, with a
+    partial last row tile and a partial last token tile; weights with special scales. Within 1e-5
+    of each token's output-row L2 norm of the bit-exact GPU output over the whole matrix and of
+    the oracle on two row windows (the first tile and the partial last one); a row slice within
+    the same bar."""
+    torch = gpu
+    rows, cols, m = 14300, 512, 500
+    raw = synth.random_weights(quant, rows, cols, seed=91 + quant, specials=True)
+    x = np.random.default_rng(92 + quant).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    expect = "gemm_q8_0_tol_dma_128" if quant == Q8_0 else "gemm_tol_kernel"
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m, expect=expect)
+    worst = assert_within_row_norm(tol, exact)
+    act = O.ActQ8(x, m, cols)
+    norms = np.linalg.norm(exact.astype(np.float64), axis=1)
+    for r0, r1 in ((0, 40), (14260, 14300)):
+        ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, act, r0, r1)
+        assert same_bits(exact[:, r0:r1], ref), (r0, mismatch(exact[:, r0:r1], ref))
+        assert np.all(np.abs(tol[:, r0:r1] - ref).max(axis=1) <= 1e-5 * norms)
+    assert_within_row_norm(gpu_gemm_tol(torch, w, x, m, 3, rows - 5), exact[:, 3:rows - 5])
+    print(f"gemm tol {quant} 14300x512 M=500 on {expect}: worst error / row norm {worst:.2e}")
+    w.free()
+
+
+@pytest.mark.parametrize("quant", [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL])
+@pytest.mark.parametrize("m,rows", [(64, 8200), (17, 16400)])
+def test_gemm_tol_32x32_tiles_partial_chunk(gpu, quant, m, rows):
+    """Tolerance-mode 32 x 32 tiles (gemm_repacked_kernel<32x32, tolerance>), the launch for K
+    that is not a whole number of 128-element chunks (here 160: five 32-element groups) where the
+    32 x 32 tiles give every CU two workgroups: 64 and 17 tokens (partial token tiles), a partial
+    last row tile, weights with special scales. Within 1e-5 of each token's output-row L2 norm of
+    the bit-exact GPU output and of the oracle on a row window."""
+    torch = gpu
+    cols = 160
+    raw = synth.random_weights(quant, rows, cols, seed=m + rows + quant, specials=True)
+    x = np.random.default_rng(m + quant).standard_normal((m, cols)).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m, expect="gemm_repacked_kernel<32x32, tolerance>")
+    assert_within_row_norm(tol, exact)
+    ref = O.gemm_repacked(quant, [rows, cols], raw, rows, cols, O.ActQ8(x, m, cols), rows - 50, rows)
+    assert same_bits(exact[:, rows - 50:], ref)
+    norms = np.linalg.norm(exact.astype(np.float64), axis=1)
+    assert np.all(np.abs(tol[:, rows - 50:] - ref).max(axis=1) <= 1e-5 * norms)
     w.free()
 
 
