@@ -384,6 +384,16 @@ jk_status jk_gemv_q8_argmax_noalloc(jk_stream s, const jk_weight *w, const void 
  * and one f32 scale per token (TQ1_0, TQ2_0, I2_S and Q8_0 weights). */
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act,
                           const float *act_scales, size_t m, size_t k, float *y, size_t y_len);
+/* bitlinear_i8_rvv (ime.rs:882-938) for m tokens in tolerance mode: the same arguments,
+ * validation and errors as jk_bitlinear_i8, with the per-block addends summed in any order --
+ * every output within 1e-5 of its token's output-row L2 norm of the reference's block-order
+ * sum. From 16 tokens on, TQ2_0 / TQ1_0 / I2_S weights with 16-byte aligned activation rows run
+ * K split over the waves of a workgroup: I2_S sums the whole row in exact integers and rounds
+ * once (f32(sum) * (scale * act_scale)), TQ2_0 adds one fused multiply-add per 256-element
+ * block. Other cases run the bit-exact kernels. No reference function has this rounding: it is
+ * the bit-exact call's alternative, as jk_gemm_repacked_tol is jk_gemm_repacked's. */
+jk_status jk_bitlinear_i8_tol(jk_stream s, const jk_weight *w, const int8_t *act,
+                              const float *act_scales, size_t m, size_t k, float *y, size_t y_len);
 
 /* convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790) on the device over a run of block pairs: TQ2_0
  * block k (66 bytes, crate layout: the f16 scale bits, then 64 bytes of 2-bit fields t + 1) holds
@@ -489,11 +499,12 @@ jk_status jk_measure_stream_read(jk_stream s, const void *buf, size_t bytes, uin
  * launcher with the launch recorded instead of made (nothing is enqueued; the arguments are
  * validated as the call itself validates them). jk_gemm_plan: jk_gemm_repacked (tolerance 0)
  * or jk_gemm_repacked_tol (1) of `act` against rows [row_begin, row_end) of w (*kernel NULL
- * for an empty range). jk_bitlinear_plan: jk_bitlinear_i8 of m tokens whose rows start at act.
+ * for an empty range). jk_bitlinear_plan: jk_bitlinear_i8 (tolerance 0) or jk_bitlinear_i8_tol (1)
+ * of m tokens whose rows start at act.
  * For tests and benchmarks; no counterpart in the reference. */
 jk_status jk_gemm_plan(const jk_weight *w, const jk_act_q8 *act, size_t row_begin, size_t row_end, int tolerance,
                        const char **kernel);
-jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, const char **kernel);
+jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, int tolerance, const char **kernel);
 
 #ifdef __cplusplus
 }

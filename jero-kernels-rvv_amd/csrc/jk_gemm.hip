@@ -1728,6 +1728,210 @@ static jk_status launch_bitlinear_wave(hipStream_t s, const WeightDev &w, const 
     return check_launch("bitlinear_wave_kernel");
 }
 
+// Tolerance-mode BitLinear token batches (jk_bitlinear_i8_tol). The order of the per-block
+// addends is free here, so K is split over the waves of a workgroup: a workgroup owns 32 RT
+// weight rows x 32 tokens with RT x KS waves; wave (rt, kq) computes rows 32 rt .. of the tile
+// over the weight blocks kq, kq + KS, ... (at most MB of them), and the KS partial tiles of each
+// row sub-tile are added through LDS at the end.
+//  - Weights: the row's plane bytes straight into registers, unpacked per step as in
+//    bitlinear_wave_kernel: I2_S (16 bytes a block) all of a wave's blocks at the start, TQ2_0
+//    (64 bytes a block) one round ahead, which keeps it at 128 VGPRs or fewer.
+//  - Activations: one round ahead. In round r the workgroup stages block kq + KS r of every K
+//    slice kq for its 32 tokens in LDS (the RT waves of a slice share the slab and load a share of
+//    it each), coalesced -- consecutive lanes read one token's contiguous bytes, so a load
+//    instruction touches 4 (TQ2_0) or 8 (I2_S) cache lines instead of one line per lane -- with
+//    the 16-byte piece p of token t at slot p ^ (t % (BE / 16)), so the 32 tokens of an MFMA
+//    operand read fall on distinct banks in each group of 16 lanes. Two slab buffers; one barrier
+//    per round (with one row sub-tile the slab is the wave's own, and a wave-level sync does).
+//  - I2_S: every block shares the tensor scale, so a wave's dot over all its blocks accumulates
+//    in the MFMA's i32 accumulator and the partials add in i32: the whole K sum is exact
+//    (|sum| <= 128 K) and converted once, y = f32(sum) * (ts * xs). TQ2_0: one fused
+//    multiply-add per block, acc = fma(f32(dot), d, acc) (d is the lane's row's block scale), and
+//    the token's scale once at the end, y = acc * xs.
+// Within 1e-5 of each token's output-row L2 norm of the reference's per-block order
+// (ime.rs:882-938).
+template <int Q> struct BlTolRegs {
+    u32x4 w[Q == JK_TQ2_0 ? 4 : 1];  // TQ2_0: the block's four planes of row jl; I2_S: plane hl
+    uint32_t d;                      // TQ2_0: the block's f16 scale
+};
+// blocks of weights a wave holds in registers
+template <int Q> constexpr int kBlTolMaxBlocks = Q == JK_TQ2_0 ? 4 : 8;
+
+template <int Q, int RT, int KS>
+__global__ __launch_bounds__(64 * RT * KS) void bitlinear_tol_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y) {
+    static_assert(Q == JK_TQ2_0 || Q == JK_I2_S, "ternary formats");
+    constexpr int GB = Q == JK_TQ2_0 ? 8 : 4, BE = 32 * GB;  // steps and elements (bytes) per weight block
+    constexpr int PR = BE / 16;                              // 16-byte pieces per token and block
+    constexpr int XL = BE / 32 / RT;                         // pieces per lane: a slab is shared by RT waves
+    static_assert(XL >= 1, "slab pieces per lane");
+    constexpr int MB = kBlTolMaxBlocks<Q>;
+    constexpr bool EXACT = Q == JK_I2_S;  // the partials are exact i32 sums
+    constexpr int NW = RT * KS;
+    union Smem {
+        uint8_t x[2][KS][32 * BE];  // [round parity][K slice]: the block's 32 token rows, swizzled
+        float part[NW][32][33];     // after the loop: [wave][token][row] (I2_S: i32 bits)
+    };
+    __shared__ __align__(16) Smem sm;
+    const int lane = threadIdx.x & 63, hl = lane >> 5, jl = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int rt = wave % RT, kq = wave / RT;  // row sub-tile, K slice
+    const int ntn = (w.rows + 32 * RT - 1) / (32 * RT), ntm = ((int)a.m + 31) / 32;
+    const int wg = (int)blockIdx.x, local = wg >> 3;
+    const int tn = (local / ntm) * 8 + (wg & 7), tm = local % ntm;
+    if (tn >= ntn) return;  // workgroup-uniform: the whole workgroup leaves before the barriers
+    const int n0 = 32 * RT * tn + 32 * rt, m0 = 32 * tm, M = (int)a.m, nb = w.nb;
+    const int row = min(n0 + jl, w.rows - 1);
+    const int rounds = (nb + KS - 1) / KS;  // <= MB (the launcher's choice of KS)
+    // every block of this wave's share into registers (past the last block a valid block is
+    // re-read and not used)
+    constexpr int NP = Q == JK_TQ2_0 ? 4 : 1;
+    constexpr bool PRE = Q == JK_I2_S;  // all blocks' weights at the start (TQ2_0: one round ahead)
+    BlTolRegs<Q> W[PRE ? MB : 2];
+    const uint8_t *pbase[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) pbase[p] = plane_ptr(w, Q == JK_TQ2_0 ? p : hl, row, 0);
+    const uint16_t *dbase = Q == JK_TQ2_0 ? w.dplane + (size_t)row * (size_t)nb : nullptr;
+    auto wload = [&](BlTolRegs<Q> &R, int r) {
+        const int b = min(kq + KS * r, nb - 1);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) R.w[p] = *reinterpret_cast<const u32x4 *>(pbase[p] + 16 * b);
+        if constexpr (Q == JK_TQ2_0) R.d = dbase[b];
+    };
+    if constexpr (PRE) {
+#pragma unroll
+        for (int r = 0; r < MB; ++r) wload(W[r], r);
+    } else {
+        wload(W[0], 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's share of its K slice's slab: piece f = 64 (RT i + rt) + lane is piece f % PR of
+    // token f / PR
+    const uint8_t *xsrc[XL];
+    int xdst[XL];
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+        const int f = 64 * (RT * i + rt) + lane, t = f / PR, p = f % PR;
+        xsrc[i] = reinterpret_cast<const uint8_t *>(a.qs) + (size_t)min(m0 + t, M - 1) * a.k_padded + 16 * p;
+        xdst[i] = t * BE + 16 * (p ^ (t & (PR - 1)));
+    }
+    u32x4 xr[XL];
+    auto xload = [&](int r) {
+        const int b = min(kq + KS * r, nb - 1);
+#pragma unroll
+        for (int i = 0; i < XL; ++i) xr[i] = *reinterpret_cast<const u32x4 *>(xsrc[i] + (size_t)b * BE);
+    };
+    v16i cacc = v16i{0};  // I2_S: the wave's i32 dot over all its blocks
+    float acc[16];        // TQ2_0: sum of f32(dot) * d over the wave's blocks
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    xload(0);
+    // round r: this wave's share of the slab (in xr) into buffer r % 2, barrier, the next round's
+    // activation loads, then the block. The buffer written in round r was last read in round
+    // r - 2, before every wave passed round r - 1's barrier.
+#pragma unroll
+    for (int r = 0; r < MB; ++r) {
+        if (r >= rounds) break;  // workgroup-uniform
+        uint8_t *xs = sm.x[r & 1][kq];
+#pragma unroll
+        for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4 *>(xs + xdst[i]) = xr[i];
+        if constexpr (RT == 1) wave_lds_sync();  // the slab is this wave's own
+        else lds_barrier();
+        xload(r + 1);
+        if constexpr (!PRE) wload(W[(r + 1) & 1], r + 1);
+        __builtin_amdgcn_sched_barrier(0);  // (left to itself the compiler sinks the loads below the MFMAs)
+        const BlTolRegs<Q> &Wr = W[PRE ? r : r & 1];
+        v16i c = EXACT ? cacc : v16i{0};
+#pragma unroll
+        for (int st = 0; st < GB; ++st) {
+            const int pc = 2 * st + hl;
+            const v4i xq = *reinterpret_cast<const v4i *>(xs + jl * BE + 16 * (pc ^ (jl & (PR - 1))));
+            u32x4 wq;
+            if constexpr (Q == JK_TQ2_0) {
+                const uint32_t wv = Wr.w[2 * (st >> 2) + ((st & 3) >> 1)][2 * (st & 1) + hl];
+                wq = u32x4{crumbs_minus1(wv & 0x03030303u), crumbs_minus1((wv >> 2) & 0x03030303u),
+                           crumbs_minus1((wv >> 4) & 0x03030303u), crumbs_minus1((wv >> 6) & 0x03030303u)};
+            } else {
+                const int sh = 6 - 2 * st;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) wq[k] = crumbs_minus1((Wr.w[0][k] >> sh) & 0x03030303u);
+            }
+            c = __builtin_amdgcn_mfma_i32_32x32x32_i8(xq, __builtin_bit_cast(v4i, wq), c, 0, 0, 0);
+        }
+        if (kq + KS * r < nb) {  // wave-uniform: false for a repeated block past this slice's last one
+            if constexpr (EXACT) {
+                cacc = c;
+            } else {
+                const float d = f16_finite(Wr.d);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[v] = __builtin_fmaf((float)c[v], d, acc[v]);
+            }
+        }
+    }
+    __syncthreads();  // every wave done with the slabs before the partials overwrite them
+    // lane holds row jl of tokens 8 (v / 4) + 4 hl + v % 4 of its sub-tile
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        sm.part[wave][8 * (v >> 2) + 4 * hl + (v & 3)][jl] = EXACT ? __int_as_float(cacc[v]) : acc[v];
+    __syncthreads();
+    const size_t ld = (size_t)w.rows;
+    const int nbase = 32 * RT * tn;
+    for (int o = (int)threadIdx.x; o < RT * 32 * 32; o += 64 * NW) {
+        const int sub = o >> 10, t = (o >> 5) & 31, rr = o & 31, n = nbase + 32 * sub + rr;
+        if (m0 + t >= M || n >= w.rows) continue;
+        const float xsc = a.scales[(size_t)(m0 + t) * a.k_blocks32];  // the token's scale (k_blocks32 = 1)
+        float out;
+        if constexpr (EXACT) {
+            int sum = 0;
+#pragma unroll
+            for (int v = 0; v < KS; ++v) sum += __float_as_int(sm.part[RT * v + sub][t][rr]);
+            out = (float)sum * (w.tensor_scale * xsc);
+        } else {
+            float sum = 0.0f;
+#pragma unroll
+            for (int v = 0; v < KS; ++v) sum += sm.part[RT * v + sub][t][rr];
+            out = sum * xsc;
+        }
+        y[(size_t)(m0 + t) * ld + (size_t)n] = out;
+    }
+}
+
+template <int Q, int RT, int KS>
+static void launch_bl_tol_t(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, const char *name) {
+    const size_t ntn = (size_t)(w.rows + 32 * RT - 1) / (32 * RT), ntm = (a.m + 31) / 32;
+    JK_LAUNCH(name, (bitlinear_tol_kernel<Q, RT, KS>), dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)), dim3(64 * RT * KS), 0,
+              s, w, a, y);
+}
+
+// K split over the fewest waves (2, 4 or 8) that leaves each at most kBlTolMaxBlocks blocks (K up
+// to 8192);
+// 64-row tiles (two row sub-tiles sharing each activation slab) where those give every CU a
+// workgroup, 32-row tiles below. (false: K too long for 8 waves; the caller runs the bit-exact
+// launch.)
+template <int Q>
+static bool launch_bitlinear_tol(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y) {
+    constexpr int MB = kBlTolMaxBlocks<Q>;
+    const int nb = w.nb;
+    const bool rt2 = (long)((w.rows + 63) / 64) * (long)((a.m + 31) / 32) >= cu_count();
+    if (nb <= 2 * MB) {
+        if (rt2) launch_bl_tol_t<Q, 2, 2>(s, w, a, y, "bitlinear_tol_kernel<2x2 waves>");
+        else launch_bl_tol_t<Q, 1, 2>(s, w, a, y, "bitlinear_tol_kernel<1x2 waves>");
+    } else if (nb <= 4 * MB) {
+        if (rt2) launch_bl_tol_t<Q, 2, 4>(s, w, a, y, "bitlinear_tol_kernel<2x4 waves>");
+        else launch_bl_tol_t<Q, 1, 4>(s, w, a, y, "bitlinear_tol_kernel<1x4 waves>");
+    } else if (nb <= 8 * MB) {
+        // (TQ2_0 on 16 waves would spill)
+        if constexpr (Q == JK_I2_S) {
+            if (rt2) launch_bl_tol_t<Q, 2, 8>(s, w, a, y, "bitlinear_tol_kernel<2x8 waves>");
+            else launch_bl_tol_t<Q, 1, 8>(s, w, a, y, "bitlinear_tol_kernel<1x8 waves>");
+        } else {
+            launch_bl_tol_t<Q, 1, 8>(s, w, a, y, "bitlinear_tol_kernel<1x8 waves>");
+        }
+    } else {  // (16 waves would spill: 1024 threads leave 128 VGPRs a lane)
+        return false;
+    }
+    return true;
+}
+
 constexpr int kBlockSplitkNW = 4;  // (8 waves measured slower on both 128-token BitLinear shapes)
 
 template <int Q, int GB>
@@ -1896,6 +2100,26 @@ jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t 
     case JK_Q8_0: return launch_gemm<JK_Q8_0, 1>(s, w, a, y, 0, w.rows);
     default: return fail(JK_CAPABILITY_MISMATCH, "bitlinear: unsupported quant %d", w.quant);
     }
+}
+
+// Tolerance mode of the token-batch BitLinear: the K-split kernel above for TQ2_0 / I2_S with
+// 16-byte aligned activation rows and K up to 16 waves' register blocks; otherwise (Q8_0,
+// unaligned rows, longer K) the bit-exact launch, whose results meet the tolerance by definition.
+jk_status launch_bitlinear_mfma_tol(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales,
+                                    int m, float *y) {
+    if ((w.quant != JK_TQ2_0 && w.quant != JK_I2_S) || (uintptr_t)act % 16 != 0)
+        return launch_bitlinear_mfma(s, w, act, act_scales, m, y);
+    jk_act_q8 a;
+    memset(&a, 0, sizeof a);
+    a.m = (size_t)m;
+    a.k = a.k_padded = (size_t)w.cols;
+    a.k_blocks32 = 1;
+    a.qs = const_cast<int8_t *>(act);
+    a.scales = const_cast<float *>(act_scales);
+    const bool done = w.quant == JK_TQ2_0 ? launch_bitlinear_tol<JK_TQ2_0>(s, w, a, y)
+                                          : launch_bitlinear_tol<JK_I2_S>(s, w, a, y);
+    if (!done) return launch_bitlinear_mfma(s, w, act, act_scales, m, y);
+    return check_launch("bitlinear_tol_kernel");
 }
 
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {

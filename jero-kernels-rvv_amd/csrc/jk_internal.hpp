@@ -239,6 +239,9 @@ jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, 
 constexpr int kBitlinearMfmaMinTokens = 16;
 jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales, int m,
                                 float *y);
+// The same products within 1e-5 of each token's output-row L2 norm, K split over waves.
+jk_status launch_bitlinear_mfma_tol(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales,
+                                    int m, float *y);
 jk_status launch_bitlinear(hipStream_t s, const WeightDev &w, const int8_t *act,
                            const float *act_scales, int m, float *y);
 jk_status launch_gemm_repacked(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y,

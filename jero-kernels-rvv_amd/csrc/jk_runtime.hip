@@ -925,11 +925,11 @@ jk_status jk_gemm_plan(const jk_weight *w, const jk_act_q8 *act, size_t r0, size
 }
 
 // ---------------------------------------------------------------- BitLinear
-jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
-                          size_t k, float *y, size_t y_len) {
+// validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
+static jk_status bitlinear_check(const jk_weight *w, const int8_t *act, const float *act_scales, size_t m, size_t k,
+                                 const float *y, size_t y_len) {
     JK_TRY(weight_usable(w, "bitlinear"));
-    int q = w->quant;
-    // validate_bitlinear_dimensions (ime.rs:660-684): other formats are a TensorBoundsError
+    const int q = w->quant;
     const Tb wt{w->name.c_str(), w->offset, w->gguf_bytes, w->gguf_bytes};
     if (!has_bitlinear(q)) return fail_tb(wt, "%s: bitlinear: unsupported quant type %s", wt.name, quant_name(q));
     if (m == 0 || k != (size_t)w->dev.cols || y_len != m * (size_t)w->dev.rows)
@@ -937,14 +937,28 @@ jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, co
                        w->dev.cols, m, k, y_len);
     if (m >= kMaxRows) return fail(JK_TENSOR_BOUNDS, "bitlinear: m=%zu too large", m);
     if (!act || !act_scales || !y) return fail(JK_TENSOR_BOUNDS, "bitlinear: null pointer");
+    return JK_OK;
+}
+
+jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
+                          size_t k, float *y, size_t y_len) {
+    JK_TRY(bitlinear_check(w, act, act_scales, m, k, y, y_len));
     // batches of tokens run as an int8-MFMA GEMM (same per-block arithmetic and block order)
     if (m >= (size_t)kBitlinearMfmaMinTokens) return launch_bitlinear_mfma((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
     return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
 }
 
-// Which kernel a jk_bitlinear_i8 call of m tokens on w launches, for activation rows at `act`
-// (their alignment can choose the kernel).
-jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, const char **kernel) {
+jk_status jk_bitlinear_i8_tol(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
+                              size_t k, float *y, size_t y_len) {
+    JK_TRY(bitlinear_check(w, act, act_scales, m, k, y, y_len));
+    if (m >= (size_t)kBitlinearMfmaMinTokens)
+        return launch_bitlinear_mfma_tol((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
+    return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);  // bit-exact rows
+}
+
+// Which kernel a jk_bitlinear_i8 (tolerance 0) or jk_bitlinear_i8_tol (1) call of m tokens on w
+// launches, for activation rows at `act` (their alignment can choose the kernel).
+jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, int tolerance, const char **kernel) {
     if (!kernel) return fail(JK_TENSOR_BOUNDS, "bitlinear_plan: null kernel");
     *kernel = nullptr;
     JK_TRY(weight_usable(w, "bitlinear"));
@@ -952,9 +966,10 @@ jk_status jk_bitlinear_plan(const jk_weight *w, const int8_t *act, size_t m, con
     if (m == 0 || m >= kMaxRows || !act) return fail(JK_TENSOR_BOUNDS, "bitlinear_plan: m=%zu", m);
     float dummy;
     t_plan = LaunchPlan{true, nullptr};
-    const jk_status st = m >= (size_t)kBitlinearMfmaMinTokens
-                             ? launch_bitlinear_mfma(nullptr, w->dev, act, &dummy, (int)m, &dummy)
-                             : launch_bitlinear(nullptr, w->dev, act, &dummy, (int)m, &dummy);
+    jk_status st;
+    if (m < (size_t)kBitlinearMfmaMinTokens) st = launch_bitlinear(nullptr, w->dev, act, &dummy, (int)m, &dummy);
+    else if (tolerance) st = launch_bitlinear_mfma_tol(nullptr, w->dev, act, &dummy, (int)m, &dummy);
+    else st = launch_bitlinear_mfma(nullptr, w->dev, act, &dummy, (int)m, &dummy);
     *kernel = t_plan.kernel;
     t_plan = LaunchPlan{};
     return st;

@@ -655,6 +655,12 @@ def dev_bitlinear_i8(w: Weight, act, act_scales, m, k, y, y_len, stream=None):
                                  _vp(_ptr(y)), _sz(y_len)))
 
 
+def dev_bitlinear_i8_tol(w: Weight, act, act_scales, m, k, y, y_len, stream=None):
+    """jk_bitlinear_i8_tol: BitLinear within 1e-5 of each token's output-row L2 norm (sums in any order)."""
+    _check(lib().jk_bitlinear_i8_tol(_vp(stream or 0), w.handle, _vp(_ptr(act)), _vp(_ptr(act_scales)), _sz(m),
+                                     _sz(k), _vp(_ptr(y)), _sz(y_len)))
+
+
 def dev_dequantize_rows(w: Weight, r0, r1, out, out_len, stream=None):
     _check(lib().jk_weight_dequantize_rows(_vp(stream or 0), w.handle, _sz(r0), _sz(r1), _vp(_ptr(out)),
                                            _sz(out_len)))
@@ -751,8 +757,8 @@ def gemm_plan(w: Weight, act: ActQ8C, r0: int, r1: int, tolerance: bool) -> str 
     return k.value.decode() if k.value else None
 
 
-def bitlinear_plan(w: Weight, act, m: int) -> str:
-    """jk_bitlinear_plan: the kernel jk_bitlinear_i8 launches for m tokens whose rows start at act."""
+def bitlinear_plan(w: Weight, act, m: int, tolerance: bool = False) -> str:
+    """jk_bitlinear_plan: the kernel jk_bitlinear_i8(_tol) launches for m tokens whose rows start at act."""
     k = C.c_char_p()
-    _check(lib().jk_bitlinear_plan(w.handle, _vp(_ptr(act)), _sz(m), C.byref(k)))
+    _check(lib().jk_bitlinear_plan(w.handle, _vp(_ptr(act)), _sz(m), C.c_int(int(tolerance)), C.byref(k)))
     return k.value.decode()

@@ -794,6 +794,69 @@ def test_bitlinear(gpu, quant, m, rows, cols):
         assert same_bits(got[i], ref), (i, mismatch(got[i], ref))
 
 
+@pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S, Q8_0])
+@pytest.mark.parametrize("m,rows,cols,offset", [(3, 64, 2560, 0), (16, 300, 2560, 0), (37, 129, 768, 0),
+                                                (50, 40, 256, 0),  # fewer blocks than waves
+                                                (20, 33, 512, 1),  # activation rows not 16-byte aligned
+                                                (128, 2560, 6912, 0), (128, 6912, 2560, 0),
+                                                (16, 40, 8448, 0)])  # K beyond the split kernel
+def test_bitlinear_tol(gpu, quant, m, rows, cols, offset):
+    """Tolerance-mode BitLinear (jk_bitlinear_i8_tol): every output within 1e-5 of its token's
+    output-row L2 norm of the bit-exact GPU result over the whole matrix and of the oracle on
+    the first and last tokens; the launch plan confirms that TQ2_0 / TQ1_0 / I2_S token batches
+    with aligned rows and K up to 8192 run the K-split kernel (2 to 8 waves; longer K and the
+    other cases the bit-exact launch), with weights with special scales and I2_S with a random
+    tensor scale."""
+    torch = gpu
+    raw = synth.random_weights(quant, rows, cols, seed=m + rows + quant, specials=True)
+    rng = np.random.default_rng(rows + cols)
+    a = rng.integers(-128, 128, (m, cols)).astype(np.int8)
+    sc = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    da = torch.zeros(m * cols + 16, dtype=torch.uint8, device="cuda")
+    da[offset:offset + m * cols] = dev(torch, a)
+    ds = dev(torch, sc)
+    kernel = jk.bitlinear_plan(w, da[offset:], m, tolerance=True)
+    split_k = cols // 256 <= 32 if quant != I2_S else cols // 128 <= 64  # K up to 8192
+    if m >= 16 and quant != Q8_0 and offset == 0 and split_k:
+        assert kernel.startswith("bitlinear_tol_kernel"), kernel
+    dy, dt = empty(torch, 4 * m * rows), empty(torch, 4 * m * rows)
+    jk.dev_bitlinear_i8(w, da[offset:], ds, m, cols, dy, m * rows)
+    jk.dev_bitlinear_i8_tol(w, da[offset:], ds, m, cols, dt, m * rows)
+    torch.cuda.synchronize()
+    exact = host(dy, np.float32, m * rows).reshape(m, rows)
+    tol = host(dt, np.float32, m * rows).reshape(m, rows)
+    worst = assert_within_row_norm(tol, exact)
+    for i in (0, m - 1):
+        ref = O.bitlinear_i8(quant, [rows, cols], raw, a[i], float(sc[i]), rows)
+        assert same_bits(exact[i], ref), (i, mismatch(exact[i], ref))
+        assert np.abs(tol[i].astype(np.float64) - ref).max() <= 1e-5 * np.linalg.norm(ref.astype(np.float64))
+    print(f"bitlinear tol {quant} {rows}x{cols} M={m} on {kernel}: worst error / row norm {worst:.2e}")
+    w.free()
+
+
+def test_bitlinear_tol_i2_s_extreme_sum(gpu):
+    """The I2_S tolerance kernel sums a whole row in exact integers before one conversion: every
+    weight +1 (2-bit field 2) and every activation +127 over K = 6912 gives 877,824 per output,
+    exact in f32, so each output is f32(877824) * (scale * act_scale) -- one rounding."""
+    torch = gpu
+    rows, cols, m = 2560, 6912, 128
+    payload = np.full(rows * cols // 4, 0b10101010, dtype=np.uint8)
+    trailer = np.zeros(32, dtype=np.uint8)
+    trailer[:4] = np.frombuffer(np.float32(0.75).tobytes(), dtype=np.uint8)
+    raw = np.concatenate([payload, trailer])
+    a = np.full((m, cols), 127, dtype=np.int8)
+    sc = np.linspace(0.001, 0.1, m).astype(np.float32)
+    w = jk.Weight(jk.TensorView("w", I2_S, [rows, cols], raw), rows, cols)
+    dt = empty(torch, 4 * m * rows)
+    jk.dev_bitlinear_i8_tol(w, dev(torch, a), dev(torch, sc), m, cols, dt, m * rows)
+    torch.cuda.synchronize()
+    tol = host(dt, np.float32, m * rows).reshape(m, rows)
+    want = (np.float32(127 * cols) * (np.float32(0.75) * sc)).astype(np.float32)
+    assert same_bits(tol, np.repeat(want[:, None], rows, axis=1))
+    w.free()
+
+
 @pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S])
 @pytest.mark.parametrize("m,rows,cols,offset", [(1, 9, 256 * 65, 0),   # more than 64 blocks a row
                                                 (2, 13, 2560, 1),     # activation not 16-byte aligned
