@@ -1011,19 +1011,25 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
                 aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ (r & 7)) << 4));
             }
             const float ws = f16_finite(S.ws[(64 * wn + lane) * 4 + st]);  // lane l: row of block l / 32
+            const float wsb = ws * -kMagicF;  // exact: 1.5 * 2^23 times an 11-bit significand
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
                 const int t = 64 * wmi + 32 * tb + jl;
                 const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ (t & 7)) << 4));
+                const float xs = S.xs[t * 4 + st];
                 v16i c[2];
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, bias, 0, 0, 0);
-                const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, S.xs[t * 4 + st], v32f{0}, 0, 0, 0);
+                const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
+                // the bias's share of the group, B * ws * xs, taken off the accumulators on the matrix
+                // core, so each output costs one fused multiply-add of the biased bits
+                tacc[tb] = __builtin_amdgcn_mfma_f32_32x32x1f32(wsb, xs, tacc[tb], 0, 0, 0);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        tacc[tb][16 * nt + v] = __builtin_fmaf(unbias(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
+                        tacc[tb][16 * nt + v] =
+                            __builtin_fmaf(__int_as_float(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
             }
         }
     };
