@@ -654,6 +654,7 @@ def main() -> int:
         hv = jk.TensorView("blk.0.ffn_gate.weight", jk.Q4_K, [cols, rows], hraw)
         hxq = jk.quantize_row_q8_k(synth.activations(cols, seed=1201))
         hout = np.zeros(rows, np.float32)
+        jk.host_cache_set_limit(16 << 30)  # weight residency (opt in)
         s0 = jk.host_stats()
         t0 = time.perf_counter()
         jk.gemv_q4_k_q8_k(hout, hv, hxq)
@@ -671,12 +672,13 @@ def main() -> int:
             "uploads_first": s1["weight_uploads"] - s0["weight_uploads"],
             "uploads_warm": s2["weight_uploads"] - s1["weight_uploads"],
             "device_allocs_warm": s2["device_allocs"] - s1["device_allocs"],
-            "workload": "host-memory TensorView + BlockQ8K slice, synchronous (copy in, GEMV, copy out); "
-                        "median of 200 warm calls, wall clock, PCIe-inclusive"}
+            "workload": "host-memory TensorView + BlockQ8K slice, synchronous (copy in, GEMV, copy out), weight "
+                        "residency on; median of 200 warm calls, wall clock, PCIe-inclusive"}
         log(f"  host tier gemv_q4_k_q8_k 14336x4096: first call {first_ms:.2f} ms, warm {warm_us:.1f} us/call "
             f"({s2['weight_uploads'] - s1['weight_uploads']} uploads, "
             f"{s2['device_allocs'] - s1['device_allocs']} device allocations over 200 warm calls)")
         jk.host_cache_invalidate(hv)
+        jk.host_cache_set_limit(0)
         del hraw, hv
         # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
         yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)

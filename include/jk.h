@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define JK_ABI_VERSION 2
+#define JK_ABI_VERSION 3
 
 typedef enum jk_status {
     JK_OK = 0,
@@ -403,25 +403,32 @@ jk_status jk_convert_i2_s_to_tq2_0(jk_stream s, const void *i2s, size_t i2s_bloc
 
 /* ------------------------------------------- host tier (synchronous mirrors) */
 /* The jk_host_* mirrors run on a per-thread stream and per-thread device scratch (grown on
- * demand, kept until jk_host_release_thread), and keep the weights of the TensorViews they are
- * given resident: a view is uploaded once, keyed by its byte range, format, shape and a
- * fingerprint of sampled bytes, and later calls with it perform no upload and no allocation
- * (tests/wave4_zero_alloc_gemv.rs:88+ is the reference's zero-allocation contract for these
- * paths). The bytes behind a cached view must not change while it is cached: after changing or
- * freeing them call jk_host_cache_invalidate (or jk_host_cache_clear). Entries beyond the byte
- * limit (default 64 GiB; 0 turns the cache off) are evicted least recently used. No reference
- * function corresponds to this control surface. */
+ * demand, kept until jk_host_release_thread). By default every call uploads its weight, as the
+ * reference reads a slice's bytes on every call. Residency is opt in: after
+ * jk_host_cache_set_limit(bytes > 0) a view is uploaded once, keyed by its byte range, format,
+ * shape and a fingerprint of sampled bytes, and later calls with it perform no upload and no
+ * allocation (tests/wave4_zero_alloc_gemv.rs:88+ is the reference's zero-allocation contract for
+ * these paths). With the cache on, the bytes behind a cached view must not change while it is
+ * cached: after changing or freeing them call jk_host_cache_invalidate (or jk_host_cache_clear).
+ * jk_host_cache_set_verify(1) removes that obligation at a cost: every hit hashes all of the
+ * view's bytes (a few ms for a 33 MB matrix) and, if they changed since the upload, drops the
+ * entry and uploads again (counted in stale_reuploads); setting it clears the cache. Entries
+ * beyond the byte limit are evicted least recently used. No reference function corresponds to
+ * this control surface. */
 typedef struct jk_host_stats {
     uint64_t weight_uploads;  /* views uploaded (cache misses, and every call with the cache off) */
     uint64_t cache_hits;      /* calls served by a resident weight */
     uint64_t cache_evictions;
     uint64_t device_allocs;   /* device allocations made by the host tier (uploads and scratch growth) */
     uint64_t cached_weights, cached_bytes, cache_limit;
+    uint64_t stale_reuploads; /* verify mode: hits whose bytes had changed, uploaded again */
+    uint64_t verify;          /* 1 while jk_host_cache_set_verify(1) is in effect */
 } jk_host_stats;
 jk_status jk_host_cache_set_limit(size_t bytes);
 /* Drops every cached weight whose view overlaps [bytes, bytes + len). */
 jk_status jk_host_cache_invalidate(const void *bytes, size_t len);
 jk_status jk_host_cache_clear(void);
+jk_status jk_host_cache_set_verify(int on);
 jk_status jk_host_get_stats(jk_host_stats *out);
 /* Frees the calling thread's host-tier stream and scratch. */
 jk_status jk_host_release_thread(void);

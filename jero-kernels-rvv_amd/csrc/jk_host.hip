@@ -4,16 +4,20 @@
 // runs the device-tier kernel on the calling thread's stream, copies the result back and
 // synchronizes that stream.
 //
-// Weights are kept resident. A weight named by a TensorView (host bytes) is uploaded once and
-// cached, keyed by the view's byte range, format and matrix shape plus a fingerprint of sampled
-// bytes; later calls with the same view reuse the device copy without any upload or allocation.
-// The reference borrows immutable weight slices (a model's tensors, typically a memory-mapped
-// file), and the cache assumes the same: bytes behind a cached view must not change while it is
-// cached, unless jk_host_cache_invalidate is called for them (the fingerprint catches a buffer
-// that is freed and refilled with a different tensor at the same address in all but contrived
-// cases). jk_host_cache_set_limit(0) turns the cache off (one upload per call). Entries are
-// evicted least-recently-used beyond the byte limit; an entry in use by a call is never freed
-// under it.
+// Weights can be kept resident (opt in). By default every call uploads its weight, as the
+// reference reads the slice's bytes on every call. After jk_host_cache_set_limit(bytes > 0), a
+// weight named by a TensorView (host bytes) is uploaded once and cached, keyed by the view's byte
+// range, format and matrix shape plus a fingerprint of sampled bytes; later calls with the same
+// view reuse the device copy without any upload or allocation. The cache then assumes what the
+// reference's callers give it, immutable weight slices (a model's tensors, typically a
+// memory-mapped file): bytes behind a cached view must not change while it is cached, unless
+// jk_host_cache_invalidate is called for them (the fingerprint catches a buffer that is freed and
+// refilled with a different tensor at the same address in all but contrived cases). With
+// jk_host_cache_set_verify(1) every cache hit also hashes all of the view's bytes and compares
+// them with the hash taken at upload; a mismatch drops the entry and uploads again
+// (stale_reuploads counts these), so an in-place edit cannot return results of the old bytes.
+// Entries are evicted least-recently-used beyond the byte limit; an entry in use by a call is
+// never freed under it.
 //
 // Per-call device memory (activations, outputs, workspaces) comes from a per-thread scratch
 // buffer that only grows; a thread's stream and scratch are kept until jk_host_release_thread.
@@ -32,7 +36,8 @@
 namespace jk {
 
 // ------------------------------------------------------------------ statistics
-static std::atomic<uint64_t> g_uploads{0}, g_hits{0}, g_evictions{0}, g_device_allocs{0};
+static std::atomic<uint64_t> g_uploads{0}, g_hits{0}, g_evictions{0}, g_device_allocs{0}, g_stale{0};
+static std::atomic<bool> g_verify{false};
 
 // ------------------------------------------------------------------ per-thread context
 struct HostCtx {
@@ -138,13 +143,14 @@ struct CacheEntry {
     CacheKey key;
     jk_weight *w = nullptr;
     size_t bytes = 0;
+    uint64_t full = 0;  // hash of every byte of the view at upload (verify mode)
     int users = 0;
     bool evicted = false;
 };
 
 struct WeightCache {
     std::mutex mu;
-    size_t limit = (size_t)64 << 30;
+    size_t limit = 0;  // residency is opt in
     size_t bytes = 0;
     std::list<std::shared_ptr<CacheEntry>> lru;  // front: most recently used
     std::unordered_map<CacheKey, std::list<std::shared_ptr<CacheEntry>>::iterator, CacheKeyHash> map;
@@ -170,6 +176,21 @@ static uint64_t fingerprint(const uint8_t *p, size_t n) {
         for (size_t k = 1; k < 256; ++k) mix(n / 256 * k, 64);
     }
     return h ^ n;
+}
+
+// A 64-bit hash of every byte of the view (verify mode): 8-byte words mixed by multiply-xor, a few
+// GB/s on one core.
+static uint64_t full_hash(const uint8_t *p, size_t n) {
+    uint64_t h = 0x9E3779B97F4A7C15ull ^ n;
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        uint64_t v;
+        memcpy(&v, p + i, 8);
+        h = (h ^ v) * 0xFF51AFD7ED558CCDull;
+        h ^= h >> 29;
+    }
+    for (; i < n; ++i) h = (h ^ p[i]) * 0x100000001B3ull;
+    return h ^ (h >> 32);
 }
 
 // Frees entries (least recent first) until the cache fits its limit; entries in use are
@@ -221,16 +242,34 @@ static jk_status resident(HostCtx *ctx, const jk_tensor_view *v, size_t rows, si
     {
         std::lock_guard<std::mutex> lock(c.mu);
         limit = c.limit;
-        auto it = c.map.find(key);
-        if (it != c.map.end()) {
-            std::shared_ptr<CacheEntry> e = *it->second;
-            c.lru.splice(c.lru.begin(), c.lru, it->second);
-            ++e->users;
-            g_hits.fetch_add(1);
-            out->entry = e;
-            out->w = e->w;
-            return JK_OK;
+    }
+    const bool verify = limit > 0 && g_verify.load();
+    const uint64_t full = verify ? full_hash(static_cast<const uint8_t *>(v->bytes), v->byte_len) : 0;
+    if (limit > 0) {
+        std::vector<jk_weight *> stale;
+        {
+            std::lock_guard<std::mutex> lock(c.mu);
+            auto it = c.map.find(key);
+            if (it != c.map.end()) {
+                std::shared_ptr<CacheEntry> e = *it->second;
+                if (!verify || e->full == full) {
+                    c.lru.splice(c.lru.begin(), c.lru, it->second);
+                    ++e->users;
+                    g_hits.fetch_add(1);
+                    out->entry = e;
+                    out->w = e->w;
+                    return JK_OK;
+                }
+                // the bytes changed since the upload: drop the entry, upload again below
+                c.map.erase(it);
+                c.lru.remove(e);
+                c.bytes -= e->bytes;
+                e->evicted = true;
+                g_stale.fetch_add(1);
+                if (e->users == 0) stale.push_back(e->w), e->w = nullptr;
+            }
         }
+        free_all(stale);
     }
     jk_weight *w = nullptr;
     JK_TRY(jk_weight_upload(ctx->stream, v, rows, cols, &w));
@@ -256,6 +295,7 @@ static jk_status resident(HostCtx *ctx, const jk_tensor_view *v, size_t rows, si
             e->key = key;
             e->w = w;
             e->bytes = w->device_bytes;
+            e->full = full;
             e->users = 1;
             c.lru.push_front(e);
             c.map[key] = c.lru.begin();
@@ -364,6 +404,12 @@ jk_status jk_host_cache_invalidate(const void *bytes, size_t len) {
 
 jk_status jk_host_cache_clear(void) { return jk_host_cache_invalidate(nullptr, SIZE_MAX); }
 
+jk_status jk_host_cache_set_verify(int on) {
+    // entries uploaded before verify mode have no full hash: start over
+    g_verify.store(on != 0);
+    return jk_host_cache_clear();
+}
+
 jk_status jk_host_get_stats(jk_host_stats *out) {
     if (!out) return fail(JK_TENSOR_BOUNDS, "host_get_stats: null pointer");
     std::lock_guard<std::mutex> lock(cache().mu);
@@ -374,6 +420,8 @@ jk_status jk_host_get_stats(jk_host_stats *out) {
     out->cached_weights = cache().lru.size();
     out->cached_bytes = cache().bytes;
     out->cache_limit = cache().limit;
+    out->stale_reuploads = g_stale.load();
+    out->verify = g_verify.load() ? 1 : 0;
     return JK_OK;
 }
 

@@ -95,7 +95,7 @@ class ErrorInfoC(C.Structure):
 class HostStatsC(C.Structure):
     _fields_ = [("weight_uploads", C.c_uint64), ("cache_hits", C.c_uint64), ("cache_evictions", C.c_uint64),
                 ("device_allocs", C.c_uint64), ("cached_weights", C.c_uint64), ("cached_bytes", C.c_uint64),
-                ("cache_limit", C.c_uint64)]
+                ("cache_limit", C.c_uint64), ("stale_reuploads", C.c_uint64), ("verify", C.c_uint64)]
 
 
 class ActQ8C(C.Structure):
@@ -203,6 +203,11 @@ def host_cache_invalidate(data) -> None:
 
 def host_cache_clear() -> None:
     _check(lib().jk_host_cache_clear())
+
+
+def host_cache_set_verify(on: bool) -> None:
+    """jk_host_cache_set_verify: every cache hit checks a hash of all of the view's bytes."""
+    _check(lib().jk_host_cache_set_verify(C.c_int(int(on))))
 
 
 def host_stats() -> dict:

@@ -1,5 +1,5 @@
-"""Host tier (jk_host_*) as a drop-in for the reference's slice signatures: weights named by a
-TensorView stay resident after the first call, and warm calls perform no upload and no device
+"""Host tier (jk_host_*) as a drop-in for the reference's slice signatures: with residency on,
+weights named by a TensorView stay resident after the first call, and warm calls perform no upload and no device
 allocation (the reference's zero-allocation contract, tests/wave4_zero_alloc_gemv.rs:88-172),
 with outputs bit-identical to the first call and to the oracle. Also the fail-closed cases of
 tests/test_repack_gemv_gemm.rs:883-917 on the device tier, with TensorBoundsError's fields.
@@ -14,6 +14,19 @@ import oracle as O
 from jk import synth
 
 pytestmark = pytest.mark.gpu
+
+RESIDENT_LIMIT = 16 << 30
+
+
+@pytest.fixture(autouse=True)
+def resident_weights(gpu):
+    """Weight residency is opt in (jk_host_cache_set_limit); these tests turn it on and leave the
+    library's limit as they found it, verify off."""
+    prev = jk.host_stats()["cache_limit"]
+    jk.host_cache_set_limit(RESIDENT_LIMIT)
+    yield
+    jk.host_cache_set_verify(False)
+    jk.host_cache_set_limit(prev)
 
 
 def same_bits(a, b) -> bool:
@@ -179,3 +192,49 @@ def test_repack_and_gemm_bounds_error_fields(gpu):
     assert (ei.value.tensor_name, ei.value.byte_len, ei.value.buffer_len) == ("gemm_repacked", 28, 32)
     torch.cuda.synchronize()
     w.free()
+
+
+def test_unannounced_edit_of_unsampled_bytes(gpu):
+    """An in-place edit of weight bytes that the cache key's fingerprint does not sample, made
+    without jk_host_cache_invalidate: with residency off (the default) every call reads the bytes,
+    as the reference does; with residency on, the stale device copy is used, as documented (the
+    immutability contract), until invalidated; with verify on, the edit is caught by the full-content
+    hash, the weight is uploaded again and the result is the oracle's for the new bytes."""
+    rows, cols = 1024, 4096
+    raw = synth.gguf_weights(jk.Q4_K, rows, cols, seed=11)
+    v = jk.TensorView("w", jk.Q4_K, [cols, rows], raw)
+    xb = O.quantize_row_q8_k(synth.activations(cols, 12))
+    off = raw.nbytes // 256 + 2000  # between the fingerprint's first two sampled windows: a qs byte of row 4
+    assert 1024 < off < raw.nbytes - 1024
+
+    def gemv():
+        out = np.zeros(rows, np.float32)
+        jk.gemv_q4_k_q8_k(out, v, xb)
+        return out
+
+    def ref():
+        return O.gemv_q8(jk.Q4_K, [rows, cols], raw, xb, rows)
+
+    jk.host_cache_set_limit(0)  # the default: no residency
+    a = gemv()
+    assert same_bits(a, ref())
+    raw[off] ^= 0x55
+    b = gemv()
+    assert same_bits(b, ref()) and not same_bits(a, b)
+    jk.host_cache_set_limit(RESIDENT_LIMIT)  # residency: the caller promises immutable bytes
+    c = gemv()
+    raw[off] ^= 0x55
+    assert same_bits(gemv(), c)  # the documented behaviour of a broken promise: the old bytes' result
+    jk.host_cache_invalidate(v)
+    assert same_bits(gemv(), ref())
+    jk.host_cache_set_verify(True)  # verify: every hit hashes all bytes
+    assert same_bits(gemv(), ref())
+    s0 = jk.host_stats()
+    assert s0["verify"] == 1
+    raw[off] ^= 0x55
+    assert same_bits(gemv(), ref())
+    s1 = jk.host_stats()
+    assert s1["stale_reuploads"] == s0["stale_reuploads"] + 1
+    assert s1["weight_uploads"] == s0["weight_uploads"] + 1
+    assert same_bits(gemv(), ref())  # and the new upload is then reused
+    assert jk.host_stats()["weight_uploads"] == s1["weight_uploads"]
