@@ -307,6 +307,13 @@ jk_status jk_gemv_q8_f32(jk_stream s, const jk_weight *w, const float *x, size_t
  * and dot it with f32 x. TQ1_0 / TQ2_0 have none (CapabilityMismatch). */
 jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y,
                          size_t y_len);
+/* The same products in tolerance mode: the same arguments, validation and errors as
+ * jk_vec_dot_f32, with each block's element products added over four fused multiply-add
+ * accumulators instead of the reference's one product and one add per element in element
+ * order; every output within 1e-5 of its row's L2 norm of the reference's result. No
+ * reference function has this rounding: it is jk_vec_dot_f32's alternative. */
+jk_status jk_vec_dot_f32_tol(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y,
+                             size_t y_len);
 
 /* ----------------------------------------------------- repacked GEMV / GEMM */
 /* Every format of jk_weight_upload. PackedNibbleMatrix::gemm / gemm_rows / gemv

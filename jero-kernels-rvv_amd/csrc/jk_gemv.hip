@@ -10,6 +10,8 @@
 //
 // The weight stream is read once with 128-bit non-temporal loads; activation blocks
 // are small and shared by all rows, so they are read through the caches.
+#include <type_traits>
+
 #include "jk_device.hpp"
 
 namespace jk {
@@ -55,9 +57,26 @@ __device__ __forceinline__ uint32_t vd_byte(const VdBlock<Q> &o, int c, int k) {
     return (comp(o.c[c], k >> 2) >> (8 * (k & 3))) & 255u;
 }
 
-template <int Q>
+// The block's element products: added one after another from +0.0 (the reference's
+// dot_product_f32_scalar), or, in tolerance mode, spread over four accumulators with fused
+// multiply-adds (the chain a lane runs is a quarter as long) and added at the end.
+struct VdSum {
+    float s = 0.0f;
+    __device__ __forceinline__ void add(float w, float x) { s += w * x; }
+    __device__ __forceinline__ float get() const { return s; }
+};
+struct VdSumTol {
+    float a = 0.0f, b = 0.0f, c = 0.0f, d = 0.0f;
+    __device__ __forceinline__ void add(float w, float x) {  // (the rotation is register renaming once unrolled)
+        const float n = __builtin_fmaf(w, x, a);
+        a = b, b = c, c = d, d = n;
+    }
+    __device__ __forceinline__ float get() const { return (a + b) + (c + d); }
+};
+
+template <int Q, bool TOL = false>
 __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__restrict__ xb, float i2s_scale) {
-    float sum = 0.0f;
+    std::conditional_t<TOL, VdSumTol, VdSum> sum;
     if constexpr (Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_Q8_0) {
         // dequantize_q4_0_block / dequantize_q8_0_block (quant.rs:550-588), dequantize_q5_0_block
         // (160-164, scale_i8_into_f32 94-102). The reference writes +0.0 for d == 0 where d * q
@@ -73,7 +92,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                 qv = (int)(((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) | (((o.h[0] >> i) & 1u) << 4)) - 16;
             else qv = (int)(int8_t)vd_byte<Q>(o, i >> 4, i & 15);
             const float wv = d * (float)qv;
-            sum += wv * xb[i];
+            sum.add(wv, xb[i]);
         }
     } else if constexpr (Q == JK_Q4_K) {
         // dequantize_q4_k_m_block (lib.rs:720-766): y = d1 * q - m1, two roundings
@@ -93,7 +112,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                 for (int l = 0; l < 32; ++l) {
                     const uint32_t q = (vd_byte<Q>(o, 1 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u;
                     const float wv = d1 * (float)q - m1;
-                    sum += wv * xb[64 * c + 32 * hi + l];
+                    sum.add(wv, xb[64 * c + 32 * hi + l]);
                 }
             }
         }
@@ -107,7 +126,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
             uint32_t q = (vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u;
             if constexpr (Q == JK_Q5_1) q |= ((o.h[1] >> i) & 1u) << 4;
             const float wv = z ? 0.0f : d * (float)q + m;
-            sum += wv * xb[i];
+            sum.add(wv, xb[i]);
         }
     } else if constexpr (Q == JK_IQ4_NL) {
         // dequantize_iq4_nl_block (quant.rs:348-356): d * KVALUES_IQ4NL[nibble] (+0.0 for d == 0,
@@ -117,13 +136,13 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
         for (int k = 0; k < 4; ++k) {
             const uint32_t lo = iq4nl_lookup(comp(o.c[0], k) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum += (d * (float)(int8_t)(lo >> (8 * i))) * xb[4 * k + i];
+            for (int i = 0; i < 4; ++i) sum.add((d * (float)(int8_t)(lo >> (8 * i))), xb[4 * k + i]);
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t hi = iq4nl_lookup((comp(o.c[0], k) >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum += (d * (float)(int8_t)(hi >> (8 * i))) * xb[16 + 4 * k + i];
+            for (int i = 0; i < 4; ++i) sum.add((d * (float)(int8_t)(hi >> (8 * i))), xb[16 + 4 * k + i]);
         }
     } else if constexpr (Q == JK_Q2_K) {
         // dequantize_q2_k_block (quant.rs:238-252): element 128 half + 32 j + 16 part + l is the
@@ -138,7 +157,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
             for (int k = 0; k < 4; ++k) {
                 const uint32_t v = (comp(o.c[1 + 2 * half + part], k) >> (2 * j)) & 0x03030303u;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sum += (dl * (float)((v >> (8 * i)) & 3u) - ml) * xb[16 * g + 4 * k + i];
+                for (int i = 0; i < 4; ++i) sum.add((dl * (float)((v >> (8 * i)) & 3u) - ml), xb[16 * g + 4 * k + i]);
             }
         }
     } else if constexpr (Q == JK_Q3_K) {
@@ -160,7 +179,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int qv = (int)((v >> (8 * i)) & 3u) - ((h >> (8 * i)) & 1u ? 0 : 4);
-                    sum += (dl * (float)qv) * xb[16 * g + 4 * k + i];
+                    sum.add((dl * (float)qv), xb[16 * g + 4 * k + i]);
                 }
             }
         }
@@ -185,7 +204,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                     const uint32_t q = ((vd_byte<Q>(o, 3 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u) |
                                        (((vd_byte<Q>(o, 1 + (l >> 4), l & 15) >> (2 * c + hi)) & 1u) << 4);
                     const float wv = d1 * (float)q - m1;
-                    sum += wv * xb[64 * c + 32 * hi + l];
+                    sum.add(wv, xb[64 * c + 32 * hi + l]);
                 }
             }
         }
@@ -215,7 +234,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const float wv = s4 * (float)(int8_t)(w4 >> (8 * i));
-                        sum += wv * xb[128 * h + 32 * quarter + l + i];
+                        sum.add(wv, xb[128 * h + 32 * quarter + l + i]);
                     }
                 }
                 // the chain is serial: an empty asm with a memory clobber keeps the next 32
@@ -227,16 +246,16 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
         for (int e = 0; e < 128; ++e) {
             const int grp = e >> 5, g = e & 31;
             const int t = (int)((vd_byte<Q>(o, g >> 4, g & 15) >> (6 - 2 * grp)) & 3u) - 1;
-            sum += (i2s_scale * (float)t) * xb[e];
+            sum.add((i2s_scale * (float)t), xb[e]);
         }
     }
-    return sum;
+    return sum.get();
 }
 
 constexpr int kVdWaves = 8;
 constexpr int kVdLdsMax = 60 * 1024;  // staged activation bytes
 
-template <int Q, int LPR, bool XL>
+template <int Q, int LPR, bool XL, bool TOL = false>
 __global__ __launch_bounds__(64 * kVdWaves) __attribute__((amdgpu_waves_per_eu(4))) void vec_dot_f32_kernel(WeightDev w, const float *__restrict__ x,
                                                                      float *__restrict__ y) {
     constexpr int RPW = 64 / LPR, E = VdFmt<Q>::E;
@@ -269,7 +288,7 @@ __global__ __launch_bounds__(64 * kVdWaves) __attribute__((amdgpu_waves_per_eu(4
     for (int it = 0; it < iters; ++it) {
         const int b = it * LPR + p;
         if (it > 0) vd_load<Q>(blk, w, r, min(b, nb - 1));
-        const float v = b < nb ? vd_block<Q>(blk, xs + (size_t)XS * min(b, nb - 1), w.tensor_scale) : -0.0f;
+        const float v = b < nb ? vd_block<Q, TOL>(blk, xs + (size_t)XS * min(b, nb - 1), w.tensor_scale) : -0.0f;
         if constexpr (LPR == 16) acc = chain_add(acc, v);
         else acc = fold_wave(acc, v, red);
     }
@@ -277,39 +296,48 @@ __global__ __launch_bounds__(64 * kVdWaves) __attribute__((amdgpu_waves_per_eu(4
     if (row < w.rows && p == writer) y[row] = acc;
 }
 
-template <int Q>
+template <int Q, bool TOL>
 static jk_status launch_vd(hipStream_t s, const WeightDev &w, const float *x, float *y) {
     const size_t lds_need = (size_t)w.nb * (VdFmt<Q>::E + 4) * 4;  // padded blocks
     const bool xl = lds_need <= (size_t)kVdLdsMax;
     const size_t lds = xl ? lds_need : 0;
     if (w.nb > 32) {
         const dim3 grid((unsigned)((w.rows + kVdWaves - 1) / kVdWaves));
-        if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, true>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
-        else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, false>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
+        if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, true, TOL>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
+        else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, false, TOL>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
     } else {
         const dim3 grid((unsigned)((w.rows + 4 * kVdWaves - 1) / (4 * kVdWaves)));
-        if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 16, true>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
-        else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 16, false>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
+        if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 16, true, TOL>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
+        else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 16, false, TOL>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
     }
     return check_launch("vec_dot_f32_kernel");
 }
 
-jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y) {
+template <bool TOL>
+static jk_status launch_vec_dot_f32_mode(hipStream_t s, const WeightDev &w, const float *x, float *y) {
     switch (w.quant) {
-    case JK_Q4_0: return launch_vd<JK_Q4_0>(s, w, x, y);
-    case JK_Q5_0: return launch_vd<JK_Q5_0>(s, w, x, y);
-    case JK_Q8_0: return launch_vd<JK_Q8_0>(s, w, x, y);
-    case JK_Q4_K: return launch_vd<JK_Q4_K>(s, w, x, y);
-    case JK_Q5_K: return launch_vd<JK_Q5_K>(s, w, x, y);
-    case JK_Q4_1: return launch_vd<JK_Q4_1>(s, w, x, y);
-    case JK_Q5_1: return launch_vd<JK_Q5_1>(s, w, x, y);
-    case JK_IQ4_NL: return launch_vd<JK_IQ4_NL>(s, w, x, y);
-    case JK_Q2_K: return launch_vd<JK_Q2_K>(s, w, x, y);
-    case JK_Q3_K: return launch_vd<JK_Q3_K>(s, w, x, y);
-    case JK_Q6_K: return launch_vd<JK_Q6_K>(s, w, x, y);
-    case JK_I2_S: return launch_vd<JK_I2_S>(s, w, x, y);
+    case JK_Q4_0: return launch_vd<JK_Q4_0, TOL>(s, w, x, y);
+    case JK_Q5_0: return launch_vd<JK_Q5_0, TOL>(s, w, x, y);
+    case JK_Q8_0: return launch_vd<JK_Q8_0, TOL>(s, w, x, y);
+    case JK_Q4_K: return launch_vd<JK_Q4_K, TOL>(s, w, x, y);
+    case JK_Q5_K: return launch_vd<JK_Q5_K, TOL>(s, w, x, y);
+    case JK_Q4_1: return launch_vd<JK_Q4_1, TOL>(s, w, x, y);
+    case JK_Q5_1: return launch_vd<JK_Q5_1, TOL>(s, w, x, y);
+    case JK_IQ4_NL: return launch_vd<JK_IQ4_NL, TOL>(s, w, x, y);
+    case JK_Q2_K: return launch_vd<JK_Q2_K, TOL>(s, w, x, y);
+    case JK_Q3_K: return launch_vd<JK_Q3_K, TOL>(s, w, x, y);
+    case JK_Q6_K: return launch_vd<JK_Q6_K, TOL>(s, w, x, y);
+    case JK_I2_S: return launch_vd<JK_I2_S, TOL>(s, w, x, y);
     default: return fail(JK_CAPABILITY_MISMATCH, "vec_dot_f32: unsupported quant %d", w.quant);
     }
+}
+
+jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y) {
+    return launch_vec_dot_f32_mode<false>(s, w, x, y);
+}
+
+jk_status launch_vec_dot_f32_tol(hipStream_t s, const WeightDev &w, const float *x, float *y) {
+    return launch_vec_dot_f32_mode<true>(s, w, x, y);
 }
 
 // ------------------------------------------------------------------------ BitLinear

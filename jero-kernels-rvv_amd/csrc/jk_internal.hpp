@@ -235,6 +235,9 @@ jk_status noalloc_setup();
 jk_status gemv_argmax_job(const char *what, const jk_weight *w, const void *x_q8, const float *x_f32, size_t x_len,
                           float *y, int32_t *index, GemvJob *out);
 jk_status launch_vec_dot_f32(hipStream_t s, const WeightDev &w, const float *x, float *y);
+// The same products with each block's element products spread over four fused multiply-add
+// accumulators: within 1e-5 of each output's row L2 norm.
+jk_status launch_vec_dot_f32_tol(hipStream_t s, const WeightDev &w, const float *x, float *y);
 // Token count from which jk_bitlinear_i8 uses the MFMA GEMM path.
 constexpr int kBitlinearMfmaMinTokens = 16;
 jk_status launch_bitlinear_mfma(hipStream_t s, const WeightDev &w, const int8_t *act, const float *act_scales, int m,

@@ -843,7 +843,7 @@ jk_status jk_convert_i2_s_to_tq2_0(jk_stream s, const void *i2s, size_t i2s_bloc
 }
 
 // -------------------------------------------------------------- vec_dot (f32)
-jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
+static jk_status vec_dot_check(const jk_weight *w, const float *x, size_t n, const float *y, size_t y_len) {
     JK_TRY(weight_usable(w, "vec_dot"));
     int q = w->quant;
     if (!has_vec_dot_f32(q))
@@ -852,7 +852,17 @@ jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t
         return fail(JK_TENSOR_BOUNDS, "vec_dot: matrix [%d, %d] does not match output len %zu and input len %zu",
                     w->dev.rows, w->dev.cols, y_len, n);
     if (!x || !y) return fail(JK_TENSOR_BOUNDS, "vec_dot: null pointer");
+    return JK_OK;
+}
+
+jk_status jk_vec_dot_f32(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
+    JK_TRY(vec_dot_check(w, x, n, y, y_len));
     return launch_vec_dot_f32((hipStream_t)s, w->dev, x, y);
+}
+
+jk_status jk_vec_dot_f32_tol(jk_stream s, const jk_weight *w, const float *x, size_t n, float *y, size_t y_len) {
+    JK_TRY(vec_dot_check(w, x, n, y, y_len));
+    return launch_vec_dot_f32_tol((hipStream_t)s, w->dev, x, y);
 }
 
 // ------------------------------------------------------------ repacked GEMM

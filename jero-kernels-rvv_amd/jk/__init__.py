@@ -634,6 +634,11 @@ def dev_vec_dot_f32(w: Weight, x, n, y, y_len, stream=None):
     _check(lib().jk_vec_dot_f32(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(n), _vp(_ptr(y)), _sz(y_len)))
 
 
+def dev_vec_dot_f32_tol(w: Weight, x, n, y, y_len, stream=None):
+    """jk_vec_dot_f32_tol: the f32-activation matvec within 1e-5 of each output's row L2 norm."""
+    _check(lib().jk_vec_dot_f32_tol(_vp(stream or 0), w.handle, _vp(_ptr(x)), _sz(n), _vp(_ptr(y)), _sz(y_len)))
+
+
 def dev_gemm_repacked(w: Weight, act: ActQ8C, y, y_len, r0, r1, stream=None):
     _check(lib().jk_gemm_repacked(_vp(stream or 0), w.handle, C.byref(act), _vp(_ptr(y)), _sz(y_len), _sz(r0),
                                   _sz(r1)))

@@ -454,6 +454,29 @@ def test_vec_dot_f32(gpu, quant, rows, cols):
     assert same_bits(got, ref), mismatch(got, ref)
 
 
+@pytest.mark.parametrize("quant", list(jk.VEC_DOT_F32_FORMATS))
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 4096), (300, 4352), (9, 256 * 90)])
+def test_vec_dot_f32_tol(gpu, quant, rows, cols):
+    """Tolerance-mode f32 vec_dot (jk_vec_dot_f32_tol): rows of up to 32 blocks (16 lanes a row),
+    longer rows (64 lanes a row), activations too long for LDS (23040 columns), weights with special
+    scales. Every output within 1e-5 of the output vector's L2 norm of the oracle and of the
+    bit-exact GPU result."""
+    torch = gpu
+    raw = synth.random_weights(quant, rows, cols, seed=3 * rows + quant, specials=True)
+    x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
+    ref = O.vec_dot_f32(quant, [rows, cols], raw, x, rows)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    dy, dt = empty(torch, 4 * rows), empty(torch, 4 * rows)
+    jk.dev_vec_dot_f32(w, dev(torch, x), cols, dy, rows)
+    jk.dev_vec_dot_f32_tol(w, dev(torch, x), cols, dt, rows)
+    torch.cuda.synchronize()
+    exact, tol = host(dy, np.float32, rows), host(dt, np.float32, rows)
+    assert same_bits(exact, ref)
+    worst = assert_within_row_norm(tol[None, :], ref[None, :])
+    print(f"vec_dot tol {quant} {rows}x{cols}: worst error / norm {worst:.2e}")
+    w.free()
+
+
 def test_vec_dot_i2_s_zero_scale_rows_are_zero(gpu):
     torch = gpu
     rows, cols = 6, 256
