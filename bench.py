@@ -132,8 +132,15 @@ def main() -> int:
                          "feed-forward block; also reported as a secondary line)")
     ap.add_argument("--down", choices=("fused", "split"), default="split",
                     help="ffn_down activation: quantized inside the GEMV launch, or by its own launch")
+    ap.add_argument("--profile-loop", choices=("bitlinear", "gemm", "vec_dot"),
+                    help="instead of the benchmark: launch one workload's kernels eagerly (no graph) 20 times each "
+                         "and exit -- the program a rocprofv3 counter pass runs (bitlinear: the 128-token C5 "
+                         "BitLinear, both modes; gemm: the Q8_0 512-token GEMM, both modes; vec_dot: the f32 "
+                         "vec_dot lines, both modes)")
     args = ap.parse_args()
 
+    if args.profile_loop:
+        return profile_loop(args.profile_loop)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
               "(the row-sharded multi-GPU design is documented, not built)", file=sys.stderr)
@@ -861,6 +868,62 @@ def main() -> int:
         "cpu_baseline_all_cores": cpu_all,
     }
     print(json.dumps(rec), flush=True)
+    return 0
+
+
+def profile_loop(which: str) -> int:
+    """Eager launches of one workload's kernels (20 per configuration and mode), for counter passes."""
+    import torch
+
+    import jk
+    from jk import synth
+
+    jk.lib()
+    jk.init(0)
+    gen = torch.Generator(device="cpu").manual_seed(99)
+    n = 20
+    if which == "bitlinear":
+        for quant in (jk.TQ2_0, jk.I2_S):
+            for rows, cols in ((6912, 2560), (2560, 6912)):
+                m = 128
+                w = jk.Weight(jk.TensorView("w", quant, (rows, cols), synth.gguf_weights(quant, rows, cols, seed=7)),
+                              rows, cols)
+                xin = torch.randn(m, cols, generator=gen).cuda()
+                aq = torch.empty(m * cols, dtype=torch.int8, device="cuda")
+                asc = torch.empty(m, dtype=torch.float32, device="cuda")
+                jk.dev_quantize_absmax_i8(xin, m, cols, aq, asc)
+                y = torch.empty(m * rows, dtype=torch.float32, device="cuda")
+                for fn in (jk.dev_bitlinear_i8, jk.dev_bitlinear_i8_tol):
+                    for _ in range(n):
+                        fn(w, aq, asc, m, cols, y, m * rows)
+                torch.cuda.synchronize()
+                w.free()
+    elif which == "gemm":
+        N, K, M = 14336, 4096, 512
+        w = jk.Weight(jk.TensorView("w", jk.Q8_0, (N, K), synth.gguf_weights(jk.Q8_0, N, K, seed=77)), N, K)
+        x = torch.randn(M, K, generator=gen).cuda()
+        need = jk.act_q8_bytes(M, K)
+        st = torch.empty(need, dtype=torch.uint8, device="cuda")
+        act = jk.act_q8_bind(st, need, M, K)
+        jk.dev_quantize_act_q8(x, M, K, act)
+        y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+        for fn in (jk.dev_gemm_repacked_tol, jk.dev_gemm_repacked):
+            for _ in range(n):
+                fn(w, act, y, M * N, 0, N)
+        torch.cuda.synchronize()
+        w.free()
+    else:
+        for quant, rows, cols in ((jk.Q4_K, 4096, 4096), (jk.Q6_K, 4096, 14336)):
+            w = jk.Weight(jk.TensorView("w", quant, (rows, cols), synth.gguf_weights(quant, rows, cols, seed=8)),
+                          rows, cols)
+            x = torch.randn(cols, generator=gen).cuda()
+            y = torch.empty(rows, dtype=torch.float32, device="cuda")
+            for fn in (jk.dev_vec_dot_f32, jk.dev_vec_dot_f32_tol):
+                for _ in range(n):
+                    fn(w, x, cols, y, rows)
+            torch.cuda.synchronize()
+            w.free()
+    print(json.dumps({"profile_loop": which, "launches_per_configuration_and_mode": n}), flush=True)
     return 0
 
 
