@@ -599,6 +599,23 @@ def main() -> int:
             for w in ws:
                 w.free()
         del xin, store, y
+        # The plain int8 GEMM (gemm_i8_vector: C = A * B^T of row-major i8, exact i32) at the same
+        # shape, B rotating over 11 device copies (646 MB)
+        a_host = torch.randint(-128, 128, (M * K,), dtype=torch.int8, generator=gen)
+        b_host = torch.randint(-128, 128, (N * K,), dtype=torch.int8, generator=gen)
+        ai8 = a_host.to(dev)
+        bi8 = [b_host.to(dev) for _ in range(11)]
+        ci8 = torch.empty(M * N, dtype=torch.int32, device=dev)
+        us = gus(lambda i, st: jk.dev_gemm_i8(ai8, M * K, M, bi8[i % len(bi8)], N * K, 0, N, K, ci8, M * N, st),
+                 len(bi8))
+        tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        name = f"gemm_i8 {M}x{N}x{K}"
+        secondary[name] = {"us": round(us, 3), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                           "bound": "mfma", "workload": f"C = A * B^T, A {M}x{K} and B {N}x{K} row-major i8, exact i32 "
+                                                        "outputs (gemm_i8_vector), kernel only"}
+        log(f"  {name:28s} {us:8.2f} us  {tops:7.2f} TOPS")
+        cpu_jobs.append(("gemm_i8", name, a_host.numpy(), b_host.numpy(), M, N, K))
+        del ai8, bi8, ci8
         # f32-activation vec_dot of the other K-quants at the 4096x4096 attention shape
         for quant in (jk.Q5_K, jk.Q2_K, jk.Q3_K):
             rows, cols = 4096, 4096
@@ -811,7 +828,14 @@ def main() -> int:
             sec = secondary.get(job[1])
             if sec is None:
                 continue
-            if job[0] == "gemv":
+            if job[0] == "gemm_i8":
+                _, name, ah, bh, M, N, K = job
+                R = 64
+                sl = [(lambda r0=r0: O.gemm_i8_vector(ah, M, bh, r0, min(N, r0 + R), K), 2.0 * M * (min(N, r0 + R) - r0) * K)
+                      for r0 in range(0, N, R)]
+                attach(sec, "TOPS", 1e12, cpu_rate(sl, 2.0, 1), cpu_rate(sl, 1.0, ncores),
+                       f"slices of {R} rows of B x {M} rows of A of the same product")
+            elif job[0] == "gemv":
                 _, name, quant, rows, cols, data, xh, b = job
                 xb = O.quantize_row_q8_0(xh)
                 one = [(lambda: O.gemv_q8(quant, (rows, cols), data, xb, rows), b)]

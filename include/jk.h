@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define JK_ABI_VERSION 3
+#define JK_ABI_VERSION 4
 
 typedef enum jk_status {
     JK_OK = 0,
@@ -407,6 +407,36 @@ jk_status jk_bitlinear_i8_tol(jk_stream s, const jk_weight *w, const int8_t *act
  * the 256 trits of I2_S blocks 2k and 2k + 1 (32 bytes each). i2s_blocks must be 2 * tq2_blocks. */
 jk_status jk_convert_i2_s_to_tq2_0(jk_stream s, const void *i2s, size_t i2s_blocks, uint16_t scale_f16_bits,
                                    void *tq2, size_t tq2_blocks);
+
+/* ------------------------------------------------------- int8 primitives */
+/* Exact i32 results on the int8 matrix cores, equal to the reference's while no sum overflows
+ * i32: k (or 16 * k_chunks) is at most 131071, JK_TENSOR_BOUNDS beyond. Device pointers; a slice
+ * shorter than its indexing needs (a panic in the reference) is JK_TENSOR_BOUNDS. */
+/* gemm_i8_vector (ime.rs:563-583): C = A * B^T for the rows n0..n1 of B. a: m x k row-major
+ * (a_len >= m * k), b: row-major rows of k (b_len >= n1 * k); c[row][n - n0], m x (n1 - n0),
+ * receives what the reference's sink(row, n, value) gets. Adds m * (n1 - n0) to the vector-dot
+ * counter. Any k and alignment; k a multiple of 16 with 16-byte aligned a and b is fastest. */
+jk_status jk_gemm_i8(jk_stream s, const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0,
+                     size_t n1, size_t k, int32_t *c, size_t c_len);
+/* gemm_i8_ime (ime.rs:449-486) on pack_tiles layouts: a_packed holds m_tiles tile rows and
+ * b_packed at least nt1, each k_chunks 128-byte tiles of 8 rows x 16 (16-byte aligned); c receives
+ * the 8 x 8 tile (mt, nt) of sink(mt, nt, tile) at c[(mt * (nt1 - nt0) + nt - nt0) * 64 ..], row i of A
+ * and row j of B at i * 8 + j. Adds m_tiles * (nt1 - nt0) * k_chunks to the matrix tile counter,
+ * as the reference adds one 8 x 8 x 16 tile step per chunk. */
+jk_status jk_gemm_i8_tiles(jk_stream s, const int8_t *a_packed, size_t a_len, size_t m_tiles, const int8_t *b_packed,
+                           size_t b_len, size_t nt0, size_t nt1, size_t k_chunks, int32_t *c, size_t c_len);
+/* pack_tiles (ime.rs:81-94): rows x k row-major (src_len == rows * k, k a multiple of 16) into
+ * [row_tile][k_chunk][8][16], rows past the last zero-filled; dst_len == tile_count(rows) * (k / 16) * 128. */
+jk_status jk_pack_tiles_i8(jk_stream s, const int8_t *src, size_t src_len, size_t rows, size_t k, int8_t *dst,
+                           size_t dst_len);
+/* dot_i8_vector (ime.rs:548-557): *out = sum of a[i] * b[i] over the min(a_len, b_len) pairs of the
+ * two slices (the reference zips them); 0 for none. */
+jk_status jk_dot_i8(jk_stream s, const int8_t *a, size_t a_len, const int8_t *b, size_t b_len, int32_t *out);
+/* ime_vmadot_count / vector_dot_count (ime.rs:53-66): monotonic per-process counters. The first
+ * counts 8 x 8 x 16 tile steps of jk_gemm_i8_tiles; the second the dot products of jk_gemm_i8 and of
+ * the BitLinear entry points (one per weight block and token, as bitlinear_i8_rvv counts). Counted
+ * when a launch is issued. Either pointer may be NULL. */
+void jk_op_counts(uint64_t *matrix_tile_steps, uint64_t *vector_dots);
 
 /* ------------------------------------------- host tier (synchronous mirrors) */
 /* The jk_host_* mirrors run on a per-thread stream and per-thread device scratch (grown on

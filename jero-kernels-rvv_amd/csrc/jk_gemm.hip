@@ -911,35 +911,8 @@ template <int TN> struct alignas(16) Q8Stage {
     uint16_t ws[TN * 4];
     float xs[128 * 4];
 };
-typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
-
-// One global-to-LDS load of 16 (or 4) bytes per lane into the LDS span starting at byte lds
-// (M0). Written as inline asm so that the compiler's wait insertion, which cannot tell the two
-// stages' loads apart across the loop, does not drain the other stage's loads before every
-// read of this one; the kernel waits for its own loads explicitly (vmcnt) instead. No
-// compiler-issued global load shares the loop, so those explicit counts are exact.
-__device__ __forceinline__ void lds_dma16(const void *src, const lds_u8_t *lds) {
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"((unsigned)(size_t)lds) : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const void *src, const lds_u8_t *lds) {
-    asm volatile("global_load_lds_dword %0, off" ::"v"(src), "{m0}"((unsigned)(size_t)lds) : "memory");
-}
-
-// s_waitcnt vmcnt(n) (GFX9 encoding; expcnt and lgkmcnt left unconstrained)
-#define JK_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | (7 << 4) | (15 << 8))
 // loads per wave and stage (NW = TN / 32 waves): 4 weight, 16 / NW activation, 1 scale, 8 / NW act scale
 template <int TN> constexpr int kQ8DmaPerWave = 4 + 16 / (TN / 32) + 1 + 8 / (TN / 32);
-
-// Workgroup barrier between the stage phases with the waits made explicit: a wave has already
-// waited for its own loads into the stage (vmcnt) and waits here for its own LDS reads (lgkmcnt);
-// the compiler-only fences keep memory accesses on their side of the barrier. (A release fence
-// would also wait for the loads into the other stage: LDS-bound loads count as LDS writes.)
-__device__ __forceinline__ void stage_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // lgkmcnt(0)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 template <int TN>
 __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_act_q8 &a, float *__restrict__ y, int r0,

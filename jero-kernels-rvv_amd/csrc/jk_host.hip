@@ -742,6 +742,7 @@ jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view 
     JK_TRY(h2d(ctx, sc.p[1], &act_scale, sizeof(float)));
     JK_TRY(launch_bitlinear(ctx->stream, rw.w->dev, (const int8_t *)sc.p[0], (const float *)sc.p[1], 1,
                             (float *)sc.p[2]));
+    count_vector_dots((uint64_t)out_len * (uint64_t)(act_len / fmt_of(q).be));  // as bitlinear_i8_rvv (ime.rs:919-936)
     return d2h_sync(ctx, out, sc.p[2], out_len * sizeof(float));
 }
 

@@ -179,6 +179,9 @@ void clear_error();
 jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, size_t in_len, size_t *rows,
                           size_t *cols);
 
+// Adds to the crate's vector-dot operation counter (vector_dot_count, ime.rs:53-66).
+void count_vector_dots(uint64_t n);
+
 // Checks the last kernel launch on the current thread.
 jk_status check_launch(const char *what);
 

@@ -950,20 +950,33 @@ static jk_status bitlinear_check(const jk_weight *w, const int8_t *act, const fl
     return JK_OK;
 }
 
+// bitlinear_i8_rvv adds one dot_i8_vector call per weight block and token to the crate's vector-dot
+// counter (ime.rs:919-936); the batched kernels count the same
+static void count_bitlinear_dots(const jk_weight *w, size_t m) {
+    count_vector_dots((uint64_t)m * (uint64_t)w->dev.rows * (uint64_t)(w->dev.cols / fmt_of(w->quant).be));
+}
+
 jk_status jk_bitlinear_i8(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
                           size_t k, float *y, size_t y_len) {
     JK_TRY(bitlinear_check(w, act, act_scales, m, k, y, y_len));
     // batches of tokens run as an int8-MFMA GEMM (same per-block arithmetic and block order)
-    if (m >= (size_t)kBitlinearMfmaMinTokens) return launch_bitlinear_mfma((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
-    return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
+    if (m >= (size_t)kBitlinearMfmaMinTokens)
+        JK_TRY(launch_bitlinear_mfma((hipStream_t)s, w->dev, act, act_scales, (int)m, y));
+    else
+        JK_TRY(launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y));
+    count_bitlinear_dots(w, m);
+    return JK_OK;
 }
 
 jk_status jk_bitlinear_i8_tol(jk_stream s, const jk_weight *w, const int8_t *act, const float *act_scales, size_t m,
                               size_t k, float *y, size_t y_len) {
     JK_TRY(bitlinear_check(w, act, act_scales, m, k, y, y_len));
     if (m >= (size_t)kBitlinearMfmaMinTokens)
-        return launch_bitlinear_mfma_tol((hipStream_t)s, w->dev, act, act_scales, (int)m, y);
-    return launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y);  // bit-exact rows
+        JK_TRY(launch_bitlinear_mfma_tol((hipStream_t)s, w->dev, act, act_scales, (int)m, y));
+    else
+        JK_TRY(launch_bitlinear((hipStream_t)s, w->dev, act, act_scales, (int)m, y));  // bit-exact rows
+    count_bitlinear_dots(w, m);
+    return JK_OK;
 }
 
 // Which kernel a jk_bitlinear_i8 (tolerance 0) or jk_bitlinear_i8_tol (1) call of m tokens on w

@@ -754,6 +754,38 @@ def dev_gemv_q8_argmax_noalloc(w: Weight, x_q8, x_f32, x_len, y, index, stream=N
                                            _sz(x_len), _vp(_ptr(y)), _vp(_ptr(index))))
 
 
+def dev_gemm_i8(a, a_len, m, b, b_len, n0, n1, k, c, c_len, stream=None):
+    """jk_gemm_i8: gemm_i8_vector (ime.rs:563-583), c[row][n - n0] in exact i32."""
+    _check(lib().jk_gemm_i8(_vp(stream or 0), _vp(_ptr(a)), _sz(a_len), _sz(m), _vp(_ptr(b)), _sz(b_len), _sz(n0),
+                            _sz(n1), _sz(k), _vp(_ptr(c)), _sz(c_len)))
+
+
+def dev_gemm_i8_tiles(a_packed, a_len, m_tiles, b_packed, b_len, nt0, nt1, k_chunks, c, c_len, stream=None):
+    """jk_gemm_i8_tiles: gemm_i8_ime (ime.rs:449-486) over pack_tiles layouts, 8 x 8 i32 tiles."""
+    _check(lib().jk_gemm_i8_tiles(_vp(stream or 0), _vp(_ptr(a_packed)), _sz(a_len), _sz(m_tiles),
+                                  _vp(_ptr(b_packed)), _sz(b_len), _sz(nt0), _sz(nt1), _sz(k_chunks), _vp(_ptr(c)),
+                                  _sz(c_len)))
+
+
+def dev_pack_tiles_i8(src, src_len, rows, k, dst, dst_len, stream=None):
+    """jk_pack_tiles_i8: pack_tiles (ime.rs:81-94) on the device."""
+    _check(lib().jk_pack_tiles_i8(_vp(stream or 0), _vp(_ptr(src)), _sz(src_len), _sz(rows), _sz(k), _vp(_ptr(dst)),
+                                  _sz(dst_len)))
+
+
+def dev_dot_i8(a, a_len, b, b_len, out, stream=None):
+    """jk_dot_i8: dot_i8_vector (ime.rs:548-557) over the zip of the two slices, one i32."""
+    _check(lib().jk_dot_i8(_vp(stream or 0), _vp(_ptr(a)), _sz(a_len), _vp(_ptr(b)), _sz(b_len), _vp(_ptr(out))))
+
+
+def op_counts() -> tuple[int, int]:
+    """jk_op_counts: (ime_vmadot_count, vector_dot_count) of ime.rs:53-66 -- tile steps of
+    jk_gemm_i8_tiles and dot products of jk_gemm_i8 and the BitLinear entry points."""
+    t, v = C.c_uint64(0), C.c_uint64(0)
+    lib().jk_op_counts(C.byref(t), C.byref(v))
+    return t.value, v.value
+
+
 def dev_measure_stream_read(buf, nbytes, sink, stream=None):
     """jk_measure_stream_read: a plain streaming read of nbytes of device memory (the roofline
     the GEMV launches are placed against)."""

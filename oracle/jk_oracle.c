@@ -1593,3 +1593,58 @@ long or_argmax_f32(const float *x, size_t n) {
     return best;
 }
 
+
+/* ------------------------------------------------------------------------- */
+/* int8 primitives (ime.rs)                                                   */
+/* ------------------------------------------------------------------------- */
+
+/* dot_i8_scalar (ime.rs:490-496): a.iter().zip(b).map(i32 product).sum() */
+int32_t or_dot_i8(const int8_t *a, size_t a_len, const int8_t *b, size_t b_len) {
+    size_t n = a_len < b_len ? a_len : b_len;
+    int32_t s = 0;
+    for (size_t i = 0; i < n; i++) s += (int32_t)a[i] * (int32_t)b[i];
+    return s;
+}
+
+/* gemm_i8_vector (ime.rs:563-583): for n in n_range, for row in 0..m, one dot per output */
+void or_gemm_i8_vector(int32_t *c, const int8_t *a, size_t m, const int8_t *b, size_t n0, size_t n1, size_t k) {
+    for (size_t n = n0; n < n1; n++)
+        for (size_t row = 0; row < m; row++)
+            c[row * (n1 - n0) + (n - n0)] = or_dot_i8(a + row * k, k, b + n * k, k);
+}
+
+/* pack_tiles (ime.rs:81-94): [row_tile][k_chunk][8][16], missing rows zero */
+int or_pack_tiles(int8_t *out, size_t out_len, const int8_t *src, size_t src_len, size_t rows, size_t k) {
+    if (k % 16 != 0 || src_len != rows * k) return OR_TENSOR_BOUNDS;
+    size_t kc = k / 16;
+    if (out_len != (rows + 7) / 8 * kc * 128) return OR_TENSOR_BOUNDS;
+    memset(out, 0, out_len);
+    for (size_t row = 0; row < rows; row++) {
+        size_t tile = row / 8, r = row % 8;
+        for (size_t chunk = 0; chunk < kc; chunk++)
+            memcpy(out + (tile * kc + chunk) * 128 + r * 16, src + row * k + chunk * 16, 16);
+    }
+    return OR_OK;
+}
+
+/* tile_dot_scalar_rows (ime.rs:127-148): c[i * 8 + j] += a[i][k] * b[j][k] per chunk, rows i < active_m */
+void or_tile_dot_scalar_rows(int32_t *c, const int8_t *a, const int8_t *b, size_t k_chunks, size_t active_m) {
+    memset(c, 0, 64 * sizeof(int32_t));
+    size_t mb = active_m < 8 ? active_m : 8;
+    for (size_t chunk = 0; chunk < k_chunks; chunk++) {
+        const int8_t *at = a + chunk * 128, *bt = b + chunk * 128;
+        for (size_t i = 0; i < mb; i++)
+            for (size_t j = 0; j < 8; j++)
+                for (size_t kk = 0; kk < 16; kk++) c[i * 8 + j] += (int32_t)at[i * 16 + kk] * (int32_t)bt[j * 16 + kk];
+    }
+}
+
+/* gemm_i8_ime (ime.rs:449-486), the non-RISC-V arm: tile_dot_scalar (ime.rs:152-156) per pair */
+void or_gemm_i8_ime(int32_t *c, const int8_t *a_packed, size_t m_tiles, const int8_t *b_packed, size_t nt0,
+                    size_t nt1, size_t k_chunks) {
+    size_t stride = k_chunks * 128;
+    for (size_t nt = nt0; nt < nt1; nt++)
+        for (size_t mt = 0; mt < m_tiles; mt++)
+            or_tile_dot_scalar_rows(c + (mt * (nt1 - nt0) + (nt - nt0)) * 64, a_packed + mt * stride,
+                                    b_packed + nt * stride, k_chunks, 8);
+}

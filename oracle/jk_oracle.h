@@ -212,6 +212,20 @@ long or_argmax_f32(const float *x, size_t n);
 int or_bitlinear_i8(float *out, size_t out_len, const or_tensor_view *w, const int8_t *act,
                     size_t act_len, float act_scale);
 
+/* ---- int8 primitives (ime.rs) ---- */
+/* dot_i8_scalar (ime.rs:490-496): the sum over the min(a_len, b_len) pairs of the zip. */
+int32_t or_dot_i8(const int8_t *a, size_t a_len, const int8_t *b, size_t b_len);
+/* gemm_i8_vector (ime.rs:563-583) with the sink storing c[row][n - n0]. */
+void or_gemm_i8_vector(int32_t *c, const int8_t *a, size_t m, const int8_t *b, size_t n0, size_t n1, size_t k);
+/* pack_tiles (ime.rs:81-94): OR_TENSOR_BOUNDS where the reference asserts (k % 16, lengths). */
+int or_pack_tiles(int8_t *out, size_t out_len, const int8_t *src, size_t src_len, size_t rows, size_t k);
+/* tile_dot_scalar_rows (ime.rs:127-148) */
+void or_tile_dot_scalar_rows(int32_t *c, const int8_t *a, const int8_t *b, size_t k_chunks, size_t active_m);
+/* gemm_i8_ime (ime.rs:449-486) off the RISC-V target: tile_dot_scalar per tile pair, the sink
+ * storing tile (mt, nt) at c[(mt * (nt1 - nt0) + nt - nt0) * 64]. */
+void or_gemm_i8_ime(int32_t *c, const int8_t *a_packed, size_t m_tiles, const int8_t *b_packed, size_t nt0,
+                    size_t nt1, size_t k_chunks);
+
 #ifdef __cplusplus
 }
 #endif

@@ -320,6 +320,52 @@ def bitlinear_i8(quant: int, shape, data: np.ndarray, act: np.ndarray, act_scale
     return out
 
 
+# ----------------------------------------------------------------- int8 primitives
+def dot_i8(a: np.ndarray, b: np.ndarray) -> int:
+    """dot_i8_scalar (ime.rs:490-496) over the zip of the two slices."""
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.int8).reshape(-1)
+    return int(lib().or_dot_i8(_p(a), _sz(a.size), _p(b), _sz(b.size)))
+
+
+def gemm_i8_vector(a: np.ndarray, m: int, b: np.ndarray, n0: int, n1: int, k: int) -> np.ndarray:
+    """gemm_i8_vector (ime.rs:563-583): [m][n1 - n0] i32."""
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.int8).reshape(-1)
+    assert a.size >= m * k and b.size >= n1 * k
+    c = np.zeros(m * (n1 - n0), dtype=np.int32)
+    lib().or_gemm_i8_vector(_p(c), _p(a), _sz(m), _p(b), _sz(n0), _sz(n1), _sz(k))
+    return c.reshape(m, n1 - n0)
+
+
+def pack_tiles(src: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """pack_tiles (ime.rs:81-94)."""
+    s = np.ascontiguousarray(src, dtype=np.int8).reshape(-1)
+    out = np.zeros((rows + 7) // 8 * (k // 16) * 128, dtype=np.int8)
+    _ok(lib().or_pack_tiles(_p(out), _sz(out.size), _p(s), _sz(s.size), _sz(rows), _sz(k)), "pack_tiles")
+    return out
+
+
+def tile_dot_scalar_rows(a: np.ndarray, b: np.ndarray, k_chunks: int, active_m: int) -> np.ndarray:
+    """tile_dot_scalar_rows (ime.rs:127-148): 64 i32."""
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.int8).reshape(-1)
+    assert a.size >= 128 * k_chunks and b.size >= 128 * k_chunks
+    c = np.zeros(64, dtype=np.int32)
+    lib().or_tile_dot_scalar_rows(_p(c), _p(a), _p(b), _sz(k_chunks), _sz(active_m))
+    return c
+
+
+def gemm_i8_ime(a_packed: np.ndarray, m_tiles: int, b_packed: np.ndarray, nt0: int, nt1: int, k_chunks: int):
+    """gemm_i8_ime (ime.rs:449-486): [m_tiles][nt1 - nt0][64] i32."""
+    a = np.ascontiguousarray(a_packed, dtype=np.int8).reshape(-1)
+    b = np.ascontiguousarray(b_packed, dtype=np.int8).reshape(-1)
+    assert a.size >= m_tiles * k_chunks * 128 and b.size >= nt1 * k_chunks * 128
+    c = np.zeros(m_tiles * (nt1 - nt0) * 64, dtype=np.int32)
+    lib().or_gemm_i8_ime(_p(c), _p(a), _sz(m_tiles), _p(b), _sz(nt0), _sz(nt1), _sz(k_chunks))
+    return c.reshape(m_tiles, nt1 - nt0, 64)
+
+
 # ----------------------------------------------------------------- gated activations, argmax
 def swiglu_f32(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     g = np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)

@@ -16,7 +16,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert len(names) > 40
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.jk_abi_version() == 3
+    assert lib.jk_abi_version() == 4
 
 
 def test_block_struct_layouts():
