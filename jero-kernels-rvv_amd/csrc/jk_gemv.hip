@@ -74,9 +74,16 @@ struct VdSumTol {
     __device__ __forceinline__ float get() const { return (a + b) + (c + d); }
 };
 
-template <int Q, bool TOL = false>
+// NP > 1 (tolerance mode only): the products of part PART of NP equal runs of the block's
+// elements; every element index below is a constant once unrolled, so the other parts' work
+// (their dequantization and, where unused, their loads) is not emitted.
+template <int Q, bool TOL = false, int NP = 1, int PART = 0>
 __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__restrict__ xb, float i2s_scale) {
+    static_assert(NP == 1 || TOL, "a block's elements split over lanes only in tolerance mode");
     std::conditional_t<TOL, VdSumTol, VdSum> sum;
+    auto add = [&](float wv, int idx) {
+        if (NP == 1 || idx * NP / VdFmt<Q>::E == PART) sum.add(wv, xb[idx]);
+    };
     if constexpr (Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_Q8_0) {
         // dequantize_q4_0_block / dequantize_q8_0_block (quant.rs:550-588), dequantize_q5_0_block
         // (160-164, scale_i8_into_f32 94-102). The reference writes +0.0 for d == 0 where d * q
@@ -92,7 +99,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                 qv = (int)(((vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u) | (((o.h[0] >> i) & 1u) << 4)) - 16;
             else qv = (int)(int8_t)vd_byte<Q>(o, i >> 4, i & 15);
             const float wv = d * (float)qv;
-            sum.add(wv, xb[i]);
+            add(wv, i);
         }
     } else if constexpr (Q == JK_Q4_K) {
         // dequantize_q4_k_m_block (lib.rs:720-766): y = d1 * q - m1, two roundings
@@ -112,7 +119,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                 for (int l = 0; l < 32; ++l) {
                     const uint32_t q = (vd_byte<Q>(o, 1 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u;
                     const float wv = d1 * (float)q - m1;
-                    sum.add(wv, xb[64 * c + 32 * hi + l]);
+                    add(wv, 64 * c + 32 * hi + l);
                 }
             }
         }
@@ -126,7 +133,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
             uint32_t q = (vd_byte<Q>(o, 0, i & 15) >> (i < 16 ? 0 : 4)) & 15u;
             if constexpr (Q == JK_Q5_1) q |= ((o.h[1] >> i) & 1u) << 4;
             const float wv = z ? 0.0f : d * (float)q + m;
-            sum.add(wv, xb[i]);
+            add(wv, i);
         }
     } else if constexpr (Q == JK_IQ4_NL) {
         // dequantize_iq4_nl_block (quant.rs:348-356): d * KVALUES_IQ4NL[nibble] (+0.0 for d == 0,
@@ -136,13 +143,13 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
         for (int k = 0; k < 4; ++k) {
             const uint32_t lo = iq4nl_lookup(comp(o.c[0], k) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum.add((d * (float)(int8_t)(lo >> (8 * i))), xb[4 * k + i]);
+            for (int i = 0; i < 4; ++i) add((d * (float)(int8_t)(lo >> (8 * i))), 4 * k + i);
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t hi = iq4nl_lookup((comp(o.c[0], k) >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum.add((d * (float)(int8_t)(hi >> (8 * i))), xb[16 + 4 * k + i]);
+            for (int i = 0; i < 4; ++i) add((d * (float)(int8_t)(hi >> (8 * i))), 16 + 4 * k + i);
         }
     } else if constexpr (Q == JK_Q2_K) {
         // dequantize_q2_k_block (quant.rs:238-252): element 128 half + 32 j + 16 part + l is the
@@ -157,7 +164,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
             for (int k = 0; k < 4; ++k) {
                 const uint32_t v = (comp(o.c[1 + 2 * half + part], k) >> (2 * j)) & 0x03030303u;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sum.add((dl * (float)((v >> (8 * i)) & 3u) - ml), xb[16 * g + 4 * k + i]);
+                for (int i = 0; i < 4; ++i) add((dl * (float)((v >> (8 * i)) & 3u) - ml), 16 * g + 4 * k + i);
             }
         }
     } else if constexpr (Q == JK_Q3_K) {
@@ -179,7 +186,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int qv = (int)((v >> (8 * i)) & 3u) - ((h >> (8 * i)) & 1u ? 0 : 4);
-                    sum.add((dl * (float)qv), xb[16 * g + 4 * k + i]);
+                    add((dl * (float)qv), 16 * g + 4 * k + i);
                 }
             }
         }
@@ -204,7 +211,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
                     const uint32_t q = ((vd_byte<Q>(o, 3 + 2 * c + (l >> 4), l & 15) >> (4 * hi)) & 15u) |
                                        (((vd_byte<Q>(o, 1 + (l >> 4), l & 15) >> (2 * c + hi)) & 1u) << 4);
                     const float wv = d1 * (float)q - m1;
-                    sum.add(wv, xb[64 * c + 32 * hi + l]);
+                    add(wv, 64 * c + 32 * hi + l);
                 }
             }
         }
@@ -234,7 +241,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const float wv = s4 * (float)(int8_t)(w4 >> (8 * i));
-                        sum.add(wv, xb[128 * h + 32 * quarter + l + i]);
+                        add(wv, 128 * h + 32 * quarter + l + i);
                     }
                 }
                 // the chain is serial: an empty asm with a memory clobber keeps the next 32
@@ -246,7 +253,7 @@ __device__ __forceinline__ float vd_block(const VdBlock<Q> &o, const float *__re
         for (int e = 0; e < 128; ++e) {
             const int grp = e >> 5, g = e & 31;
             const int t = (int)((vd_byte<Q>(o, g >> 4, g & 15) >> (6 - 2 * grp)) & 3u) - 1;
-            sum.add((i2s_scale * (float)t), xb[e]);
+            add((i2s_scale * (float)t), e);
         }
     }
     return sum.get();
@@ -296,12 +303,80 @@ __global__ __launch_bounds__(64 * kVdWaves) __attribute__((amdgpu_waves_per_eu(4
     if (row < w.rows && p == writer) y[row] = acc;
 }
 
+// Tolerance mode for rows of at most 32 blocks: the lane mapping of the 16-lane kernel (16 lanes
+// per row, lane p on blocks p and p + 16), with each block's elements split in four runs over
+// four waves of the workgroup (wave w: run w % 4). A lane's chain is a quarter as long and the
+// launch has four times the waves (Q4_K 4096 rows: 4096 waves instead of 1024 on 128 of the
+// CUs). The 16 lanes of a row and the four runs are added in any order (shuffles, then LDS).
+constexpr int kVdParts = 4;
+constexpr int kVdPartRows = kVdWaves / kVdParts * 4;  // rows per workgroup
+
+// One wave's share: the runs PART of the blocks of its lanes (one or two blocks a lane), summed
+// over the 16 lanes of each row into s_part.
+template <int Q, int PART>
+__device__ __forceinline__ void vd_parts_wave(const WeightDev &w, const float *xs, int xstride, int r, int p, int sub,
+                                              float *s_part_wave) {
+    const int nb = w.nb;
+    VdBlock<Q> b0, b1;
+    vd_load<Q>(b0, w, r, min(p, nb - 1));
+    if (nb > 16) vd_load<Q>(b1, w, r, min(16 + p, nb - 1));
+    float v = p < nb ? vd_block<Q, true, kVdParts, PART>(b0, xs + (size_t)xstride * p, w.tensor_scale) : 0.0f;
+    if (nb > 16 && 16 + p < nb)
+        v += vd_block<Q, true, kVdParts, PART>(b1, xs + (size_t)xstride * (16 + p), w.tensor_scale);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 16);
+    if (p == 0) s_part_wave[sub] = v;
+}
+
+template <int Q, bool XL>
+__global__ __launch_bounds__(64 * kVdWaves) __attribute__((amdgpu_waves_per_eu(4))) void vec_dot_f32_parts_kernel(
+    WeightDev w, const float *__restrict__ x, float *__restrict__ y) {
+    constexpr int E = VdFmt<Q>::E, XS = XL ? E + 4 : E;
+    extern __shared__ __align__(16) float s_xf[];
+    __shared__ float s_part[kVdWaves][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int part = wave % kVdParts, grp = wave / kVdParts;
+    const int sub = lane >> 4, p = lane & 15;
+    const int row0 = (int)blockIdx.x * kVdPartRows;
+    const int r = min(row0 + 4 * grp + sub, w.rows - 1);
+    if (Q == JK_I2_S && w.tensor_scale == 0.0f) {  // zero trailer scale: all outputs 0 (quant.rs:2219)
+        if (tid < kVdPartRows && row0 + tid < w.rows) y[row0 + tid] = 0.0f;
+        return;
+    }
+    const float *xs = x;
+    if constexpr (XL) {
+        const int n4 = w.cols / 4;
+        for (int i = tid; i < n4; i += 64 * kVdWaves)
+            reinterpret_cast<float4 *>(s_xf)[i + i / (E / 4)] = reinterpret_cast<const float4 *>(x)[i];
+        __syncthreads();
+        xs = s_xf;
+    }
+    switch (part) {  // wave-uniform
+    case 0: vd_parts_wave<Q, 0>(w, xs, XS, r, p, sub, s_part[wave]); break;
+    case 1: vd_parts_wave<Q, 1>(w, xs, XS, r, p, sub, s_part[wave]); break;
+    case 2: vd_parts_wave<Q, 2>(w, xs, XS, r, p, sub, s_part[wave]); break;
+    default: vd_parts_wave<Q, 3>(w, xs, XS, r, p, sub, s_part[wave]); break;
+    }
+    __syncthreads();
+    if (tid < kVdPartRows && row0 + tid < w.rows) {
+        const int g = tid >> 2, sr = tid & 3;
+        float t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kVdParts; ++k) t += s_part[g * kVdParts + k][sr];
+        y[row0 + tid] = t;
+    }
+}
+
 template <int Q, bool TOL>
 static jk_status launch_vd(hipStream_t s, const WeightDev &w, const float *x, float *y) {
     const size_t lds_need = (size_t)w.nb * (VdFmt<Q>::E + 4) * 4;  // padded blocks
     const bool xl = lds_need <= (size_t)kVdLdsMax;
     const size_t lds = xl ? lds_need : 0;
-    if (w.nb > 32) {
+    if (TOL && w.nb <= 32) {
+        const dim3 grid((unsigned)((w.rows + kVdPartRows - 1) / kVdPartRows));
+        if (xl) hipLaunchKernelGGL((vec_dot_f32_parts_kernel<Q, true>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
+        else hipLaunchKernelGGL((vec_dot_f32_parts_kernel<Q, false>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);
+    } else if (w.nb > 32) {
         const dim3 grid((unsigned)((w.rows + kVdWaves - 1) / kVdWaves));
         if (xl) hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, true, TOL>), grid, dim3(64 * kVdWaves), lds, s, w, x, y);
         else hipLaunchKernelGGL((vec_dot_f32_kernel<Q, 64, false, TOL>), grid, dim3(64 * kVdWaves), 0, s, w, x, y);

@@ -455,12 +455,13 @@ def test_vec_dot_f32(gpu, quant, rows, cols):
 
 
 @pytest.mark.parametrize("quant", list(jk.VEC_DOT_F32_FORMATS))
-@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 4096), (300, 4352), (9, 256 * 90)])
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 4096), (300, 4352), (11, 1024), (5, 8192), (9, 256 * 90)])
 def test_vec_dot_f32_tol(gpu, quant, rows, cols):
-    """Tolerance-mode f32 vec_dot (jk_vec_dot_f32_tol): rows of up to 32 blocks (16 lanes a row),
-    longer rows (64 lanes a row), activations too long for LDS (23040 columns), weights with special
-    scales. Every output within 1e-5 of the output vector's L2 norm of the oracle and of the
-    bit-exact GPU result."""
+    """Tolerance-mode f32 vec_dot (jk_vec_dot_f32_tol): rows of up to 32 blocks (each block's
+    elements split over four waves; one and two blocks a lane, exactly 32 blocks), longer rows
+    (64 lanes a row), activations too long for LDS (23040 columns), weights with special scales.
+    Every output within 1e-5 of the output vector's L2 norm of the oracle and of the bit-exact GPU
+    result."""
     torch = gpu
     raw = synth.random_weights(quant, rows, cols, seed=3 * rows + quant, specials=True)
     x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
@@ -487,6 +488,10 @@ def test_vec_dot_i2_s_zero_scale_rows_are_zero(gpu):
     jk.dev_vec_dot_f32(w, dev(torch, np.ones(cols, np.float32)), cols, dy, rows)
     torch.cuda.synchronize()
     assert same_bits(host(dy, np.float32, rows), np.zeros(rows, np.float32))
+    dt = empty(torch, 4 * rows)
+    jk.dev_vec_dot_f32_tol(w, dev(torch, np.ones(cols, np.float32)), cols, dt, rows)
+    torch.cuda.synchronize()
+    assert same_bits(host(dt, np.float32, rows), np.zeros(rows, np.float32))
 
 
 # ------------------------------------------------------------------ repacked GEMM
