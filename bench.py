@@ -885,7 +885,8 @@ def main() -> int:
                    "parallelism": "single_gpu"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "decode_tok_s_equiv": round(1e3 / ms_per_step * args.layers / 32, 1),
-        "roofline": roofline, "per_stage": per_stage, "gemm_q8_0": gemm, "gemm_q8_0_sweep": sweep,
+        "roofline": roofline, "per_stage": per_stage, "stream_read_ceiling": stream_ceiling,
+        "gemm_q8_0": gemm, "gemm_q8_0_sweep": sweep,
         "gemm_q8_0_bit_exact": gemm_exact, "gemm_q8_0_bit_exact_sweep": sweep_exact,
         "secondary": secondary,
         "cpu_baseline": cpu,

@@ -23,7 +23,9 @@
  * Numerics: activation quantization and block dequantization are bit-exact with the
  * reference's portable scalar fallback; dot products, GEMV, GEMM and BitLinear are
  * evaluated with the reference's per-block arithmetic and its block-order f32
- * accumulation, so they are bit-exact as well.
+ * accumulation, so they are bit-exact as well. The *_tol entry points (GEMM, BitLinear,
+ * f32 vec_dot) are opt-in alternatives held to 1e-5 of the output-row L2 norm instead, and
+ * the int8 primitives are exact integer sums.
  */
 #ifndef JK_H
 #define JK_H
@@ -329,10 +331,15 @@ jk_status jk_gemm_repacked(jk_stream s, const jk_weight *w, const jk_act_q8 *act
  * multiply-add (acc = fma(partial, xs * ws, acc); formats with mins add -(xsum * wm) as one more
  * rounded step) instead of the reference's separately rounded product and sum. Every output is
  * within 1e-5 of its token's output-row L2 norm of the bit-exact result (the tolerance the port
- * is held to for f32 products). From one 128 x 128 tile per CU on (14336 rows: 512 tokens), the
+ * is held to for f32 products). From 1.5 128 x 128 tiles per CU on (14336 rows: 448 tokens), the
  * 32-element-group formats run larger tiles with fewer VALU operations per scale group, about
- * 1.2x the throughput of jk_gemm_repacked; Q2_K, Q3_K and Q6_K run the bit-exact kernel. No
- * reference function has this rounding: it is the bit-exact call's alternative. */
+ * 1.2x the throughput of jk_gemm_repacked; Q8_0 there applies each group as
+ * fma(B + partial, ws * xs, acc - B * ws * xs) with B = 1.5 * 2^23 (the second product accumulated on
+ * the matrix core), so a scale product |ws * xs| above 2^104 can overflow to infinity where the
+ * bit-exact call stays finite. Q6_K and Q3_K combine a step's two 16-element groups in integers;
+ * Q2_K, and launches where the bit-exact tiles measured faster, run the bit-exact kernels (whose
+ * results meet the bar by definition). No reference function has this rounding: it is the
+ * bit-exact call's alternative. */
 jk_status jk_gemm_repacked_tol(jk_stream s, const jk_weight *w, const jk_act_q8 *act, float *y,
                                size_t y_len, size_t row_begin, size_t row_end);
 /* gemv_repacked_view_rows (repack.rs:4045-4061): requires act->m == 1. */
