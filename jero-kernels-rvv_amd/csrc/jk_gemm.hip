@@ -914,7 +914,9 @@ template <int TN> struct alignas(16) Q8Stage {
 // loads per wave and stage (NW = TN / 32 waves): 4 weight, 16 / NW activation, 1 scale, 8 / NW act scale
 template <int TN> constexpr int kQ8DmaPerWave = 4 + 16 / (TN / 32) + 1 + 8 / (TN / 32);
 
-template <int TN>
+// EXACT: the reference's epilogue instead, bit for bit -- the integer MFMA from zero, the scale
+// product from the outer-product MFMA, then acc = acc + f32(dot) * (xs * ws), each rounded, in K order.
+template <int TN, bool EXACT = false>
 __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_act_q8 &a, float *__restrict__ y, int r0,
                                                   int r1) {
     constexpr int TM = 128, NW = TN / 32, WR = TN / 64;  // waves; waves along the rows (64 rows each)
@@ -991,18 +993,31 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
                 const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ (t & 7)) << 4));
                 const float xs = S.xs[t * 4 + st];
                 v16i c[2];
+                if constexpr (EXACT) {
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, bias, 0, 0, 0);
-                const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
-                // the bias's share of the group, B * ws * xs, taken off the accumulators on the matrix
-                // core, so each output costs one fused multiply-add of the biased bits
-                tacc[tb] = __builtin_amdgcn_mfma_f32_32x32x1f32(wsb, xs, tacc[tb], 0, 0, 0);
+                    for (int nt = 0; nt < 2; ++nt)
+                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, v16i{0}, 0, 0, 0);
+                    const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
+                    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v)
-                        tacc[tb][16 * nt + v] =
-                            __builtin_fmaf(__int_as_float(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
+                        for (int v = 0; v < 16; ++v)
+                            tacc[tb][16 * nt + v] = tacc[tb][16 * nt + v] + (float)c[nt][v] * pr[16 * nt + v];
+                } else {
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, bias, 0, 0, 0);
+                    const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
+                    // the bias's share of the group, B * ws * xs, taken off the accumulators on the matrix
+                    // core, so each output costs one fused multiply-add of the biased bits
+                    tacc[tb] = __builtin_amdgcn_mfma_f32_32x32x1f32(wsb, xs, tacc[tb], 0, 0, 0);
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            tacc[tb][16 * nt + v] =
+                                __builtin_fmaf(__int_as_float(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
+                }
             }
         }
     };
@@ -1045,6 +1060,13 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 gemm_q8_0_tol_dma_128(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
     gemm_q8_0_tol_dma<128>(w, a, y, r0, r1);
+}
+
+// The bit-exact Q8_0 prefill on the same staging (one round of resident workgroups: 8% faster than
+// the register-staged 128 x 64 tiles at 448-512 tokens on 14336 rows, 2-3% slower at 768-1536)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gemm_q8_0_exact_dma_128(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
+    gemm_q8_0_tol_dma<128, true>(w, a, y, r0, r1);
 }
 
 static long cu_count() {
@@ -1951,6 +1973,19 @@ static void launch_tile(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, f
 
 template <int Q, int GB>
 static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
+    if constexpr (Q == JK_Q8_0 && GB == 1) {
+        // Q8_0 with per-32 activation scales (not BitLinear's one scale per token), whole 128-element
+        // chunks, 1.5 to 2 128 x 128 tiles per CU (one round of two resident workgroups a CU): the
+        // global-to-LDS staged tiles
+        const long ncu = cu_count();
+        const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
+        if (2 * t128 >= 3 * ncu && t128 <= 2 * ncu && w.cols % 128 == 0 && a.k_blocks32 * 32 == (size_t)w.cols) {
+            const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
+            JK_LAUNCH("gemm_q8_0_exact_dma_128", gemm_q8_0_exact_dma_128, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
+                      dim3(256), 0, s, w, a, y, r0, r1);
+            return check_launch("gemm_q8_0_exact_dma");
+        }
+    }
     switch (gemm_tile(Q, r1 - r0, (long)a.m)) {
     case 0:
         if constexpr (GemmFmt<Q>::GK == 32) launch_tile<Q, GB, 128, 64>(s, w, a, y, r0, r1);

@@ -714,6 +714,31 @@ def test_gemm_tol_extreme_group_dots(gpu):
     w.free()
 
 
+def test_gemm_q8_0_exact_staged_tiles(gpu):
+    """The bit-exact Q8_0 GEMM on the global-to-LDS staged 128 x 128 tiles (launched for 1.5 to 2 such
+    tiles per CU): ragged rows (12328 = 96 x 128 + 40) and tokens (500 = 3 x 128 + 116), adversarial
+    weights and activations, a row slice; equal to the oracle bit for bit on row windows at both ends
+    and inside, every token. BitLinear's Q8_0 weights (one activation scale per token) keep the
+    register-staged tiles."""
+    torch = gpu
+    rows, cols, m = 12328, 512, 500
+    raw = synth.random_weights(Q8_0, rows, cols, seed=11, specials=True)
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((m, cols)) * rng.choice([1e-3, 1, 40], (m, cols))).astype(np.float32)
+    x[rng.random((m, cols)) < 0.002] = np.nan
+    w = jk.Weight(jk.TensorView("w", Q8_0, [rows, cols], raw), rows, cols)
+    storage, act = gpu_act(torch, x, m, cols)
+    assert jk.gemm_plan(w, act, 0, rows, False) == "gemm_q8_0_exact_dma_128"
+    got = gpu_gemm(torch, w, x, m)
+    oact = O.ActQ8(x, m, cols)
+    for r0 in (0, 6000, rows - 40):
+        ref = O.gemm_repacked(Q8_0, [rows, cols], raw, rows, cols, oact, r0, r0 + 40)
+        assert same_bits(got[:, r0:r0 + 40], ref), (r0, mismatch(got[:, r0:r0 + 40], ref))
+    sub = gpu_gemm(torch, w, x, m, 1000, rows - 17)  # a row slice (ragged at both ends of its tiles)
+    assert same_bits(sub, got[:, 1000:rows - 17])
+    w.free()
+
+
 TOL128_FORMATS = [Q8_0, Q4_0, Q5_0, Q4_1, Q5_1, IQ4_NL, Q4_K, Q5_K, TQ2_0, I2_S]
 
 
