@@ -514,7 +514,7 @@ def main() -> int:
             us = gus(lambda i, st: jk.dev_vec_dot_f32_tol(ws[i % len(ws)], acts[xa], cols, y, rows, st), len(ws))
             hbm_line(name.replace(" f32", " f32 tolerance"), b, us,
                      f"{rows}x{cols}, f32 activation, within 1e-5 of the output's L2 norm (four FMA accumulators "
-                     "a block)")
+                     "a block; rows of up to 32 blocks: each block over four waves)")
             for w in ws:
                 w.free()
         # C5: ternary GEMV (Q8_K caller blocks) and BitLinear at batch 1 and 128
