@@ -536,6 +536,11 @@ jk_status jk_host_convert_i2_s_blocks_to_tq2_0(const uint8_t *blk0, const uint8_
 /* bitlinear_i8_rvv (ime.rs:882-938). */
 jk_status jk_host_bitlinear_i8(float *out, size_t out_len, const jk_tensor_view *w, const int8_t *act,
                                size_t act_len, float act_scale);
+/* gemm_i8_vector (ime.rs:563-583) and dot_i8_vector (ime.rs:548-557) on host slices: the arguments,
+ * checks and results of jk_gemm_i8 / jk_dot_i8 (c[row][n - n0]; the zip of the two slices). */
+jk_status jk_host_gemm_i8(const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0,
+                          size_t n1, size_t k, int32_t *c, size_t c_len);
+jk_status jk_host_dot_i8(const int8_t *a, size_t a_len, const int8_t *b, size_t b_len, int32_t *out);
 
 /* ---------------------------------------------------------------- measurement */
 

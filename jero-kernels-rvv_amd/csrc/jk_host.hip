@@ -686,6 +686,40 @@ jk_status jk_host_argmax_f32(const float *x, size_t n, int64_t *index) {
     return JK_OK;
 }
 
+// gemm_i8_vector (ime.rs:563-583) on host slices: c[row][n - n0]. Only A's m x k bytes and B's rows
+// n0..n1 cross PCIe.
+jk_status jk_host_gemm_i8(const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0,
+                          size_t n1, size_t k, int32_t *c, size_t c_len) {
+    clear_error();
+    JK_TRY(gemm_i8_check(a, a_len, m, b, b_len, n0, n1, k, c, c_len));
+    if (m == 0 || n1 == n0) return JK_OK;
+    HostCtx *ctx;
+    JK_TRY(ctx_get(&ctx));
+    Scratch sc{ctx};
+    const size_t na = m * k, nb = (n1 - n0) * k;
+    JK_TRY(sc.take({na, nb, c_len * sizeof(int32_t)}));
+    JK_TRY(h2d(ctx, sc.p[0], a, na));
+    JK_TRY(h2d(ctx, sc.p[1], b + n0 * k, nb));
+    JK_TRY(jk_gemm_i8(ctx->stream, (const int8_t *)sc.p[0], na, m, (const int8_t *)sc.p[1], nb, 0, n1 - n0, k,
+                      (int32_t *)sc.p[2], c_len));
+    return d2h_sync(ctx, c, sc.p[2], c_len * sizeof(int32_t));
+}
+
+// dot_i8_vector (ime.rs:548-557) on host slices, over the zip of the two.
+jk_status jk_host_dot_i8(const int8_t *a, size_t a_len, const int8_t *b, size_t b_len, int32_t *out) {
+    clear_error();
+    JK_TRY(dot_i8_check(a, a_len, b, b_len, out));
+    const size_t k = a_len < b_len ? a_len : b_len;
+    HostCtx *ctx;
+    JK_TRY(ctx_get(&ctx));
+    Scratch sc{ctx};
+    JK_TRY(sc.take({k, k, sizeof(int32_t)}));
+    JK_TRY(h2d(ctx, sc.p[0], a, k));
+    JK_TRY(h2d(ctx, sc.p[1], b, k));
+    JK_TRY(jk_dot_i8(ctx->stream, (const int8_t *)sc.p[0], k, (const int8_t *)sc.p[1], k, (int32_t *)sc.p[2]));
+    return d2h_sync(ctx, out, sc.p[2], sizeof(int32_t));
+}
+
 // convert_i2_s_blocks_to_tq2_0 (ime.rs:767-790): two 32-byte I2_S blocks and an f16 scale -> one
 // 66-byte TQ2_0 block.
 jk_status jk_host_convert_i2_s_blocks_to_tq2_0(const uint8_t *blk0, const uint8_t *blk1, uint16_t scale_f16_bits,

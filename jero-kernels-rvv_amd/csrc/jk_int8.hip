@@ -322,13 +322,12 @@ constexpr size_t kI8MaxRows = (size_t)1 << 28;
 
 }  // namespace jk
 
-using namespace jk;
+namespace jk {
 
-extern "C" {
-
-jk_status jk_gemm_i8(jk_stream s, const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0,
-                     size_t n1, size_t k, int32_t *c, size_t c_len) {
-    clear_error();
+// gemm_i8_vector's slice indexing (ime.rs:563-583) as argument checks: a panic there is
+// JK_TENSOR_BOUNDS here, before any copy or launch. Shared by the device and host entry points.
+jk_status gemm_i8_check(const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0, size_t n1,
+                        size_t k, const int32_t *c, size_t c_len) {
     if (m > kI8MaxRows || n1 > kI8MaxRows)
         return fail(JK_TENSOR_BOUNDS, "gemm_i8: %zu rows of A or n_range end %zu exceed 2^28", m, n1);
     if (k > (size_t)kI8MaxK)
@@ -342,6 +341,29 @@ jk_status jk_gemm_i8(jk_stream s, const int8_t *a, size_t a_len, size_t m, const
         return fail(JK_TENSOR_BOUNDS, "gemm_i8: output length %zu != m (%zu) * n_range (%zu)", c_len, m, n1 - n0);
     if (m == 0 || n1 == n0) return JK_OK;
     if (!c || (k > 0 && (!a || !b))) return fail(JK_TENSOR_BOUNDS, "gemm_i8: null pointer");
+    return JK_OK;
+}
+
+jk_status dot_i8_check(const int8_t *a, size_t a_len, const int8_t *b, size_t b_len, const int32_t *out) {
+    const size_t k = a_len < b_len ? a_len : b_len;  // the pairs of a zip of the two slices
+    if (k > (size_t)kI8MaxK)
+        return fail(JK_TENSOR_BOUNDS, "dot_i8: %zu pairs exceed %d (an i32 sum of products of i8 could overflow)", k,
+                    kI8MaxK);
+    if (!out || (k > 0 && (!a || !b))) return fail(JK_TENSOR_BOUNDS, "dot_i8: null pointer");
+    return JK_OK;
+}
+
+}  // namespace jk
+
+using namespace jk;
+
+extern "C" {
+
+jk_status jk_gemm_i8(jk_stream s, const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0,
+                     size_t n1, size_t k, int32_t *c, size_t c_len) {
+    clear_error();
+    JK_TRY(gemm_i8_check(a, a_len, m, b, b_len, n0, n1, k, c, c_len));
+    if (m == 0 || n1 == n0) return JK_OK;
     I8Args g{};
     g.a = a;
     g.b = b ? b + n0 * k : b;
@@ -418,11 +440,8 @@ jk_status jk_pack_tiles_i8(jk_stream s, const int8_t *src, size_t src_len, size_
 
 jk_status jk_dot_i8(jk_stream s, const int8_t *a, size_t a_len, const int8_t *b, size_t b_len, int32_t *out) {
     clear_error();
-    const size_t k = a_len < b_len ? a_len : b_len;  // the pairs of a zip of the two slices
-    if (k > (size_t)kI8MaxK)
-        return fail(JK_TENSOR_BOUNDS, "dot_i8: %zu pairs exceed %d (an i32 sum of products of i8 could overflow)", k,
-                    kI8MaxK);
-    if (!out || (k > 0 && (!a || !b))) return fail(JK_TENSOR_BOUNDS, "dot_i8: null pointer");
+    JK_TRY(dot_i8_check(a, a_len, b, b_len, out));
+    const size_t k = a_len < b_len ? a_len : b_len;
     hipLaunchKernelGGL(dot_i8_kernel, dim3(1), dim3(256), 0, (hipStream_t)s, a, b, (int)k,
                        (int)(aligned16(a) && aligned16(b)), out);
     return check_launch("dot_i8");

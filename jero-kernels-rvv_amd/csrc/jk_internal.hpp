@@ -181,6 +181,10 @@ jk_status validate_matvec(const jk_tensor_view *w, int quant, size_t out_len, si
 
 // Adds to the crate's vector-dot operation counter (vector_dot_count, ime.rs:53-66).
 void count_vector_dots(uint64_t n);
+// Argument checks of jk_gemm_i8 / jk_dot_i8, shared with their host-tier mirrors.
+jk_status gemm_i8_check(const int8_t *a, size_t a_len, size_t m, const int8_t *b, size_t b_len, size_t n0, size_t n1,
+                        size_t k, const int32_t *c, size_t c_len);
+jk_status dot_i8_check(const int8_t *a, size_t a_len, const int8_t *b, size_t b_len, const int32_t *out);
 
 // Checks the last kernel launch on the current thread.
 jk_status check_launch(const char *what);

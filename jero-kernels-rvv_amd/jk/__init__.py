@@ -778,6 +778,25 @@ def dev_dot_i8(a, a_len, b, b_len, out, stream=None):
     _check(lib().jk_dot_i8(_vp(stream or 0), _vp(_ptr(a)), _sz(a_len), _vp(_ptr(b)), _sz(b_len), _vp(_ptr(out))))
 
 
+def gemm_i8_vector(a: np.ndarray, m: int, b: np.ndarray, n0: int, n1: int, k: int) -> np.ndarray:
+    """gemm_i8_vector (ime.rs:563-583) through jk_host_gemm_i8: [m][n1 - n0] i32 of host slices."""
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.int8).reshape(-1)
+    c = np.zeros(max(m * (n1 - n0), 0), dtype=np.int32)
+    _check(lib().jk_host_gemm_i8(_vp(_ptr(a)), _sz(a.size), _sz(m), _vp(_ptr(b)), _sz(b.size), _sz(n0), _sz(n1),
+                                 _sz(k), _vp(_ptr(c)), _sz(c.size)))
+    return c.reshape(m, n1 - n0)
+
+
+def dot_i8_vector(a: np.ndarray, b: np.ndarray) -> int:
+    """dot_i8_vector (ime.rs:548-557) through jk_host_dot_i8, over the zip of the two slices."""
+    a = np.ascontiguousarray(a, dtype=np.int8).reshape(-1)
+    b = np.ascontiguousarray(b, dtype=np.int8).reshape(-1)
+    out = C.c_int32(0)
+    _check(lib().jk_host_dot_i8(_vp(_ptr(a)), _sz(a.size), _vp(_ptr(b)), _sz(b.size), C.byref(out)))
+    return out.value
+
+
 def op_counts() -> tuple[int, int]:
     """jk_op_counts: (ime_vmadot_count, vector_dot_count) of ime.rs:53-66 -- tile steps of
     jk_gemm_i8_tiles and dot products of jk_gemm_i8 and the BitLinear entry points."""

@@ -148,3 +148,23 @@ def test_op_counts(gpu):
     w.free()
     t3, v3 = jk.op_counts()
     assert (t3, v3 - v2) == (t2, m * rows * (cols // 256))
+
+
+def test_host_mirrors(gpu):
+    """jk_host_gemm_i8 / jk_host_dot_i8: gemm_i8_vector and dot_i8_vector on host slices (the
+    reference's signatures), equal to the oracle; short slices are TensorBoundsError."""
+    import jk
+
+    m, rows, k = 6, 12, 64
+    a, b = fill(m * k, 1), fill(rows * k, 2)
+    assert np.array_equal(jk.gemm_i8_vector(a, m, b, 3, 11, k), O.gemm_i8_vector(a, m, b, 3, 11, k))
+    rng = np.random.default_rng(9)
+    a2 = rng.integers(-128, 128, 33 * 1000, dtype=np.int8)
+    b2 = rng.integers(-128, 128, 70 * 1000, dtype=np.int8)
+    assert np.array_equal(jk.gemm_i8_vector(a2, 33, b2, 0, 70, 1000), O.gemm_i8_vector(a2, 33, b2, 0, 70, 1000))
+    assert jk.dot_i8_vector(a2[:999], b2[:1003]) == O.dot_i8(a2[:999], b2[:1003])
+    assert jk.dot_i8_vector(a2[:0], b2) == 0
+    with pytest.raises(jk.TensorBoundsError):
+        jk.gemm_i8_vector(a[:-1], m, b, 0, rows, k)  # A one byte short of m * k
+    with pytest.raises(jk.TensorBoundsError):
+        jk.gemm_i8_vector(a, m, b, 0, rows + 1, k)  # the range runs past B
