@@ -407,6 +407,15 @@ def main() -> int:
     # the graph's inter-launch gap). Bytes are algorithmic (weight bytes + activation + output).
     secondary = {}
     cpu_jobs = []  # (kind, line, ...): the same tensors and inputs, timed on the host by the CPU leg
+
+    def cpu_slices(name, make, unit, scale, what):
+        """The CPU leg times make(O) -> [(callable, units)] (row or token slices of the line's work,
+        built from the same host tensors) on one thread and on all cores."""
+        cpu_jobs.append(("slices", name, make, unit, scale, what))
+
+    def rows_of(data, quant, r0, r1, cols):
+        rb = cols // jk.BLOCK_ELEMENTS[quant] * jk.BLOCK_BYTES[quant]
+        return data[r0 * rb:r1 * rb]
     if not args.no_secondary and graph is not None:
         # The same step with ffn_down's input computed as in a Llama feed-forward block:
         # SwiGLU(gate, up) of the layer's own outputs, fused into the Q8_K quantizer.
@@ -479,6 +488,14 @@ def main() -> int:
             us = gus(lambda i, st: jk.dev_gemv_repacked(ws[i % len(ws)], act1, y, rows, 0, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + need + 4 * rows
             hbm_line(name, b, us, f"{rows}x{cols}, one token's QuantizedActQ8")
+
+            def mk(O, quant=quant, rows=rows, cols=cols, data=copies.data, b=b,
+                   x1=acts["x" if cols == 4096 else "h"].cpu().numpy()[None, :]):
+                q, sc, mn, cps = O.repack_logical(quant, (rows, cols), data, rows, cols)
+                a1, R = O.ActQ8(x1, 1, cols), 512
+                return [(lambda r0=r0: O.gemm_logical_rows(q, sc, mn, cps, cols, a1, 0, 1, r0, min(rows, r0 + R)),
+                         b * (min(rows, r0 + R) - r0) / rows) for r0 in range(0, rows, R)]
+            cpu_slices(name, mk, "GB/s", 1e9, "row slices of the repacked GEMV (the load-time repack not timed)")
             for w in ws:
                 w.free()
         # Q5_0 / Q5_K / TQ1_0 quant_q8 GEMV with caller blocks (GGUF bytes; TQ1_0 streams its
@@ -501,6 +518,12 @@ def main() -> int:
             us = gus(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // be, y, rows, st), len(ws))
             b = (gemv_bytes_q80 if small else gemv_bytes)(quant, rows, cols, jk)
             hbm_line(name, b, us, f"{rows}x{cols}, {'Q8_0' if small else 'Q8_K'} activation blocks")
+
+            def mk(O, quant=quant, rows=rows, cols=cols, data=copies.data, b=b, small=small, xh=xin.cpu().numpy()):
+                xb, R = (O.quantize_row_q8_0 if small else O.quantize_row_q8_k)(xh), 512
+                return [(lambda r0=r0: O.gemv_rows(quant, data, rows, cols, xb, r0, min(rows, r0 + R)),
+                         b * (min(rows, r0 + R) - r0) / rows) for r0 in range(0, rows, R)]
+            cpu_slices(name, mk, "GB/s", 1e9, "row slices of the GEMV")
             for w in ws:
                 w.free()
         # A8: f32-activation vec_dot (dequantize x f32 dot) at the Q4_K attn shape and Q6_K down
@@ -511,6 +534,15 @@ def main() -> int:
             us = gus(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts[xa], cols, y, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + 4 * cols + 4 * rows
             hbm_line(name, b, us, f"{rows}x{cols}, f32 activation")
+
+            def mk(O, quant=quant, rows=rows, cols=cols, data=copies.data, b=b, xh=acts[xa].cpu().numpy()):
+                R = 256
+                return [(lambda r0=r0: O.vec_dot_f32(quant, (min(rows, r0 + R) - r0, cols),
+                                                     rows_of(data, quant, r0, min(rows, r0 + R), cols), xh,
+                                                     min(rows, r0 + R) - r0),
+                         b * (min(rows, r0 + R) - r0) / rows) for r0 in range(0, rows, R)]
+            cpu_slices(name, mk, "GB/s", 1e9, "row slices of the f32 vec_dot")
+            cpu_jobs.append(("same", name.replace(" f32", " f32 tolerance"), name))
             us = gus(lambda i, st: jk.dev_vec_dot_f32_tol(ws[i % len(ws)], acts[xa], cols, y, rows, st), len(ws))
             hbm_line(name.replace(" f32", " f32 tolerance"), b, us,
                      f"{rows}x{cols}, f32 activation, within 1e-5 of the output's L2 norm (four FMA accumulators "
@@ -530,6 +562,13 @@ def main() -> int:
                     us = gus(lambda i, st: jk.dev_gemv_q8(ws[i % len(ws)], xq, cols // 256, y, rows, st), len(ws))
                     hbm_line(f"gemv_tq2_0_q8_k {rows}x{cols}", wbytes + cols // 256 * 292 + 4 * rows, us,
                              "C5, Q8_K activation blocks")
+
+                    def mk(O, rows=rows, cols=cols, data=copies.data, b=wbytes + cols // 256 * 292 + 4 * rows,
+                           xh=xin.cpu().numpy()):
+                        xb, R = O.quantize_row_q8_k(xh), 512
+                        return [(lambda r0=r0: O.gemv_rows(jk.TQ2_0, data, rows, cols, xb, r0, min(rows, r0 + R)),
+                                 b * (min(rows, r0 + R) - r0) / rows) for r0 in range(0, rows, R)]
+                    cpu_slices(f"gemv_tq2_0_q8_k {rows}x{cols}", mk, "GB/s", 1e9, "row slices of the GEMV")
                 for m in (1, 128):
                     xin = torch.randn(m, cols, generator=gen).to(dev)
                     aq = torch.empty(m * cols, dtype=torch.int8, device=dev)
@@ -540,9 +579,8 @@ def main() -> int:
                                   len(ws))
                     b = wbytes + m * (cols + 4) + 4 * m * rows
                     name = f"bitlinear_{qname} {rows}x{cols} M={m}"
-                    if quant in (jk.TQ2_0, jk.I2_S):
-                        cpu_jobs.append(("bitlinear", name, quant, rows, cols, copies.data, aq.cpu().numpy(),
-                                         asc.cpu().numpy(), m, b))
+                    cpu_jobs.append(("bitlinear", name, quant, rows, cols, copies.data, aq.cpu().numpy(),
+                                     asc.cpu().numpy(), m, b))
                     if m == 1:
                         hbm_line(name, b, us, "C5, per-token absmax i8 activation")
                     else:
@@ -586,6 +624,14 @@ def main() -> int:
             name = f"gemm_repacked {jk.QUANT_NAMES[quant]} M=512"
             secondary[name] = {"us": round(us, 3), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                                "bound": "mfma", "workload": f"{N}x{K} weights x {M} tokens, kernel only"}
+
+            def mk(O, quant=quant, data=copies.data, xh=xin.cpu().numpy(), M=M, N=N, K=K):
+                q, sc, mn, cps = O.repack_logical(quant, (N, K), data, N, K)
+                ga, R = O.ActQ8(xh, M, K), 64
+                return [(lambda r0=r0: O.gemm_logical_rows(q, sc, mn, cps, K, ga, 0, M, r0, min(N, r0 + R)),
+                         2.0 * M * (min(N, r0 + R) - r0) * K) for r0 in range(0, N, R)]
+            cpu_slices(name, mk, "TOPS", 1e12, f"slices of 64 weight rows x {M} tokens (the load-time repack not timed)")
+            cpu_jobs.append(("same", f"gemm_repacked_tol {jk.QUANT_NAMES[quant]} M=512", name))
             log(f"  {name:28s} {us:8.2f} us  {tops:7.2f} TOPS")
             if quant in (jk.Q4_K, jk.Q6_K, jk.Q3_K):  # tolerance mode of the K-quant prefill formats
                 us = gus(lambda i, st: jk.dev_gemm_repacked_tol(ws[i % len(ws)], act, y, M * N, 0, N, st), len(ws))
@@ -624,6 +670,14 @@ def main() -> int:
             us = gus(lambda i, st: jk.dev_vec_dot_f32(ws[i % len(ws)], acts["x"], cols, y, rows, st), len(ws))
             b = rows * (cols // jk.BLOCK_ELEMENTS[quant]) * jk.BLOCK_BYTES[quant] + 4 * cols + 4 * rows
             hbm_line(f"vec_dot_{jk.QUANT_NAMES[quant].lower()} f32", b, us, f"{rows}x{cols}, f32 activation")
+
+            def mk(O, quant=quant, rows=rows, cols=cols, data=copies.data, b=b, xh=acts["x"].cpu().numpy()):
+                R = 256
+                return [(lambda r0=r0: O.vec_dot_f32(quant, (min(rows, r0 + R) - r0, cols),
+                                                     rows_of(data, quant, r0, min(rows, r0 + R), cols), xh,
+                                                     min(rows, r0 + R) - r0),
+                         b * (min(rows, r0 + R) - r0) / rows) for r0 in range(0, rows, R)]
+            cpu_slices(f"vec_dot_{jk.QUANT_NAMES[quant].lower()} f32", mk, "GB/s", 1e9, "row slices of the f32 vec_dot")
             for w in ws:
                 w.free()
         # Greedy lm_head: Q6_K 128256 x 4096 GEMV with argmax_f32 fused into the launch, against
@@ -639,6 +693,13 @@ def main() -> int:
         us = gus(lambda i, st: jk.dev_gemv_q8_argmax(ws_lm[i % len(ws_lm)], xq, None, cols // 256, None, idx, amw, st),
                       len(ws_lm))
         hbm_line("lm_head Q6_K gemv+argmax", b - 4 * rows, us, f"{rows}x{cols}, fused argmax, no logits written")
+
+        def mk(O, rows=rows, cols=cols, data=copies.data, b=b, xh=acts["x"].cpu().numpy()):
+            xb, R = O.quantize_row_q8_k(xh), 2048
+            return [(lambda r0=r0: O.gemv_rows(jk.Q6_K, data, rows, cols, xb, r0, min(rows, r0 + R)),
+                     b * (min(rows, r0 + R) - r0) / rows) for r0 in range(0, rows, R)]
+        cpu_slices("lm_head Q6_K gemv, argmax", mk, "GB/s", 1e9, "row slices of the lm_head GEMV (the argmax not timed)")
+        cpu_jobs.append(("same", "lm_head Q6_K gemv+argmax", "lm_head Q6_K gemv, argmax"))
 
         def two(i, st):
             jk.dev_gemv_q8(ws_lm[i % len(ws_lm)], xq, cols // 256, y, rows, st)
@@ -718,12 +779,20 @@ def main() -> int:
             f"{s2['device_allocs'] - s1['device_allocs']} device allocations over 200 warm calls)")
         jk.host_cache_invalidate(hv)
         jk.host_cache_set_limit(0)
-        del hraw, hv
+        cpu_jobs.append(("percall", "host_tier gemv_q4_k_q8_k 14336x4096",
+                         lambda O, d=hraw, rows=rows, cols=cols: (
+                             lambda xb=O.quantize_row_q8_k(synth.activations(cols, seed=1201)):
+                             (lambda: O.gemv_q8(jk.Q4_K, (rows, cols), d, xb, rows)))(),
+                         "gemv_q4_k_q8_k over the same host slices"))
+        del hv
         # A3-A5: quantizers (one activation row of the decode step; the prefill activation)
         yq = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device=dev)
         us = gus(lambda i, st: jk.dev_quantize_row_q8_k(acts["h"], 14336, yq, 56, st), 64)
         secondary["quantize_row_q8_k 14336"] = {"us": round(us, 3), "bound": "latency",
                                                 "workload": "ffn_down input, 56 blocks"}
+        cpu_jobs.append(("percall", "quantize_row_q8_k 14336",
+                         lambda O, xh=acts["h"].cpu().numpy(): (lambda: O.quantize_row_q8_k(xh)),
+                         "quantize_row_q8_k of the same 14336 values"))
         log(f"  {'quantize_row_q8_k 14336':28s} {us:8.2f} us")
         M, K = 512, 4096
         xin = torch.randn(M, K, generator=gen).to(dev)
@@ -733,6 +802,11 @@ def main() -> int:
         us = gus(lambda i, st: jk.dev_quantize_act_q8(xin, M, K, act, st), 32)
         b = M * K * 4 + M * K + M * (K // 32) * 8
         hbm_line("quantize_act_q8 512x4096", b, us, "QuantizedActQ8::quantize_into for the prefill GEMM")
+
+        def mk(O, xh=xin.cpu().numpy(), M=M, K=K, b=b):
+            R = 32
+            return [(lambda t0=t0: O.ActQ8(xh[t0:t0 + R], R, K), b * R / M) for t0 in range(0, M, R)]
+        cpu_slices("quantize_act_q8 512x4096", mk, "GB/s", 1e9, "32-token slices of the same quantization")
         del xin, store
 
     del rd_buf
@@ -826,7 +900,24 @@ def main() -> int:
             del q, sc, mn, gact
         for job in cpu_jobs:
             sec = secondary.get(job[1])
-            if sec is None:
+            if sec is None or job[0] == "same":
+                continue
+            if job[0] == "slices":
+                _, name, make, unit, scale, what = job
+                attach(sec, unit, scale, *(lambda sl: (cpu_rate(sl, 1.5, 1), cpu_rate(sl, 0.75, ncores)))(make(O)), what)
+                continue
+            if job[0] == "percall":
+                _, name, make, what = job
+                fn = make(O)
+                calls, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < 1.0:
+                    fn()
+                    calls += 1
+                el = time.perf_counter() - t0
+                sec["cpu_baseline"] = {"value": round(el / calls * 1e6, 2), "unit": "us per call", "cores": 1,
+                                       "kind": "port", "sample": f"{calls} calls of {what} in {el:.1f} s, oracle C "
+                                                                 "restatement of the scalar fallback, 1 thread"}
+                log(f"cpu baseline {name}: {el / calls * 1e6:.1f} us per call")
                 continue
             if job[0] == "gemm_i8":
                 _, name, ah, bh, M, N, K = job
@@ -870,6 +961,16 @@ def main() -> int:
                     if tsec is not None:  # the same reference computation beside the tolerance-mode line
                         tsec["cpu_baseline"] = sec["cpu_baseline"]
                         tsec["cpu_baseline_all_cores"] = sec["cpu_baseline_all_cores"]
+        # lines whose reference computation is another line's (tolerance modes, the fused argmax, the
+        # synthetic-input decode step) carry that line's CPU figures
+        for job in cpu_jobs:
+            if job[0] == "same" and job[1] in secondary and "cpu_baseline" in secondary.get(job[2], {}):
+                for key in ("cpu_baseline", "cpu_baseline_all_cores"):
+                    if key in secondary[job[2]]:
+                        secondary[job[1]][key] = secondary[job[2]][key]
+        for k, v in secondary.items():
+            if k.startswith("decode step") and isinstance(v, dict):
+                v["cpu_baseline"], v["cpu_baseline_all_cores"] = cpu, cpu_all
 
     rec = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
