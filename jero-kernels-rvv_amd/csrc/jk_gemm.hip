@@ -975,7 +975,7 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
     tacc[0] = tacc[1] = v32f{0};
     const v16i bias = magic_acc();
     const int arow = 64 * wn + jl;
-    auto chunk = [&](const Q8Stage<TN> &S) {
+    auto chunk_tol = [&](const Q8Stage<TN> &S) {
 #pragma unroll 1
         for (int st = 0; st < kSteps; ++st) {
             const int pc = 2 * st + hl;  // 16-byte piece: block st, half hl
@@ -993,32 +993,59 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
                 const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ (t & 7)) << 4));
                 const float xs = S.xs[t * 4 + st];
                 v16i c[2];
-                if constexpr (EXACT) {
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, v16i{0}, 0, 0, 0);
-                    const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
+                for (int nt = 0; nt < 2; ++nt) c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, bias, 0, 0, 0);
+                const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
+                // the bias's share of the group, B * ws * xs, taken off the accumulators on the matrix
+                // core, so each output costs one fused multiply-add of the biased bits
+                tacc[tb] = __builtin_amdgcn_mfma_f32_32x32x1f32(wsb, xs, tacc[tb], 0, 0, 0);
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
+                for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-                        for (int v = 0; v < 16; ++v)
-                            tacc[tb][16 * nt + v] = tacc[tb][16 * nt + v] + (float)c[nt][v] * pr[16 * nt + v];
-                } else {
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-                        c[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, bias, 0, 0, 0);
-                    const v32f pr = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
-                    // the bias's share of the group, B * ws * xs, taken off the accumulators on the matrix
-                    // core, so each output costs one fused multiply-add of the biased bits
-                    tacc[tb] = __builtin_amdgcn_mfma_f32_32x32x1f32(wsb, xs, tacc[tb], 0, 0, 0);
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v)
-                            tacc[tb][16 * nt + v] =
-                                __builtin_fmaf(__int_as_float(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
-                }
+                    for (int v = 0; v < 16; ++v)
+                        tacc[tb][16 * nt + v] =
+                            __builtin_fmaf(__int_as_float(c[nt][v]), pr[16 * nt + v], tacc[tb][16 * nt + v]);
             }
+        }
+    };
+
+    // Bit-exact mode: the chunk's 8 (step, token block) pairs software-pipelined, the MFMAs of pair
+    // t + 1 issued before the epilogue of pair t on a ring of two register sets, a scheduling barrier
+    // after each pair so the compiler keeps that shape (unconstrained, it hoists further and spills);
+    // each output still takes its groups in K order. 146.1 against 150.7 us at 512 tokens.
+    auto chunk_exact = [&](const Q8Stage<TN> &S) {
+        v16i c[2][2];
+        v32f pr[2];
+        auto mfmas = [&](int t, int slot) {
+            const int st = t >> 1, tb = t & 1, pc = 2 * st + hl;
+            v4i aq[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int r = arow + 32 * nt;
+                aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ (r & 7)) << 4));
+            }
+            const float ws = f16_finite(S.ws[(64 * wn + lane) * 4 + st]);
+            const int tk = 64 * wmi + 32 * tb + jl;
+            const v4i bq = *reinterpret_cast<const v4i *>(S.x + tk * 128 + ((pc ^ (tk & 7)) << 4));
+            const float xs = S.xs[tk * 4 + st];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) c[slot][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, v16i{0}, 0, 0, 0);
+            pr[slot] = __builtin_amdgcn_mfma_f32_32x32x1f32(ws, xs, v32f{0}, 0, 0, 0);
+        };
+        auto epilogue = [&](int t, int slot) {
+            const int tb = t & 1;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    tacc[tb][16 * nt + v] = tacc[tb][16 * nt + v] + (float)c[slot][nt][v] * pr[slot][16 * nt + v];
+        };
+        mfmas(0, 0);
+#pragma unroll
+        for (int t = 0; t < 2 * kSteps; ++t) {
+            if (t + 1 < 2 * kSteps) mfmas(t + 1, (t + 1) & 1);
+            epilogue(t, t & 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -1032,12 +1059,14 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
         else JK_WAIT_VMCNT(0);
         stage_barrier();
         if (kc >= 2 && kc + 1 < nchunks) issue(sB, kc + 1);
-        chunk(sA);
+        if constexpr (EXACT) chunk_exact(sA);
+        else chunk_tol(sA);
         if (kc + 1 >= nchunks) break;
         JK_WAIT_VMCNT(0);
         stage_barrier();
         if (kc + 2 < nchunks) issue(sA, kc + 2);
-        chunk(sB);
+        if constexpr (EXACT) chunk_exact(sB);
+        else chunk_tol(sB);
     }
 
     const size_t ld = (size_t)(r1 - r0);
