@@ -1091,8 +1091,8 @@ gemm_q8_0_tol_dma_128(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, i
     gemm_q8_0_tol_dma<128>(w, a, y, r0, r1);
 }
 
-// The bit-exact Q8_0 prefill on the same staging (one round of resident workgroups: 8% faster than
-// the register-staged 128 x 64 tiles at 448-512 tokens on 14336 rows, 2-3% slower at 768-1536)
+// The bit-exact Q8_0 prefill on the same staging (launched where it measured faster than the
+// register-staged 128 x 64 tiles; see launch_gemm)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 gemm_q8_0_exact_dma_128(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r1) {
     gemm_q8_0_tol_dma<128, true>(w, a, y, r0, r1);
@@ -2004,11 +2004,13 @@ template <int Q, int GB>
 static jk_status launch_gemm(hipStream_t s, const WeightDev &w, const jk_act_q8 &a, float *y, int r0, int r1) {
     if constexpr (Q == JK_Q8_0 && GB == 1) {
         // Q8_0 with per-32 activation scales (not BitLinear's one scale per token), whole 128-element
-        // chunks, 1.5 to 2 128 x 128 tiles per CU (one round of two resident workgroups a CU): the
-        // global-to-LDS staged tiles
+        // chunks, 1.5 to 2 128 x 128 tiles per CU (one round of two resident workgroups a CU) or 6 and
+        // more: the global-to-LDS staged tiles (14336 x 4096: 144 against 164 us at 512 tokens, 477
+        // against 505 at 2048; at 768-1536 tokens the register-staged 128 x 64 tiles tie or win by 2%)
         const long ncu = cu_count();
         const long t128 = (long)(r1 - r0 + 127) / 128 * (((long)a.m + 127) / 128);
-        if (2 * t128 >= 3 * ncu && t128 <= 2 * ncu && w.cols % 128 == 0 && a.k_blocks32 * 32 == (size_t)w.cols) {
+        const bool one_round = 2 * t128 >= 3 * ncu && t128 <= 2 * ncu;
+        if ((one_round || t128 >= 6 * ncu) && w.cols % 128 == 0 && a.k_blocks32 * 32 == (size_t)w.cols) {
             const size_t ntn = (size_t)(r1 - r0 + 127) / 128, ntm = (a.m + 127) / 128;
             JK_LAUNCH("gemm_q8_0_exact_dma_128", gemm_q8_0_exact_dma_128, dim3((unsigned)((ntn + 7) / 8 * 8 * ntm)),
                       dim3(256), 0, s, w, a, y, r0, r1);
