@@ -168,3 +168,80 @@ def test_host_mirrors(gpu):
         jk.gemm_i8_vector(a[:-1], m, b, 0, rows, k)  # A one byte short of m * k
     with pytest.raises(jk.TensorBoundsError):
         jk.gemm_i8_vector(a, m, b, 0, rows + 1, k)  # the range runs past B
+
+
+def test_graph_replays_of_staged_and_tolerance_kernels(gpu):
+    """The kernels staged by global-to-LDS loads (jk_gemm_i8 on 128 x 256 tiles, the Q8_0 tolerance
+    and bit-exact 128 x 128 GEMM tiles) and the tolerance BitLinear / split-block vec_dot kernels,
+    captured once in one HIP graph and replayed with new inputs, eager work and synchronizations in
+    between: every replay equals the same calls made eagerly, bit for bit."""
+    import jk
+    from jk import synth
+
+    torch = gpu
+    M, N, K = 512, 14336, 256
+    a = torch.empty(M * K, dtype=torch.int8, device="cuda")
+    b = torch.from_numpy(np.random.default_rng(1).integers(-128, 128, N * K, dtype=np.int8)).cuda()
+    c = torch.empty(M * N, dtype=torch.int32, device="cuda")
+    wq = jk.Weight(jk.TensorView("wq", jk.Q8_0, (N, K), synth.gguf_weights(jk.Q8_0, N, K, seed=5)), N, K)
+    x = torch.empty(M, K, device="cuda")
+    need = jk.act_q8_bytes(M, K)
+    st = torch.empty(need, dtype=torch.uint8, device="cuda")
+    act = jk.act_q8_bind(st, need, M, K)
+    assert jk.gemm_plan(wq, act, 0, N, True) == "gemm_q8_0_tol_dma_128"
+    assert jk.gemm_plan(wq, act, 0, N, False) == "gemm_q8_0_exact_dma_128"
+    yt = torch.empty(M * N, device="cuda")
+    ye = torch.empty(M * N, device="cuda")
+    rows, cols, m = 6912, 2560, 128
+    wt = jk.Weight(jk.TensorView("wt", jk.TQ2_0, (rows, cols), synth.gguf_weights(jk.TQ2_0, rows, cols, seed=6)),
+                   rows, cols)
+    aq = torch.empty(m * cols, dtype=torch.int8, device="cuda")
+    asc = torch.empty(m, device="cuda")
+    yb = torch.empty(m * rows, device="cuda")
+    wv = jk.Weight(jk.TensorView("wv", jk.Q4_K, (4096, 4096), synth.gguf_weights(jk.Q4_K, 4096, 4096, seed=7)),
+                   4096, 4096)
+    xv = torch.empty(4096, device="cuda")
+    yv = torch.empty(4096, device="cuda")
+
+    def step(s):
+        jk.dev_gemm_i8(a, M * K, M, b, N * K, 0, N, K, c, M * N, s)
+        jk.dev_quantize_act_q8(x, M, K, act, s)
+        jk.dev_gemm_repacked_tol(wq, act, yt, M * N, 0, N, s)
+        jk.dev_gemm_repacked(wq, act, ye, M * N, 0, N, s)
+        jk.dev_bitlinear_i8_tol(wt, aq, asc, m, cols, yb, m * rows, s)
+        jk.dev_vec_dot_f32_tol(wv, xv, 4096, yv, 4096, s)
+
+    def fill(seed):
+        g = torch.Generator().manual_seed(seed)
+        a.copy_(torch.randint(-128, 128, (M * K,), dtype=torch.int8, generator=g))
+        x.copy_(torch.randn(M, K, generator=g))
+        aq.copy_(torch.randint(-127, 128, (m * cols,), dtype=torch.int8, generator=g))
+        asc.copy_(torch.rand(m, generator=g) * 0.05)
+        xv.copy_(torch.randn(4096, generator=g))
+
+    outs = (c, yt, ye, yb, yv)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    fill(0)
+    with torch.cuda.stream(side):
+        step(side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(torch.cuda.current_stream().cuda_stream)
+    for seed in (1, 2, 3):
+        fill(seed)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        replay = [o.clone() for o in outs]
+        for o in outs:
+            o.fill_(7)
+        step(torch.cuda.current_stream().cuda_stream)  # the same calls, eagerly
+        torch.cuda.synchronize()
+        for name, r, e in zip(("gemm_i8", "gemm tol", "gemm exact", "bitlinear tol", "vec_dot tol"), replay, outs):
+            assert torch.equal(r.view(torch.int32), e.view(torch.int32)), (seed, name)
+    del g
+    for w in (wq, wt, wv):
+        w.free()
