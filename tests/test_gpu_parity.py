@@ -828,6 +828,7 @@ def test_gemm_tol_split_k(gpu, quant, m, chunks):
 # ------------------------------------------------------------------ BitLinear
 @pytest.mark.parametrize("quant", [TQ1_0, TQ2_0, I2_S, Q8_0])
 @pytest.mark.parametrize("m,rows,cols", [(1, 7, 256), (3, 64, 2560), (2, 2560, 6912),
+                                         (1, 6912, 2560), (1, 2560, 6912),  # one token, the C5 shapes
                                          # token batches take the int8-MFMA path
                                          (16, 300, 2560), (37, 129, 768), (128, 2560, 6912), (128, 6912, 2560)])
 def test_bitlinear(gpu, quant, m, rows, cols):
