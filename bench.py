@@ -132,11 +132,12 @@ def main() -> int:
                          "feed-forward block; also reported as a secondary line)")
     ap.add_argument("--down", choices=("fused", "split"), default="split",
                     help="ffn_down activation: quantized inside the GEMV launch, or by its own launch")
-    ap.add_argument("--profile-loop", choices=("bitlinear", "gemm", "vec_dot"),
+    ap.add_argument("--profile-loop", choices=("bitlinear", "gemm", "vec_dot", "decode"),
                     help="instead of the benchmark: launch one workload's kernels eagerly (no graph) 20 times each "
                          "and exit -- the program a rocprofv3 counter pass runs (bitlinear: the 128-token C5 "
                          "BitLinear, both modes; gemm: the Q8_0 512-token GEMM, both modes; vec_dot: the f32 "
-                         "vec_dot lines, both modes)")
+                         "vec_dot lines, both modes; decode: the decode step's launches over eight layers, then "
+                         "the streaming read of each launch's byte count)")
     args = ap.parse_args()
 
     if args.profile_loop:
@@ -1038,6 +1039,36 @@ def profile_loop(which: str) -> int:
                 fn(w, act, y, M * N, 0, N)
         torch.cuda.synchronize()
         w.free()
+    elif which == "decode":
+        # the decode step's launches on eight distinct layers (so the weights stream from HBM), in
+        # the step's order, then the streaming read of each launch's byte count
+        L = 8
+        mats = {name: (q, r, c) for name, q, r, c in synth.LLAMA3_8B_LAYER}
+        raw = {name: synth.gguf_weights(q, r, c, seed=3 + i) for i, (name, (q, r, c)) in enumerate(mats.items())}
+        ws = [{name: jk.Weight(jk.TensorView(name, q, (r, c), raw[name]), r, c) for name, (q, r, c) in mats.items()}
+              for _ in range(L)]
+        x = torch.randn(4096, generator=gen).cuda()
+        outs = {name: torch.empty(r, dtype=torch.float32, device="cuda") for name, (q, r, c) in mats.items()}
+        h_q8 = torch.empty(56 * jk.BLOCK_Q8K.itemsize, dtype=torch.uint8, device="cuda")
+        groups = (("attn_q", "attn_k", "attn_v"), ("attn_output",), ("ffn_gate", "ffn_up"))
+        for i in range(n):
+            lw = ws[i % L]
+            for names in groups:
+                jk.dev_gemv_q8_batch([(lw[nm], None, x, outs[nm], 0, mats[nm][1]) for nm in names])
+            jk.dev_quantize_row_q8_k_gated(jk.ACT_SWIGLU, outs["ffn_gate"], outs["ffn_up"], 14336, h_q8, 56)
+            jk.dev_gemv_q8_batch([(lw["ffn_down"], h_q8, None, outs["ffn_down"], 0, 4096)])
+        torch.cuda.synchronize()
+        buf = torch.empty(800_000_000, dtype=torch.uint8, device="cuda")
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        for names in groups + (("ffn_down",),):
+            nb = sum(gemv_bytes(*mats[nm], jk) for nm in names)
+            span = (nb + 65535) // 65536 * 65536
+            for i in range(n):
+                jk.dev_measure_stream_read(buf.data_ptr() + (i % (buf.numel() // span)) * span, nb, sink)
+        torch.cuda.synchronize()
+        for lw in ws:
+            for w in lw.values():
+                w.free()
     else:
         for quant, rows, cols in ((jk.Q4_K, 4096, 4096), (jk.Q6_K, 4096, 14336)):
             w = jk.Weight(jk.TensorView("w", quant, (rows, cols), synth.gguf_weights(quant, rows, cols, seed=8)),

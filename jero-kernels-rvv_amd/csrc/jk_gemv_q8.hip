@@ -34,6 +34,7 @@ namespace jk {
 constexpr int kXkBytes = 336;
 // Q8_0 block staged in LDS: qs[32] @0, d f32 @32, sum of qs i32 @36: 48 bytes.
 constexpr int kX0Bytes = 48;
+constexpr int kMaxLdsX = 60 * 1024;  // staged activation; static LDS stays within the 64 KB default
 
 struct XkLds {
     const uint8_t *p;
@@ -446,6 +447,11 @@ __device__ __forceinline__ void xstage_raw(const XRegs<NW, false, Q> &xr, int nd
     }
 }
 
+// Formats whose block value reads the recomputed sums of the staged caller quants: the block sum
+// (Q4_0, Q5_0) or the per-16 sums (Q6_K, TQ2_0 / TQ1_0). Q8_0 reads neither, Q4_K and Q5_K read the
+// caller's bsums as given.
+template <int Q> constexpr bool kStagedSums = Q == JK_Q4_0 || Q == JK_Q5_0 || Q == JK_Q6_K || Q == JK_TQ2_0;
+
 // Sums of the staged caller quants: per-16 sums (Q8_K) or the block sum (Q8_0).
 template <int Q, int NW>
 __device__ __forceinline__ void xstage_sums(int nb, uint8_t *s_x) {
@@ -488,6 +494,22 @@ __device__ __forceinline__ void stage_finish(XRegs<NW, F32, Q> &xr, const GemvJo
     const int n4 = nb * T::XE / 4;         // f32 input: float4 count
     const int ndw = nb * (T::K ? 73 : 9);  // caller blocks: dword count
     const int nrounds = F32 ? (n4 + RD / 4 - 1) / (RD / 4) : (ndw + RD - 1) / RD;
+    if constexpr (!F32 && kStagedSums<Q> && QTraits<Q>::K) {
+        if (nrounds == 1) {
+            // (kept apart from the round loop below: after that loop the compiler's wait analysis
+            // treated registers its loads wrote as possibly pending and waited for every load --
+            // the weights included -- before the sums reused them, so the barrier after the sums
+            // held every wave of the workgroup until all their weights had arrived. Measured: Q6_K
+            // 4096 x 14336 11.45 -> 11.26 us, TQ2_0 2560 x 6912 4.82 -> 4.56 us; the 32-element
+            // formats keep the loop, as the split's registers cost them a wave per SIMD and
+            // 0.3 us)
+            xstage_raw<Q, NW>(xr, ndw, 0, s_x);
+            lds_barrier();
+            xstage_sums<Q, NW>(nb, s_x);
+            lds_barrier();
+            return;
+        }
+    }
     for (int rr = 0; rr < nrounds; ++rr) {
         if (rr > 0) {
             if constexpr (F32) xload_f32<NW, Q>(xr, job.xf, n4, rr);
@@ -497,7 +519,7 @@ __device__ __forceinline__ void stage_finish(XRegs<NW, F32, Q> &xr, const GemvJo
         else xstage_raw<Q, NW>(xr, ndw, rr, s_x);
     }
     lds_barrier();
-    if constexpr (!F32) {
+    if constexpr (!F32 && kStagedSums<Q>) {
         xstage_sums<Q, NW>(nb, s_x);
         lds_barrier();
     }
@@ -1062,7 +1084,6 @@ __global__ __launch_bounds__(256) void gemv_q8_global_kernel(WeightDev w, const 
 }
 
 // ------------------------------------------------------------------ launchers
-constexpr int kMaxLdsX = 60 * 1024;  // staged activation; static LDS stays within the 64 KB default
 
 // Resident workgroups per CU of a kernel at a given dynamic LDS size (queried once).
 template <class K>
