@@ -268,7 +268,8 @@ __device__ __forceinline__ float val_q6_k(const WReg<JK_Q6_K> &wr, const X &x) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int sc = (int)(int8_t)(comp(scv, j >> 2) >> (8 * (j & 3)));
-        sumi += sc * (S[j] - 32 * x.s16(j));
+        // (24-bit multiply, exact: |sc| <= 128 and |S - 32 s16| <= 16 * 63 * 128 + 32 * 16 * 128)
+        sumi += __mul24(sc, S[j] - 32 * x.s16(j));
     }
     return (d * xd) * (float)sumi;
 }
