@@ -135,7 +135,7 @@ def main() -> int:
     ap.add_argument("--profile-loop", choices=("bitlinear", "gemm", "vec_dot", "decode"),
                     help="instead of the benchmark: launch one workload's kernels eagerly (no graph) 20 times each "
                          "and exit -- the program a rocprofv3 counter pass runs (bitlinear: the 128-token C5 "
-                         "BitLinear, both modes; gemm: the Q8_0 512-token GEMM, both modes; vec_dot: the f32 "
+                         "BitLinear, both modes; gemm: the Q8_0 GEMM at 512, 64 and 128 tokens, both modes; vec_dot: the f32 "
                          "vec_dot lines, both modes; decode: the decode step's launches over eight layers, then "
                          "the streaming read of each launch's byte count)")
     args = ap.parse_args()
@@ -1026,18 +1026,19 @@ def profile_loop(which: str) -> int:
                 torch.cuda.synchronize()
                 w.free()
     elif which == "gemm":
-        N, K, M = 14336, 4096, 512
+        N, K = 14336, 4096
         w = jk.Weight(jk.TensorView("w", jk.Q8_0, (N, K), synth.gguf_weights(jk.Q8_0, N, K, seed=77)), N, K)
-        x = torch.randn(M, K, generator=gen).cuda()
-        need = jk.act_q8_bytes(M, K)
-        st = torch.empty(need, dtype=torch.uint8, device="cuda")
-        act = jk.act_q8_bind(st, need, M, K)
-        jk.dev_quantize_act_q8(x, M, K, act)
-        y = torch.empty(M * N, dtype=torch.float32, device="cuda")
-        for fn in (jk.dev_gemm_repacked_tol, jk.dev_gemm_repacked):
-            for _ in range(n):
-                fn(w, act, y, M * N, 0, N)
-        torch.cuda.synchronize()
+        for M in (512, 64, 128):
+            x = torch.randn(M, K, generator=gen).cuda()
+            need = jk.act_q8_bytes(M, K)
+            st = torch.empty(need, dtype=torch.uint8, device="cuda")
+            act = jk.act_q8_bind(st, need, M, K)
+            jk.dev_quantize_act_q8(x, M, K, act)
+            y = torch.empty(M * N, dtype=torch.float32, device="cuda")
+            for fn in (jk.dev_gemm_repacked_tol, jk.dev_gemm_repacked):
+                for _ in range(n):
+                    fn(w, act, y, M * N, 0, N)
+            torch.cuda.synchronize()
         w.free()
     elif which == "decode":
         # the decode step's launches on eight distinct layers (so the weights stream from HBM), in
