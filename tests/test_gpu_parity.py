@@ -308,6 +308,22 @@ def test_gemv_q8_long_rows_caller_blocks(gpu, quant, cols):
     assert same_bits(got, ref), mismatch(got, ref)
 
 
+@pytest.mark.parametrize("quant", [Q6_K, TQ2_0])
+@pytest.mark.parametrize("rows,cols", [(100, 256 * 40), (2000, 256 * 60), (2000, 256 * 56), (7, 256 * 33)])
+def test_gemv_q8_caller_blocks_staging_rounds(gpu, quant, rows, cols):
+    """The single-pass GEMV (one row a wave for rows of 33-64 blocks) with caller blocks of the formats
+    whose dots read the recomputed per-16 sums: activations staged in two rounds (4-wave workgroups
+    at 33 and 40 blocks, 8-wave ones at 60) and in one (8-wave workgroups at 56 blocks, the ffn_down
+    shape), each == the oracle bit for bit."""
+    torch = gpu
+    raw = synth.random_weights(quant, rows, cols, seed=rows + cols, specials=True)
+    xq = x_blocks(quant, synth.activations(cols, 4))
+    ref = O.gemv_q8(quant, [rows, cols], raw, xq, rows)
+    w = jk.Weight(jk.TensorView("w", quant, [rows, cols], raw), rows, cols)
+    got = gpu_gemv(torch, w, xq)
+    assert same_bits(got, ref), mismatch(got, ref)
+
+
 def test_gemv_q8_caller_q8k_with_inconsistent_bsums(gpu):
     """Q6_K / TQ2_0 dots use the quants themselves, Q4_K uses bsums as given (quant_q8.rs:1834-2003)."""
     torch = gpu
