@@ -630,6 +630,34 @@ def test_gemm_q8_0_prefill_shape_rows_sample(gpu, m):
     w.free()
 
 
+def test_gemm_q8_0_prefill_full_matrix_vs_exact_product(gpu):
+    """The C4 prefill GEMM at 512 tokens over all 14336 x 512 outputs against the exact product of
+    its operands: the Q8_0 weights (d * q) times the QuantizedActQ8 activations (scale * q), both
+    exact in float64, multiplied and summed in float64 -- a reference computed without the
+    reference's recipe. Both modes within 1e-5 of each token's output-row L2 norm (the bit-exact
+    mode's distance is the recipe's own f32 rounding)."""
+    torch = gpu
+    rows, cols, m = 14336, 4096, 512
+    raw = synth.gguf_weights(Q8_0, rows, cols, seed=21)
+    x = synth.activations((m, cols), 22)
+    w = jk.Weight(jk.TensorView("ffn", Q8_0, [cols, rows], raw), rows, cols)
+    blk = np.frombuffer(raw, dtype=np.dtype([("d", "<f2"), ("qs", "i1", (32,))])).reshape(rows, cols // 32)
+    d = blk["d"].astype(np.float64)
+    d = np.where(np.isfinite(d), d, 0.0)  # f16_to_f32_finite
+    w64 = (d[..., None] * blk["qs"].astype(np.float64)).reshape(rows, cols)
+    act = O.ActQ8(x, m, cols)
+    x64 = (act.qs[:, :cols].astype(np.float64).reshape(m, cols // 32, 32)
+           * act.scales[:, : cols // 32].astype(np.float64)[..., None]).reshape(m, cols)
+    y64 = x64 @ w64.T
+    del w64
+    exact = gpu_gemm(torch, w, x, m)
+    tol = gpu_gemm_tol(torch, w, x, m, expect="gemm_q8_0_tol_dma_128")
+    we = assert_within_row_norm(exact, y64)
+    wt = assert_within_row_norm(tol, y64)
+    print(f"Q8_0 14336x4096 M=512 against the float64 product: bit-exact {we:.2e}, tolerance {wt:.2e} of the row norm")
+    w.free()
+
+
 @pytest.mark.parametrize("quant", ALL_FORMATS)
 @pytest.mark.parametrize("m", [500, 250, 128, 30])
 def test_gemm_tol_tile_shapes(gpu, quant, m):
