@@ -902,9 +902,11 @@ gemm_tol16_kernel(WeightDev w, jk_act_q8 a, float *__restrict__ y, int r0, int r
 // the compiler's dependency tracking keeps the reads of one stage free of the loads into the
 // other; each wave waits for its own loads of a stage (vmcnt) before a barrier publishes it.
 // A stage (35 KB): weights [row][8 x 16 B] and activation quants [token][8 x 16 B] with the
-// 16-byte piece p of row r at slot p ^ (r & 7) (the 32 rows or tokens an MFMA operand read
-// covers then fall on distinct banks in every group of 8 lanes), the f16 scales of the
-// chunk's four blocks per row, and the f32 activation scales per token.
+// 16-byte piece p of row r at slot p ^ ((r >> 1) & 7) (16 consecutive rows or tokens of an MFMA
+// operand read, which the LDS serves together, then fall on 16 distinct 16-byte bank groups: with
+// slot p ^ (r & 7) rows r and r + 8 collided, and the counters put bank conflicts in 58% of the
+// LDS-active cycles), the f16 scales of the chunk's four blocks per row, and the f32 activation
+// scales per token.
 template <int TN> struct alignas(16) Q8Stage {
     uint8_t a[TN * 128];
     uint8_t x[128 * 128];
@@ -941,13 +943,13 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
     const uint8_t *xsrc[XPW];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int n = 8 * (4 * wave + i) + rr, p = slot ^ (n & 7);
+        const int n = 8 * (4 * wave + i) + rr, p = slot ^ ((n >> 1) & 7);
         const int gn = min(n0 + n, r1 - 1);
         asrc[i] = w.planes + (size_t)(p & 1) * pstride + ((size_t)gn * (size_t)nb + (size_t)(p >> 1)) * 16;
     }
 #pragma unroll
     for (int i = 0; i < XPW; ++i) {
-        const int t = 8 * (XPW * wave + i) + rr, q = slot ^ (t & 7);
+        const int t = 8 * (XPW * wave + i) + rr, q = slot ^ ((t >> 1) & 7);
         const int gt = min(m0 + t, M - 1);
         xsrc[i] = reinterpret_cast<const uint8_t *>(a.qs) + (size_t)gt * a.k_padded + (size_t)(16 * q);
     }
@@ -983,14 +985,14 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const int r = arow + 32 * nt;
-                aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ (r & 7)) << 4));
+                aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ ((r >> 1) & 7)) << 4));
             }
             const float ws = f16_finite(S.ws[(64 * wn + lane) * 4 + st]);  // lane l: row of block l / 32
             const float wsb = ws * -kMagicF;  // exact: 1.5 * 2^23 times an 11-bit significand
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
                 const int t = 64 * wmi + 32 * tb + jl;
-                const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ (t & 7)) << 4));
+                const v4i bq = *reinterpret_cast<const v4i *>(S.x + t * 128 + ((pc ^ ((t >> 1) & 7)) << 4));
                 const float xs = S.xs[t * 4 + st];
                 v16i c[2];
 #pragma unroll
@@ -1022,11 +1024,11 @@ __device__ __forceinline__ void gemm_q8_0_tol_dma(const WeightDev &w, const jk_a
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const int r = arow + 32 * nt;
-                aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ (r & 7)) << 4));
+                aq[nt] = *reinterpret_cast<const v4i *>(S.a + r * 128 + ((pc ^ ((r >> 1) & 7)) << 4));
             }
             const float ws = f16_finite(S.ws[(64 * wn + lane) * 4 + st]);
             const int tk = 64 * wmi + 32 * tb + jl;
-            const v4i bq = *reinterpret_cast<const v4i *>(S.x + tk * 128 + ((pc ^ (tk & 7)) << 4));
+            const v4i bq = *reinterpret_cast<const v4i *>(S.x + tk * 128 + ((pc ^ ((tk >> 1) & 7)) << 4));
             const float xs = S.xs[tk * 4 + st];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) c[slot][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aq[nt], bq, v16i{0}, 0, 0, 0);
