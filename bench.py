@@ -143,7 +143,7 @@ def main() -> int:
     if args.profile_loop:
         return profile_loop(args.profile_loop)
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+        print(f"bench.py: the library runs on one GPU; --gpus {args.gpus} is not supported "
               "(the row-sharded multi-GPU design is documented, not built)", file=sys.stderr)
         return 2
 
